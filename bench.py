@@ -1,0 +1,265 @@
+"""Benchmark of the MI355X fp32 BLAS hot path (BASELINE.json metric):
+
+    fp32 GEMM TFLOP/s at 4096^3 (% MFMA peak); gemv HBM GB/s (% peak)
+
+A step is one call of the hot path on inputs already resident in HBM:
+  * value: the GEMM of BASELINE configs[2] -- C = 1.5 * A * B^T + 0.5 * C0 at M=N=K=4096 (one
+    mfr_sgemm launch);
+  * gemv: configs[1] -- y = 2 * op(A) * x + 0.5 * y0 with A [16384, 16384], for A and A^T.
+Inputs are synthetic (seeded numpy uniform[-1,1] / N(0,1)), as the configs describe.
+
+Timing: W untimed warmup steps, then K steps bracketed by stream synchronisation; the
+per-launch duration of the dominant kernel comes from HIP events recorded on the stream the
+kernel runs on. The CPU baseline (rank 0, N=1 only) times the reference's own packed
+AVX2/OpenMP GEMM (oracle/_ref, compiled from the reference sources) on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "fp32 GEMM TFLOP/s at 4096^3 (% MFMA peak); gemv HBM GB/s (% peak)"
+PEAK_FP32_MFMA_TFLOPS = 157.3   # MI355X dense fp32 matrix peak (AMD published)
+PEAK_HBM_GBS = 8000.0           # MI355X HBM3E peak (AMD published)
+GEMM_N = 4096
+GEMV_N = 16384
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def load_traffic(kernel: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE), scaled by
+    the copy-kernel calibration; None until profiles/traffic.json holds the kernel."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            data = json.load(f)
+        entry = data.get(kernel)
+        return None if entry is None else float(entry["bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def time_launches(mf, stream, launch, steps: int, warmup: int):
+    """(ms per step from host-synchronised wall clock, ms per step from HIP events)."""
+    for _ in range(warmup):
+        launch()
+    stream.synchronize()
+    start, end = mf.Event(), mf.Event()
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        launch()
+    end.record(stream)
+    stream.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    event_ms = start.elapsed_ms(end) / steps
+    return wall_ms, event_ms
+
+
+def bench_gemm(mf, stream, steps, warmup):
+    rng = np.random.default_rng(0)
+    n = GEMM_N
+    a = mf.DeviceArray.from_numpy(rng.uniform(-1, 1, (n, n)).astype(np.float32), stream)
+    b = mf.DeviceArray.from_numpy(rng.uniform(-1, 1, (n, n)).astype(np.float32), stream)
+    c0 = mf.DeviceArray.from_numpy(rng.standard_normal((n, n)).astype(np.float32), stream)
+    c = mf.DeviceArray.empty((n, n), stream)
+
+    def launch():
+        mf.gemm(a, b, alpha=1.5, c0=c0, beta=0.5, trans_b=True, out=c)
+
+    wall_ms, event_ms = time_launches(mf, stream, launch, steps, warmup)
+    flops = 2.0 * n * n * n
+    return {"wall_ms": wall_ms, "event_ms": event_ms, "flops": flops}
+
+
+def bench_gemv(mf, stream, steps, warmup, trans):
+    rng = np.random.default_rng(1)
+    n = GEMV_N
+    a = mf.DeviceArray.from_numpy(rng.uniform(-1, 1, (n, n)).astype(np.float32), stream)
+    x = mf.DeviceArray.from_numpy(rng.uniform(-1, 1, n).astype(np.float32), stream)
+    y0 = mf.DeviceArray.from_numpy(rng.standard_normal(n).astype(np.float32), stream)
+    y = mf.DeviceArray.empty((n,), stream)
+
+    def launch():
+        mf.sgemv(a, x, alpha=2.0, y0=y0, beta=0.5, trans=trans, out=y)
+
+    wall_ms, event_ms = time_launches(mf, stream, launch, steps, warmup)
+    nbytes = 4.0 * (n * n + 3 * n)  # A, x, y0 read; y written
+    a.close()
+    return {"wall_ms": wall_ms, "event_ms": event_ms, "bytes": nbytes}
+
+
+def bench_mlp(mf, stream, steps, warmup):
+    """X[4093,1023] x W[1023,4099] + bias with gelu-tanh fused (reported)."""
+    rng = np.random.default_rng(2)
+    m, k, n = 4093, 1023, 4099
+    x = mf.DeviceArray.from_numpy(rng.standard_normal((m, k)).astype(np.float32), stream)
+    w = mf.DeviceArray.from_numpy((rng.standard_normal((k, n)) / np.sqrt(k)).astype(np.float32),
+                                  stream)
+    bias = mf.DeviceArray.from_numpy(rng.uniform(-0.1, 0.1, n).astype(np.float32), stream)
+    out = mf.DeviceArray.empty((m, n), stream)
+
+    def launch():
+        mf.gemm(x, w, bias=bias, act=mf.ACT_GELU_TANH, out=out)
+
+    wall_ms, event_ms = time_launches(mf, stream, launch, steps, warmup)
+    return {"event_ms": event_ms, "flops": 2.0 * m * n * k}
+
+
+def cpu_baseline(seconds: float = 12.0):
+    """The reference's packed AVX2/OpenMP GEMM (oracle/_ref) on the box's host cores: the
+    matmul of configs[2] (4096^3, B read transposed), repeated for about `seconds`."""
+    import oracle
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+    n = GEMM_N
+    rng = np.random.default_rng(3)
+    a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    b_stored = rng.uniform(-1, 1, (n, n)).astype(np.float32)
+    c = np.empty((n, n), np.float32)
+    if oracle.has_reference():
+        ref = oracle.Reference()
+        ref.set_threads(threads)
+        kind = "reference"
+
+        def run():
+            ref.matmul(a, b_stored.T, parallel=True, out=c)
+    else:
+        port = oracle.Oracle()
+        port.set_threads(threads)
+        kind = "port"
+
+        def run():
+            port.matmul(a, b_stored.T)
+    run()  # warm-up (thread pool, page faults)
+    times = []
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < seconds or len(times) < 3:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 200:
+            break
+    median = float(np.median(times))
+    return {
+        "value": round(2.0 * n ** 3 / median / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": kind,
+        "sample": (f"{len(times)} calls of the packed CPU GEMM at 4096^3 (A * B^T, fp32), median "
+                   f"{median * 1e3:.1f} ms; the alpha/beta passes (memory-bound, <1% of the "
+                   f"work) not included"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["all", "gemm", "gemv", "mlp"], default="all",
+                    help="run one leg (for profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
+              f"--gpus {args.gpus}). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import mensurflow_amd as mf
+
+    if mf.device_count() < 1:
+        print("no gfx950 device visible", file=sys.stderr)
+        return 1
+    info = mf.device_info(0)
+    log(f"device: {info.name}, {info.compute_units} CUs, {info.clock_khz / 1e6:.2f} GHz, "
+        f"{info.memory_bytes / 2**30:.0f} GiB")
+    stream = mf.Stream(0)
+
+    result = {}
+    if args.only in ("all", "gemm"):
+        log("gemm 4096^3 NT ...")
+        result["gemm"] = bench_gemm(mf, stream, args.steps, args.warmup)
+    if args.only in ("all", "gemv"):
+        log("gemv 16384^2 N ...")
+        result["gemv_n"] = bench_gemv(mf, stream, args.steps, args.warmup, trans=False)
+        log("gemv 16384^2 T ...")
+        result["gemv_t"] = bench_gemv(mf, stream, args.steps, args.warmup, trans=True)
+    if args.only in ("all", "mlp"):
+        log("mlp 4093x1023x4099 + bias + gelu ...")
+        result["mlp"] = bench_mlp(mf, stream, max(5, args.steps // 5), args.warmup)
+    if args.only != "all":
+        print(json.dumps(result))
+        return 0
+
+    g = result["gemm"]
+    tflops = g["flops"] / (g["wall_ms"] * 1e-3) / 1e12
+    kernel_tflops = g["flops"] / (g["event_ms"] * 1e-3) / 1e12
+    gemv = {}
+    for key, trans in (("gemv_n", False), ("gemv_t", True)):
+        r = result[key]
+        gbs = r["bytes"] / (r["wall_ms"] * 1e-3) / 1e9
+        kernel_gbs = r["bytes"] / (r["event_ms"] * 1e-3) / 1e9
+        traffic = load_traffic("sgemv_t" if trans else "sgemv_n")
+        gemv["T" if trans else "N"] = {
+            "value": round(gbs, 1),
+            "unit": "GB/s",
+            "us_per_call": round(r["event_ms"] * 1e3, 2),
+            "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(kernel_gbs / PEAK_HBM_GBS, 4),
+                         "traffic": traffic},
+        }
+    mlp = result["mlp"]
+    line = {
+        "metric": METRIC,
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(g["wall_ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "sgemm M=N=K=4096, transB, alpha=1.5, beta=0.5 (BASELINE configs[2]); "
+                        "gemv 16384^2 N and T, alpha=2, beta=0.5 (configs[1])",
+            "m": GEMM_N, "n": GEMM_N, "k": GEMM_N,
+            "device": info.name, "compute_units": info.compute_units,
+        },
+        "roofline": {"bound": "mfma", "achieved": round(kernel_tflops, 3),
+                     "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(kernel_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
+                     "traffic": load_traffic("sgemm_4096_nt")},
+        "gemv": gemv,
+        "mlp_fused": {"tflops": round(mlp["flops"] / (mlp["event_ms"] * 1e-3) / 1e12, 3),
+                      "ms_per_call": round(mlp["event_ms"], 4),
+                      "frac": round(mlp["flops"] / (mlp["event_ms"] * 1e-3) / 1e12
+                                    / PEAK_FP32_MFMA_TFLOPS, 4)},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline (reference packed GEMM on host cores) ...")
+        line["cpu_baseline"] = cpu_baseline()
+    stream.close()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,219 @@
+/*
+ * mfr_rocm.h -- the C ABI of the MI355X (gfx950) backend for mensurflow's fp32 BLAS hot path.
+ *
+ * Everything the C++17 backend (mensurflow_amd/host/src/backends/rocm/) needs from HIP goes
+ * through these functions; nothing above this header includes a HIP header. The library is
+ * built by hipcc into libmfr_rocm.so.
+ *
+ * Conventions
+ *   - Every function returns 0 on success and a nonzero MFR_E_* code on failure; the message of
+ *     the last failure on the calling thread is returned by mfr_last_error(). No C++ exception
+ *     crosses this boundary.
+ *   - Sizes and strides are int64 element counts (not bytes). A "row stride" rs and "column
+ *     stride" cs locate element (r, c) of a matrix at base + r*rs + c*cs.
+ *   - Compute entry points enqueue work on a stream and return before the device finishes.
+ *     mfr_memcpy_d2h and mfr_stream_sync wait for it.
+ *   - Pointers passed to compute entry points are device pointers from mfr_malloc (or another
+ *     HIP allocation on the stream's device).
+ *
+ * Each entry point names the interface of the reference (bakir004/mensurflow) it replaces.
+ */
+#ifndef MFR_ROCM_H
+#define MFR_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    MFR_OK = 0,
+    MFR_E_INVALID = 1,     /* bad argument (the reference throws std::invalid_argument) */
+    MFR_E_RUNTIME = 2,     /* HIP runtime failure (the reference throws std::runtime_error) */
+    MFR_E_UNSUPPORTED = 3, /* a layout or size this build does not handle */
+    MFR_E_NO_DEVICE = 4    /* no usable gfx950 device */
+};
+
+/* Activation applied in a GEMM epilogue or by mfr_bias_act.
+ * GELU_TANH is mensurflow::gelu(x, approximate=true), GELU_ERF is gelu(x, false). */
+enum { MFR_ACT_NONE = 0, MFR_ACT_GELU_TANH = 1, MFR_ACT_GELU_ERF = 2 };
+
+/* Opaque stream: a HIP stream on one device plus the workspace its kernels use
+ * (the reference keeps one Stream per device: src/backends/backend.hpp:32-44). */
+typedef struct mfr_stream* mfr_stream_t;
+typedef struct mfr_event* mfr_event_t;
+
+/* ---- errors ------------------------------------------------------------------------------ */
+
+/* Message of the last failure on this thread ("" if none). Replaces the reference's
+ * runtime_error("CUDA <what> failed: ...") convention, src/backends/cuda/backend.cpp:22-34. */
+const char* mfr_last_error(void);
+
+/* ---- devices (Backend::device_count / Backend::info, src/backends/backend.hpp:51-60) ------ */
+
+/* Number of usable gfx950 devices; 0 (and MFR_OK) when there is no driver or no device, so a
+ * registry can drop the backend without an exception (src/core/registry.cpp:33-38). */
+int mfr_get_device_count(int* count);
+
+/* Device name (NUL-terminated, truncated to cap), total memory in bytes, compute units and the
+ * peak engine clock in kHz. Any output pointer may be NULL. (DeviceInfo, backend.hpp:46-49) */
+int mfr_get_device_info(int device, char* name, size_t cap, size_t* memory_bytes,
+                        int* compute_units, int* clock_khz);
+
+/* ---- memory (Backend::allocate / Buffer, src/backends/backend.hpp:16-30,62) --------------- */
+
+/* bytes == 0 gives *ptr == NULL, as the reference's zero-byte Buffer has a null native(). */
+int mfr_malloc(int device, size_t bytes, void** ptr);
+/* NULL is accepted and ignored. */
+int mfr_free(int device, void* ptr);
+
+/* ---- streams (Stream, src/backends/backend.hpp:32-44) ------------------------------------- */
+
+int mfr_stream_create(int device, mfr_stream_t* stream);
+/* Wraps an existing hipStream_t (passed as void*) of `device`, e.g. a framework's current
+ * stream; the HIP stream is not destroyed by mfr_stream_destroy. */
+int mfr_stream_wrap(int device, void* hip_stream, mfr_stream_t* stream);
+int mfr_stream_destroy(mfr_stream_t stream);
+/* Blocks until all work queued on the stream has finished (Stream::synchronize). */
+int mfr_stream_sync(mfr_stream_t stream);
+/* The underlying hipStream_t (as void*), for interop and profiling. */
+void* mfr_stream_handle(mfr_stream_t stream);
+int mfr_stream_device(mfr_stream_t stream);
+
+/* Host -> device; complete on return, so src may be reused (Stream::copy_h2d). */
+int mfr_memcpy_h2d(mfr_stream_t stream, void* dst, const void* src, size_t bytes);
+/* Device -> host; waits for all earlier work on the stream (Stream::copy_d2h). */
+int mfr_memcpy_d2h(mfr_stream_t stream, void* dst, const void* src, size_t bytes);
+/* Device -> device, ordered on the stream; returns before it finishes. */
+int mfr_memcpy_d2d(mfr_stream_t stream, void* dst, const void* src, size_t bytes);
+
+/* ---- events (device-side timing; the reference times with host clocks, benchmarks/bench.hpp) */
+
+int mfr_event_create(mfr_event_t* event);
+int mfr_event_destroy(mfr_event_t event);
+int mfr_event_record(mfr_event_t event, mfr_stream_t stream);
+/* Milliseconds between two recorded events; waits for `end`. */
+int mfr_event_elapsed_ms(mfr_event_t start, mfr_event_t end, float* ms);
+
+/* ---- GEMM -------------------------------------------------------------------------------- */
+
+#define MFR_MAX_BATCH_DIMS 4
+
+/* One (batched) GEMM with a fused epilogue:
+ *
+ *   C[b](i,j) = act( fl( fl( fl(alpha * sum_p A[b](i,p) * B[b](p,j)) + fl(beta * C0[b](i,j)) )
+ *                        + bias[j] ) )
+ *
+ * for every batch index b of a batch shape of up to MFR_MAX_BATCH_DIMS dimensions (outermost
+ * first); matrix b of an operand starts at base + sum_d b_d * batch_stride_d, and a batch
+ * stride of 0 repeats one matrix (a broadcast batch dimension). A is op(A) [m, k] and B is
+ * op(B) [k, n], each given by its own row and column strides, so a transposed operand is a
+ * swapped stride pair. The fl() steps are the reference's separate roundings: matmul, then
+ * mul by alpha, scal by beta and add (src/ops/blas.cpp:234-262), or the batched GEMM's finish
+ * pass (src/backends/cpu/ops/gemm/gemm_batched.cpp:12-28); the bias step is bias_add
+ * (src/backends/cpu/ops/elementwise/elementwise.cpp:128-137) and act is gelu
+ * (elementwise.cpp:173-194). alpha == 1 skips the multiply, c0 == NULL or beta == 0 skips the
+ * C0 term, bias == NULL skips the bias.
+ *
+ * Each operand needs a unit stride in one of its two matrix dimensions (row-major or
+ * transposed); C has column stride 1. c0 may equal c (in place). k == 0 gives the epilogue of
+ * a zero product. The products are summed in fp32 on the fp32 matrix cores
+ * (v_mfma_f32_32x32x2_f32), in a different order from the CPU's packed kernel.
+ *
+ * Replaces: the Matmul kernel (src/backends/cpu/backend.cpp:131-164), the GemmBatched kernel
+ * (backend.cpp:239-291), and the 4-dispatch composition of mensurflow::gemm
+ * (src/ops/blas.cpp:234-262) when called as one fused op.
+ */
+typedef struct mfr_gemm_desc {
+    int64_t m, n, k;
+    int32_t batch_dims;                       /* 0 .. MFR_MAX_BATCH_DIMS */
+    int32_t act;                              /* MFR_ACT_* */
+    int64_t batch[MFR_MAX_BATCH_DIMS];        /* batch sizes, outermost first */
+    const float* a;
+    int64_t a_rs, a_cs;
+    int64_t a_bs[MFR_MAX_BATCH_DIMS];
+    const float* b;
+    int64_t b_rs, b_cs;
+    int64_t b_bs[MFR_MAX_BATCH_DIMS];
+    float* c;
+    int64_t c_rs;
+    int64_t c_bs[MFR_MAX_BATCH_DIMS];
+    const float* c0;                          /* may be NULL; may equal c */
+    int64_t c0_rs;
+    int64_t c0_bs[MFR_MAX_BATCH_DIMS];
+    const float* bias;                        /* [n] or NULL; shared by every batch */
+    float alpha, beta;
+} mfr_gemm_desc;
+
+int mfr_sgemm(mfr_stream_t stream, const mfr_gemm_desc* desc);
+
+/* Plain row-major convenience form: C[m,n] = alpha*op(A)*op(B) + beta*C0 with leading
+ * dimensions lda/ldb/ldc (BLAS-style trans flags, row-major storage). c0 may be NULL. */
+int mfr_sgemm_rm(mfr_stream_t stream, int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
+                 float alpha, const float* a, int64_t lda, const float* b, int64_t ldb, float beta,
+                 const float* c0, float* c, int64_t ldc);
+
+/* ---- GEMV / matvec ------------------------------------------------------------------------- */
+
+/* y = alpha * op(A) * x + beta * y0, A row-major [rows, cols] with row stride lda >= cols,
+ * op(A) = A (trans == 0, y has `rows` entries) or A^T (trans != 0, y has `cols` entries).
+ * y0 may be NULL (then beta is ignored). Accumulates in double and rounds once, as
+ * mensurflow::cpu::gemv_f32 (src/backends/cpu/ops/blas/blas.cpp:66-79):
+ *   y[i] = (float)( (double)alpha * sum + (double)(float)(beta * y0[i]) ).
+ * Deterministic: the same inputs give the same bits on every call (fixed reduction order, no
+ * float atomics). Replaces the Gemv kernel (src/backends/cpu/backend.cpp:121-126). */
+int mfr_sgemv(mfr_stream_t stream, int trans, int64_t rows, int64_t cols, float alpha,
+              const float* a, int64_t lda, const float* x, float beta, const float* y0, float* y);
+
+/* y[m] = A[m,k] * x[k], double accumulation (mensurflow::cpu::matvec_f32, blas.cpp:55-64).
+ * Replaces the Matvec kernel (src/backends/cpu/backend.cpp:115-119). */
+int mfr_smatvec(mfr_stream_t stream, int64_t m, int64_t k, const float* a, int64_t lda,
+                const float* x, float* y);
+
+/* ---- elementwise, softmax, argmax ---------------------------------------------------------- */
+
+/* y[r, j] = act(x[r, j] + bias[j]) over a contiguous [rows, cols] matrix; bias may be NULL
+ * (then y = act(x), the Gelu kernel). act = MFR_ACT_NONE with a bias is bias_add.
+ * Replaces BiasAdd (src/backends/cpu/backend.cpp:762-767, elementwise.cpp:128-137) and Gelu
+ * (backend.cpp:658-661, elementwise.cpp:173-194). x may equal y. */
+int mfr_bias_act(mfr_stream_t stream, const float* x, const float* bias, float* y, int64_t rows,
+                 int64_t cols, int act);
+
+/* out[i] = cond[i] ? x[i] : y[i] over n contiguous elements (cond is 1 byte per element).
+ * Replaces Where (src/backends/cpu/backend.cpp:625-630, elementwise.cpp:64-70). */
+int mfr_where(mfr_stream_t stream, const uint8_t* cond, const float* x, const float* y, float* out,
+              int64_t n);
+
+/* Softmax of x viewed as [outer, length, inner] along the middle axis (contiguous).
+ * Float maximum (a NaN poisons the line), float exp(x - max), double sum, one float scale;
+ * a line whose maximum is -inf (every element masked) gives zeros.
+ * Replaces Softmax (src/backends/cpu/backend.cpp:549-553, softmax/softmax.cpp:13-49). */
+int mfr_softmax(mfr_stream_t stream, const float* x, float* y, int64_t outer, int64_t length,
+                int64_t inner);
+
+/* out[r] = index of the first maximum of row r of a contiguous [rows, width] matrix; the first
+ * NaN wins. Replaces Argmax (src/backends/cpu/backend.cpp:799-803, reduction.cpp:284-296). */
+int mfr_argmax(mfr_stream_t stream, const float* x, int64_t* out, int64_t rows, int64_t width);
+
+/* ---- layout ------------------------------------------------------------------------------- */
+
+#define MFR_MAX_COPY_DIMS 8
+
+/* Packs a strided view (shape/strides in elements, up to MFR_MAX_COPY_DIMS dimensions, stride 0
+ * allowed) into contiguous row-major dst, element size 1, 2, 4 or 8 bytes. The device-side
+ * form of Tensor::contiguous(), which the reference stages through host memory for non-CPU
+ * devices (src/core/tensor.cpp:208-230). */
+int mfr_strided_copy(mfr_stream_t stream, const void* src, void* dst, int32_t elem_size,
+                     int32_t ndim, const int64_t* shape, const int64_t* strides);
+
+/* Fills n elements of elem_size bytes (1, 2, 4 or 8) with the bit pattern `value`
+ * (the low elem_size bytes are used). */
+int mfr_fill(mfr_stream_t stream, void* dst, int32_t elem_size, int64_t n, uint64_t value);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MFR_ROCM_H */

@@ -1,0 +1,420 @@
+"""mensurflow_amd -- an MI355X (gfx950) backend for mensurflow's fp32 BLAS hot path.
+
+The product is two native libraries built in-tree (``mensurflow_amd/build.py``):
+
+* ``_lib/libmfr_rocm.so``: hand-written HIP kernels behind the C ABI of
+  ``include/mfr_rocm.h`` (fp32-MFMA GEMM with a fused epilogue, HBM-bound gemv, softmax,
+  where, bias+gelu, argmax, strided copy);
+* ``_lib/libmensurflow.so``: the C++17 host layer that plugs those kernels into mensurflow's
+  ``Backend``/``Dispatcher`` API as the ``rocm`` device.
+
+This Python module is a thin driver over the C ABI (device buffers, streams, events and the
+compute entry points), used by the tests and ``bench.py``. It has no CPU fallback: without the
+library, or without a gfx950 device, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import abi
+from .abi import ACT_GELU_ERF, ACT_GELU_TANH, ACT_NONE, GemmDesc  # noqa: F401
+
+__all__ = [
+    "ACT_NONE", "ACT_GELU_TANH", "ACT_GELU_ERF", "GemmDesc", "device_count", "device_info",
+    "Stream", "DeviceArray", "Event", "sgemm", "gemm", "gemm_batched", "sgemv", "matvec",
+    "bias_act", "where", "softmax", "argmax", "strided_copy", "fill",
+]
+
+
+def device_count() -> int:
+    """Usable gfx950 devices (0 without a driver or device)."""
+    lib = abi.load()
+    n = ctypes.c_int(0)
+    abi.check(lib.mfr_get_device_count(ctypes.byref(n)), "mfr_get_device_count")
+    return n.value
+
+
+@dataclass
+class DeviceInfo:
+    name: str
+    memory_bytes: int
+    compute_units: int
+    clock_khz: int
+
+
+def device_info(device: int = 0) -> DeviceInfo:
+    lib = abi.load()
+    name = ctypes.create_string_buffer(256)
+    mem = ctypes.c_size_t(0)
+    cus = ctypes.c_int(0)
+    clk = ctypes.c_int(0)
+    abi.check(lib.mfr_get_device_info(device, name, 256, ctypes.byref(mem), ctypes.byref(cus),
+                                      ctypes.byref(clk)), "mfr_get_device_info")
+    return DeviceInfo(name.value.decode(), mem.value, cus.value, clk.value)
+
+
+class Stream:
+    """An mfr_stream_t: one HIP stream on one device with its kernel workspace."""
+
+    def __init__(self, device: int = 0):
+        lib = abi.load()
+        self.device = device
+        handle = ctypes.c_void_p()
+        abi.check(lib.mfr_stream_create(device, ctypes.byref(handle)), "mfr_stream_create")
+        self.handle = handle
+
+    def synchronize(self) -> None:
+        abi.check(abi.load().mfr_stream_sync(self.handle), "mfr_stream_sync")
+
+    def hip_stream(self) -> int:
+        return abi.load().mfr_stream_handle(self.handle) or 0
+
+    def close(self) -> None:
+        if self.handle is not None and self.handle.value:
+            abi.check(abi.load().mfr_stream_destroy(self.handle), "mfr_stream_destroy")
+        self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self):
+        handle = ctypes.c_void_p()
+        abi.check(abi.load().mfr_event_create(ctypes.byref(handle)), "mfr_event_create")
+        self.handle = handle
+
+    def record(self, stream: Stream) -> None:
+        abi.check(abi.load().mfr_event_record(self.handle, stream.handle), "mfr_event_record")
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = ctypes.c_float(0.0)
+        abi.check(abi.load().mfr_event_elapsed_ms(self.handle, end.handle, ctypes.byref(ms)),
+                  "mfr_event_elapsed_ms")
+        return ms.value
+
+    def __del__(self):
+        try:
+            if self.handle is not None and self.handle.value:
+                abi.load().mfr_event_destroy(self.handle)
+            self.handle = None
+        except Exception:
+            pass
+
+
+class DeviceArray:
+    """A contiguous device allocation viewed with numpy-style shape and element strides.
+
+    Views (``transpose``, ``T``, ``view``, ``slice_rows``) share the allocation; the owner frees
+    it when it is garbage collected or closed.
+    """
+
+    def __init__(self, shape, dtype=np.float32, stream: Stream | None = None, *, _base=None,
+                 _offset=0, _strides=None, _ptr=None):
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = np.dtype(dtype)
+        self.stream = stream
+        self._base = _base
+        self.offset = int(_offset)  # elements from the allocation start
+        if _strides is None:
+            strides, step = [], 1
+            for s in reversed(self.shape):
+                strides.append(step)
+                step *= s
+            _strides = tuple(reversed(strides))
+        self.strides = tuple(int(s) for s in _strides)
+        if _base is None:
+            nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+            self.nbytes_alloc = nbytes
+            ptr = ctypes.c_void_p()
+            dev = stream.device if stream is not None else 0
+            abi.check(abi.load().mfr_malloc(dev, nbytes, ctypes.byref(ptr)), "mfr_malloc")
+            self._ptr = ptr.value or 0
+            self._device = dev
+        else:
+            self._ptr = _ptr
+            self._device = _base._device
+
+    # -- construction --------------------------------------------------------------------------
+    @classmethod
+    def from_numpy(cls, array: np.ndarray, stream: Stream) -> "DeviceArray":
+        host = np.ascontiguousarray(array)
+        out = cls(host.shape, host.dtype, stream)
+        out.upload(host)
+        return out
+
+    @classmethod
+    def empty(cls, shape, stream: Stream, dtype=np.float32) -> "DeviceArray":
+        return cls(shape, dtype, stream)
+
+    # -- data movement ---------------------------------------------------------------------------
+    @property
+    def ptr(self) -> int:
+        """Device address of the first element of this view."""
+        return self._ptr + self.offset * self.dtype.itemsize
+
+    @property
+    def size(self) -> int:
+        return int(np.prod(self.shape, dtype=np.int64))
+
+    def is_contiguous(self) -> bool:
+        step = 1
+        for s, st in zip(reversed(self.shape), reversed(self.strides)):
+            if s != 1 and st != step:
+                return False
+            step *= s
+        return True
+
+    def upload(self, host: np.ndarray) -> None:
+        assert self.is_contiguous(), "upload needs a contiguous view"
+        host = np.ascontiguousarray(host, dtype=self.dtype)
+        assert host.shape == self.shape, (host.shape, self.shape)
+        abi.check(abi.load().mfr_memcpy_h2d(self.stream.handle, self.ptr, host.ctypes.data,
+                                            host.nbytes), "mfr_memcpy_h2d")
+
+    def numpy(self) -> np.ndarray:
+        """Copy to the host (waits for queued work), following strides for views."""
+        if self.is_contiguous():
+            out = np.empty(self.shape, dtype=self.dtype)
+            abi.check(abi.load().mfr_memcpy_d2h(self.stream.handle, out.ctypes.data, self.ptr,
+                                                out.nbytes), "mfr_memcpy_d2h")
+            return out
+        packed = strided_copy(self)
+        return packed.numpy()
+
+    # -- views -------------------------------------------------------------------------------------
+    def _view(self, shape, strides, offset) -> "DeviceArray":
+        base = self._base if self._base is not None else self
+        v = DeviceArray(shape, self.dtype, self.stream, _base=base, _offset=offset,
+                        _strides=strides, _ptr=self._ptr)
+        return v
+
+    def transpose(self, d0=-2, d1=-1) -> "DeviceArray":
+        nd = len(self.shape)
+        d0 %= nd
+        d1 %= nd
+        shape = list(self.shape)
+        strides = list(self.strides)
+        shape[d0], shape[d1] = shape[d1], shape[d0]
+        strides[d0], strides[d1] = strides[d1], strides[d0]
+        return self._view(shape, strides, self.offset)
+
+    @property
+    def T(self) -> "DeviceArray":
+        return self.transpose(-2, -1)
+
+    def view(self, shape) -> "DeviceArray":
+        assert self.is_contiguous()
+        shape = list(shape)
+        if -1 in shape:
+            i = shape.index(-1)
+            rest = int(np.prod([s for j, s in enumerate(shape) if j != i], dtype=np.int64))
+            shape[i] = self.size // rest
+        assert int(np.prod(shape, dtype=np.int64)) == self.size
+        strides, step = [], 1
+        for s in reversed(shape):
+            strides.append(step)
+            step *= s
+        return self._view(shape, tuple(reversed(strides)), self.offset)
+
+    def expand(self, shape) -> "DeviceArray":
+        shape = tuple(int(s) for s in shape)
+        lead = len(shape) - len(self.shape)
+        strides = [0] * lead
+        for i, (s, st) in enumerate(zip(self.shape, self.strides)):
+            want = shape[lead + i]
+            if s == want:
+                strides.append(st)
+            else:
+                assert s == 1
+                strides.append(0)
+        return self._view(shape, strides, self.offset)
+
+    def slice(self, dim, start, end) -> "DeviceArray":
+        shape = list(self.shape)
+        shape[dim] = end - start
+        return self._view(shape, self.strides, self.offset + start * self.strides[dim])
+
+    def close(self) -> None:
+        if self._base is None and self._ptr:
+            # Kernels queued on the stream may still read or write this memory.
+            if self.stream is not None and self.stream.handle is not None:
+                self.stream.synchronize()
+            abi.check(abi.load().mfr_free(self._device, self._ptr), "mfr_free")
+            self._ptr = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---- compute entry points -------------------------------------------------------------------------
+
+
+def _ptr_or_none(arr):
+    return None if arr is None else arr.ptr
+
+
+def sgemm(stream: Stream, desc: GemmDesc) -> None:
+    """mfr_sgemm on a filled descriptor."""
+    abi.check(abi.load().mfr_sgemm(stream.handle, ctypes.byref(desc)), "mfr_sgemm")
+
+
+def _fill_batch(field, values, dims):
+    for i in range(dims):
+        field[i] = int(values[i])
+
+
+def gemm_batched(a: DeviceArray, b: DeviceArray, c: DeviceArray, *, alpha=1.0,
+                 c0: DeviceArray | None = None, beta=0.0, bias: DeviceArray | None = None,
+                 act=ACT_NONE) -> None:
+    """c[...] = act(alpha*a@b + beta*c0 + bias) over the leading (batch) dimensions.
+
+    a is [..., m, k], b is [..., k, n] (any strides with a unit stride in one matrix dimension;
+    batch strides may be 0), c and c0 are [..., m, n] with unit column stride. The batch shapes
+    must already agree (expand them first).
+    """
+    m, k = a.shape[-2:]
+    k2, n = b.shape[-2:]
+    if k != k2:
+        raise ValueError(f"inner dimensions differ: {a.shape} x {b.shape}")
+    batch = c.shape[:-2]
+    dims = len(batch)
+    if dims > abi.MAX_BATCH_DIMS:
+        raise ValueError("too many batch dimensions")
+    for t in (a, b) + ((c0,) if c0 is not None else ()):
+        if t.shape[:-2] != batch:
+            raise ValueError(f"batch shapes differ: {t.shape} vs {c.shape}")
+    if c.strides[-1] != 1 or (c0 is not None and c0.strides[-1] != 1):
+        raise ValueError("c and c0 need a unit column stride")
+    d = GemmDesc()
+    d.m, d.n, d.k = m, n, k
+    d.batch_dims = dims
+    d.act = act
+    _fill_batch(d.batch, batch, dims)
+    d.a = a.ptr
+    d.a_rs, d.a_cs = a.strides[-2], a.strides[-1]
+    _fill_batch(d.a_bs, a.strides[:-2], dims)
+    d.b = b.ptr
+    d.b_rs, d.b_cs = b.strides[-2], b.strides[-1]
+    _fill_batch(d.b_bs, b.strides[:-2], dims)
+    d.c = c.ptr
+    d.c_rs = c.strides[-2]
+    _fill_batch(d.c_bs, c.strides[:-2], dims)
+    if c0 is not None:
+        d.c0 = c0.ptr
+        d.c0_rs = c0.strides[-2]
+        _fill_batch(d.c0_bs, c0.strides[:-2], dims)
+    d.bias = _ptr_or_none(bias)
+    d.alpha = alpha
+    d.beta = beta
+    sgemm(c.stream, d)
+
+
+def gemm(a: DeviceArray, b: DeviceArray, *, alpha=1.0, c0: DeviceArray | None = None, beta=0.0,
+         trans_a=False, trans_b=False, bias: DeviceArray | None = None, act=ACT_NONE,
+         out: DeviceArray | None = None) -> DeviceArray:
+    """mensurflow::gemm's semantics (plus the fused bias/activation): a new [m, n] result."""
+    left = a.T if trans_a else a
+    right = b.T if trans_b else b
+    m, n = left.shape[-2], right.shape[-1]
+    if out is None:
+        out = DeviceArray.empty((m, n), a.stream)
+    gemm_batched(left, right, out, alpha=alpha, c0=c0, beta=beta, bias=bias, act=act)
+    return out
+
+
+def sgemv(a: DeviceArray, x: DeviceArray, *, alpha=1.0, y0: DeviceArray | None = None, beta=0.0,
+          trans=False, out: DeviceArray | None = None) -> DeviceArray:
+    rows, cols = a.shape
+    if a.strides[1] != 1:
+        raise ValueError("gemv needs a row-major matrix (unit column stride)")
+    n_out = cols if trans else rows
+    if out is None:
+        out = DeviceArray.empty((n_out,), a.stream)
+    abi.check(abi.load().mfr_sgemv(a.stream.handle, 1 if trans else 0, rows, cols, alpha, a.ptr,
+                                   a.strides[0], x.ptr, beta, _ptr_or_none(y0), out.ptr),
+              "mfr_sgemv")
+    return out
+
+
+def matvec(a: DeviceArray, x: DeviceArray, out: DeviceArray | None = None) -> DeviceArray:
+    m, k = a.shape
+    if out is None:
+        out = DeviceArray.empty((m,), a.stream)
+    abi.check(abi.load().mfr_smatvec(a.stream.handle, m, k, a.ptr, a.strides[0], x.ptr, out.ptr),
+              "mfr_smatvec")
+    return out
+
+
+def bias_act(x: DeviceArray, bias: DeviceArray | None, act=ACT_NONE,
+             out: DeviceArray | None = None) -> DeviceArray:
+    rows, cols = (x.shape if len(x.shape) == 2 else (1, x.size))
+    if out is None:
+        out = DeviceArray.empty(x.shape, x.stream)
+    abi.check(abi.load().mfr_bias_act(x.stream.handle, x.ptr, _ptr_or_none(bias), out.ptr, rows,
+                                      cols, act), "mfr_bias_act")
+    return out
+
+
+def where(cond: DeviceArray, x: DeviceArray, y: DeviceArray,
+          out: DeviceArray | None = None) -> DeviceArray:
+    if out is None:
+        out = DeviceArray.empty(x.shape, x.stream)
+    abi.check(abi.load().mfr_where(x.stream.handle, cond.ptr, x.ptr, y.ptr, out.ptr, x.size),
+              "mfr_where")
+    return out
+
+
+def softmax(x: DeviceArray, axis=-1, out: DeviceArray | None = None) -> DeviceArray:
+    shape = x.shape if x.shape else (1,)
+    axis %= len(shape)
+    outer = int(np.prod(shape[:axis], dtype=np.int64))
+    length = int(shape[axis])
+    inner = int(np.prod(shape[axis + 1:], dtype=np.int64))
+    if out is None:
+        out = DeviceArray.empty(x.shape, x.stream)
+    abi.check(abi.load().mfr_softmax(x.stream.handle, x.ptr, out.ptr, outer, length, inner),
+              "mfr_softmax")
+    return out
+
+
+def argmax(x: DeviceArray, out: DeviceArray | None = None) -> DeviceArray:
+    width = x.shape[-1]
+    rows = x.size // width if width else int(np.prod(x.shape[:-1], dtype=np.int64))
+    if out is None:
+        out = DeviceArray.empty(x.shape[:-1], x.stream, np.int64)
+    abi.check(abi.load().mfr_argmax(x.stream.handle, x.ptr, out.ptr, rows, width), "mfr_argmax")
+    return out
+
+
+def strided_copy(x: DeviceArray, out: DeviceArray | None = None) -> DeviceArray:
+    if out is None:
+        out = DeviceArray.empty(x.shape, x.stream, x.dtype)
+    nd = len(x.shape)
+    shape = (ctypes.c_int64 * max(nd, 1))(*x.shape)
+    strides = (ctypes.c_int64 * max(nd, 1))(*x.strides)
+    abi.check(abi.load().mfr_strided_copy(x.stream.handle, x.ptr, out.ptr, x.dtype.itemsize, nd,
+                                          shape, strides), "mfr_strided_copy")
+    return out
+
+
+def fill(x: DeviceArray, value) -> None:
+    bits = np.array([value], dtype=x.dtype).view(
+        {1: np.uint8, 2: np.uint16, 4: np.uint32, 8: np.uint64}[x.dtype.itemsize])[0]
+    abi.check(abi.load().mfr_fill(x.stream.handle, x.ptr, x.dtype.itemsize, x.size, int(bits)),
+              "mfr_fill")

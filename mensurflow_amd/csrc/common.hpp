@@ -1,0 +1,182 @@
+// Shared pieces of libmfr_rocm.so: error reporting across the C ABI, the stream object and its
+// workspace, and small device helpers. Only .hip files of this library include it.
+#pragma once
+
+#include "mfr_rocm.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace mfr {
+
+// An error that becomes a status code at the C boundary (no exception leaves an extern "C"
+// function). `code` is one of MFR_E_*.
+struct Error : std::runtime_error {
+    int code;
+    Error(int c, const std::string& what) : std::runtime_error(what), code(c) {}
+};
+
+void set_last_error(const std::string& message);
+
+// Throws Error(MFR_E_RUNTIME, "ROCm <what> failed: <hip message>") on failure, the message shape
+// of the reference's CUDA backend (src/backends/cuda/backend.cpp:22-34).
+inline void check(hipError_t status, const char* what) {
+    if (status != hipSuccess) {
+        throw Error(MFR_E_RUNTIME, std::string("ROCm ") + what + " failed: " +
+                                       hipGetErrorString(status));
+    }
+}
+
+inline void require(bool condition, const std::string& message) {
+    if (!condition) {
+        throw Error(MFR_E_INVALID, message);
+    }
+}
+
+// Runs `body` and turns any exception into a status code plus mfr_last_error().
+template <typename Body> int guarded(Body&& body) {
+    try {
+        body();
+        return MFR_OK;
+    } catch (const Error& e) {
+        set_last_error(e.what());
+        return e.code;
+    } catch (const std::exception& e) {
+        set_last_error(e.what());
+        return MFR_E_RUNTIME;
+    } catch (...) {
+        set_last_error("unknown error");
+        return MFR_E_RUNTIME;
+    }
+}
+
+} // namespace mfr
+
+// One HIP stream on one device, plus the device workspace its kernels use for partial results
+// (gemv-T partial sums). The workspace belongs to the stream: kernels queued on one stream run
+// in order, so they can share it; two streams never share one.
+struct mfr_stream {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool owned = true;
+    void* workspace = nullptr;
+    size_t workspace_bytes = 0;
+
+    // Makes this stream's device current on the calling thread (each ABI call does, as the
+    // reference's CudaStream::activate does per call).
+    void activate() const { mfr::check(hipSetDevice(device), "hipSetDevice"); }
+
+    // At least `bytes` of workspace. Growing it waits for the stream (the old buffer may still be
+    // in use by queued kernels) and is rare: the size only ever grows.
+    void* reserve(size_t bytes) {
+        if (bytes <= workspace_bytes) {
+            return workspace;
+        }
+        if (workspace != nullptr) {
+            mfr::check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+            mfr::check(hipFree(workspace), "hipFree");
+            workspace = nullptr;
+            workspace_bytes = 0;
+        }
+        const size_t rounded = (bytes + (size_t{1} << 20) - 1) & ~((size_t{1} << 20) - 1);
+        mfr::check(hipMalloc(&workspace, rounded), "hipMalloc(workspace)");
+        workspace_bytes = rounded;
+        return workspace;
+    }
+};
+
+struct mfr_event {
+    hipEvent_t event = nullptr;
+};
+
+namespace mfr {
+
+inline mfr_stream& stream_of(mfr_stream_t s) {
+    require(s != nullptr, "null stream");
+    s->activate();
+    return *s;
+}
+
+inline unsigned grid_blocks(int64_t work, int64_t per_block, int64_t cap = int64_t{1} << 30) {
+    int64_t blocks = (work + per_block - 1) / per_block;
+    if (blocks < 1) {
+        blocks = 1;
+    }
+    return static_cast<unsigned>(blocks < cap ? blocks : cap);
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Launch-time check: a kernel launch error is reported by the next HIP call otherwise.
+inline void check_launch(const char* what) { check(hipGetLastError(), what); }
+
+} // namespace mfr
+
+// ---- device helpers --------------------------------------------------------------------------
+
+namespace mfr::dev {
+
+constexpr int kWave = 64;
+
+typedef float native_float4 __attribute__((ext_vector_type(4)));
+
+// 16-byte load marked non-temporal: streamed data that is read once should not displace
+// reused data (x, C0) from the caches. p must be 16-byte aligned.
+__device__ inline float4 load_streaming(const float* p) {
+    const native_float4 v = __builtin_nontemporal_load(reinterpret_cast<const native_float4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
+__device__ inline double wave_sum(double v) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        v += __shfl_xor(v, offset, kWave);
+    }
+    return v;
+}
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        v = fmaxf(v, __shfl_xor(v, offset, kWave));
+    }
+    return v;
+}
+
+__device__ inline int wave_or(int v) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        v |= __shfl_xor(v, offset, kWave);
+    }
+    return v;
+}
+
+// exp(-|v|) form of the logistic function (the reference's stable_sigmoid,
+// src/backends/cpu/ops/elementwise/elementwise.cpp:24-27).
+__device__ inline double stable_sigmoid(double value) {
+    const double z = exp(-fabs(value));
+    return value < 0.0 ? z / (1.0 + z) : 1.0 / (1.0 + z);
+}
+
+// mensurflow::gelu in double, rounded once to float (elementwise.cpp:173-194). The library is
+// compiled with -ffp-contract=off, so the products and sums round as in the reference.
+__device__ inline float gelu(float value, int act) {
+    if (__builtin_isinf(value)) {
+        return value < 0.0f ? -0.0f : value;
+    }
+    const double v = static_cast<double>(value);
+    if (act == MFR_ACT_GELU_TANH) {
+        const double u = 0.79788456080286535588 * v * (1.0 + 0.044715 * v * v);
+        return static_cast<float>(v * stable_sigmoid(2.0 * u));
+    }
+    return static_cast<float>(0.5 * v * erfc(-v * 0.70710678118654752440));
+}
+
+__device__ inline float activate(float value, int act) {
+    return act == MFR_ACT_NONE ? value : gelu(value, act);
+}
+
+} // namespace mfr::dev

@@ -1,0 +1,368 @@
+// Devices, memory, streams, events and copies of the C ABI (include/mfr_rocm.h). These are the
+// runtime half of the reference's Backend/Buffer/Stream interface (src/backends/backend.hpp).
+#include "common.hpp"
+
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+namespace mfr {
+
+namespace {
+thread_local std::string g_last_error;
+
+// HIP device ids of the usable devices, in order: mensurflow device index i is hip id ids[i].
+// Only gfx950 (MI355X/MI350X) devices are usable: the kernels are compiled for it alone.
+const std::vector<int>& usable_devices() {
+    static std::vector<int> ids;
+    static std::once_flag once;
+    std::call_once(once, [] {
+        int count = 0;
+        if (hipGetDeviceCount(&count) != hipSuccess) {
+            (void)hipGetLastError(); // no driver: no devices, not an error
+            return;
+        }
+        for (int id = 0; id < count; ++id) {
+            hipDeviceProp_t prop;
+            if (hipGetDeviceProperties(&prop, id) != hipSuccess) {
+                (void)hipGetLastError();
+                continue;
+            }
+            if (std::strncmp(prop.gcnArchName, "gfx950", 6) == 0) {
+                ids.push_back(id);
+            }
+        }
+    });
+    return ids;
+}
+
+int hip_id(int device) {
+    const auto& ids = usable_devices();
+    if (device < 0 || device >= static_cast<int>(ids.size())) {
+        throw Error(MFR_E_NO_DEVICE, "device rocm:" + std::to_string(device) + " is not available");
+    }
+    return ids[static_cast<size_t>(device)];
+}
+} // namespace
+
+void set_last_error(const std::string& message) { g_last_error = message; }
+
+} // namespace mfr
+
+using mfr::check;
+using mfr::guarded;
+using mfr::require;
+
+namespace {
+
+__global__ void fill_kernel(unsigned char* dst, int elem_size, int64_t n, uint64_t value) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += stride) {
+        switch (elem_size) {
+        case 1:
+            dst[i] = static_cast<unsigned char>(value);
+            break;
+        case 2:
+            reinterpret_cast<uint16_t*>(dst)[i] = static_cast<uint16_t>(value);
+            break;
+        case 4:
+            reinterpret_cast<uint32_t*>(dst)[i] = static_cast<uint32_t>(value);
+            break;
+        default:
+            reinterpret_cast<uint64_t*>(dst)[i] = value;
+            break;
+        }
+    }
+}
+
+struct CopyShape {
+    int ndim;
+    int64_t shape[MFR_MAX_COPY_DIMS];
+    int64_t strides[MFR_MAX_COPY_DIMS];
+};
+
+// dst[i] = src[offset(i)] where offset walks the strided view in row-major order. One thread
+// per element; the index is decomposed from the last (fastest) dimension.
+template <typename T>
+__global__ void strided_copy_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t n,
+                                    CopyShape s) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += stride) {
+        int64_t rest = i;
+        int64_t offset = 0;
+        for (int d = s.ndim - 1; d >= 0; --d) {
+            const int64_t size = s.shape[d];
+            const int64_t index = rest % size;
+            rest /= size;
+            offset += index * s.strides[d];
+        }
+        dst[i] = src[offset];
+    }
+}
+
+} // namespace
+
+extern "C" {
+
+const char* mfr_last_error(void) { return mfr::g_last_error.c_str(); }
+
+int mfr_get_device_count(int* count) {
+    return guarded([&] {
+        require(count != nullptr, "mfr_get_device_count: null output");
+        *count = static_cast<int>(mfr::usable_devices().size());
+    });
+}
+
+int mfr_get_device_info(int device, char* name, size_t cap, size_t* memory_bytes,
+                        int* compute_units, int* clock_khz) {
+    return guarded([&] {
+        hipDeviceProp_t prop;
+        check(hipGetDeviceProperties(&prop, mfr::hip_id(device)), "hipGetDeviceProperties");
+        if (name != nullptr && cap > 0) {
+            std::strncpy(name, prop.name, cap - 1);
+            name[cap - 1] = '\0';
+        }
+        if (memory_bytes != nullptr) {
+            *memory_bytes = prop.totalGlobalMem;
+        }
+        if (compute_units != nullptr) {
+            *compute_units = prop.multiProcessorCount;
+        }
+        if (clock_khz != nullptr) {
+            *clock_khz = prop.clockRate;
+        }
+    });
+}
+
+int mfr_malloc(int device, size_t bytes, void** ptr) {
+    return guarded([&] {
+        require(ptr != nullptr, "mfr_malloc: null output");
+        *ptr = nullptr;
+        if (bytes == 0) {
+            return;
+        }
+        check(hipSetDevice(mfr::hip_id(device)), "hipSetDevice");
+        check(hipMalloc(ptr, bytes), "hipMalloc");
+    });
+}
+
+int mfr_free(int device, void* ptr) {
+    return guarded([&] {
+        if (ptr == nullptr) {
+            return;
+        }
+        check(hipSetDevice(mfr::hip_id(device)), "hipSetDevice");
+        check(hipFree(ptr), "hipFree");
+    });
+}
+
+int mfr_stream_create(int device, mfr_stream_t* stream) {
+    return guarded([&] {
+        require(stream != nullptr, "mfr_stream_create: null output");
+        auto s = new mfr_stream;
+        s->device = mfr::hip_id(device);
+        try {
+            s->activate();
+            // Default priority on purpose: streams of different priorities are not mixed.
+            check(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking),
+                  "hipStreamCreateWithFlags");
+        } catch (...) {
+            delete s;
+            throw;
+        }
+        *stream = s;
+    });
+}
+
+int mfr_stream_wrap(int device, void* hip_stream, mfr_stream_t* stream) {
+    return guarded([&] {
+        require(stream != nullptr, "mfr_stream_wrap: null output");
+        auto s = new mfr_stream;
+        s->device = mfr::hip_id(device);
+        s->stream = static_cast<hipStream_t>(hip_stream);
+        s->owned = false;
+        *stream = s;
+    });
+}
+
+int mfr_stream_destroy(mfr_stream_t stream) {
+    return guarded([&] {
+        if (stream == nullptr) {
+            return;
+        }
+        stream->activate();
+        check(hipStreamSynchronize(stream->stream), "hipStreamSynchronize");
+        if (stream->workspace != nullptr) {
+            check(hipFree(stream->workspace), "hipFree(workspace)");
+        }
+        if (stream->owned && stream->stream != nullptr) {
+            check(hipStreamDestroy(stream->stream), "hipStreamDestroy");
+        }
+        delete stream;
+    });
+}
+
+int mfr_stream_sync(mfr_stream_t stream) {
+    return guarded([&] {
+        auto& s = mfr::stream_of(stream);
+        check(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+    });
+}
+
+void* mfr_stream_handle(mfr_stream_t stream) {
+    return stream == nullptr ? nullptr : static_cast<void*>(stream->stream);
+}
+
+int mfr_stream_device(mfr_stream_t stream) {
+    if (stream == nullptr) {
+        return -1;
+    }
+    const auto& ids = mfr::usable_devices();
+    for (size_t i = 0; i < ids.size(); ++i) {
+        if (ids[i] == stream->device) {
+            return static_cast<int>(i);
+        }
+    }
+    return -1;
+}
+
+int mfr_memcpy_h2d(mfr_stream_t stream, void* dst, const void* src, size_t bytes) {
+    return guarded([&] {
+        auto& s = mfr::stream_of(stream);
+        if (bytes == 0) {
+            return;
+        }
+        require(dst != nullptr && src != nullptr, "mfr_memcpy_h2d: null pointer");
+        check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s.stream), "hipMemcpyAsync");
+        // Pageable source: complete before returning so the caller may reuse it.
+        check(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+    });
+}
+
+int mfr_memcpy_d2h(mfr_stream_t stream, void* dst, const void* src, size_t bytes) {
+    return guarded([&] {
+        auto& s = mfr::stream_of(stream);
+        if (bytes == 0) {
+            check(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+            return;
+        }
+        require(dst != nullptr && src != nullptr, "mfr_memcpy_d2h: null pointer");
+        check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s.stream), "hipMemcpyAsync");
+        check(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+    });
+}
+
+int mfr_memcpy_d2d(mfr_stream_t stream, void* dst, const void* src, size_t bytes) {
+    return guarded([&] {
+        auto& s = mfr::stream_of(stream);
+        if (bytes == 0) {
+            return;
+        }
+        require(dst != nullptr && src != nullptr, "mfr_memcpy_d2d: null pointer");
+        check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s.stream),
+              "hipMemcpyAsync");
+    });
+}
+
+int mfr_event_create(mfr_event_t* event) {
+    return guarded([&] {
+        require(event != nullptr, "mfr_event_create: null output");
+        auto e = new mfr_event;
+        const hipError_t status = hipEventCreate(&e->event);
+        if (status != hipSuccess) {
+            delete e;
+            check(status, "hipEventCreate");
+        }
+        *event = e;
+    });
+}
+
+int mfr_event_destroy(mfr_event_t event) {
+    return guarded([&] {
+        if (event == nullptr) {
+            return;
+        }
+        check(hipEventDestroy(event->event), "hipEventDestroy");
+        delete event;
+    });
+}
+
+int mfr_event_record(mfr_event_t event, mfr_stream_t stream) {
+    return guarded([&] {
+        require(event != nullptr, "mfr_event_record: null event");
+        auto& s = mfr::stream_of(stream);
+        check(hipEventRecord(event->event, s.stream), "hipEventRecord");
+    });
+}
+
+int mfr_event_elapsed_ms(mfr_event_t start, mfr_event_t end, float* ms) {
+    return guarded([&] {
+        require(start != nullptr && end != nullptr && ms != nullptr,
+                "mfr_event_elapsed_ms: null argument");
+        check(hipEventSynchronize(end->event), "hipEventSynchronize");
+        check(hipEventElapsedTime(ms, start->event, end->event), "hipEventElapsedTime");
+    });
+}
+
+int mfr_fill(mfr_stream_t stream, void* dst, int32_t elem_size, int64_t n, uint64_t value) {
+    return guarded([&] {
+        auto& s = mfr::stream_of(stream);
+        require(elem_size == 1 || elem_size == 2 || elem_size == 4 || elem_size == 8,
+                "mfr_fill: element size must be 1, 2, 4 or 8");
+        require(n >= 0, "mfr_fill: negative count");
+        if (n == 0) {
+            return;
+        }
+        require(dst != nullptr, "mfr_fill: null destination");
+        fill_kernel<<<mfr::grid_blocks(n, 256, 65536), 256, 0, s.stream>>>(
+            static_cast<unsigned char*>(dst), elem_size, n, value);
+        mfr::check_launch("fill_kernel");
+    });
+}
+
+int mfr_strided_copy(mfr_stream_t stream, const void* src, void* dst, int32_t elem_size,
+                     int32_t ndim, const int64_t* shape, const int64_t* strides) {
+    return guarded([&] {
+        auto& s = mfr::stream_of(stream);
+        require(ndim >= 0 && ndim <= MFR_MAX_COPY_DIMS, "mfr_strided_copy: too many dimensions");
+        require(elem_size == 1 || elem_size == 2 || elem_size == 4 || elem_size == 8,
+                "mfr_strided_copy: element size must be 1, 2, 4 or 8");
+        CopyShape cs{};
+        cs.ndim = ndim;
+        int64_t n = 1;
+        for (int d = 0; d < ndim; ++d) {
+            require(shape[d] >= 0, "mfr_strided_copy: negative dimension");
+            cs.shape[d] = shape[d];
+            cs.strides[d] = strides[d];
+            n *= shape[d];
+        }
+        if (n == 0) {
+            return;
+        }
+        require(src != nullptr && dst != nullptr, "mfr_strided_copy: null pointer");
+        const unsigned blocks = mfr::grid_blocks(n, 256, 65536);
+        switch (elem_size) {
+        case 1:
+            strided_copy_kernel<<<blocks, 256, 0, s.stream>>>(
+                static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), n, cs);
+            break;
+        case 2:
+            strided_copy_kernel<<<blocks, 256, 0, s.stream>>>(
+                static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), n, cs);
+            break;
+        case 4:
+            strided_copy_kernel<<<blocks, 256, 0, s.stream>>>(
+                static_cast<const uint32_t*>(src), static_cast<uint32_t*>(dst), n, cs);
+            break;
+        default:
+            strided_copy_kernel<<<blocks, 256, 0, s.stream>>>(
+                static_cast<const uint64_t*>(src), static_cast<uint64_t*>(dst), n, cs);
+            break;
+        }
+        mfr::check_launch("strided_copy_kernel");
+    });
+}
+
+} // extern "C"

@@ -1,0 +1,134 @@
+"""GPU parity of the elementwise, softmax, argmax and layout kernels against the vectors the
+reference's own kernels wrote (tests/golden/ref_vectors.npz) and the oracle.
+
+bias_add, where and argmax must match bit for bit. gelu and softmax call libm-class functions
+(exp, erfc) whose device versions may differ from glibc in the last bit before the final
+rounding, so they are held to a few ulps and must be bit-identical on almost every element."""
+import os
+
+import numpy as np
+import pytest
+
+import mensurflow_amd as mf
+from helpers import normal, same_bits, uniform
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module")
+def vectors():
+    with np.load(os.path.join(GOLDEN, "ref_vectors.npz"), allow_pickle=False) as data:
+        return {k: data[k] for k in data.files}
+
+
+def dev(x, stream):
+    return mf.DeviceArray.from_numpy(np.ascontiguousarray(x), stream)
+
+
+def ulp_diff(a, b):
+    """Distance in units in the last place between float32 arrays (NaN == NaN)."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    both_nan = np.isnan(a) & np.isnan(b)
+    ia = a.view(np.int32).astype(np.int64)
+    ib = b.view(np.int32).astype(np.int64)
+    ia = np.where(ia < 0, -(ia & 0x7FFFFFFF), ia)
+    ib = np.where(ib < 0, -(ib & 0x7FFFFFFF), ib)
+    d = np.abs(ia - ib)
+    return np.where(both_nan, 0, d)
+
+
+def test_bias_add_and_where_bit_exact(stream, vectors):
+    v = vectors
+    got = mf.bias_act(dev(v["bias_x"], stream), dev(v["bias_b"], stream)).numpy()
+    assert same_bits(got, v["bias_out"])
+    got = mf.where(dev(v["where_c"], stream), dev(v["where_x"], stream),
+                   dev(v["where_y"], stream)).numpy()
+    assert same_bits(got, v["where_out"])
+
+
+@pytest.mark.parametrize("rows,cols", [(7, 11), (4093, 4099), (64, 256)])
+def test_bias_add_shapes(stream, oracle, rows, cols):
+    x = normal(oracle, (rows, cols), 0.0, 1.0, 3, 0)
+    b = uniform(oracle, (cols,), -0.1, 0.1, 4, 0)
+    got = mf.bias_act(dev(x, stream), dev(b, stream)).numpy()
+    assert same_bits(got, oracle.bias_add(x, b))
+
+
+@pytest.mark.parametrize("act,key", [(mf.ACT_GELU_TANH, "gelu_tanh"), (mf.ACT_GELU_ERF, "gelu_erf")])
+def test_gelu_against_reference_vectors(stream, vectors, act, key):
+    x = vectors["gelu_x"]
+    got = mf.bias_act(dev(x, stream), None, act).numpy()
+    want = vectors[key]
+    d = ulp_diff(got, want)
+    assert int(d.max()) <= 2, f"max ulp difference {int(d.max())}"
+    assert float(np.mean(d == 0)) > 0.995
+    # the special values exactly: +-inf, NaN, signed zeros
+    special = ~np.isfinite(x) | (x == 0)
+    assert same_bits(got[special], want[special])
+
+
+def test_gelu_known_value(stream):
+    got = mf.bias_act(dev(np.array([1.0], np.float32), stream), None, mf.ACT_GELU_ERF).numpy()
+    assert abs(float(got[0]) - 0.841344746) < 1e-7
+
+
+def test_fused_bias_gelu_matches_chain(stream, oracle):
+    x = normal(oracle, (300, 257), 0.0, 2.0, 5, 0)
+    b = uniform(oracle, (257,), -0.1, 0.1, 6, 0)
+    got = mf.bias_act(dev(x, stream), dev(b, stream), mf.ACT_GELU_TANH).numpy()
+    want = oracle.gelu(oracle.bias_add(x, b), approximate=True)
+    assert int(ulp_diff(got, want).max()) <= 2
+
+
+def test_softmax_against_reference_vectors(stream, vectors):
+    v = vectors
+    got = mf.softmax(dev(v["softmax_x"], stream)).numpy()
+    want = v["softmax_last"]
+    assert int(ulp_diff(got, want).max()) <= 4
+    assert np.all(got[1] == 0.0)           # fully masked line
+    assert np.all(np.isnan(got[3]))        # a NaN poisons its line
+    got3 = mf.softmax(dev(v["softmax3_x"], stream), axis=1).numpy()
+    assert int(ulp_diff(got3, v["softmax3_axis1"]).max()) <= 4
+
+
+@pytest.mark.parametrize("length", [1, 63, 64, 257, 1024, 2048, 5000])
+def test_softmax_rows(stream, oracle, length):
+    x = normal(oracle, (33, length), 0.0, 4.0, length, 0)
+    x[5, : length // 2] = -np.inf
+    got = mf.softmax(dev(x, stream)).numpy()
+    want = oracle.softmax(x)
+    assert int(ulp_diff(got, want).max()) <= 4
+    np.testing.assert_allclose(got.sum(axis=1, dtype=np.float64), 1.0, rtol=1e-5)
+
+
+def test_argmax_bit_exact(stream, vectors, oracle):
+    got = mf.argmax(dev(vectors["argmax_x"], stream)).numpy()
+    assert got.tolist() == vectors["argmax_out"].tolist()
+    x = normal(oracle, (1000, 4099), 0.0, 1.0, 77, 0)
+    x[3, 100] = np.nan
+    x[4, :] = 1.0
+    assert mf.argmax(dev(x, stream)).numpy().tolist() == oracle.argmax(x).tolist()
+
+
+def test_strided_copy_views(stream, oracle):
+    base = uniform(oracle, (6, 7, 9), -1.0, 1.0, 88, 0)
+    d = dev(base, stream)
+    assert same_bits(d.transpose(0, 2).numpy(), np.ascontiguousarray(base.transpose(2, 1, 0)))
+    assert same_bits(d.slice(1, 2, 6).numpy(), np.ascontiguousarray(base[:, 2:6, :]))
+    row = dev(base[0, 0], stream).expand((4, 9))
+    assert same_bits(row.numpy(), np.broadcast_to(base[0, 0], (4, 9)).copy())
+    mask = dev(np.tril(np.ones((5, 5), np.uint8)), stream).expand((2, 3, 5, 5))
+    assert same_bits(mask.numpy(), np.broadcast_to(np.tril(np.ones((5, 5), np.uint8)),
+                                                   (2, 3, 5, 5)).copy())
+
+
+def test_fill(stream):
+    buf = mf.DeviceArray.empty((1001,), stream)
+    mf.fill(buf, -np.inf)
+    assert np.all(buf.numpy() == -np.inf)
+    ints = mf.DeviceArray.empty((77,), stream, np.int64)
+    mf.fill(ints, -5)
+    assert np.all(ints.numpy() == -5)

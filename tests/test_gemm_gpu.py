@@ -1,0 +1,241 @@
+"""GPU parity of mfr_sgemm (fp32 MFMA GEMM with fused epilogue) against the oracle.
+
+Bit-exact cases use quarter-integer inputs (the reference tests' generator): every partial sum
+is exact in fp32, so the GPU result must equal the exact product in every bit whatever the
+summation order -- this pins indexing, edges, transposes, strides, batching and the epilogue.
+Realistic cases (Philox uniform/normal inputs, the BASELINE configs) are held to the north-star
+bar: max relative error 1e-5*sqrt(K) against the per-entry magnitude sum|a*b| and against
+max|C| (helpers.assert_gemm_parity). Outputs start poisoned and sit between guard bands.
+"""
+import numpy as np
+import pytest
+
+import mensurflow_amd as mf
+from helpers import (assert_gemm_parity, magnitude, normal, quarter_input, quarter_matrix,
+                     same_bits, uniform)
+
+pytestmark = pytest.mark.gpu
+
+POISON = np.float32(123.0)
+
+
+def dev(x, stream):
+    return mf.DeviceArray.from_numpy(np.ascontiguousarray(x), stream)
+
+
+def guarded_output(stream, shape, guard=64):
+    """A [rows, cols] output in the middle of a poisoned buffer; returns (view, buffer)."""
+    rows, cols = shape
+    buf = mf.DeviceArray.empty((rows * cols + 2 * guard,), stream)
+    mf.fill(buf, POISON)
+    view = buf.slice(0, guard, guard + rows * cols).view((rows, cols))
+    return view, buf
+
+
+def check_guards(buf, guard=64):
+    host = buf.numpy()
+    assert np.all(host[:guard] == POISON) and np.all(host[-guard:] == POISON), "stray write"
+
+
+def make_view(stream, values, kind):
+    """The reference's matmul layouts (tests/ops/matmul_test.cpp:189-214): 0 contiguous,
+    1 sliced out of a wider matrix, 2 transposed storage, 3 transposed and sliced."""
+    rows, cols = values.shape
+    if kind == 0:
+        return dev(values, stream)
+    if kind == 1:
+        stored = np.full((rows + 2, cols + 9), -77.0, np.float32)
+        stored[1:1 + rows, 3:3 + cols] = values
+        return dev(stored, stream).slice(0, 1, 1 + rows).slice(1, 3, 3 + cols)
+    if kind == 2:
+        return dev(np.ascontiguousarray(values.T), stream).T
+    stored = np.full((cols + 3, rows + 5), -77.0, np.float32)
+    stored[2:2 + cols, 4:4 + rows] = values.T
+    return dev(stored, stream).slice(0, 2, 2 + cols).slice(1, 4, 4 + rows).T
+
+
+def exact_product(a, b):
+    return (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
+
+
+def test_known_values(stream):
+    a = dev(np.array([[1, 2, 3], [4, 5, 6]], np.float32), stream)
+    b = dev(np.array([[7, 8], [9, 10], [11, 12]], np.float32), stream)
+    assert mf.gemm(a, b).numpy().tolist() == [[58, 64], [139, 154]]
+    values = quarter_input(5 * 7, 3).reshape(5, 7)
+    ident = mf.gemm(dev(values, stream), dev(np.eye(7, dtype=np.float32), stream)).numpy()
+    assert same_bits(ident, values)
+
+
+# Sizes around the 128x128x32 tile and the reference's block edges.
+SHAPES = [(1, 1, 1), (1, 5, 1), (5, 1, 3), (3, 5, 7), (16, 16, 16), (17, 31, 13), (64, 64, 64),
+          (65, 129, 130), (100, 300, 50), (200, 100, 300), (2, 1000, 3), (1000, 2, 3),
+          (257, 129, 257), (127, 128, 31), (128, 128, 32), (129, 255, 33), (256, 256, 256),
+          (300, 77, 1000)]
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_exact_shapes(stream, m, n, k):
+    a = quarter_matrix(m, k, m + 1)
+    b = quarter_matrix(k, n, n + 2)
+    c, buf = guarded_output(stream, (m, n))
+    mf.gemm(dev(a, stream), dev(b, stream), out=c)
+    assert same_bits(c.numpy(), exact_product(a, b)), f"{m}x{n}x{k}"
+    check_guards(buf)
+
+
+@pytest.mark.parametrize("m,n,k", [(70, 60, 90), (130, 200, 150), (300, 300, 300)])
+def test_exact_strided_layouts(stream, m, n, k):
+    a = quarter_matrix(m, k, 21)
+    b = quarter_matrix(k, n, 22)
+    want = exact_product(a, b)
+    for kind_a in range(4):
+        for kind_b in range(4):
+            c, buf = guarded_output(stream, (m, n))
+            mf.gemm(make_view(stream, a, kind_a), make_view(stream, b, kind_b), out=c)
+            assert same_bits(c.numpy(), want), f"A{kind_a} B{kind_b}"
+            check_guards(buf)
+
+
+@pytest.mark.parametrize("trans_a,trans_b", [(False, False), (False, True), (True, False),
+                                             (True, True)])
+def test_exact_alpha_beta_in_place(stream, trans_a, trans_b):
+    m, n, k = 190, 133, 300
+    a = quarter_matrix(k if trans_a else m, m if trans_a else k, 31)
+    b = quarter_matrix(n if trans_b else k, k if trans_b else n, 32)
+    c0 = quarter_matrix(m, n, 33)
+    left = a.T if trans_a else a
+    right = b.T if trans_b else b
+    want = (np.float32(1.5) * exact_product(left, right)) + np.float32(0.5) * c0
+    c = dev(c0, stream)
+    # c0 == c: the epilogue reads and writes the same element in place.
+    mf.gemm(dev(a, stream), dev(b, stream), alpha=1.5, c0=c, beta=0.5, trans_a=trans_a,
+            trans_b=trans_b, out=c)
+    assert same_bits(c.numpy(), want.astype(np.float32))
+
+
+def test_k_zero_gives_epilogue_of_zero_product(stream):
+    m, n = 33, 17
+    c0 = quarter_matrix(m, n, 41)
+    a = mf.DeviceArray.empty((m, 0), stream)
+    b = mf.DeviceArray.empty((0, n), stream)
+    c, _ = guarded_output(stream, (m, n))
+    mf.gemm(a, b, out=c)
+    assert np.all(c.numpy() == 0.0)
+    mf.gemm(a, b, alpha=2.0, c0=dev(c0, stream), beta=0.5, out=c)
+    assert same_bits(c.numpy(), (np.float32(0.5) * c0).astype(np.float32))
+
+
+def test_empty_outputs_touch_nothing(stream):
+    c, buf = guarded_output(stream, (0, 5))
+    mf.gemm(mf.DeviceArray.empty((0, 4), stream), dev(np.ones((4, 5), np.float32), stream), out=c)
+    check_guards(buf)
+
+
+def test_batched_broadcast_and_transposed(stream):
+    """gemm_strided_batched semantics: a [2,3,m,k] batch times a b broadcast over the first
+    batch dimension (stride 0), read transposed."""
+    bsz, heads, m, n, k = 2, 3, 70, 45, 96
+    a = quarter_matrix(bsz * heads * m, k, 51).reshape(bsz, heads, m, k)
+    bt = quarter_matrix(heads * n, k, 52).reshape(1, heads, n, k)  # stored [.., n, k]
+    c0 = quarter_matrix(bsz * heads * m, n, 53).reshape(bsz, heads, m, n)
+    a_d = dev(a, stream)
+    b_d = dev(bt, stream).expand((bsz, heads, n, k)).transpose(-2, -1)  # [2,3,k,n], batch stride 0
+    c0_d = dev(c0, stream)
+    out = mf.DeviceArray.empty((bsz, heads, m, n), stream)
+    mf.gemm_batched(a_d, b_d, out, alpha=0.25, c0=c0_d, beta=-2.0)
+    got = out.numpy()
+    for i in range(bsz):
+        for h in range(heads):
+            prod = exact_product(a[i, h], bt[0, h].T)
+            want = (np.float32(0.25) * prod) + (np.float32(-2.0) * c0[i, h])
+            assert same_bits(got[i, h], want.astype(np.float32)), (i, h)
+
+
+def test_config1_matmul_1024_realistic(stream, oracle):
+    """A, B [1024,1024] uniform[-1,1] from seed 0 (A at offset 0, B after
+    it), alpha 1, beta 0 -- against the packed CPU GEMM's arithmetic."""
+    n = 1024
+    a = uniform(oracle, (n, n), -1.0, 1.0, 0, 0)
+    b = uniform(oracle, (n, n), -1.0, 1.0, 0, n * n)
+    got = mf.gemm(dev(a, stream), dev(b, stream)).numpy()
+    want = oracle.matmul(a, b)
+    rel_mag, rel_max = assert_gemm_parity(got, want, magnitude(oracle, a, b), n, "cfg1")
+    print(f"cfg1 1024^3: rel err vs magnitude {rel_mag:.3e}, vs max|C| {rel_max:.3e}")
+
+
+def test_config3_gemm_4096_nt_exact(stream):
+    """BASELINE configs[2] shape and epilogue (transB, alpha 1.5, beta 0.5) at full size with
+    quarter-integer inputs: exact in any order, so every bit must match."""
+    n = 4096
+    a = quarter_matrix(n, n, 61)
+    b_stored = quarter_matrix(n, n, 62)  # B is read transposed
+    c0 = quarter_matrix(n, n, 63)
+    c = mf.gemm(dev(a, stream), dev(b_stored, stream), alpha=1.5, c0=dev(c0, stream), beta=0.5,
+                trans_b=True).numpy()
+    exact = a.astype(np.float64) @ b_stored.T.astype(np.float64)
+    want = (np.float32(1.5) * exact.astype(np.float32)) + np.float32(0.5) * c0
+    assert same_bits(c, want.astype(np.float32))
+
+
+def test_config3_gemm_4096_nt_realistic(stream, oracle):
+    """BASELINE configs[2] with its own inputs at full size: A, B uniform[-1,1], C0 ~ N(0,1),
+    from a seed; against the packed CPU GEMM's arithmetic and mensurflow::gemm's roundings."""
+    n = 4096
+    seed = 3
+    a = uniform(oracle, (n, n), -1.0, 1.0, seed, 0)
+    b_stored = uniform(oracle, (n, n), -1.0, 1.0, seed, n * n)
+    c0 = normal(oracle, (n, n), 0.0, 1.0, seed + 1, 0)
+    got = mf.gemm(dev(a, stream), dev(b_stored, stream), alpha=1.5, c0=dev(c0, stream), beta=0.5,
+                  trans_b=True).numpy()
+    want = oracle.gemm(a, b_stored, 1.5, c0, 0.5, trans_b=True)
+    scale = 1.5 * magnitude(oracle, a, b_stored.T) + 0.5 * np.abs(c0)
+    rel_mag, rel_max = assert_gemm_parity(got, want, scale, n, "cfg3")
+    print(f"cfg3 4096^3 NT: rel err vs magnitude {rel_mag:.3e}, vs max|C| {rel_max:.3e}")
+
+
+def test_config4_mlp_fused_bias_gelu(stream, oracle):
+    """X[4093,1023] x W[1023,4099] + bias, gelu-tanh fused in the epilogue,
+    against the reference's three-op chain gelu(bias_add(matmul(X, W), b), true). The row
+    argmax must agree exactly except on rows whose top two values are within the error bar."""
+    m, k, n = 4093, 1023, 4099
+    x = normal(oracle, (m, k), 0.0, 1.0, 7, 0)
+    w = normal(oracle, (k, n), 0.0, float(np.sqrt(1.0 / 1023.0)), 8, 0)
+    bias = uniform(oracle, (n,), -0.1, 0.1, 9, 0)
+    out_d = mf.gemm(dev(x, stream), dev(w, stream), bias=dev(bias, stream), act=mf.ACT_GELU_TANH)
+    out = out_d.numpy()
+    gpu_argmax = mf.argmax(out_d).numpy()
+    want = oracle.gelu(oracle.bias_add(oracle.matmul(x, w), bias), approximate=True)
+    # gelu'(v) <= 1.13, so the pre-activation scale bounds the output's error scale.
+    scale = 1.13 * (magnitude(oracle, x, w) + np.abs(bias))
+    rel_mag, rel_max = assert_gemm_parity(out, want, scale, k, "cfg4")
+    want_arg = oracle.argmax(want)
+    top2 = np.sort(want, axis=1)[:, -2:]
+    margin = top2[:, 1] - top2[:, 0]
+    bar = 1e-5 * np.sqrt(k) * scale.max(axis=1)
+    decided = margin > 2 * bar
+    assert np.array_equal(gpu_argmax[decided], want_arg[decided])
+    print(f"cfg4: rel err vs magnitude {rel_mag:.3e}, vs max|C| {rel_max:.3e}; argmax equal on "
+          f"{int(decided.sum())} decided rows, {int((~decided).sum())} near-tie rows, "
+          f"{int(np.sum(gpu_argmax != want_arg))} rows differ in total")
+
+
+def test_deterministic(stream):
+    a = dev(np.random.default_rng(5).standard_normal((300, 500)).astype(np.float32), stream)
+    b = dev(np.random.default_rng(6).standard_normal((500, 260)).astype(np.float32), stream)
+    first = mf.gemm(a, b).numpy()
+    second = mf.gemm(a, b).numpy()
+    assert same_bits(first, second)
+
+
+def test_unsupported_and_invalid(stream):
+    a = dev(np.ones((8, 8), np.float32), stream)
+    # a view with no unit stride (every other row and column)
+    odd = dev(np.ones((16, 16), np.float32), stream)
+    odd = mf.DeviceArray(odd.shape, np.float32, stream, _base=odd, _offset=0,
+                         _strides=(32, 2), _ptr=odd._ptr)
+    odd.shape = (8, 8)
+    with pytest.raises(NotImplementedError):
+        mf.gemm(odd, a)
+    with pytest.raises(ValueError):
+        mf.gemm(a, dev(np.ones((7, 8), np.float32), stream))
