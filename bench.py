@@ -119,6 +119,21 @@ def bench_mlp(mf, stream, steps, warmup):
     return {"event_ms": event_ms, "flops": 2.0 * m * n * k}
 
 
+def bench_copy(mf, stream, steps, warmup):
+    """A plain 1 GiB device copy (the strided-copy kernel on a contiguous view): the measured
+    HBM ceiling, and the calibration kernel for rocprofv3's FETCH_SIZE / WRITE_SIZE."""
+    n = 1 << 28
+    src = mf.DeviceArray.empty((n,), stream)
+    dst = mf.DeviceArray.empty((n,), stream)
+    mf.fill(src, 1.0)
+
+    def launch():
+        mf.strided_copy(src, out=dst)
+
+    wall_ms, event_ms = time_launches(mf, stream, launch, steps, warmup)
+    return {"event_ms": event_ms, "bytes": 8.0 * n}
+
+
 def cpu_baseline(seconds: float = 12.0):
     """The reference's packed AVX2/OpenMP GEMM (oracle/_ref) on the box's host cores: the
     matmul of configs[2] (4096^3, B read transposed), repeated for about `seconds`."""
@@ -171,7 +186,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["all", "gemm", "gemv", "mlp"], default="all",
+    ap.add_argument("--only", choices=["all", "gemm", "gemv", "mlp", "copy"], default="all",
                     help="run one leg (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -201,6 +216,9 @@ def main() -> int:
     if args.only in ("all", "mlp"):
         log("mlp 4093x1023x4099 + bias + gelu ...")
         result["mlp"] = bench_mlp(mf, stream, max(5, args.steps // 5), args.warmup)
+    if args.only in ("all", "copy"):
+        log("copy 1 GiB ...")
+        result["copy"] = bench_copy(mf, stream, max(5, args.steps // 5), args.warmup)
     if args.only != "all":
         print(json.dumps(result))
         return 0
@@ -251,6 +269,9 @@ def main() -> int:
                       "ms_per_call": round(mlp["event_ms"], 4),
                       "frac": round(mlp["flops"] / (mlp["event_ms"] * 1e-3) / 1e12
                                     / PEAK_FP32_MFMA_TFLOPS, 4)},
+        "copy_1gib": {"gbs": round(result["copy"]["bytes"] / (result["copy"]["event_ms"] * 1e-3)
+                                   / 1e9, 1),
+                      "note": "plain device copy, read+write bytes; the practical HBM ceiling"},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

@@ -7,10 +7,11 @@
 // fused multiply-add in double rounds exactly like the reference's multiply-then-add; only the
 // order of the additions differs, and it is fixed, so every call gives the same bits.
 //
-// N form (y has `rows` entries): one wavefront owns kRowsPerWave rows and walks them with
-// 16-byte loads, four independent loads per lane in flight per row; the row's x chunk is read
-// once per step for all of its rows. The partial sums are reduced across the wavefront with
-// shuffles. Every byte of A is read once, coalesced.
+// N form (y has `rows` entries): one wavefront owns kRowsPerWave (4) rows and walks them with
+// 16-byte loads, kUnrollN loads per row in flight per lane; each x chunk is read once for all 4
+// rows. The partial sums are reduced across the wavefront with shuffles. Every byte of A is read
+// once, coalesced. At 16384 rows this is 4096 wavefronts: one full round of the chip at 4
+// wavefronts per SIMD, so no tail of half-empty rounds.
 //
 // T form (y has `cols` entries): a workgroup owns a strip of 256 columns (64 lanes x 4) and a
 // chunk of rows; its four wavefronts split the chunk's rows, each lane keeps 4 column sums, and
@@ -23,7 +24,7 @@ namespace {
 
 using mfr::dev::kWave;
 
-constexpr int kRowsPerWave = 2;
+constexpr int kRowsPerWave = 4;
 constexpr int kWavesPerBlockN = 4;
 constexpr int kUnrollN = 4;
 
@@ -221,7 +222,8 @@ __global__ void gemv_t_finish_kernel(const double* __restrict__ partial, int64_t
 // Rows per chunk of the T form: enough (strip, chunk) tiles to cover the chip several times
 // (256 CUs), each chunk a multiple of the unrolled row step, at least 64 rows.
 int64_t t_rows_per_chunk(int64_t rows, int64_t strips) {
-    const int64_t target_tiles = 2048;
+    // 1024 workgroups of 4 wavefronts: one full round of 256 CUs x 4 SIMDs x 4 wavefronts.
+    const int64_t target_tiles = 1024;
     int64_t chunks = (target_tiles + strips - 1) / strips;
     if (chunks < 1) {
         chunks = 1;

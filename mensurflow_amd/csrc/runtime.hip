@@ -102,6 +102,56 @@ __global__ void strided_copy_kernel(const T* __restrict__ src, T* __restrict__ d
     }
 }
 
+// dst[i] = src[i] in 16-byte units, grid-stride, four loads in flight per thread before the
+// stores (both pointers 16-byte aligned).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__global__ void copy16_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst, int64_t n) {
+    constexpr int kUnroll = 4;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    for (; i + (kUnroll - 1) * stride < n; i += kUnroll * stride) {
+        u32x4 v[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            v[u] = __builtin_nontemporal_load(src + i + u * stride);
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            __builtin_nontemporal_store(v[u], dst + i + u * stride);
+        }
+    }
+    for (; i < n; i += stride) {
+        dst[i] = src[i];
+    }
+}
+
+// Drops size-1 dimensions and merges neighbours that are contiguous with each other
+// (stride[d] == shape[d+1] * stride[d+1]), so a packed view becomes one dimension of stride 1.
+void collapse(CopyShape& s) {
+    CopyShape out{};
+    out.ndim = 0;
+    for (int d = 0; d < s.ndim; ++d) {
+        if (s.shape[d] == 1) {
+            continue;
+        }
+        if (out.ndim > 0 && out.strides[out.ndim - 1] == s.shape[d] * s.strides[d]) {
+            out.shape[out.ndim - 1] *= s.shape[d];
+            out.strides[out.ndim - 1] = s.strides[d];
+        } else {
+            out.shape[out.ndim] = s.shape[d];
+            out.strides[out.ndim] = s.strides[d];
+            ++out.ndim;
+        }
+    }
+    if (out.ndim == 0) { // a single element
+        out.ndim = 1;
+        out.shape[0] = 1;
+        out.strides[0] = 1;
+    }
+    s = out;
+}
+
 } // namespace
 
 extern "C" {
@@ -121,7 +171,9 @@ int mfr_get_device_info(int device, char* name, size_t cap, size_t* memory_bytes
         hipDeviceProp_t prop;
         check(hipGetDeviceProperties(&prop, mfr::hip_id(device)), "hipGetDeviceProperties");
         if (name != nullptr && cap > 0) {
-            std::strncpy(name, prop.name, cap - 1);
+            // Some drivers leave the marketing name empty; the architecture name is always set.
+            const char* source = prop.name[0] != '\0' ? prop.name : prop.gcnArchName;
+            std::strncpy(name, source, cap - 1);
             name[cap - 1] = '\0';
         }
         if (memory_bytes != nullptr) {
@@ -342,6 +394,21 @@ int mfr_strided_copy(mfr_stream_t stream, const void* src, void* dst, int32_t el
             return;
         }
         require(src != nullptr && dst != nullptr, "mfr_strided_copy: null pointer");
+        collapse(cs);
+        if (cs.ndim == 1 && cs.strides[0] == 1) {
+            // Packed source: a plain copy.
+            const size_t bytes = static_cast<size_t>(n) * static_cast<size_t>(elem_size);
+            if (bytes % 16 == 0 && mfr::aligned16(src) && mfr::aligned16(dst)) {
+                const int64_t units = static_cast<int64_t>(bytes / 16);
+                copy16_kernel<<<mfr::grid_blocks(units, 256 * 4, 8192), 256, 0, s.stream>>>(
+                    static_cast<const u32x4*>(src), static_cast<u32x4*>(dst), units);
+                mfr::check_launch("copy16_kernel");
+            } else {
+                check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s.stream),
+                      "hipMemcpyAsync");
+            }
+            return;
+        }
         const unsigned blocks = mfr::grid_blocks(n, 256, 65536);
         switch (elem_size) {
         case 1:
