@@ -197,6 +197,15 @@ int mfr_softmax(mfr_stream_t stream, const float* x, float* y, int64_t outer, in
  * NaN wins. Replaces Argmax (src/backends/cpu/backend.cpp:799-803, reduction.cpp:284-296). */
 int mfr_argmax(mfr_stream_t stream, const float* x, int64_t* out, int64_t rows, int64_t width);
 
+/* out[i] = a[i] + b[i] (op MFR_EW_ADD), a[i] * b[i] (MFR_EW_MUL), or alpha * a[i] (MFR_EW_SCAL,
+ * b unused) over n contiguous elements, one fp32 rounding each. Replaces the Add, Mul and Scal
+ * kernels (registered at src/backends/cpu/backend.cpp:856-867; add_f32/mul_f32 at
+ * src/backends/cpu/ops/elementwise/elementwise.cpp:72-91, scal_f32 at ops/blas/blas.cpp:23-28) that
+ * mensurflow::gemm's unfused composition dispatches (src/ops/blas.cpp:246-257). */
+enum { MFR_EW_ADD = 0, MFR_EW_MUL = 1, MFR_EW_SCAL = 2 };
+int mfr_elementwise(mfr_stream_t stream, int op, const float* a, const float* b, float alpha,
+                    float* out, int64_t n);
+
 /* ---- layout ------------------------------------------------------------------------------- */
 
 #define MFR_MAX_COPY_DIMS 8

@@ -23,6 +23,10 @@ ACT_NONE = 0
 ACT_GELU_TANH = 1
 ACT_GELU_ERF = 2
 
+EW_ADD = 0
+EW_MUL = 1
+EW_SCAL = 2
+
 MAX_BATCH_DIMS = 4
 MAX_COPY_DIMS = 8
 
@@ -82,6 +86,7 @@ SIGNATURES = {
     "mfr_where": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64]),
     "mfr_softmax": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64]),
     "mfr_argmax": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64]),
+    "mfr_elementwise": (ctypes.c_int, [_vp, ctypes.c_int, _vp, _vp, _f32, _vp, _i64]),
     "mfr_strided_copy": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, ctypes.POINTER(_i64),
                                         ctypes.POINTER(_i64)]),
     "mfr_fill": (ctypes.c_int, [_vp, _vp, _i32, _i64, ctypes.c_uint64]),

@@ -207,9 +207,44 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ x
     }
 }
 
+__global__ void binary_kernel(int op, const float* __restrict__ a, const float* __restrict__ b,
+                              float alpha, float* __restrict__ out, int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += stride) {
+        float v;
+        if (op == MFR_EW_ADD) {
+            v = a[i] + b[i];
+        } else if (op == MFR_EW_MUL) {
+            v = a[i] * b[i];
+        } else {
+            v = alpha * a[i];
+        }
+        out[i] = v;
+    }
+}
+
 } // namespace
 
 extern "C" {
+
+int mfr_elementwise(mfr_stream_t stream, int op, const float* a, const float* b, float alpha,
+                    float* out, int64_t n) {
+    return mfr::guarded([&] {
+        auto& s = mfr::stream_of(stream);
+        mfr::require(op == MFR_EW_ADD || op == MFR_EW_MUL || op == MFR_EW_SCAL,
+                     "elementwise: unknown op");
+        mfr::require(n >= 0, "elementwise: negative count");
+        if (n == 0) {
+            return;
+        }
+        mfr::require(a != nullptr && out != nullptr && (op == MFR_EW_SCAL || b != nullptr),
+                     "elementwise: null pointer");
+        binary_kernel<<<mfr::grid_blocks(n, 256, 16384), 256, 0, s.stream>>>(op, a, b, alpha, out,
+                                                                             n);
+        mfr::check_launch("binary_kernel");
+    });
+}
 
 int mfr_bias_act(mfr_stream_t stream, const float* x, const float* bias, float* y, int64_t rows,
                  int64_t cols, int act) {

@@ -1,0 +1,382 @@
+// The ROCm backend: MI355X (gfx950) devices behind mensurflow's Backend/Buffer/Stream interface
+// (src/backends/backend.hpp), with kernel adapters for the fp32 BLAS hot path. It reaches HIP
+// only through the C ABI of include/mfr_rocm.h (libmfr_rocm.so): no HIP header is included
+// here. Patterned on the reference's GPU backends: errors become exceptions carrying the
+// runtime's message (src/backends/cuda/backend.cpp:22-34), one stream per device created lazily
+// under a mutex (:222-229), zero devices when the runtime is missing (:200-220).
+//
+// Kernel adapters read tensor strides directly, so transposed, sliced and broadcast views reach
+// the GPU without a host round trip; an operand without a unit stride is first packed on the
+// device (OpId::StridedCopy).
+#include "backends/backend.hpp"
+#include "core/dispatcher.hpp"
+#include "core/registry.hpp"
+#include "core/tensor_access.hpp"
+#include "mfr_rocm.h"
+
+#include <algorithm>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace mensurflow::detail {
+
+namespace {
+
+// Status -> the exception the reference throws for the same failure.
+void check(int status) {
+    if (status == MFR_OK) {
+        return;
+    }
+    const std::string message = mfr_last_error();
+    if (status == MFR_E_INVALID) {
+        throw std::invalid_argument(message);
+    }
+    if (status == MFR_E_UNSUPPORTED) {
+        throw NotImplemented(message);
+    }
+    throw std::runtime_error(message);
+}
+
+class RocmBuffer final : public Buffer {
+  public:
+    RocmBuffer(int device, std::size_t bytes) : device_(device), size_(bytes) {
+        check(mfr_malloc(device, bytes, &data_));
+    }
+    ~RocmBuffer() override { (void)mfr_free(device_, data_); } // errors ignored, as the reference
+    RocmBuffer(const RocmBuffer&) = delete;
+    RocmBuffer& operator=(const RocmBuffer&) = delete;
+    std::size_t size() const override { return size_; }
+    void* native() const override { return data_; }
+
+  private:
+    int device_;
+    std::size_t size_;
+    void* data_ = nullptr;
+};
+
+std::byte* bytes_of(const Buffer& buffer) { return static_cast<std::byte*>(buffer.native()); }
+
+class RocmStream final : public Stream {
+  public:
+    explicit RocmStream(int device) { check(mfr_stream_create(device, &stream_)); }
+    ~RocmStream() override { (void)mfr_stream_destroy(stream_); }
+    RocmStream(const RocmStream&) = delete;
+    RocmStream& operator=(const RocmStream&) = delete;
+
+    void copy_h2d(Buffer& dst, std::size_t offset, const void* src, std::size_t bytes) override {
+        check(mfr_memcpy_h2d(stream_, bytes_of(dst) + offset, src, bytes));
+    }
+    void copy_d2h(void* dst, const Buffer& src, std::size_t offset, std::size_t bytes) override {
+        check(mfr_memcpy_d2h(stream_, dst, bytes_of(src) + offset, bytes));
+    }
+    void copy_d2d(Buffer& dst, std::size_t dst_offset, const Buffer& src, std::size_t src_offset,
+                  std::size_t bytes) override {
+        check(mfr_memcpy_d2d(stream_, bytes_of(dst) + dst_offset, bytes_of(src) + src_offset,
+                             bytes));
+    }
+    void synchronize() override { check(mfr_stream_sync(stream_)); }
+
+    mfr_stream_t handle() const { return stream_; }
+
+  private:
+    mfr_stream_t stream_ = nullptr;
+};
+
+mfr_stream_t handle(Stream& stream) { return static_cast<RocmStream&>(stream).handle(); }
+
+template <typename T> T* ptr(const Tensor& t) { return TensorAccess::data<T>(t); }
+
+// ---- GEMM family -------------------------------------------------------------------------------
+
+// A matrix operand the GEMM kernel can read: a unit stride in one of its two dimensions (or an
+// extent of 1 there). Otherwise a packed copy on the device.
+Tensor readable_matrix(const Tensor& t) {
+    const int nd = t.dim();
+    const auto& s = t.strides();
+    const bool rows_unit = s[nd - 2] == 1 || t.size(-2) == 1;
+    const bool cols_unit = s[nd - 1] == 1 || t.size(-1) == 1;
+    return rows_unit || cols_unit ? t : t.contiguous();
+}
+
+void fill_matrix(mfr_gemm_desc& d, const Tensor& a, const Tensor& b, const Tensor& out) {
+    d.m = out.size(-2);
+    d.n = out.size(-1);
+    d.k = a.size(-1);
+    d.a = ptr<float>(a);
+    d.a_rs = a.strides()[a.dim() - 2];
+    d.a_cs = a.strides()[a.dim() - 1];
+    d.b = ptr<float>(b);
+    d.b_rs = b.strides()[b.dim() - 2];
+    d.b_cs = b.strides()[b.dim() - 1];
+    d.c = ptr<float>(out);
+    d.c_rs = out.size(-1);
+}
+
+// Inputs: op(a) [m,k] and op(b) [k,n] as views; out contiguous [m,n].
+void matmul_kernel(const OpArgs& args, Stream& stream) {
+    const Tensor a = readable_matrix(args.inputs[0]);
+    const Tensor b = readable_matrix(args.inputs[1]);
+    mfr_gemm_desc d{};
+    fill_matrix(d, a, b, args.outputs[0]);
+    d.alpha = 1.0f;
+    d.beta = 0.0f;
+    d.act = MFR_ACT_NONE;
+    check(mfr_sgemm(handle(stream), &d));
+}
+
+// OpId::Gemm: inputs op(a), op(b), then c0 [m,n] when beta != 0, then bias [n] when has_bias.
+void gemm_kernel(const OpArgs& args, Stream& stream) {
+    const Tensor a = readable_matrix(args.inputs[0]);
+    const Tensor b = readable_matrix(args.inputs[1]);
+    const Tensor& out = args.outputs[0];
+    mfr_gemm_desc d{};
+    fill_matrix(d, a, b, out);
+    d.alpha = args.alpha;
+    d.beta = args.beta;
+    std::size_t next = 2;
+    if (args.beta != 0.0f) {
+        const Tensor& c0 = args.inputs[next++];
+        d.c0 = ptr<float>(c0);
+        d.c0_rs = out.size(-1);
+    }
+    if (args.has_bias) {
+        d.bias = ptr<float>(args.inputs[next]);
+    }
+    d.act = args.activation;
+    check(mfr_sgemm(handle(stream), &d));
+}
+
+// OpId::GemmBatched: a [batch..., m, k] and b [batch..., k, n] as views with the full batch shape
+// (stride 0 on broadcast dimensions), out contiguous, and c0 (contiguous, out's shape) when
+// beta != 0. Batch dimensions that step through memory together are merged, size-1 dimensions
+// dropped; more than MFR_MAX_BATCH_DIMS left are walked on the host, one launch per index.
+void gemm_batched_kernel(const OpArgs& args, Stream& stream) {
+    const Tensor a = readable_matrix(args.inputs[0]);
+    const Tensor b = readable_matrix(args.inputs[1]);
+    const Tensor& out = args.outputs[0];
+    const bool with_c0 = args.inputs.size() > 2;
+    const Tensor* c0 = with_c0 ? &args.inputs[2] : nullptr;
+    const int batch_dims = out.dim() - 2;
+    struct Dim {
+        std::int64_t size, a, b, c, c0;
+    };
+    std::vector<Dim> dims;
+    for (int d = 0; d < batch_dims; ++d) {
+        const auto du = static_cast<std::size_t>(d);
+        const Dim dim{out.size(d), a.strides()[du], b.strides()[du], out.strides()[du],
+                      c0 != nullptr ? c0->strides()[du] : 0};
+        if (dim.size == 1) {
+            continue;
+        }
+        if (!dims.empty()) {
+            Dim& prev = dims.back();
+            if (prev.a == dim.size * dim.a && prev.b == dim.size * dim.b &&
+                prev.c == dim.size * dim.c && prev.c0 == dim.size * dim.c0) {
+                prev.size *= dim.size;
+                prev.a = dim.a;
+                prev.b = dim.b;
+                prev.c = dim.c;
+                prev.c0 = dim.c0;
+                continue;
+            }
+        }
+        dims.push_back(dim);
+    }
+    mfr_gemm_desc d{};
+    fill_matrix(d, a, b, out);
+    d.alpha = args.alpha;
+    d.beta = with_c0 ? args.beta : 0.0f;
+    d.act = MFR_ACT_NONE;
+    if (with_c0) {
+        d.c0 = ptr<float>(*c0);
+        d.c0_rs = out.size(-1);
+    }
+    const std::size_t inner = std::min<std::size_t>(dims.size(), MFR_MAX_BATCH_DIMS);
+    const std::size_t outer = dims.size() - inner;
+    d.batch_dims = static_cast<std::int32_t>(inner);
+    for (std::size_t i = 0; i < inner; ++i) {
+        const Dim& dim = dims[outer + i];
+        d.batch[i] = dim.size;
+        d.a_bs[i] = dim.a;
+        d.b_bs[i] = dim.b;
+        d.c_bs[i] = dim.c;
+        d.c0_bs[i] = dim.c0;
+    }
+    // Host loop over the outermost dimensions beyond what one launch takes.
+    std::int64_t launches = 1;
+    for (std::size_t i = 0; i < outer; ++i) {
+        launches *= dims[i].size;
+    }
+    const float* a0 = d.a;
+    const float* b0 = d.b;
+    float* c_base = d.c;
+    const float* c0_base = d.c0;
+    for (std::int64_t l = 0; l < launches; ++l) {
+        std::int64_t rest = l, oa = 0, ob = 0, oc = 0, oc0 = 0;
+        for (std::size_t i = outer; i-- > 0;) {
+            const std::int64_t idx = rest % dims[i].size;
+            rest /= dims[i].size;
+            oa += idx * dims[i].a;
+            ob += idx * dims[i].b;
+            oc += idx * dims[i].c;
+            oc0 += idx * dims[i].c0;
+        }
+        d.a = a0 + oa;
+        d.b = b0 + ob;
+        d.c = c_base + oc;
+        d.c0 = c0_base != nullptr ? c0_base + oc0 : nullptr;
+        check(mfr_sgemm(handle(stream), &d));
+    }
+}
+
+// ---- GEMV --------------------------------------------------------------------------------------
+
+// Inputs: a contiguous [rows, cols], x, and y0 when given; args.transpose = A^T.
+void gemv_kernel(const OpArgs& args, Stream& stream) {
+    const Tensor& a = args.inputs[0];
+    const float* y0 = args.inputs.size() > 2 ? ptr<float>(args.inputs[2]) : nullptr;
+    check(mfr_sgemv(handle(stream), args.transpose ? 1 : 0, a.size(0), a.size(1), args.alpha,
+                    ptr<float>(a), a.size(1), ptr<float>(args.inputs[1]), y0 ? args.beta : 0.0f,
+                    y0, ptr<float>(args.outputs[0])));
+}
+
+void matvec_kernel(const OpArgs& args, Stream& stream) {
+    const Tensor& a = args.inputs[0];
+    check(mfr_smatvec(handle(stream), a.size(0), a.size(1), ptr<float>(a), a.size(1),
+                      ptr<float>(args.inputs[1]), ptr<float>(args.outputs[0])));
+}
+
+// ---- elementwise, softmax, argmax, layout ------------------------------------------------------
+
+void bias_add_kernel(const OpArgs& args, Stream& stream) {
+    const Tensor& out = args.outputs[0];
+    check(mfr_bias_act(handle(stream), ptr<float>(args.inputs[0]), ptr<float>(args.inputs[1]),
+                       ptr<float>(out), out.size(0), out.size(1), MFR_ACT_NONE));
+}
+
+void gelu_kernel(const OpArgs& args, Stream& stream) {
+    const Tensor& out = args.outputs[0];
+    check(mfr_bias_act(handle(stream), ptr<float>(args.inputs[0]), nullptr, ptr<float>(out), 1,
+                       out.numel(), args.approximate ? MFR_ACT_GELU_TANH : MFR_ACT_GELU_ERF));
+}
+
+// Inputs: x, y, condition (values first: the dispatch key is their dtype), all out's shape.
+void where_kernel(const OpArgs& args, Stream& stream) {
+    const Tensor& out = args.outputs[0];
+    check(mfr_where(handle(stream), ptr<std::uint8_t>(args.inputs[2]), ptr<float>(args.inputs[0]),
+                    ptr<float>(args.inputs[1]), ptr<float>(out), out.numel()));
+}
+
+void softmax_kernel(const OpArgs& args, Stream& stream) {
+    const Tensor& x = args.inputs[0];
+    std::int64_t outer = 1, length = 1, inner = 1;
+    for (int d = 0; d < x.dim(); ++d) {
+        if (d < args.axis) {
+            outer *= x.size(d);
+        } else if (d == args.axis) {
+            length = x.size(d);
+        } else {
+            inner *= x.size(d);
+        }
+    }
+    check(mfr_softmax(handle(stream), ptr<float>(x), ptr<float>(args.outputs[0]), outer, length,
+                      inner));
+}
+
+void argmax_kernel(const OpArgs& args, Stream& stream) {
+    const Tensor& x = args.inputs[0];
+    const std::int64_t width = x.size(x.dim() - 1);
+    check(mfr_argmax(handle(stream), ptr<float>(x), ptr<std::int64_t>(args.outputs[0]),
+                     x.numel() / width, width));
+}
+
+template <int Op> void binary_kernel(const OpArgs& args, Stream& stream) {
+    const Tensor& out = args.outputs[0];
+    const float* b = Op == MFR_EW_SCAL ? nullptr : ptr<float>(args.inputs[1]);
+    check(mfr_elementwise(handle(stream), Op, ptr<float>(args.inputs[0]), b, args.alpha,
+                          ptr<float>(out), out.numel()));
+}
+
+// Packs a strided view (any dtype) into the contiguous output on the device.
+void strided_copy_kernel(const OpArgs& args, Stream& stream) {
+    const Tensor& x = args.inputs[0];
+    if (x.dim() > MFR_MAX_COPY_DIMS) {
+        throw NotImplemented("strided_copy: more than " + std::to_string(MFR_MAX_COPY_DIMS) +
+                             " dimensions on rocm");
+    }
+    check(mfr_strided_copy(handle(stream), ptr<std::byte>(x), ptr<std::byte>(args.outputs[0]),
+                           static_cast<std::int32_t>(x.itemsize()), x.dim(), x.shape().data(),
+                           x.strides().data()));
+}
+
+class RocmBackend final : public Backend {
+  public:
+    RocmBackend() {
+        int count = 0;
+        if (mfr_get_device_count(&count) == MFR_OK) {
+            count_ = count;
+        }
+        streams_.resize(static_cast<std::size_t>(count_));
+    }
+
+    DeviceType type() const override { return DeviceType::ROCm; }
+    int device_count() const override { return count_; }
+
+    DeviceInfo info(int index) const override {
+        char name[256] = {0};
+        std::size_t bytes = 0;
+        check(mfr_get_device_info(index, name, sizeof(name), &bytes, nullptr, nullptr));
+        return {name, bytes};
+    }
+
+    std::shared_ptr<Buffer> allocate(int index, std::size_t bytes) override {
+        return std::make_shared<RocmBuffer>(index, bytes);
+    }
+
+    Stream& stream(int index) override {
+        std::lock_guard<std::mutex> lock(mutex_);
+        auto& slot = streams_.at(static_cast<std::size_t>(index));
+        if (!slot) {
+            slot = std::make_unique<RocmStream>(index);
+        }
+        return *slot;
+    }
+
+    void register_kernels(Dispatcher& dispatcher) override {
+        auto add = [&dispatcher](OpId op, KernelFn kernel) {
+            dispatcher.register_kernel({op, DeviceType::ROCm, DType::F32}, kernel);
+        };
+        add(OpId::Matmul, matmul_kernel);
+        add(OpId::Gemm, gemm_kernel);
+        add(OpId::GemmBatched, gemm_batched_kernel);
+        add(OpId::Gemv, gemv_kernel);
+        add(OpId::Matvec, matvec_kernel);
+        add(OpId::BiasAdd, bias_add_kernel);
+        add(OpId::Gelu, gelu_kernel);
+        add(OpId::Where, where_kernel);
+        add(OpId::Softmax, softmax_kernel);
+        add(OpId::Argmax, argmax_kernel);
+        add(OpId::Add, binary_kernel<MFR_EW_ADD>);
+        add(OpId::Mul, binary_kernel<MFR_EW_MUL>);
+        add(OpId::Scal, binary_kernel<MFR_EW_SCAL>);
+        for (DType type : {DType::F32, DType::I32, DType::I64, DType::U8, DType::Bool,
+                           DType::F16, DType::BF16}) {
+            dispatcher.register_kernel({OpId::StridedCopy, DeviceType::ROCm, type},
+                                       strided_copy_kernel);
+        }
+    }
+
+  private:
+    int count_ = 0;
+    std::mutex mutex_;
+    std::vector<std::unique_ptr<RocmStream>> streams_;
+};
+
+} // namespace
+
+void register_rocm_backend(Registry& registry) { registry.add(std::make_unique<RocmBackend>()); }
+
+} // namespace mensurflow::detail

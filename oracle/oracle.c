@@ -203,6 +203,20 @@ void orc_axpby_f32(float* out, const float* x, float alpha, const float* y0, flo
     }
 }
 
+void orc_add_f32(const float* a, const float* b, float* out, int64_t n) {
+#pragma omp parallel for schedule(static) if (n > 65536)
+    for (int64_t i = 0; i < n; ++i) {
+        out[i] = a[i] + b[i];
+    }
+}
+
+void orc_mul_f32(const float* a, const float* b, float* out, int64_t n) {
+#pragma omp parallel for schedule(static) if (n > 65536)
+    for (int64_t i = 0; i < n; ++i) {
+        out[i] = a[i] * b[i];
+    }
+}
+
 /* ---- GEMV ---------------------------------------------------------------------------------- */
 
 void orc_matvec_f32(const float* a, const float* x, float* y, int64_t m, int64_t k) {

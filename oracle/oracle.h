@@ -5,10 +5,10 @@
  * links or calls it.
  *
  * Each function restates the behaviour (not the text) of the reference function it cites, as
- * path:line into bakir004/mensurflow. How each one is pinned (golden vectors from the
- * reference's tests, the compiled reference in oracle/_ref, closed forms) is recorded in
- * DESIGN.md; a function without such a check would say "parity unpinned" here. All functions
- * are pinned.
+ * path:line into bakir004/mensurflow. Every function is pinned by tests/test_oracle.py: golden
+ * vectors from the reference's own tests, vectors written by the reference's kernels compiled
+ * from their sources (oracle/_ref, tests/golden/ref_vectors.npz), and closed forms. A function
+ * without such a check would say "parity unpinned" here; none does.
  */
 #ifndef MFR_ORACLE_H
 #define MFR_ORACLE_H
@@ -41,6 +41,10 @@ void orc_sgemm_packed(int64_t m, int64_t n, int64_t k, const float* a, int64_t r
  * y0 == NULL or beta == 0 drops the second term. The alpha/beta passes of mensurflow::gemm
  * (src/ops/blas.cpp:246-257) and of the batched finish pass (gemm_batched.cpp:12-28). */
 void orc_axpby_f32(float* out, const float* x, float alpha, const float* y0, float beta, int64_t n);
+
+/* add_f32 / mul_f32 (src/backends/cpu/ops/elementwise/elementwise.cpp:72-91). */
+void orc_add_f32(const float* a, const float* b, float* out, int64_t n);
+void orc_mul_f32(const float* a, const float* b, float* out, int64_t n);
 
 /* matvec_f32 / gemv_f32 (src/backends/cpu/ops/blas/blas.cpp:55-79): double accumulation in
  * increasing index, one rounding. */

@@ -1,0 +1,173 @@
+// Host-layer core: device naming, the op table, execution-device rules, registry, Tensor views
+// and transfers on every device (the behaviours the reference's tests/core/dispatcher_test.cpp,
+// transfer_test.cpp and device tests pin).
+#include "core/dispatcher.hpp"
+#include "core/registry.hpp"
+#include "oracle_cpu.hpp"
+#include "test_util.hpp"
+
+#include <cstdlib>
+#include <numeric>
+
+using namespace mensurflow;
+using detail::Dispatcher;
+using detail::KernelKey;
+using detail::OpArgs;
+using detail::OpId;
+
+namespace {
+
+void noop_kernel(const OpArgs&, detail::Stream&) {}
+
+void test_device_names() {
+    test::require(to_string(Device{DeviceType::ROCm, 1}) == "rocm:1", "rocm:1 name");
+    test::require(parse_device("ROCm") == (Device{DeviceType::ROCm, 0}), "parse rocm");
+    test::require(parse_device("rocm:3") == (Device{DeviceType::ROCm, 3}), "parse rocm:3");
+    test::require(parse_device("cpu") == (Device{DeviceType::CPU, 0}), "parse cpu");
+    test::require_throws<std::invalid_argument>([] { parse_device("tpu:0"); }, "unknown type");
+    test::require_throws<std::invalid_argument>([] { parse_device("rocm:-1"); }, "negative index");
+    test::require_throws<std::invalid_argument>([] { parse_device("rocm:"); }, "empty index");
+}
+
+void test_dispatcher_table() {
+    Dispatcher d;
+    const KernelKey key{OpId::Matmul, DeviceType::ROCm, DType::F32};
+    test::require(d.find(key) == nullptr, "empty table");
+    d.register_kernel(key, noop_kernel);
+    test::require(d.find(key) == noop_kernel, "registered kernel is found");
+    test::require_throws<std::logic_error>([&] { d.register_kernel(key, noop_kernel); },
+                                           "duplicate registration");
+    test::require_throws<std::invalid_argument>(
+        [&] { d.register_kernel({OpId::Gemv, DeviceType::ROCm, DType::F32}, nullptr); },
+        "null kernel");
+    try {
+        d.lookup({OpId::Softmax, DeviceType::ROCm, DType::I32});
+        throw std::runtime_error("lookup of a missing kernel did not throw");
+    } catch (const detail::NotImplemented& e) {
+        const std::string what = e.what();
+        test::require(what.find("softmax") != std::string::npos &&
+                          what.find("rocm") != std::string::npos &&
+                          what.find("i32") != std::string::npos,
+                      "NotImplemented names op, device and dtype: " + what);
+    }
+}
+
+void test_execution_device() {
+    test::require(detail::execution_device(Execution::CPU, {DeviceType::ROCm, 0}) ==
+                      (Device{DeviceType::CPU, 0}),
+                  "CPU runs on cpu:0");
+    test::require(detail::execution_device(Execution::Auto, {DeviceType::CPU, 0}) ==
+                      (Device{DeviceType::CPU, 0}),
+                  "Auto runs on cpu:0");
+    test::require(detail::execution_device(Execution::GPU, {DeviceType::ROCm, 0}) ==
+                      (Device{DeviceType::ROCm, 0}),
+                  "GPU keeps the data's GPU");
+    const bool has_gpu = detail::Registry::instance().find(DeviceType::ROCm) != nullptr;
+    if (has_gpu) {
+        test::require(detail::execution_device(Execution::GPU, {DeviceType::CPU, 0}) ==
+                          (Device{DeviceType::ROCm, 0}),
+                      "GPU from CPU data picks rocm:0");
+    } else {
+        test::require_throws<std::runtime_error>(
+            [] { detail::execution_device(Execution::GPU, {DeviceType::CPU, 0}); },
+            "GPU with no GPU throws");
+    }
+}
+
+void test_registry_and_default_device() {
+    const auto devices = list_devices();
+    test::require(!devices.empty() && devices[0] == (Device{DeviceType::CPU, 0}), "CPU first");
+    test::require_throws<std::runtime_error>(
+        [] { Tensor::empty({2}, DType::F32, {DeviceType::ROCm, 99}); }, "unavailable device");
+    setenv("MENSURFLOW_DEVICE", "vulkan:0", 1);
+    test::require_throws<std::runtime_error>([] { default_device(); },
+                                             "MENSURFLOW_DEVICE names a missing device");
+    setenv("MENSURFLOW_DEVICE", "cpu", 1);
+    test::require(default_device() == (Device{DeviceType::CPU, 0}), "MENSURFLOW_DEVICE=cpu");
+    unsetenv("MENSURFLOW_DEVICE");
+    const bool has_gpu = device_available({DeviceType::ROCm, 0});
+    test::require(default_device().type == (has_gpu ? DeviceType::ROCm : DeviceType::CPU),
+                  "default device prefers a GPU");
+}
+
+std::vector<float> iota(std::int64_t n) {
+    std::vector<float> v(static_cast<std::size_t>(n));
+    std::iota(v.begin(), v.end(), 0.0f);
+    return v;
+}
+
+void test_transfers(Device device) {
+    const auto values = iota(2 * 3 * 4);
+    const Tensor t = Tensor::from_vector(values, {2, 3, 4}, device);
+    test::require(t.device() == device && t.is_contiguous(), "from_vector");
+    test::require(t.to_vector<float>() == values, "round trip");
+    // A transposed view read back follows strides; contiguous() packs it (on the device for rocm).
+    const Tensor tt = t.transpose(0, 2);
+    std::vector<float> want;
+    for (int c = 0; c < 4; ++c) {
+        for (int b = 0; b < 3; ++b) {
+            for (int a = 0; a < 2; ++a) {
+                want.push_back(values[static_cast<std::size_t>(a * 12 + b * 4 + c)]);
+            }
+        }
+    }
+    test::require(tt.to_vector<float>() == want, "strided read-back");
+    const Tensor packed = tt.contiguous();
+    test::require(packed.is_contiguous() && packed.device() == device &&
+                      packed.to_vector<float>() == want,
+                  "contiguous() on " + to_string(device));
+    // Slices and broadcasts.
+    test::require(t.slice(1, 1, 3).to_vector<float>().size() == 16, "slice");
+    const Tensor row = Tensor::from_vector(std::vector<float>{1, 2, 3}, {3}, device);
+    const auto expanded = row.expand({2, 3}).contiguous().to_vector<float>();
+    test::require(expanded == (std::vector<float>{1, 2, 3, 1, 2, 3}), "expand + contiguous");
+    // Bool and I64 tensors move too.
+    const Tensor mask = Tensor::full({2, 2}, 1.0, DType::Bool, device);
+    std::vector<std::uint8_t> bytes(4);
+    mask.transpose(0, 1).copy_to_host(bytes.data());
+    test::require(bytes == (std::vector<std::uint8_t>{1, 1, 1, 1}), "bool round trip");
+    const Tensor idx = Tensor::from_vector(std::vector<std::int64_t>{7, -3}, {2}, device);
+    test::require(idx.to_vector<std::int64_t>() == (std::vector<std::int64_t>{7, -3}), "i64");
+    // copy_from into a contiguous destination stays on the device.
+    Tensor dst = Tensor::zeros({4, 3, 2}, DType::F32, device);
+    dst.copy_from(tt);
+    test::require(dst.to_vector<float>() == want, "copy_from a view");
+    // to() between devices.
+    const Tensor back = t.to({DeviceType::CPU, 0});
+    test::require(back.device() == (Device{DeviceType::CPU, 0}) && back.to_vector<float>() == values,
+                  "to(cpu)");
+    // Empty tensors.
+    test::require(Tensor::empty({0, 5}, DType::F32, device).to_vector<float>().empty(), "empty");
+}
+
+void test_run_elsewhere() {
+    // Data on the CPU, op on the GPU: inputs copied over, result written back into the CPU output.
+    if (!device_available({DeviceType::ROCm, 0}) || test::options().cpu_only) {
+        return;
+    }
+    const Tensor a = Tensor::from_vector(std::vector<float>{1, 2, 3, 4, 5, 6}, {2, 3});
+    const Tensor b = Tensor::from_vector(std::vector<float>{7, 8, 9, 10, 11, 12}, {3, 2});
+    const Tensor c = matmul(a, b, Execution::GPU);
+    test::require(c.device() == (Device{DeviceType::CPU, 0}), "result stays on the data's device");
+    test::require(c.to_vector<float>() == (std::vector<float>{58, 64, 139, 154}),
+                  "GPU result written back");
+    test::require_throws<std::invalid_argument>(
+        [&] { matmul(a, b.to({DeviceType::ROCm, 0}), Execution::GPU); }, "mixed devices");
+}
+
+} // namespace
+
+int main(int argc, char** argv) {
+    return test::run("core_test", argc, argv, [] {
+        test::register_oracle_cpu_kernels();
+        test_device_names();
+        test_dispatcher_table();
+        test_execution_device();
+        test_registry_and_default_device();
+        for (Device device : test::devices()) {
+            std::cout << "  transfers on " << to_string(device) << '\n';
+            test_transfers(device);
+        }
+        test_run_elsewhere();
+    });
+}

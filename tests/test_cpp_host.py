@@ -1,0 +1,37 @@
+"""Runs the C++ tests of the host layer (tests/cpp): the mirrored mensurflow API -- Tensor,
+Dispatcher, Registry and the ops -- with the CPU side served by the oracle and, under -m gpu,
+the rocm device served by the HIP kernels through the C ABI."""
+import os
+import subprocess
+
+import pytest
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CPP = os.path.join(HERE, "cpp")
+TESTS = ["core_test", "blas_test", "attention_test"]
+
+
+def binary(name):
+    path = os.path.join(CPP, "bin", name)
+    if not os.path.exists(path):
+        subprocess.run(["make", "-s", "-C", CPP], check=True)
+    return path
+
+
+def run(name, *flags, timeout=600):
+    proc = subprocess.run([binary(name), *flags], capture_output=True, text=True, timeout=timeout)
+    out = proc.stdout + proc.stderr
+    print(out)
+    assert proc.returncode == 0, out
+    assert f"{name} passed" in out
+
+
+@pytest.mark.parametrize("name", TESTS)
+def test_host_layer_cpu(name):
+    run(name, "--cpu-only")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", TESTS)
+def test_host_layer_rocm(name):
+    run(name, "--require-gpu")
