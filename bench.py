@@ -119,6 +119,28 @@ def bench_mlp(mf, stream, steps, warmup):
     return {"event_ms": event_ms, "flops": 2.0 * m * n * k}
 
 
+def bench_attention(mf, stream, steps, warmup):
+    """attention q, k, v [8, 16, 1024, 64], causal -- the reference's composition
+    (batched GEMM, where, softmax, batched GEMM), reported per stage and end to end."""
+    rng = np.random.default_rng(4)
+    b, h, s, d = 8, 16, 1024, 64
+    q, k, v = (mf.DeviceArray.from_numpy(rng.standard_normal((b, h, s, d)).astype(np.float32),
+                                         stream) for _ in range(3))
+    scores = mf.DeviceArray.empty((b, h, s, s), stream)
+    out = mf.DeviceArray.empty((b, h, s, d), stream)
+    _, qk_ms = time_launches(mf, stream, lambda: mf.gemm_batched(
+        q, k.transpose(-2, -1), scores, alpha=0.125), steps, warmup)
+    _, sm_ms = time_launches(mf, stream, lambda: mf.softmax(scores, out=scores), steps, warmup)
+    _, pv_ms = time_launches(mf, stream, lambda: mf.gemm_batched(scores, v, out), steps, warmup)
+    total_steps = max(3, steps // 5)
+    wall_ms, _ = time_launches(mf, stream, lambda: mf.attention(q, k, v, causal=True),
+                               total_steps, 1)
+    gemm_flops = 2.0 * b * h * s * s * d
+    return {"qk_ms": qk_ms, "softmax_ms": sm_ms, "pv_ms": pv_ms, "total_ms": wall_ms,
+            "flops": 2 * gemm_flops, "gemm_flops": gemm_flops,
+            "scores_bytes": 4.0 * b * h * s * s}
+
+
 def bench_copy(mf, stream, steps, warmup):
     """A plain 1 GiB device copy (the strided-copy kernel on a contiguous view): the measured
     HBM ceiling, and the calibration kernel for rocprofv3's FETCH_SIZE / WRITE_SIZE."""
@@ -186,7 +208,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["all", "gemm", "gemv", "mlp", "copy"], default="all",
+    ap.add_argument("--only", choices=["all", "gemm", "gemv", "mlp", "copy", "attention"],
+                    default="all",
                     help="run one leg (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -216,6 +239,9 @@ def main() -> int:
     if args.only in ("all", "mlp"):
         log("mlp 4093x1023x4099 + bias + gelu ...")
         result["mlp"] = bench_mlp(mf, stream, max(5, args.steps // 5), args.warmup)
+    if args.only in ("all", "attention"):
+        log("attention 8x16x1024x64 causal ...")
+        result["attention"] = bench_attention(mf, stream, max(5, args.steps // 5), args.warmup)
     if args.only in ("all", "copy"):
         log("copy 1 GiB ...")
         result["copy"] = bench_copy(mf, stream, max(5, args.steps // 5), args.warmup)
@@ -269,6 +295,16 @@ def main() -> int:
                       "ms_per_call": round(mlp["event_ms"], 4),
                       "frac": round(mlp["flops"] / (mlp["event_ms"] * 1e-3) / 1e12
                                     / PEAK_FP32_MFMA_TFLOPS, 4)},
+        "attention": {
+            "ms_per_call": round(result["attention"]["total_ms"], 3),
+            "qk_gemm_tflops": round(result["attention"]["gemm_flops"]
+                                    / (result["attention"]["qk_ms"] * 1e-3) / 1e12, 2),
+            "pv_gemm_tflops": round(result["attention"]["gemm_flops"]
+                                    / (result["attention"]["pv_ms"] * 1e-3) / 1e12, 2),
+            "softmax_gbs": round(2 * result["attention"]["scores_bytes"]
+                                 / (result["attention"]["softmax_ms"] * 1e-3) / 1e9, 1),
+            "note": "reference composition: 2 batched GEMMs (4*B*H*S^2*D FLOP, dense), where "
+                    "with packed mask and -inf operands, softmax over materialized scores"},
         "copy_1gib": {"gbs": round(result["copy"]["bytes"] / (result["copy"]["event_ms"] * 1e-3)
                                    / 1e9, 1),
                       "note": "plain device copy, read+write bytes; the practical HBM ceiling"},

@@ -25,7 +25,7 @@ from .abi import ACT_GELU_ERF, ACT_GELU_TANH, ACT_NONE, GemmDesc  # noqa: F401
 __all__ = [
     "ACT_NONE", "ACT_GELU_TANH", "ACT_GELU_ERF", "GemmDesc", "device_count", "device_info",
     "Stream", "DeviceArray", "Event", "sgemm", "gemm", "gemm_batched", "sgemv", "matvec",
-    "bias_act", "where", "softmax", "argmax", "strided_copy", "fill",
+    "bias_act", "where", "softmax", "argmax", "strided_copy", "fill", "attention",
 ]
 
 
@@ -418,3 +418,41 @@ def fill(x: DeviceArray, value) -> None:
         {1: np.uint8, 2: np.uint16, 4: np.uint32, 8: np.uint64}[x.dtype.itemsize])[0]
     abi.check(abi.load().mfr_fill(x.stream.handle, x.ptr, x.dtype.itemsize, x.size, int(bits)),
               "mfr_fill")
+
+
+def attention(q: DeviceArray, k: DeviceArray, v: DeviceArray, mask: DeviceArray | None = None,
+              causal: bool = False, scale: float = 0.0) -> DeviceArray:
+    """mensurflow::attention's composition on the device (src/ops/attention.cpp:48-98): scores =
+    gemm_batched(q, k^T, alpha=scale), where(mask, scores, -inf) with the mask and the -inf
+    scalar packed to the scores' shape (as mensurflow::where packs them), the causal mask the
+    same way, softmax over the keys, gemm_batched(weights, v). q [..., Lq, D], k [..., Lk, D],
+    v [..., Lk, Dv] with equal batch shapes; mask a Bool (uint8) array broadcastable to
+    [..., Lq, Lk]."""
+    stream = q.stream
+    lq, depth = q.shape[-2:]
+    lk = k.shape[-2]
+    batch = q.shape[:-2]
+    if scale == 0.0:
+        scale = float(np.float32(1.0 / np.sqrt(depth))) if depth > 0 else 1.0
+    scores = DeviceArray.empty(batch + (lq, lk), stream)
+    gemm_batched(q, k.transpose(-2, -1), scores, alpha=scale)
+    minus_inf = None
+
+    def masked(keep: DeviceArray) -> DeviceArray:
+        nonlocal minus_inf
+        if minus_inf is None:
+            scalar = DeviceArray.empty((1,), stream)
+            fill(scalar, -np.inf)
+            minus_inf = strided_copy(scalar.expand(scores.shape))
+        full_mask = strided_copy(keep.expand(scores.shape))
+        return where(full_mask, scores, minus_inf, out=scores)
+
+    if mask is not None:
+        masked(mask)
+    if causal:
+        lower = np.tril(np.ones((lq, lk), dtype=np.uint8))
+        masked(DeviceArray.from_numpy(lower, stream))
+    weights = softmax(scores, axis=-1, out=scores)
+    out = DeviceArray.empty(batch + (lq, v.shape[-1]), stream)
+    gemm_batched(weights, v, out)
+    return out
