@@ -145,7 +145,23 @@ typedef struct mfr_gemm_desc {
     int64_t c0_bs[MFR_MAX_BATCH_DIMS];
     const float* bias;                        /* [n] or NULL; shared by every batch */
     float alpha, beta;
+    int32_t tile;                             /* MFR_TILE_AUTO or a fixed MFR_TILE_* */
+    int32_t reserved;
 } mfr_gemm_desc;
+
+/* Workgroup tile of mfr_sgemm (rows x cols x depth slice). AUTO picks one from the shape: a cost
+ * model of ceil(tiles / CUs) * tile area / measured efficiency, and the high-occupancy tiles for
+ * a short depth. A fixed tile is what a tuner sets (the reference's TuningConfig,
+ * src/core/dispatcher.hpp:145-149). Every tile gives the same results up to summation order. */
+enum {
+    MFR_TILE_AUTO = 0,
+    MFR_TILE_256x256 = 1, /* 8 wavefronts of 128x64, 1 workgroup per CU */
+    MFR_TILE_128x128 = 2, /* 4 wavefronts of 64x64, 2 per CU */
+    MFR_TILE_128x64 = 3,  /* 4 wavefronts of 64x32, depth slice 16, up to 5 per CU */
+    MFR_TILE_64x128 = 4,  /* 4 wavefronts of 32x64, depth slice 16 */
+    MFR_TILE_64x64 = 5,   /* 4 wavefronts of 32x32, 4 per CU */
+    MFR_TILE_COUNT = 6
+};
 
 int mfr_sgemm(mfr_stream_t stream, const mfr_gemm_desc* desc);
 

@@ -281,7 +281,7 @@ def _fill_batch(field, values, dims):
 
 def gemm_batched(a: DeviceArray, b: DeviceArray, c: DeviceArray, *, alpha=1.0,
                  c0: DeviceArray | None = None, beta=0.0, bias: DeviceArray | None = None,
-                 act=ACT_NONE) -> None:
+                 act=ACT_NONE, tile=0) -> None:
     """c[...] = act(alpha*a@b + beta*c0 + bias) over the leading (batch) dimensions.
 
     a is [..., m, k], b is [..., k, n] (any strides with a unit stride in one matrix dimension;
@@ -322,19 +322,20 @@ def gemm_batched(a: DeviceArray, b: DeviceArray, c: DeviceArray, *, alpha=1.0,
     d.bias = _ptr_or_none(bias)
     d.alpha = alpha
     d.beta = beta
+    d.tile = tile
     sgemm(c.stream, d)
 
 
 def gemm(a: DeviceArray, b: DeviceArray, *, alpha=1.0, c0: DeviceArray | None = None, beta=0.0,
          trans_a=False, trans_b=False, bias: DeviceArray | None = None, act=ACT_NONE,
-         out: DeviceArray | None = None) -> DeviceArray:
+         out: DeviceArray | None = None, tile=0) -> DeviceArray:
     """mensurflow::gemm's semantics (plus the fused bias/activation): a new [m, n] result."""
     left = a.T if trans_a else a
     right = b.T if trans_b else b
     m, n = left.shape[-2], right.shape[-1]
     if out is None:
         out = DeviceArray.empty((m, n), a.stream)
-    gemm_batched(left, right, out, alpha=alpha, c0=c0, beta=beta, bias=bias, act=act)
+    gemm_batched(left, right, out, alpha=alpha, c0=c0, beta=beta, bias=bias, act=act, tile=tile)
     return out
 
 

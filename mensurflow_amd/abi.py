@@ -27,6 +27,14 @@ EW_ADD = 0
 EW_MUL = 1
 EW_SCAL = 2
 
+TILE_AUTO = 0
+TILE_256x256 = 1
+TILE_128x128 = 2
+TILE_128x64 = 3
+TILE_64x128 = 4
+TILE_64x64 = 5
+TILE_COUNT = 6
+
 MAX_BATCH_DIMS = 4
 MAX_COPY_DIMS = 8
 
@@ -50,6 +58,7 @@ class GemmDesc(ctypes.Structure):
         ("c0", _vp), ("c0_rs", _i64), ("c0_bs", _i64 * MAX_BATCH_DIMS),
         ("bias", _vp),
         ("alpha", _f32), ("beta", _f32),
+        ("tile", _i32), ("reserved", _i32),
     ]
 
 

@@ -64,6 +64,7 @@ struct mfr_stream {
     bool owned = true;
     void* workspace = nullptr;
     size_t workspace_bytes = 0;
+    int compute_units = 256; // of the stream's device, read at creation
 
     // Makes this stream's device current on the calling thread (each ABI call does, as the
     // reference's CudaStream::activate does per call).

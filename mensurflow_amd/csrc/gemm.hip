@@ -3,7 +3,7 @@
 //
 //   C[b] = act( fl( fl( fl(alpha * op(A[b]) op(B[b])) + fl(beta * C0[b]) ) + bias ) )
 //
-// Design (one workgroup = 256 threads = 4 wavefronts of 64):
+// Design (a workgroup of 4 or 8 wavefronts of 64 lanes; five tile shapes, chosen per call):
 //   - The workgroup computes a BM x BN tile of C; its wavefronts form a WAVES_M x WAVES_N grid,
 //     each owning a (BM/WAVES_M) x (BN/WAVES_N) sub-tile held in 32x32 accumulator blocks of
 //     v_mfma_f32_32x32x2_f32 (16 fp32 accumulators per lane per block).
@@ -23,303 +23,99 @@
 //     logical tiles are remapped onto the same XCD (sharing its L2), and the logical order walks
 //     GROUP_M tile-rows at a time so concurrently running tiles share A and B panels.
 //   - Edges (M, N, K not multiples of the tile) are zero-filled on load and masked on store.
-#include "common.hpp"
-
-#include <type_traits>
+#include "gemm_kernel.hpp"
 
 namespace {
 
-typedef float floatx16 __attribute__((ext_vector_type(16)));
+using namespace mfr::gemm;
 
-struct GemmParams {
-    const float* a;
-    const float* b;
-    float* c;
-    const float* c0;
-    const float* bias;
-    int64_t m, n, k;
-    int64_t a_rs, a_cs, b_rs, b_cs, c_rs, c0_rs;
-    int64_t batch[MFR_MAX_BATCH_DIMS];
-    int64_t a_bs[MFR_MAX_BATCH_DIMS], b_bs[MFR_MAX_BATCH_DIMS];
-    int64_t c_bs[MFR_MAX_BATCH_DIMS], c0_bs[MFR_MAX_BATCH_DIMS];
-    int32_t batch_dims;
-    int32_t act;
-    int64_t batch_count;
-    int32_t tiles_m, tiles_n;
-    int32_t group_m;
-    float alpha, beta;
+// ---- tile configurations ----------------------------------------------------------------------
+//
+// Five workgroup tiles (include/mfr_rocm.h, MFR_TILE_*). `tflops` is each tile's measured rate on
+// the 4096^3 NT problem (one MI355X) and `occupancy` its resident workgroups per CU (LDS and
+// registers); the automatic choice uses both.
+struct TileInfo {
+    int bm, bn, occupancy, waves;
+    double tflops;
 };
-
-constexpr int kThreads = 256;
-
-// Global -> register -> LDS copy of one operand slice: ROWS rows (M for A, N for B) by KT depth.
-// KMAJ: unit stride along the depth (element (r, p) at base + r*row_stride + p).
-// otherwise: unit stride along the rows (element (r, p) at base + p*k_stride + r).
-// V: 4 = 16-byte loads along the unit-stride dimension (its extent and the other stride are
-// multiples of 4, the base 16-byte aligned), 1 = 4-byte loads.
-template <int ROWS, int KT, bool KMAJ, int V> struct SliceLoader {
-    static constexpr int kUnits = ROWS * KT / V;        // loads per slice
-    static constexpr int kPerThread = kUnits / kThreads;
-    static_assert(kUnits % kThreads == 0, "slice must split evenly over the workgroup");
-    // LDS row pitch: [ROWS][KT+4] (K-major) or [KT][ROWS+8].
-    static constexpr int kPitch = KMAJ ? KT + 4 : ROWS + 8;
-    static constexpr int kFloats = KMAJ ? ROWS * (KT + 4) : KT * (ROWS + 8);
-
-    using Vec = typename std::conditional<V == 4, float4, float>::type;
-    Vec reg[kPerThread];
-
-    // (row, depth) of this thread's i-th load, in elements.
-    __device__ static void coords(int i, int& r, int& p) {
-        const int u = static_cast<int>(threadIdx.x) + i * kThreads;
-        if constexpr (KMAJ) {
-            constexpr int per_row = KT / V;
-            r = u / per_row;
-            p = (u % per_row) * V;
-        } else {
-            constexpr int per_depth = ROWS / V;
-            p = u / per_depth;
-            r = (u % per_depth) * V;
-        }
-    }
-
-    // base points at element (row 0, depth k0) of the slice. rows_left / k_left: how many rows
-    // and depths of the slice are inside the matrix (>= ROWS / KT for an interior slice).
-    __device__ void load(const float* base, int64_t row_stride, int64_t k_stride, int rows_left,
-                         int k_left) {
-        const bool full = rows_left >= ROWS && k_left >= KT;
-#pragma unroll
-        for (int i = 0; i < kPerThread; ++i) {
-            int r, p;
-            coords(i, r, p);
-            const float* src = KMAJ ? base + r * row_stride + p : base + p * k_stride + r;
-            if (full || (r < rows_left && p < k_left)) {
-                if constexpr (V == 4) {
-                    reg[i] = *reinterpret_cast<const float4*>(src);
-                } else {
-                    reg[i] = *src;
-                }
-            } else {
-                if constexpr (V == 4) {
-                    reg[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-                } else {
-                    reg[i] = 0.f;
-                }
-            }
-        }
-    }
-
-    __device__ void store(float* lds) const {
-#pragma unroll
-        for (int i = 0; i < kPerThread; ++i) {
-            int r, p;
-            coords(i, r, p);
-            float* dst = KMAJ ? lds + r * kPitch + p : lds + p * kPitch + r;
-            if constexpr (V == 4) {
-                *reinterpret_cast<float4*>(dst) = reg[i];
-            } else {
-                *dst = reg[i];
-            }
-        }
-    }
-
-    // The four MFMA-step values of fragment row `row` (0..ROWS-1) for depth group g (8 depths):
-    // lanes 0-31 (half 0) take depths 8g+0..3, lanes 32-63 (half 1) depths 8g+4..7.
-    __device__ static void fragment(const float* lds, int row, int g, int half, float out[4]) {
-        if constexpr (KMAJ) {
-            const float4 v = *reinterpret_cast<const float4*>(lds + row * kPitch + 8 * g + 4 * half);
-            out[0] = v.x;
-            out[1] = v.y;
-            out[2] = v.z;
-            out[3] = v.w;
-        } else {
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                out[s] = lds[(8 * g + 4 * half + s) * kPitch + row];
-            }
-        }
-    }
+constexpr TileInfo kTiles[MFR_TILE_COUNT] = {
+    {0, 0, 0, 0, 0.0},         // AUTO
+    {256, 256, 1, 8, 127.8},   // 8 wavefronts of 128x64, depth slice 32
+    {128, 128, 2, 4, 122.0},   // 4 wavefronts of 64x64, depth slice 32
+    {128, 64, 5, 4, 110.9},    // 4 wavefronts of 64x32, depth slice 16
+    {64, 128, 5, 4, 114.7},    // 4 wavefronts of 32x64, depth slice 16
+    {64, 64, 4, 4, 112.9},     // 4 wavefronts of 32x32, depth slice 32
 };
+constexpr int kGroupM = 8;
 
-template <int BM, int BN, int KT, int WAVES_M, int WAVES_N, bool AK, bool BK, int VA, int VB>
-__global__ __launch_bounds__(kThreads) void sgemm_kernel(GemmParams p) {
-    static_assert(WAVES_M * WAVES_N * 64 == kThreads, "4 wavefronts per workgroup");
-    constexpr int WM = BM / WAVES_M;
-    constexpr int WN = BN / WAVES_N;
-    constexpr int FM = WM / 32; // 32x32 accumulator blocks per wavefront, along M
-    constexpr int FN = WN / 32;
-    static_assert(KT % 8 == 0 && WM % 32 == 0 && WN % 32 == 0, "tile shape");
-    using LoadA = SliceLoader<BM, KT, AK, VA>;
-    using LoadB = SliceLoader<BN, KT, BK, VB>;
-    __shared__ float smem[2 * (LoadA::kFloats + LoadB::kFloats)];
-    // Buffer `which` (0 or 1) of each operand's double-buffered slice.
-    auto lds_a = [&](int which) { return smem + which * LoadA::kFloats; };
-    auto lds_b = [&](int which) { return smem + 2 * LoadA::kFloats + which * LoadB::kFloats; };
-
-    // ---- which tile: XCD-aware remap, then grouped row-major order within the batch ----
-    const int64_t tiles_per_batch = static_cast<int64_t>(p.tiles_m) * p.tiles_n;
-    const int64_t total = tiles_per_batch * p.batch_count;
-    const int64_t hw = blockIdx.x;
-    const int64_t per_xcd = total / 8;
-    const int64_t logical = hw < per_xcd * 8 ? (hw % 8) * per_xcd + hw / 8 : hw;
-    int64_t batch_index = logical / tiles_per_batch;
-    const int64_t t = logical % tiles_per_batch;
-    const int64_t group_tiles = static_cast<int64_t>(p.group_m) * p.tiles_n;
-    const int64_t group = t / group_tiles;
-    const int64_t first_m = group * p.group_m;
-    const int64_t rows_in_group =
-        p.tiles_m - first_m < p.group_m ? p.tiles_m - first_m : p.group_m;
-    const int64_t in_group = t % group_tiles;
-    const int64_t tile_m = first_m + in_group % rows_in_group;
-    const int64_t tile_n = in_group / rows_in_group;
-
-    int64_t off_a = 0, off_b = 0, off_c = 0, off_c0 = 0;
-    for (int d = p.batch_dims - 1; d >= 0; --d) {
-        const int64_t idx = batch_index % p.batch[d];
-        batch_index /= p.batch[d];
-        off_a += idx * p.a_bs[d];
-        off_b += idx * p.b_bs[d];
-        off_c += idx * p.c_bs[d];
-        off_c0 += idx * p.c0_bs[d];
-    }
-    const int64_t m0 = tile_m * BM;
-    const int64_t n0 = tile_n * BN;
-    const int rows_a = p.m - m0 < BM ? static_cast<int>(p.m - m0) : BM;
-    const int rows_b = p.n - n0 < BN ? static_cast<int>(p.n - n0) : BN;
-
-    const float* a_base = p.a + off_a + m0 * p.a_rs;
-    const float* b_base = p.b + off_b + n0 * p.b_cs;
-    // Per slice the bases advance by KT depths.
-    const int64_t a_step = KT * p.a_cs;
-    const int64_t b_step = KT * p.b_rs;
-
-    const int lane = threadIdx.x % 64;
-    const int wave = threadIdx.x / 64;
-    const int wave_m = wave / WAVES_N;
-    const int wave_n = wave % WAVES_N;
-    const int half = lane / 32;
-    const int r32 = lane % 32;
-
-    floatx16 acc[FM][FN];
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                acc[i][j][e] = 0.0f;
-            }
-        }
-    }
-
-    const int64_t slices = (p.k + KT - 1) / KT;
-    LoadA la;
-    LoadB lb;
-    if (slices > 0) {
-        const int k_left = p.k < KT ? static_cast<int>(p.k) : KT;
-        la.load(a_base, p.a_rs, p.a_cs, rows_a, k_left);
-        lb.load(b_base, p.b_cs, p.b_rs, rows_b, k_left);
-        la.store(lds_a(0));
-        lb.store(lds_b(0));
-        __syncthreads();
-    }
-    for (int64_t s = 0; s < slices; ++s) {
-        const int cur = static_cast<int>(s & 1);
-        const bool more = s + 1 < slices;
-        if (more) {
-            const int64_t k_next = (s + 1) * KT;
-            const int k_left = p.k - k_next < KT ? static_cast<int>(p.k - k_next) : KT;
-            la.load(a_base + (s + 1) * a_step, p.a_rs, p.a_cs, rows_a, k_left);
-            lb.load(b_base + (s + 1) * b_step, p.b_cs, p.b_rs, rows_b, k_left);
-        }
-        const float* sa = lds_a(cur);
-        const float* sb = lds_b(cur);
-#pragma unroll
-        for (int g = 0; g < KT / 8; ++g) {
-            float fa[FM][4];
-            float fb[FN][4];
-#pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                LoadA::fragment(sa, wave_m * WM + i * 32 + r32, g, half, fa[i]);
-            }
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                LoadB::fragment(sb, wave_n * WN + j * 32 + r32, g, half, fb[j]);
-            }
-#pragma unroll
-            for (int st = 0; st < 4; ++st) {
-#pragma unroll
-                for (int i = 0; i < FM; ++i) {
-#pragma unroll
-                    for (int j = 0; j < FN; ++j) {
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][st], fb[j][st],
-                                                                          acc[i][j], 0, 0, 0);
-                    }
-                }
-            }
-        }
-        if (more) {
-            la.store(lds_a(cur ^ 1));
-            lb.store(lds_b(cur ^ 1));
-        }
-        __syncthreads();
-    }
-
-    // ---- epilogue: accumulator e of block (i, j) is C(row, col) with
-    //      row = 32i + 8(e/4) + 4*half + e%4, col = 32j + lane%32 (v_mfma_f32_32x32x2_f32 layout)
-    float* c_base = p.c + off_c;
-    const float* c0_base = p.c0 != nullptr ? p.c0 + off_c0 : nullptr;
-    const bool use_c0 = c0_base != nullptr && p.beta != 0.0f;
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int64_t col = n0 + wave_n * WN + j * 32 + r32;
-            if (col >= p.n) {
-                continue;
-            }
-            const float bias = p.bias != nullptr ? p.bias[col] : 0.0f;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int64_t row = m0 + wave_m * WM + i * 32 + 8 * (e / 4) + 4 * half + e % 4;
-                if (row >= p.m) {
-                    continue;
-                }
-                float v = acc[i][j][e];
-                if (p.alpha != 1.0f) {
-                    v = p.alpha * v;
-                }
-                if (use_c0) {
-                    const float scaled = p.beta * c0_base[row * p.c0_rs + col];
-                    v = v + scaled;
-                }
-                if (p.bias != nullptr) {
-                    v = v + bias;
-                }
-                c_base[row * p.c_rs + col] = mfr::dev::activate(v, p.act);
-            }
-        }
-    }
+int64_t tile_count(int tile, int64_t m, int64_t n, int64_t batch) {
+    return ((m + kTiles[tile].bm - 1) / kTiles[tile].bm) *
+           ((n + kTiles[tile].bn - 1) / kTiles[tile].bn) * batch;
 }
 
-// Tile configuration of the one kernel family built so far.
-constexpr int kBM = 128, kBN = 128, kKT = 32, kWavesM = 2, kWavesN = 2, kGroupM = 8;
+// The automatic tile. A short depth (K <= 128) is latency-bound per tile, so it takes the
+// high-occupancy 128x64 / 64x128 tiles (the one padding the output less). Otherwise the cost of a
+// tile is the work of the busiest CU, ceil(tiles / CUs) * tile area, at the tile's measured rate,
+// 15% slower when that CU runs fewer than 2 wavefronts per SIMD (nothing hides the latencies of
+// a lone wavefront). The 256x256 tile needs 16-byte loads on both operands.
+int choose_tile(int64_t m, int64_t n, int64_t k, int64_t batch, int cus, bool wide_loads) {
+    if (k <= 128) {
+        const int64_t a = tile_count(MFR_TILE_128x64, m, n, batch) * 128 * 64;
+        const int64_t b = tile_count(MFR_TILE_64x128, m, n, batch) * 64 * 128;
+        return b < a ? MFR_TILE_64x128 : MFR_TILE_128x64;
+    }
+    int best = MFR_TILE_128x128;
+    double best_cost = 1e300;
+    for (int t = 1; t < MFR_TILE_COUNT; ++t) {
+        if (t == MFR_TILE_256x256 && !wide_loads) {
+            continue;
+        }
+        const int64_t per_cu = (tile_count(t, m, n, batch) + cus - 1) / cus;
+        const int64_t concurrent = per_cu < kTiles[t].occupancy ? per_cu : kTiles[t].occupancy;
+        const int64_t waves_per_simd = concurrent * kTiles[t].waves / 4;
+        const double cost = static_cast<double>(per_cu) * kTiles[t].bm * kTiles[t].bn /
+                            kTiles[t].tflops / (waves_per_simd >= 2 ? 1.0 : 0.85);
+        if (cost < best_cost) {
+            best_cost = cost;
+            best = t;
+        }
+    }
+    return best;
+}
 
-template <bool AK, bool BK, int VA, int VB>
-void launch_tile(const GemmParams& p, unsigned blocks, hipStream_t stream) {
-    sgemm_kernel<kBM, kBN, kKT, kWavesM, kWavesN, AK, BK, VA, VB>
-        <<<blocks, kThreads, 0, stream>>>(p);
+template <int BM, int BN, int KT, int WAVES_M, int WAVES_N, bool AK, bool BK>
+void launch_vec(const GemmParams& p, int va, int vb, unsigned blocks, hipStream_t stream) {
+    constexpr int threads = WAVES_M * WAVES_N * 64;
+    if (va == 4 && vb == 4) {
+        sgemm_kernel<BM, BN, KT, WAVES_M, WAVES_N, AK, BK, 4, 4><<<blocks, threads, 0, stream>>>(p);
+    } else if (va == 4) {
+        sgemm_kernel<BM, BN, KT, WAVES_M, WAVES_N, AK, BK, 4, 1><<<blocks, threads, 0, stream>>>(p);
+    } else if (vb == 4) {
+        sgemm_kernel<BM, BN, KT, WAVES_M, WAVES_N, AK, BK, 1, 4><<<blocks, threads, 0, stream>>>(p);
+    } else {
+        sgemm_kernel<BM, BN, KT, WAVES_M, WAVES_N, AK, BK, 1, 1><<<blocks, threads, 0, stream>>>(p);
+    }
 }
 
 template <bool AK, bool BK>
-void launch_vec(const GemmParams& p, int va, int vb, unsigned blocks, hipStream_t stream) {
-    if (va == 4 && vb == 4) {
-        launch_tile<AK, BK, 4, 4>(p, blocks, stream);
-    } else if (va == 4) {
-        launch_tile<AK, BK, 4, 1>(p, blocks, stream);
-    } else if (vb == 4) {
-        launch_tile<AK, BK, 1, 4>(p, blocks, stream);
-    } else {
-        launch_tile<AK, BK, 1, 1>(p, blocks, stream);
+void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned blocks,
+                   hipStream_t stream) {
+    switch (tile) {
+    case MFR_TILE_256x256: // 16-byte loads only (checked by the caller)
+        sgemm_kernel<256, 256, 32, 2, 4, AK, BK, 4, 4><<<blocks, 512, 0, stream>>>(p);
+        break;
+    case MFR_TILE_128x64:
+        launch_vec<128, 64, 16, 2, 2, AK, BK>(p, va, vb, blocks, stream);
+        break;
+    case MFR_TILE_64x128:
+        launch_vec<64, 128, 16, 2, 2, AK, BK>(p, va, vb, blocks, stream);
+        break;
+    case MFR_TILE_64x64:
+        launch_vec<64, 64, 32, 2, 2, AK, BK>(p, va, vb, blocks, stream);
+        break;
+    default:
+        launch_vec<128, 128, 32, 2, 2, AK, BK>(p, va, vb, blocks, stream);
+        break;
     }
 }
 
@@ -418,8 +214,17 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
     if (p.beta != 0.0f && p.c0 != nullptr) {
         require(p.m == 1 || p.c0_rs >= p.n, "sgemm: c0 row stride smaller than n");
     }
-    const int64_t tiles_m = (p.m + kBM - 1) / kBM;
-    const int64_t tiles_n = (p.n + kBN - 1) / kBN;
+    require(d.tile >= MFR_TILE_AUTO && d.tile < MFR_TILE_COUNT, "sgemm: unknown tile");
+    const bool wide = va == 4 && vb == 4;
+    int tile = d.tile;
+    if (tile == MFR_TILE_AUTO) {
+        tile = choose_tile(p.m, p.n, p.k, batch_count, s.compute_units, wide);
+    } else if (tile == MFR_TILE_256x256 && !wide) {
+        throw mfr::Error(MFR_E_UNSUPPORTED,
+                         "sgemm: the 256x256 tile needs 16-byte aligned operands");
+    }
+    const int64_t tiles_m = (p.m + kTiles[tile].bm - 1) / kTiles[tile].bm;
+    const int64_t tiles_n = (p.n + kTiles[tile].bn - 1) / kTiles[tile].bn;
     const int64_t blocks = tiles_m * tiles_n * batch_count;
     require(tiles_m < (int64_t{1} << 30) && tiles_n < (int64_t{1} << 30) &&
                 blocks < (int64_t{1} << 31),
@@ -429,13 +234,13 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
     p.group_m = kGroupM;
     const unsigned grid = static_cast<unsigned>(blocks);
     if (ak && bk) {
-        launch_vec<true, true>(p, va, vb, grid, s.stream);
+        launch_layout<true, true>(tile, p, va, vb, grid, s.stream);
     } else if (ak) {
-        launch_vec<true, false>(p, va, vb, grid, s.stream);
+        launch_layout<true, false>(tile, p, va, vb, grid, s.stream);
     } else if (bk) {
-        launch_vec<false, true>(p, va, vb, grid, s.stream);
+        launch_layout<false, true>(tile, p, va, vb, grid, s.stream);
     } else {
-        launch_vec<false, false>(p, va, vb, grid, s.stream);
+        launch_layout<false, false>(tile, p, va, vb, grid, s.stream);
     }
     mfr::check_launch("sgemm_kernel");
 }

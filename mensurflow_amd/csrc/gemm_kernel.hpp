@@ -1,0 +1,281 @@
+// Device code of the fp32 MFMA GEMM: the tile kernel and its operand loader. Included by
+// gemm.hip (the C ABI entry points and tile selection). See gemm.hip for the design.
+#pragma once
+
+#include "common.hpp"
+
+#include <type_traits>
+
+namespace mfr::gemm {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+struct GemmParams {
+    const float* a;
+    const float* b;
+    float* c;
+    const float* c0;
+    const float* bias;
+    int64_t m, n, k;
+    int64_t a_rs, a_cs, b_rs, b_cs, c_rs, c0_rs;
+    int64_t batch[MFR_MAX_BATCH_DIMS];
+    int64_t a_bs[MFR_MAX_BATCH_DIMS], b_bs[MFR_MAX_BATCH_DIMS];
+    int64_t c_bs[MFR_MAX_BATCH_DIMS], c0_bs[MFR_MAX_BATCH_DIMS];
+    int32_t batch_dims;
+    int32_t act;
+    int64_t batch_count;
+    int32_t tiles_m, tiles_n;
+    int32_t group_m;
+    float alpha, beta;
+};
+
+// Global -> register -> LDS copy of one operand slice: ROWS rows (M for A, N for B) by KT depth.
+// KMAJ: unit stride along the depth (element (r, p) at base + r*row_stride + p).
+// otherwise: unit stride along the rows (element (r, p) at base + p*k_stride + r).
+// V: 4 = 16-byte loads along the unit-stride dimension (its extent and the other stride are
+// multiples of 4, the base 16-byte aligned), 1 = 4-byte loads.
+template <int ROWS, int KT, bool KMAJ, int V, int THREADS> struct SliceLoader {
+    static constexpr int kUnits = ROWS * KT / V;        // loads per slice
+    static constexpr int kPerThread = kUnits / THREADS;
+    static_assert(kUnits % THREADS == 0, "slice must split evenly over the workgroup");
+    // LDS row pitch: [ROWS][KT+4] (K-major) or [KT][ROWS+8].
+    static constexpr int kPitch = KMAJ ? KT + 4 : ROWS + 8;
+    static constexpr int kFloats = KMAJ ? ROWS * (KT + 4) : KT * (ROWS + 8);
+
+    using Vec = typename std::conditional<V == 4, float4, float>::type;
+    Vec reg[kPerThread];
+
+    // (row, depth) of this thread's i-th load, in elements.
+    __device__ static void coords(int i, int& r, int& p) {
+        const int u = static_cast<int>(threadIdx.x) + i * THREADS;
+        if constexpr (KMAJ) {
+            constexpr int per_row = KT / V;
+            r = u / per_row;
+            p = (u % per_row) * V;
+        } else {
+            constexpr int per_depth = ROWS / V;
+            p = u / per_depth;
+            r = (u % per_depth) * V;
+        }
+    }
+
+    // base points at element (row 0, depth k0) of the slice. rows_left / k_left: how many rows
+    // and depths of the slice are inside the matrix (>= ROWS / KT for an interior slice).
+    __device__ void load(const float* base, int64_t row_stride, int64_t k_stride, int rows_left,
+                         int k_left) {
+        const bool full = rows_left >= ROWS && k_left >= KT;
+#pragma unroll
+        for (int i = 0; i < kPerThread; ++i) {
+            int r, p;
+            coords(i, r, p);
+            const float* src = KMAJ ? base + r * row_stride + p : base + p * k_stride + r;
+            if (full || (r < rows_left && p < k_left)) {
+                if constexpr (V == 4) {
+                    reg[i] = *reinterpret_cast<const float4*>(src);
+                } else {
+                    reg[i] = *src;
+                }
+            } else {
+                if constexpr (V == 4) {
+                    reg[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                } else {
+                    reg[i] = 0.f;
+                }
+            }
+        }
+    }
+
+    __device__ void store(float* lds) const {
+#pragma unroll
+        for (int i = 0; i < kPerThread; ++i) {
+            int r, p;
+            coords(i, r, p);
+            float* dst = KMAJ ? lds + r * kPitch + p : lds + p * kPitch + r;
+            if constexpr (V == 4) {
+                *reinterpret_cast<float4*>(dst) = reg[i];
+            } else {
+                *dst = reg[i];
+            }
+        }
+    }
+
+    // The four MFMA-step values of fragment row `row` (0..ROWS-1) for depth group g (8 depths):
+    // lanes 0-31 (half 0) take depths 8g+0..3, lanes 32-63 (half 1) depths 8g+4..7.
+    __device__ static void fragment(const float* lds, int row, int g, int half, float out[4]) {
+        if constexpr (KMAJ) {
+            const float4 v = *reinterpret_cast<const float4*>(lds + row * kPitch + 8 * g + 4 * half);
+            out[0] = v.x;
+            out[1] = v.y;
+            out[2] = v.z;
+            out[3] = v.w;
+        } else {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                out[s] = lds[(8 * g + 4 * half + s) * kPitch + row];
+            }
+        }
+    }
+};
+
+template <int BM, int BN, int KT, int WAVES_M, int WAVES_N, bool AK, bool BK, int VA, int VB>
+__global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_kernel(GemmParams p) {
+    constexpr int THREADS = WAVES_M * WAVES_N * 64;
+    constexpr int WM = BM / WAVES_M;
+    constexpr int WN = BN / WAVES_N;
+    constexpr int FM = WM / 32; // 32x32 accumulator blocks per wavefront, along M
+    constexpr int FN = WN / 32;
+    static_assert(KT % 8 == 0 && WM % 32 == 0 && WN % 32 == 0, "tile shape");
+    using LoadA = SliceLoader<BM, KT, AK, VA, THREADS>;
+    using LoadB = SliceLoader<BN, KT, BK, VB, THREADS>;
+    __shared__ float smem[2 * (LoadA::kFloats + LoadB::kFloats)];
+    // Buffer `which` (0 or 1) of each operand's double-buffered slice.
+    auto lds_a = [&](int which) { return smem + which * LoadA::kFloats; };
+    auto lds_b = [&](int which) { return smem + 2 * LoadA::kFloats + which * LoadB::kFloats; };
+
+    // ---- which tile: XCD-aware remap, then grouped row-major order within the batch ----
+    const int64_t tiles_per_batch = static_cast<int64_t>(p.tiles_m) * p.tiles_n;
+    const int64_t total = tiles_per_batch * p.batch_count;
+    const int64_t hw = blockIdx.x;
+    const int64_t per_xcd = total / 8;
+    const int64_t logical = hw < per_xcd * 8 ? (hw % 8) * per_xcd + hw / 8 : hw;
+    int64_t batch_index = logical / tiles_per_batch;
+    const int64_t t = logical % tiles_per_batch;
+    const int64_t group_tiles = static_cast<int64_t>(p.group_m) * p.tiles_n;
+    const int64_t group = t / group_tiles;
+    const int64_t first_m = group * p.group_m;
+    const int64_t rows_in_group =
+        p.tiles_m - first_m < p.group_m ? p.tiles_m - first_m : p.group_m;
+    const int64_t in_group = t % group_tiles;
+    const int64_t tile_m = first_m + in_group % rows_in_group;
+    const int64_t tile_n = in_group / rows_in_group;
+
+    int64_t off_a = 0, off_b = 0, off_c = 0, off_c0 = 0;
+    for (int d = p.batch_dims - 1; d >= 0; --d) {
+        const int64_t idx = batch_index % p.batch[d];
+        batch_index /= p.batch[d];
+        off_a += idx * p.a_bs[d];
+        off_b += idx * p.b_bs[d];
+        off_c += idx * p.c_bs[d];
+        off_c0 += idx * p.c0_bs[d];
+    }
+    const int64_t m0 = tile_m * BM;
+    const int64_t n0 = tile_n * BN;
+    const int rows_a = p.m - m0 < BM ? static_cast<int>(p.m - m0) : BM;
+    const int rows_b = p.n - n0 < BN ? static_cast<int>(p.n - n0) : BN;
+
+    const float* a_base = p.a + off_a + m0 * p.a_rs;
+    const float* b_base = p.b + off_b + n0 * p.b_cs;
+    // Per slice the bases advance by KT depths.
+    const int64_t a_step = KT * p.a_cs;
+    const int64_t b_step = KT * p.b_rs;
+
+    const int lane = threadIdx.x % 64;
+    const int wave = threadIdx.x / 64;
+    const int wave_m = wave / WAVES_N;
+    const int wave_n = wave % WAVES_N;
+    const int half = lane / 32;
+    const int r32 = lane % 32;
+
+    floatx16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                acc[i][j][e] = 0.0f;
+            }
+        }
+    }
+
+    const int64_t slices = (p.k + KT - 1) / KT;
+    LoadA la;
+    LoadB lb;
+    if (slices > 0) {
+        const int k_left = p.k < KT ? static_cast<int>(p.k) : KT;
+        la.load(a_base, p.a_rs, p.a_cs, rows_a, k_left);
+        lb.load(b_base, p.b_cs, p.b_rs, rows_b, k_left);
+        la.store(lds_a(0));
+        lb.store(lds_b(0));
+        __syncthreads();
+    }
+    for (int64_t s = 0; s < slices; ++s) {
+        const int cur = static_cast<int>(s & 1);
+        const bool more = s + 1 < slices;
+        if (more) {
+            const int64_t k_next = (s + 1) * KT;
+            const int k_left = p.k - k_next < KT ? static_cast<int>(p.k - k_next) : KT;
+            la.load(a_base + (s + 1) * a_step, p.a_rs, p.a_cs, rows_a, k_left);
+            lb.load(b_base + (s + 1) * b_step, p.b_cs, p.b_rs, rows_b, k_left);
+        }
+        const float* sa = lds_a(cur);
+        const float* sb = lds_b(cur);
+#pragma unroll
+        for (int g = 0; g < KT / 8; ++g) {
+            float fa[FM][4];
+            float fb[FN][4];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+                LoadA::fragment(sa, wave_m * WM + i * 32 + r32, g, half, fa[i]);
+            }
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                LoadB::fragment(sb, wave_n * WN + j * 32 + r32, g, half, fb[j]);
+            }
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) {
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][st], fb[j][st],
+                                                                          acc[i][j], 0, 0, 0);
+                    }
+                }
+            }
+        }
+        if (more) {
+            la.store(lds_a(cur ^ 1));
+            lb.store(lds_b(cur ^ 1));
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue: accumulator e of block (i, j) is C(row, col) with
+    //      row = 32i + 8(e/4) + 4*half + e%4, col = 32j + lane%32 (v_mfma_f32_32x32x2_f32 layout)
+    float* c_base = p.c + off_c;
+    const float* c0_base = p.c0 != nullptr ? p.c0 + off_c0 : nullptr;
+    const bool use_c0 = c0_base != nullptr && p.beta != 0.0f;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int64_t col = n0 + wave_n * WN + j * 32 + r32;
+            if (col >= p.n) {
+                continue;
+            }
+            const float bias = p.bias != nullptr ? p.bias[col] : 0.0f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int64_t row = m0 + wave_m * WM + i * 32 + 8 * (e / 4) + 4 * half + e % 4;
+                if (row >= p.m) {
+                    continue;
+                }
+                float v = acc[i][j][e];
+                if (p.alpha != 1.0f) {
+                    v = p.alpha * v;
+                }
+                if (use_c0) {
+                    const float scaled = p.beta * c0_base[row * p.c0_rs + col];
+                    v = v + scaled;
+                }
+                if (p.bias != nullptr) {
+                    v = v + bias;
+                }
+                c_base[row * p.c_rs + col] = mfr::dev::activate(v, p.act);
+            }
+        }
+    }
+}
+
+} // namespace mfr::gemm

@@ -220,6 +220,9 @@ int mfr_stream_create(int device, mfr_stream_t* stream) {
             // Default priority on purpose: streams of different priorities are not mixed.
             check(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking),
                   "hipStreamCreateWithFlags");
+            check(hipDeviceGetAttribute(&s->compute_units, hipDeviceAttributeMultiprocessorCount,
+                                        s->device),
+                  "hipDeviceGetAttribute");
         } catch (...) {
             delete s;
             throw;
@@ -235,6 +238,9 @@ int mfr_stream_wrap(int device, void* hip_stream, mfr_stream_t* stream) {
         s->device = mfr::hip_id(device);
         s->stream = static_cast<hipStream_t>(hip_stream);
         s->owned = false;
+        check(hipDeviceGetAttribute(&s->compute_units, hipDeviceAttributeMultiprocessorCount,
+                                    s->device),
+              "hipDeviceGetAttribute");
         *stream = s;
     });
 }

@@ -114,6 +114,61 @@ def test_exact_alpha_beta_in_place(stream, trans_a, trans_b):
     assert same_bits(c.numpy(), want.astype(np.float32))
 
 
+TILES = list(range(1, mf.abi.TILE_COUNT))
+
+
+def wide_loads_possible(a_stored, b_stored):
+    """Whether both stored (row-major) operands qualify for 16-byte loads: the unit-stride extent
+    and the row stride are the row length, which must be a multiple of 4."""
+    return all(x.shape[1] % 4 == 0 for x in (a_stored, b_stored))
+
+
+@pytest.mark.parametrize("tile", TILES)
+@pytest.mark.parametrize("m,n,k", [(300, 260, 1000), (257, 129, 257), (1, 300, 64),
+                                   (513, 7, 96), (64, 64, 2000), (129, 65, 36)])
+def test_exact_every_tile(stream, tile, m, n, k):
+    """Every workgroup tile on edge shapes and all four layouts: bits equal the exact product."""
+    a = quarter_matrix(m, k, 71)
+    b = quarter_matrix(k, n, 72)
+    c0 = quarter_matrix(m, n, 73)
+    bias = quarter_matrix(1, n, 74)[0]
+    want = (np.float32(1.5) * exact_product(a, b)) + np.float32(0.5) * c0
+    want = (want + bias).astype(np.float32)
+    for trans_a in (False, True):
+        for trans_b in (False, True):
+            a_st = np.ascontiguousarray(a.T) if trans_a else a
+            b_st = np.ascontiguousarray(b.T) if trans_b else b
+            c, buf = guarded_output(stream, (m, n))
+            run = lambda: mf.gemm(dev(a_st, stream), dev(b_st, stream), alpha=1.5,  # noqa: E731
+                                  c0=dev(c0, stream), beta=0.5, trans_a=trans_a,
+                                  trans_b=trans_b, bias=dev(bias, stream), out=c, tile=tile)
+            if tile == mf.abi.TILE_256x256 and not wide_loads_possible(a_st, b_st):
+                # Degenerate extents (m or n of 1) may still qualify; otherwise it is refused.
+                try:
+                    run()
+                except NotImplementedError:
+                    continue
+            else:
+                run()
+            assert same_bits(c.numpy(), want), (tile, trans_a, trans_b)
+            check_guards(buf)
+
+
+@pytest.mark.parametrize("tile", TILES)
+def test_exact_batched_every_tile(stream, tile):
+    bsz, heads, m, n, k = 2, 3, 100, 68, 64
+    a = quarter_matrix(bsz * heads * m, k, 81).reshape(bsz, heads, m, k)
+    bt = quarter_matrix(heads * n, k, 82).reshape(1, heads, n, k)
+    out = mf.DeviceArray.empty((bsz, heads, m, n), stream)
+    b_d = dev(bt, stream).expand((bsz, heads, n, k)).transpose(-2, -1)
+    mf.gemm_batched(dev(a, stream), b_d, out, alpha=0.5, tile=tile)
+    got = out.numpy()
+    for i in range(bsz):
+        for h in range(heads):
+            want = (np.float32(0.5) * exact_product(a[i, h], bt[0, h].T)).astype(np.float32)
+            assert same_bits(got[i, h], want), (tile, i, h)
+
+
 def test_k_zero_gives_epilogue_of_zero_product(stream):
     m, n = 33, 17
     c0 = quarter_matrix(m, n, 41)
