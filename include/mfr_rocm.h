@@ -146,8 +146,16 @@ typedef struct mfr_gemm_desc {
     const float* bias;                        /* [n] or NULL; shared by every batch */
     float alpha, beta;
     int32_t tile;                             /* MFR_TILE_AUTO or a fixed MFR_TILE_* */
-    int32_t reserved;
+    int32_t stage;                            /* MFR_STAGE_* */
 } mfr_gemm_desc;
+
+/* Operand staging of mfr_sgemm. The fast loads read 4 floats at once, which needs an operand's
+ * unit-stride extent and its other strides to be multiples of 4 and its base 16-byte aligned
+ * (X[4093,1023] row-major is not). Such an operand can first be copied, zero-padded to that
+ * shape, into the stream's workspace (one extra pass over it). AUTO stages when the product is
+ * large (>= 2^30 flops) and the copy is small next to it (<= 1 byte per 64 flops); the result
+ * is the same either way. */
+enum { MFR_STAGE_AUTO = 0, MFR_STAGE_NEVER = 1, MFR_STAGE_ALWAYS = 2 };
 
 /* Workgroup tile of mfr_sgemm (rows x cols x depth slice). AUTO picks one from the shape: a cost
  * model of ceil(tiles / CUs) * tile area / measured efficiency, and the high-occupancy tiles for

@@ -281,12 +281,13 @@ def _fill_batch(field, values, dims):
 
 def gemm_batched(a: DeviceArray, b: DeviceArray, c: DeviceArray, *, alpha=1.0,
                  c0: DeviceArray | None = None, beta=0.0, bias: DeviceArray | None = None,
-                 act=ACT_NONE, tile=0) -> None:
+                 act=ACT_NONE, tile=0, stage=0) -> None:
     """c[...] = act(alpha*a@b + beta*c0 + bias) over the leading (batch) dimensions.
 
     a is [..., m, k], b is [..., k, n] (any strides with a unit stride in one matrix dimension;
     batch strides may be 0), c and c0 are [..., m, n] with unit column stride. The batch shapes
-    must already agree (expand them first).
+    must already agree (expand them first). tile is an abi.TILE_* value, stage an abi.STAGE_*
+    value (copy operands that 16-byte loads cannot read into an aligned workspace first).
     """
     m, k = a.shape[-2:]
     k2, n = b.shape[-2:]
@@ -323,19 +324,21 @@ def gemm_batched(a: DeviceArray, b: DeviceArray, c: DeviceArray, *, alpha=1.0,
     d.alpha = alpha
     d.beta = beta
     d.tile = tile
+    d.stage = stage
     sgemm(c.stream, d)
 
 
 def gemm(a: DeviceArray, b: DeviceArray, *, alpha=1.0, c0: DeviceArray | None = None, beta=0.0,
          trans_a=False, trans_b=False, bias: DeviceArray | None = None, act=ACT_NONE,
-         out: DeviceArray | None = None, tile=0) -> DeviceArray:
+         out: DeviceArray | None = None, tile=0, stage=0) -> DeviceArray:
     """mensurflow::gemm's semantics (plus the fused bias/activation): a new [m, n] result."""
     left = a.T if trans_a else a
     right = b.T if trans_b else b
     m, n = left.shape[-2], right.shape[-1]
     if out is None:
         out = DeviceArray.empty((m, n), a.stream)
-    gemm_batched(left, right, out, alpha=alpha, c0=c0, beta=beta, bias=bias, act=act, tile=tile)
+    gemm_batched(left, right, out, alpha=alpha, c0=c0, beta=beta, bias=bias, act=act, tile=tile,
+                 stage=stage)
     return out
 
 

@@ -34,6 +34,9 @@ TILE_128x64 = 3
 TILE_64x128 = 4
 TILE_64x64 = 5
 TILE_COUNT = 6
+STAGE_AUTO = 0
+STAGE_NEVER = 1
+STAGE_ALWAYS = 2
 
 MAX_BATCH_DIMS = 4
 MAX_COPY_DIMS = 8
@@ -58,7 +61,7 @@ class GemmDesc(ctypes.Structure):
         ("c0", _vp), ("c0_rs", _i64), ("c0_bs", _i64 * MAX_BATCH_DIMS),
         ("bias", _vp),
         ("alpha", _f32), ("beta", _f32),
-        ("tile", _i32), ("reserved", _i32),
+        ("tile", _i32), ("stage", _i32),
     ]
 
 

@@ -23,6 +23,11 @@
 //     logical tiles are remapped onto the same XCD (sharing its L2), and the logical order walks
 //     GROUP_M tile-rows at a time so concurrently running tiles share A and B panels.
 //   - Edges (M, N, K not multiples of the tile) are zero-filled on load and masked on store.
+//   - Operand staging: the 16-byte loads need an operand's lines (runs along its unit stride) to
+//     start 16-byte aligned and hold a multiple of 4 floats. An operand that is not laid out so
+//     (X[4093,1023] row-major) is copied first into the stream's workspace with its lines padded
+//     to a multiple of 4 by zeros (stage_kernel); vector loads that reach past the end of a line
+//     then read zeros of its own line, and the zeros add nothing to any sum.
 #include "gemm_kernel.hpp"
 
 namespace {
@@ -137,6 +142,109 @@ int vector_width(const float* base, int64_t extent, int64_t other_stride, int64_
     return 4;
 }
 
+// ---- operand staging --------------------------------------------------------------------------
+
+// Batch dimensions of an operand that are not broadcast (nonzero stride), outermost first.
+struct StageBatch {
+    int dims;
+    int64_t size[MFR_MAX_BATCH_DIMS];
+    int64_t stride[MFR_MAX_BATCH_DIMS];
+};
+
+// dst line r (r = matrix * lines + line, matrices in the order of StageBatch) gets the `inner`
+// unit-stride floats of source line `line` of that matrix, then zeros up to `pitch` (a multiple
+// of 4); dst is 16-byte aligned and matrix-contiguous. One workgroup per line.
+__global__ __launch_bounds__(256) void stage_kernel(const float* src, float* dst, int64_t lines,
+                                                    int64_t inner, int64_t line_stride,
+                                                    int64_t pitch, StageBatch sb) {
+    const int64_t r = blockIdx.x;
+    int64_t matrix = r / lines;
+    const int64_t line = r - matrix * lines;
+    int64_t offset = line * line_stride;
+    for (int d = sb.dims - 1; d >= 0; --d) {
+        const int64_t idx = matrix % sb.size[d];
+        matrix /= sb.size[d];
+        offset += idx * sb.stride[d];
+    }
+    const float* in = src + offset;
+    float4* out = reinterpret_cast<float4*>(dst + r * pitch);
+    for (int64_t u = threadIdx.x; u < pitch / 4; u += blockDim.x) {
+        const int64_t c = 4 * u;
+        float4 v;
+        v.x = c < inner ? in[c] : 0.0f;
+        v.y = c + 1 < inner ? in[c + 1] : 0.0f;
+        v.z = c + 2 < inner ? in[c + 2] : 0.0f;
+        v.w = c + 3 < inner ? in[c + 3] : 0.0f;
+        out[u] = v;
+    }
+}
+
+// One operand as the loader reads it: `lines` lines of `inner` unit-stride floats, `line_stride`
+// apart (the stride of its other matrix dimension), plus its batch strides. For A that is
+// (m lines of k) when K-major, else (k lines of m); for B (n lines of k) or (k lines of n).
+struct Operand {
+    const float* base;
+    int64_t lines, inner;
+    int64_t* line_stride; // the GemmParams field holding it, rewritten when staged
+    int64_t* unit_stride; // the GemmParams field holding the unit stride
+    int64_t* batch_stride;
+};
+
+int64_t round4(int64_t v) { return (v + 3) / 4 * 4; }
+
+// Floats of the staged copy of `o` under batch shape p.batch (broadcast dimensions once).
+int64_t staged_floats(const Operand& o, const GemmParams& p) {
+    int64_t count = o.lines * round4(o.inner);
+    for (int d = 0; d < p.batch_dims; ++d) {
+        if (o.batch_stride[d] != 0) {
+            count *= p.batch[d];
+        }
+    }
+    return count;
+}
+
+// Copies `o` into dst (staged_floats(o, p) floats, 16-byte aligned) and points the GEMM at it.
+void stage_operand(Operand& o, float* dst, const GemmParams& p, hipStream_t stream) {
+    const int64_t pitch = round4(o.inner);
+    StageBatch sb{};
+    int64_t matrices = 1;
+    for (int d = 0; d < p.batch_dims; ++d) {
+        if (o.batch_stride[d] != 0) {
+            sb.size[sb.dims] = p.batch[d];
+            sb.stride[sb.dims] = o.batch_stride[d];
+            ++sb.dims;
+            matrices *= p.batch[d];
+        }
+    }
+    const int64_t rows = matrices * o.lines;
+    mfr::require(rows < (int64_t{1} << 31), "sgemm: operand too large to stage");
+    stage_kernel<<<static_cast<unsigned>(rows), 256, 0, stream>>>(o.base, dst, o.lines, o.inner,
+                                                                  *o.line_stride, pitch, sb);
+    mfr::check_launch("stage_kernel");
+    // New strides: lines `pitch` apart, matrices contiguous in the order of StageBatch.
+    int64_t next = o.lines * pitch;
+    for (int d = p.batch_dims - 1; d >= 0; --d) {
+        if (o.batch_stride[d] != 0) {
+            o.batch_stride[d] = next;
+            next *= p.batch[d];
+        }
+    }
+    *o.line_stride = pitch;
+    *o.unit_stride = 1;
+    o.base = dst;
+}
+
+// Workspace of `bytes`, or nullptr when it cannot be had (the failed allocation's error is
+// cleared so the next launch check does not report it).
+void* try_reserve(mfr_stream& s, size_t bytes) {
+    try {
+        return s.reserve(bytes);
+    } catch (const mfr::Error&) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+}
+
 void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
     using mfr::require;
     require(d.m >= 0 && d.n >= 0 && d.k >= 0, "sgemm: negative dimension");
@@ -215,6 +323,40 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
         require(p.m == 1 || p.c0_rs >= p.n, "sgemm: c0 row stride smaller than n");
     }
     require(d.tile >= MFR_TILE_AUTO && d.tile < MFR_TILE_COUNT, "sgemm: unknown tile");
+    require(d.stage == MFR_STAGE_AUTO || d.stage == MFR_STAGE_NEVER || d.stage == MFR_STAGE_ALWAYS,
+            "sgemm: unknown stage mode");
+
+    // Stage the operands that would take 4-byte loads (see the design notes at the top).
+    if (d.k > 0 && (va == 1 || vb == 1) && d.stage != MFR_STAGE_NEVER) {
+        Operand oa{p.a, ak ? p.m : p.k, ak ? p.k : p.m, ak ? &p.a_rs : &p.a_cs,
+                   ak ? &p.a_cs : &p.a_rs, p.a_bs};
+        Operand ob{p.b, bk ? p.n : p.k, bk ? p.k : p.n, bk ? &p.b_cs : &p.b_rs,
+                   bk ? &p.b_rs : &p.b_cs, p.b_bs};
+        const int64_t fa = va == 1 ? (staged_floats(oa, p) + 63) / 64 * 64 : 0;
+        const int64_t fb = vb == 1 ? (staged_floats(ob, p) + 63) / 64 * 64 : 0;
+        const double flops = 2.0 * static_cast<double>(p.m) * p.n * p.k * batch_count;
+        const double staged_bytes = 4.0 * static_cast<double>(fa + fb);
+        const bool worth = flops >= 1073741824.0 && staged_bytes * 64.0 <= flops &&
+                           staged_bytes <= 4294967296.0;
+        if (d.stage == MFR_STAGE_ALWAYS || worth) {
+            float* ws = static_cast<float*>(try_reserve(s, static_cast<size_t>(staged_bytes)));
+            if (ws == nullptr && d.stage == MFR_STAGE_ALWAYS) {
+                throw mfr::Error(MFR_E_RUNTIME, "sgemm: no workspace for operand staging");
+            }
+            if (ws != nullptr) {
+                if (fa > 0) {
+                    stage_operand(oa, ws, p, s.stream);
+                    p.a = oa.base;
+                    va = 4;
+                }
+                if (fb > 0) {
+                    stage_operand(ob, ws + fa, p, s.stream);
+                    p.b = ob.base;
+                    vb = 4;
+                }
+            }
+        }
+    }
     const bool wide = va == 4 && vb == 4;
     int tile = d.tile;
     if (tile == MFR_TILE_AUTO) {

@@ -141,7 +141,8 @@ def test_exact_every_tile(stream, tile, m, n, k):
             c, buf = guarded_output(stream, (m, n))
             run = lambda: mf.gemm(dev(a_st, stream), dev(b_st, stream), alpha=1.5,  # noqa: E731
                                   c0=dev(c0, stream), beta=0.5, trans_a=trans_a,
-                                  trans_b=trans_b, bias=dev(bias, stream), out=c, tile=tile)
+                                  trans_b=trans_b, bias=dev(bias, stream), out=c, tile=tile,
+                                  stage=mf.abi.STAGE_NEVER)
             if tile == mf.abi.TILE_256x256 and not wide_loads_possible(a_st, b_st):
                 # Degenerate extents (m or n of 1) may still qualify; otherwise it is refused.
                 try:
@@ -167,6 +168,69 @@ def test_exact_batched_every_tile(stream, tile):
         for h in range(heads):
             want = (np.float32(0.5) * exact_product(a[i, h], bt[0, h].T)).astype(np.float32)
             assert same_bits(got[i, h], want), (tile, i, h)
+
+
+@pytest.mark.parametrize("tile", TILES)
+@pytest.mark.parametrize("m,n,k", [(300, 261, 1023), (257, 129, 257), (5, 300, 63),
+                                   (129, 66, 35)])
+def test_exact_staged_every_tile(stream, tile, m, n, k):
+    """Operands copied to the aligned workspace first (stage ALWAYS), on every tile and every
+    pair of the reference's matmul layouts -- sliced views start at unaligned addresses with odd
+    strides: bits equal the exact product."""
+    a = quarter_matrix(m, k, 91)
+    b = quarter_matrix(k, n, 92)
+    c0 = quarter_matrix(m, n, 93)
+    bias = quarter_matrix(1, n, 94)[0]
+    want = (np.float32(1.5) * exact_product(a, b)) + np.float32(0.5) * c0
+    want = (want + bias).astype(np.float32)
+    c0_d, bias_d = dev(c0, stream), dev(bias, stream)
+    for kind_a in range(4):
+        for kind_b in range(4):
+            c, buf = guarded_output(stream, (m, n))
+            mf.gemm(make_view(stream, a, kind_a), make_view(stream, b, kind_b), alpha=1.5,
+                    c0=c0_d, beta=0.5, bias=bias_d, out=c, tile=tile,
+                    stage=mf.abi.STAGE_ALWAYS)
+            assert same_bits(c.numpy(), want), (tile, kind_a, kind_b)
+            check_guards(buf)
+
+
+def test_exact_staged_batched_broadcast(stream):
+    """Staging a batched operand copies each distinct matrix once: a broadcast batch dimension
+    (stride 0) stays broadcast in the staged copy."""
+    bsz, heads, m, n, k = 3, 2, 70, 45, 63
+    a = quarter_matrix(heads * m, k, 95).reshape(1, heads, m, k)
+    b = quarter_matrix(bsz * heads * k, n, 96).reshape(bsz, heads, k, n)
+    out = mf.DeviceArray.empty((bsz, heads, m, n), stream)
+    a_d = dev(a, stream).expand((bsz, heads, m, k))
+    for tile in TILES:
+        mf.gemm_batched(a_d, dev(b, stream), out, alpha=0.5, tile=tile,
+                        stage=mf.abi.STAGE_ALWAYS)
+        got = out.numpy()
+        for i in range(bsz):
+            for h in range(heads):
+                want = (np.float32(0.5) * exact_product(a[0, h], b[i, h])).astype(np.float32)
+                assert same_bits(got[i, h], want), (tile, i, h)
+
+
+def test_stage_modes_agree_bitwise(stream, oracle):
+    """Staging changes only where operands are read from: with the same tile, realistic inputs
+    give the same bits staged and unstaged (the zero padding adds +0 to each sum)."""
+    m, n, k = 1021, 515, 1023
+    x = oracle.normal(m * k, 0.0, 1.0, 11, 0).reshape(m, k)
+    w = oracle.normal(k * n, 0.0, 1.0 / np.sqrt(k), 12, 0).reshape(k, n)
+    x_d, w_d = dev(x, stream), dev(w, stream)
+    for tile in TILES[1:]:
+        plain = mf.gemm(x_d, w_d, tile=tile, stage=mf.abi.STAGE_NEVER).numpy()
+        staged = mf.gemm(x_d, w_d, tile=tile, stage=mf.abi.STAGE_ALWAYS).numpy()
+        assert np.array_equal(plain.view(np.uint32), staged.view(np.uint32)), tile
+    got = mf.gemm(x_d, w_d, tile=mf.abi.TILE_256x256, stage=mf.abi.STAGE_ALWAYS).numpy()
+    assert_gemm_parity(got, oracle.gemm(x, w), magnitude(oracle, x, w), k, "staged 256x256")
+
+
+def test_unknown_stage_mode_is_invalid(stream):
+    a = dev(np.ones((4, 4), np.float32), stream)
+    with pytest.raises(ValueError):
+        mf.gemm(a, a, stage=7)
 
 
 def test_k_zero_gives_epilogue_of_zero_product(stream):
