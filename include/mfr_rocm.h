@@ -230,6 +230,50 @@ enum { MFR_EW_ADD = 0, MFR_EW_MUL = 1, MFR_EW_SCAL = 2 };
 int mfr_elementwise(mfr_stream_t stream, int op, const float* a, const float* b, float alpha,
                     float* out, int64_t n);
 
+/* ---- fused attention ---------------------------------------------------------------------- */
+
+/* Scaled dot-product attention in one kernel, without materialising the [.., lq, lk] scores:
+ *
+ *   out[b](i, :) = sum_j p_ij v[b](j, :),  p_ij = softmax_j(s_ij),
+ *   s_ij = fl(scale * q[b](i, :) . k[b](j, :)), or -inf where the mask is 0, where causal and
+ *   j > i (top-left aligned), or where j >= lk.
+ *
+ * The softmax is the online (running-maximum) form: each block of keys rescales the partial
+ * sums by exp(m_old - m_new), and the output is divided by the row's sum once at the end; a row
+ * with every key removed gives zeros, a NaN score gives a NaN row. q [.., lq, d], k [.., lk, d],
+ * v [.., lk, d] and out [.., lq, d] have unit stride along d, row strides and batch strides
+ * (0 = broadcast) that are multiples of 4 floats and 16-byte aligned bases; d is 32, 64 or 128.
+ * Anything else is MFR_E_UNSUPPORTED (the caller composes the op instead). The mask (NULL, or
+ * 1 byte per element: nonzero keeps) has any strides, 0 for broadcast dimensions. scale 0 means
+ * fl(1/sqrt(d)).
+ *
+ * Replaces: mensurflow::attention's composition (src/ops/attention.cpp:48-98) -- a batched GEMM
+ * for the scores, where() with -inf for masked and causal positions, softmax over the keys
+ * (src/backends/cpu/ops/softmax/softmax.cpp:13-49) and a batched GEMM with v -- as one op. It
+ * sums in a different order and normalises after the weighted sum, so it agrees with the
+ * composition to fp32 rounding (max relative error 1e-5*sqrt(lk) of sum_j |p_ij v_jc|), not
+ * bit for bit. */
+typedef struct mfr_attention_desc {
+    int64_t lq, lk, d;
+    int32_t batch_dims;                       /* 0 .. MFR_MAX_BATCH_DIMS */
+    int32_t causal;
+    int64_t batch[MFR_MAX_BATCH_DIMS];
+    const float* q;
+    int64_t q_rs, q_bs[MFR_MAX_BATCH_DIMS];
+    const float* k;
+    int64_t k_rs, k_bs[MFR_MAX_BATCH_DIMS];
+    const float* v;
+    int64_t v_rs, v_bs[MFR_MAX_BATCH_DIMS];
+    float* out;
+    int64_t out_rs, out_bs[MFR_MAX_BATCH_DIMS];
+    const uint8_t* mask;                      /* may be NULL */
+    int64_t mask_rs, mask_cs, mask_bs[MFR_MAX_BATCH_DIMS];
+    float scale;
+    int32_t reserved;
+} mfr_attention_desc;
+
+int mfr_attention(mfr_stream_t stream, const mfr_attention_desc* desc);
+
 /* ---- layout ------------------------------------------------------------------------------- */
 
 #define MFR_MAX_COPY_DIMS 8

@@ -26,6 +26,7 @@ __all__ = [
     "ACT_NONE", "ACT_GELU_TANH", "ACT_GELU_ERF", "GemmDesc", "device_count", "device_info",
     "Stream", "DeviceArray", "Event", "sgemm", "gemm", "gemm_batched", "sgemv", "matvec",
     "bias_act", "where", "softmax", "argmax", "strided_copy", "fill", "attention",
+    "attention_fused", "attention_composed",
 ]
 
 
@@ -237,9 +238,10 @@ class DeviceArray:
             want = shape[lead + i]
             if s == want:
                 strides.append(st)
-            else:
-                assert s == 1
+            elif s == 1:
                 strides.append(0)
+            else:
+                raise ValueError(f"cannot expand {self.shape} to {shape}")
         return self._view(shape, strides, self.offset)
 
     def slice(self, dim, start, end) -> "DeviceArray":
@@ -424,8 +426,62 @@ def fill(x: DeviceArray, value) -> None:
               "mfr_fill")
 
 
+def attention_fused(q: DeviceArray, k: DeviceArray, v: DeviceArray,
+                    mask: DeviceArray | None = None, causal: bool = False, scale: float = 0.0,
+                    out: DeviceArray | None = None) -> DeviceArray:
+    """mfr_attention: the whole op in one kernel (online softmax, no score matrix). q [..., Lq, D],
+    k and v [..., Lk, D] with equal batch shapes (stride 0 for broadcast), D in {32, 64, 128};
+    mask a uint8 array broadcastable to [..., Lq, Lk]. Raises NotImplementedError for layouts
+    the kernel does not take."""
+    lq, depth = q.shape[-2:]
+    lk = k.shape[-2]
+    batch = q.shape[:-2]
+    dims = len(batch)
+    if dims > abi.MAX_BATCH_DIMS:
+        raise ValueError("too many batch dimensions")
+    if k.shape != batch + (lk, depth) or v.shape != batch + (lk, depth):
+        raise ValueError(f"attention: q {q.shape}, k {k.shape}, v {v.shape} do not agree")
+    for t in (q, k, v):
+        if t.strides[-1] != 1:
+            raise NotImplementedError("attention: fused kernel needs unit stride along d")
+    if out is None:
+        out = DeviceArray.empty(batch + (lq, depth), q.stream)
+    d = abi.AttentionDesc()
+    d.lq, d.lk, d.d = lq, lk, depth
+    d.batch_dims = dims
+    d.causal = 1 if causal else 0
+    _fill_batch(d.batch, batch, dims)
+    for name, t in (("q", q), ("k", k), ("v", v), ("out", out)):
+        setattr(d, name, t.ptr)
+        setattr(d, name + "_rs", t.strides[-2])
+        _fill_batch(getattr(d, name + "_bs"), t.strides[:-2], dims)
+    if mask is not None:
+        full = mask.expand(batch + (lq, lk))
+        d.mask = full.ptr
+        d.mask_rs, d.mask_cs = full.strides[-2], full.strides[-1]
+        _fill_batch(d.mask_bs, full.strides[:-2], dims)
+    d.scale = scale
+    abi.check(abi.load().mfr_attention(q.stream.handle, ctypes.byref(d)), "mfr_attention")
+    return out
+
+
 def attention(q: DeviceArray, k: DeviceArray, v: DeviceArray, mask: DeviceArray | None = None,
-              causal: bool = False, scale: float = 0.0) -> DeviceArray:
+              causal: bool = False, scale: float = 0.0, fused: bool | None = None) -> DeviceArray:
+    """mensurflow::attention (src/ops/attention.cpp:48-98). fused=None runs the fused kernel
+    (attention_fused) when it takes the layout and the composition otherwise; True only the
+    fused kernel; False only the composition."""
+    if fused is not False:
+        try:
+            return attention_fused(q, k, v, mask=mask, causal=causal, scale=scale)
+        except NotImplementedError:
+            if fused:
+                raise
+    return attention_composed(q, k, v, mask=mask, causal=causal, scale=scale)
+
+
+def attention_composed(q: DeviceArray, k: DeviceArray, v: DeviceArray,
+                       mask: DeviceArray | None = None, causal: bool = False,
+                       scale: float = 0.0) -> DeviceArray:
     """mensurflow::attention's composition on the device (src/ops/attention.cpp:48-98): scores =
     gemm_batched(q, k^T, alpha=scale), where(mask, scores, -inf) with the mask and the -inf
     scalar packed to the scores' shape (as mensurflow::where packs them), the causal mask the

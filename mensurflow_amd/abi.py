@@ -65,6 +65,22 @@ class GemmDesc(ctypes.Structure):
     ]
 
 
+class AttentionDesc(ctypes.Structure):
+    """mfr_attention_desc (include/mfr_rocm.h)."""
+
+    _fields_ = [
+        ("lq", _i64), ("lk", _i64), ("d", _i64),
+        ("batch_dims", _i32), ("causal", _i32),
+        ("batch", _i64 * MAX_BATCH_DIMS),
+        ("q", _vp), ("q_rs", _i64), ("q_bs", _i64 * MAX_BATCH_DIMS),
+        ("k", _vp), ("k_rs", _i64), ("k_bs", _i64 * MAX_BATCH_DIMS),
+        ("v", _vp), ("v_rs", _i64), ("v_bs", _i64 * MAX_BATCH_DIMS),
+        ("out", _vp), ("out_rs", _i64), ("out_bs", _i64 * MAX_BATCH_DIMS),
+        ("mask", _vp), ("mask_rs", _i64), ("mask_cs", _i64), ("mask_bs", _i64 * MAX_BATCH_DIMS),
+        ("scale", _f32), ("reserved", _i32),
+    ]
+
+
 # name -> (restype, argtypes). Every symbol the header declares is here; tests check that the
 # library exports each of them.
 SIGNATURES = {
@@ -99,6 +115,7 @@ SIGNATURES = {
     "mfr_softmax": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64]),
     "mfr_argmax": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64]),
     "mfr_elementwise": (ctypes.c_int, [_vp, ctypes.c_int, _vp, _vp, _f32, _vp, _i64]),
+    "mfr_attention": (ctypes.c_int, [_vp, ctypes.POINTER(AttentionDesc)]),
     "mfr_strided_copy": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, ctypes.POINTER(_i64),
                                         ctypes.POINTER(_i64)]),
     "mfr_fill": (ctypes.c_int, [_vp, _vp, _i32, _i64, ctypes.c_uint64]),

@@ -1,0 +1,433 @@
+// Fused scaled dot-product attention on the fp32 matrix cores (include/mfr_rocm.h,
+// mfr_attention). One kernel computes softmax(scale * q k^T, masked) v without writing the
+// [.., lq, lk] scores to memory; the reference composes the same op from a batched GEMM, where(),
+// softmax and a second batched GEMM (src/ops/attention.cpp:48-98).
+//
+// Design (a workgroup of 4 wavefronts, 32 queries each; keys in blocks of BK):
+//   - Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x2_f32: the accumulator
+//     of a 32-key x 32-query block puts one query in each lane column (lanes l and l+32 hold
+//     query l % 32, 16 keys each). Every per-query quantity of the softmax (running maximum,
+//     running sum, rescale factor) is then lane-local, with one exchange between the two lane
+//     halves per key block for the maximum.
+//   - The output is also computed transposed, O^T += V^T P^T. Its B operand P^T needs, in lane l
+//     at step s of depth group g, the weight of query l % 32 and key 8g + 4(l / 32) + s, which is
+//     exactly accumulator element 4g + s of that lane in S^T: the probabilities feed the second
+//     product straight from registers, with no shuffle and no trip through LDS.
+//   - q's fragments stay in registers for the whole key loop. K and V tiles are double-buffered
+//     in LDS through the GEMM's slice loader: K [keys][d+4] (K-major, 16-byte fragment reads),
+//     V [keys][d+8] (read as V^T fragments, four 4-byte reads).
+//   - Causal attention skips, per wavefront, every key block lying wholly above its queries'
+//     diagonal, and the key loop stops at the workgroup's last query. Workgroups are
+//     issued longest first (the last query blocks of every batch entry) so the short ones fill
+//     the tail.
+//   - The result is scaled by the reciprocal of the row sum, staged through LDS and stored as
+//     16-byte rows.
+#include "gemm_kernel.hpp"
+
+#include <cmath>
+
+namespace {
+
+using mfr::gemm::floatx16;
+using mfr::gemm::SliceLoader;
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kBlockQ = kWaves * 32; // queries per workgroup
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct AttnParams {
+    const float* q;
+    const float* k;
+    const float* v;
+    float* out;
+    const uint8_t* mask;
+    int64_t lq, lk;
+    int64_t q_rs, k_rs, v_rs, out_rs, mask_rs, mask_cs;
+    int64_t batch[MFR_MAX_BATCH_DIMS];
+    int64_t q_bs[MFR_MAX_BATCH_DIMS], k_bs[MFR_MAX_BATCH_DIMS], v_bs[MFR_MAX_BATCH_DIMS];
+    int64_t out_bs[MFR_MAX_BATCH_DIMS], mask_bs[MFR_MAX_BATCH_DIMS];
+    int64_t batch_count;
+    int32_t batch_dims;
+    int32_t causal;
+    int32_t q_blocks;
+    float scale;
+};
+
+// exp(x - m) through the hardware's 2^x (v_exp_f32, 1 ulp; results below 2^-126 may flush to
+// zero, which is below the rounding of any row sum, whose largest term is exp(0) = 1). m is
+// never -inf here (the caller substitutes 0), so x = -inf gives exp2(-inf) = 0 without a NaN.
+__device__ inline float weight(float x, float m) {
+    return __builtin_amdgcn_exp2f((x - m) * kLog2e);
+}
+
+// MASKED: a mask tensor is given (read for every score). Without it only the key count and the
+// causal diagonal remove scores, and only blocks that reach past either are checked.
+template <int D, int BK, bool MASKED>
+__global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnParams p) {
+    constexpr int SUB = BK / 32; // 32-key sub-blocks per key block
+    constexpr int DB = D / 32;   // 32-wide output column blocks
+    constexpr int G = D / 8;     // depth groups of q . k
+    constexpr int kStagePitch = D + 4;
+    using LoadK = SliceLoader<BK, D, true, 4, kThreads>;  // rows = keys, depth = d
+    using LoadV = SliceLoader<D, BK, false, 4, kThreads>; // rows = d, depth = keys
+    __shared__ float smem[2 * (LoadK::kFloats + LoadV::kFloats)];
+    static_assert(kWaves * 32 * kStagePitch <= 2 * (LoadK::kFloats + LoadV::kFloats),
+                  "output staging must fit in the tile buffers");
+    auto lds_k = [&](int which) { return smem + which * LoadK::kFloats; };
+    auto lds_v = [&](int which) { return smem + 2 * LoadK::kFloats + which * LoadV::kFloats; };
+
+    // ---- which (batch entry, query block): the longest (last) query blocks first ----
+    const int64_t bid = blockIdx.x;
+    const int64_t qb = p.q_blocks - 1 - bid / p.batch_count;
+    int64_t bi = bid % p.batch_count;
+    int64_t off_q = 0, off_k = 0, off_v = 0, off_o = 0, off_m = 0;
+    for (int d = p.batch_dims - 1; d >= 0; --d) {
+        const int64_t idx = bi % p.batch[d];
+        bi /= p.batch[d];
+        off_q += idx * p.q_bs[d];
+        off_k += idx * p.k_bs[d];
+        off_v += idx * p.v_bs[d];
+        off_o += idx * p.out_bs[d];
+        off_m += idx * p.mask_bs[d];
+    }
+
+    const int lane = threadIdx.x % 64;
+    // Uniform across the wavefront; read into a scalar register so that the branches on it
+    // (active sub-blocks, edge blocks) are scalar branches.
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / 64));
+    const int half = lane / 32;
+    const int r32 = lane % 32;
+    const int64_t q0 = qb * kBlockQ;
+    const int64_t wq0 = q0 + wave * 32; // first query of this wavefront
+    const int64_t query = wq0 + r32;    // this lane's query
+    const bool wave_live = wq0 < p.lq;
+
+    // q fragments: B operand of S^T = K Q^T, depth 8g + 4*half + s at step s of group g.
+    float qf[G][4];
+    {
+        const float* qrow = p.q + off_q + query * p.q_rs + 4 * half;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (query < p.lq) {
+                v = *reinterpret_cast<const float4*>(qrow + 8 * g);
+            }
+            qf[g][0] = v.x;
+            qf[g][1] = v.y;
+            qf[g][2] = v.z;
+            qf[g][3] = v.w;
+        }
+    }
+    const uint8_t* mask_row = nullptr;
+    if constexpr (MASKED) {
+        mask_row = p.mask + off_m + (query < p.lq ? query : 0) * p.mask_rs;
+    }
+
+    // Keys this workgroup needs: all of them, or (causal) up to its last query.
+    int64_t k_end = p.lk;
+    if (p.causal) {
+        const int64_t last_query = (q0 + kBlockQ < p.lq ? q0 + kBlockQ : p.lq) - 1;
+        k_end = last_query + 1 < k_end ? last_query + 1 : k_end;
+    }
+    const int64_t blocks = (k_end + BK - 1) / BK;
+
+    float m_run = -INFINITY; // running maximum of this lane's query
+    float l_run = 0.0f;      // this lane's share of the running sum (its 16 keys per sub-block)
+    floatx16 oacc[DB];
+#pragma unroll
+    for (int b = 0; b < DB; ++b) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            oacc[b][e] = 0.0f;
+        }
+    }
+
+    const float* k_base = p.k + off_k;
+    const float* v_base = p.v + off_v;
+    LoadK lk_;
+    LoadV lv_;
+    if (blocks > 0) {
+        const int keys = p.lk < BK ? static_cast<int>(p.lk) : BK;
+        lk_.load(k_base, p.k_rs, 1, keys, D);
+        lv_.load(v_base, 1, p.v_rs, D, keys);
+        lk_.store(lds_k(0));
+        lv_.store(lds_v(0));
+        __syncthreads();
+    }
+    for (int64_t kb = 0; kb < blocks; ++kb) {
+        const int cur = static_cast<int>(kb & 1);
+        const bool more = kb + 1 < blocks;
+        const int64_t k0 = kb * BK;
+        if (more) {
+            const int64_t left = p.lk - (k0 + BK);
+            const int keys = left < BK ? static_cast<int>(left) : BK;
+            lk_.load(k_base + (k0 + BK) * p.k_rs, p.k_rs, 1, keys, D);
+            lv_.load(v_base + (k0 + BK) * p.v_rs, 1, p.v_rs, D, keys);
+        }
+        const float* sk = lds_k(cur);
+        const float* sv = lds_v(cur);
+
+        // Whether this wavefront needs the block at all (uniform across the wavefront): causal
+        // attention skips blocks lying wholly above its queries' diagonal. Inside, every MFMA
+        // runs unconditionally (masking removes what is not wanted), which keeps the
+        // accumulators in place.
+        if (wave_live && (!p.causal || k0 <= wq0 + 31)) {
+            // ---- S^T = K Q^T, the sub-blocks' accumulator chains interleaved ----
+            floatx16 sacc[SUB];
+#pragma unroll
+            for (int sb = 0; sb < SUB; ++sb) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    sacc[sb][e] = 0.0f;
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float kf[SUB][4];
+#pragma unroll
+                for (int sb = 0; sb < SUB; ++sb) {
+                    LoadK::fragment(sk, 32 * sb + r32, g, half, kf[sb]);
+                }
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+#pragma unroll
+                    for (int sb = 0; sb < SUB; ++sb) {
+                        sacc[sb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[sb][st], qf[g][st],
+                                                                         sacc[sb], 0, 0, 0);
+                    }
+                }
+            }
+
+            // ---- scale and mask (per lane: query `query`, 16 keys per sub-block) ----
+            // Key of element e of sub-block sb, relative to k0: 32*sb + 8*(e/4) + e%4 + 4*half.
+            // A block needs checking when it reaches past the last key or (causal) past the
+            // wavefront's first query; both tests are uniform across the wavefront.
+            const bool edge = k0 + BK > p.lk || (p.causal && k0 + BK - 1 > wq0);
+            if (MASKED || edge) {
+                const int64_t keys_left = p.lk - k0;
+                const int64_t diag = query - k0; // causal keeps relative keys <= diag
+                const int lim_k = static_cast<int>(keys_left < BK ? keys_left : BK) - 4 * half;
+                const int lim_q = static_cast<int>(!p.causal || diag >= BK ? BK
+                                                   : diag < -1 ? -1
+                                                               : diag) -
+                                  4 * half;
+#pragma unroll
+                for (int sb = 0; sb < SUB; ++sb) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int rel = 32 * sb + 8 * (e / 4) + e % 4; // minus 4*half (above)
+                        bool keep = rel < lim_k && rel <= lim_q;
+                        if constexpr (MASKED) {
+                            if (keep) {
+                                keep = mask_row[(k0 + rel + 4 * half) * p.mask_cs] != 0;
+                            }
+                        }
+                        sacc[sb][e] = keep ? p.scale * sacc[sb][e] : -INFINITY;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int sb = 0; sb < SUB; ++sb) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        sacc[sb][e] = p.scale * sacc[sb][e];
+                    }
+                }
+            }
+
+            // ---- online softmax: running maximum, rescale, weights ----
+            float block_max = -INFINITY;
+#pragma unroll
+            for (int sb = 0; sb < SUB; ++sb) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    block_max = fmaxf(block_max, sacc[sb][e]);
+                }
+            }
+            block_max = fmaxf(block_max, __shfl_xor(block_max, 32, 64));
+            const float m_new = fmaxf(m_run, block_max);
+            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+            const float rescale = weight(m_run, m_use); // exactly 1 where the maximum stayed
+            m_run = m_new;
+            l_run *= rescale;
+#pragma unroll
+            for (int b = 0; b < DB; ++b) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    oacc[b][e] *= rescale;
+                }
+            }
+#pragma unroll
+            for (int sb = 0; sb < SUB; ++sb) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const float w = weight(sacc[sb][e], m_use);
+                    sacc[sb][e] = w;
+                    l_run += w;
+                }
+            }
+
+            // ---- O^T += V^T P^T: P^T's fragments are the S^T accumulators themselves ----
+#pragma unroll
+            for (int sb = 0; sb < SUB; ++sb) {
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    float vf[DB][4];
+#pragma unroll
+                    for (int b = 0; b < DB; ++b) {
+                        LoadV::fragment(sv, 32 * b + r32, 4 * sb + g, half, vf[b]);
+                    }
+#pragma unroll
+                    for (int st = 0; st < 4; ++st) {
+#pragma unroll
+                        for (int b = 0; b < DB; ++b) {
+                            oacc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                                vf[b][st], sacc[sb][4 * g + st], oacc[b], 0, 0, 0);
+                        }
+                    }
+                }
+            }
+        }
+
+        if (more) {
+            lk_.store(lds_k(cur ^ 1));
+            lv_.store(lds_v(cur ^ 1));
+        }
+        __syncthreads();
+    }
+
+    // ---- normalise, stage [32 queries][D] per wavefront in LDS, store 16-byte rows ----
+    const float l_total = l_run + __shfl_xor(l_run, 32, 64);
+    // A row whose every key was removed has l_total == 0 and gives zeros; a NaN score makes
+    // l_total NaN and so the whole row.
+    const float inv = l_total == 0.0f ? 0.0f : 1.0f / l_total;
+    float* stage = smem + wave * 32 * kStagePitch;
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < DB; ++b) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int col = 32 * b + 8 * (e / 4) + 4 * half + e % 4;
+            stage[r32 * kStagePitch + col] = oacc[b][e] * inv;
+        }
+    }
+    __syncthreads();
+    float* out_base = p.out + off_o;
+    constexpr int kRowUnits = D / 4;
+#pragma unroll
+    for (int i = 0; i < 32 * kRowUnits / 64; ++i) {
+        const int u = lane + 64 * i;
+        const int row = u / kRowUnits;
+        const int c4 = u % kRowUnits;
+        const int64_t qrow = wq0 + row;
+        if (qrow < p.lq) {
+            *reinterpret_cast<float4*>(out_base + qrow * p.out_rs + 4 * c4) =
+                *reinterpret_cast<const float4*>(stage + row * kStagePitch + 4 * c4);
+        }
+    }
+}
+
+template <bool MASKED> void launch(int64_t d, const AttnParams& p, unsigned grid, hipStream_t st) {
+    switch (d) {
+    case 32:
+        attention_kernel<32, 64, MASKED><<<grid, kThreads, 0, st>>>(p);
+        break;
+    case 64:
+        attention_kernel<64, 64, MASKED><<<grid, kThreads, 0, st>>>(p);
+        break;
+    default:
+        attention_kernel<128, 32, MASKED><<<grid, kThreads, 0, st>>>(p);
+        break;
+    }
+}
+
+bool aligned_rows(const void* base, int64_t row_stride, const int64_t* bs, int dims) {
+    if (!mfr::aligned16(base) || row_stride % 4 != 0) {
+        return false;
+    }
+    for (int d = 0; d < dims; ++d) {
+        if (bs[d] % 4 != 0) {
+            return false;
+        }
+    }
+    return true;
+}
+
+void run_attention(mfr_stream& s, const mfr_attention_desc& d) {
+    using mfr::require;
+    require(d.lq >= 0 && d.lk >= 0 && d.d >= 0, "attention: negative dimension");
+    require(d.batch_dims >= 0 && d.batch_dims <= MFR_MAX_BATCH_DIMS,
+            "attention: batch_dims out of range");
+    int64_t batch_count = 1;
+    for (int i = 0; i < d.batch_dims; ++i) {
+        require(d.batch[i] >= 0, "attention: negative batch size");
+        batch_count *= d.batch[i];
+    }
+    if (d.lq == 0 || batch_count == 0) {
+        return;
+    }
+    if (d.d != 32 && d.d != 64 && d.d != 128) {
+        throw mfr::Error(MFR_E_UNSUPPORTED, "attention: fused kernel takes d = 32, 64 or 128");
+    }
+    require(d.q != nullptr && d.out != nullptr, "attention: null q or out");
+    require(d.lk == 0 || (d.k != nullptr && d.v != nullptr), "attention: null k or v");
+    require(d.q_rs >= d.d && d.out_rs >= d.d, "attention: row stride smaller than d");
+    const bool aligned =
+        aligned_rows(d.q, d.q_rs, d.q_bs, d.batch_dims) &&
+        aligned_rows(d.out, d.out_rs, d.out_bs, d.batch_dims) &&
+        (d.lk == 0 || (aligned_rows(d.k, d.k_rs, d.k_bs, d.batch_dims) &&
+                       aligned_rows(d.v, d.v_rs, d.v_bs, d.batch_dims)));
+    if (!aligned) {
+        throw mfr::Error(MFR_E_UNSUPPORTED,
+                         "attention: fused kernel needs 16-byte aligned rows and strides");
+    }
+    AttnParams p{};
+    p.q = d.q;
+    p.k = d.k;
+    p.v = d.v;
+    p.out = d.out;
+    p.mask = d.mask;
+    p.lq = d.lq;
+    p.lk = d.lk;
+    p.q_rs = d.q_rs;
+    p.k_rs = d.k_rs;
+    p.v_rs = d.v_rs;
+    p.out_rs = d.out_rs;
+    p.mask_rs = d.mask != nullptr ? d.mask_rs : 0;
+    p.mask_cs = d.mask != nullptr ? d.mask_cs : 0;
+    p.batch_dims = d.batch_dims;
+    for (int i = 0; i < d.batch_dims; ++i) {
+        p.batch[i] = d.batch[i];
+        p.q_bs[i] = d.q_bs[i];
+        p.k_bs[i] = d.k_bs[i];
+        p.v_bs[i] = d.v_bs[i];
+        p.out_bs[i] = d.out_bs[i];
+        p.mask_bs[i] = d.mask != nullptr ? d.mask_bs[i] : 0;
+    }
+    p.batch_count = batch_count;
+    p.causal = d.causal != 0;
+    p.scale = d.scale != 0.0f ? d.scale
+                              : static_cast<float>(1.0 / std::sqrt(static_cast<double>(d.d)));
+    const int64_t q_blocks = (d.lq + kBlockQ - 1) / kBlockQ;
+    const int64_t blocks = q_blocks * batch_count;
+    require(blocks < (int64_t{1} << 31), "attention: problem too large for one launch");
+    p.q_blocks = static_cast<int32_t>(q_blocks);
+    const unsigned grid = static_cast<unsigned>(blocks);
+    if (d.mask != nullptr) {
+        launch<true>(d.d, p, grid, s.stream);
+    } else {
+        launch<false>(d.d, p, grid, s.stream);
+    }
+    mfr::check_launch("attention_kernel");
+}
+
+} // namespace
+
+extern "C" int mfr_attention(mfr_stream_t stream, const mfr_attention_desc* desc) {
+    return mfr::guarded([&] {
+        auto& s = mfr::stream_of(stream);
+        mfr::require(desc != nullptr, "attention: null descriptor");
+        run_attention(s, *desc);
+    });
+}
