@@ -120,8 +120,9 @@ def bench_mlp(mf, stream, steps, warmup):
 
 
 def bench_attention(mf, stream, steps, warmup):
-    """attention q, k, v [8, 16, 1024, 64], causal -- the reference's composition
-    (batched GEMM, where, softmax, batched GEMM), reported per stage and end to end."""
+    """attention q, k, v [8, 16, 1024, 64], causal -- the fused kernel, and the
+    reference's composition (batched GEMM, where, softmax, batched GEMM) per stage and end to
+    end."""
     rng = np.random.default_rng(4)
     b, h, s, d = 8, 16, 1024, 64
     q, k, v = (mf.DeviceArray.from_numpy(rng.standard_normal((b, h, s, d)).astype(np.float32),
@@ -133,12 +134,18 @@ def bench_attention(mf, stream, steps, warmup):
     _, sm_ms = time_launches(mf, stream, lambda: mf.softmax(scores, out=scores), steps, warmup)
     _, pv_ms = time_launches(mf, stream, lambda: mf.gemm_batched(scores, v, out), steps, warmup)
     total_steps = max(3, steps // 5)
-    wall_ms, _ = time_launches(mf, stream, lambda: mf.attention(q, k, v, causal=True),
+    wall_ms, _ = time_launches(mf, stream, lambda: mf.attention(q, k, v, causal=True, fused=False),
                                total_steps, 1)
+    scores.close()
+    _, fused_ms = time_launches(mf, stream, lambda: mf.attention_fused(q, k, v, causal=True,
+                                                                       out=out), steps, warmup)
     gemm_flops = 2.0 * b * h * s * s * d
+    # What causal attention needs: both products over the s(s+1)/2 kept (query, key) pairs.
+    causal_flops = 4.0 * b * h * d * s * (s + 1) / 2
     return {"qk_ms": qk_ms, "softmax_ms": sm_ms, "pv_ms": pv_ms, "total_ms": wall_ms,
             "flops": 2 * gemm_flops, "gemm_flops": gemm_flops,
-            "scores_bytes": 4.0 * b * h * s * s}
+            "scores_bytes": 4.0 * b * h * s * s, "fused_ms": fused_ms,
+            "causal_flops": causal_flops}
 
 
 def bench_copy(mf, stream, steps, warmup):
@@ -267,6 +274,7 @@ def main() -> int:
                          "traffic": traffic},
         }
     mlp = result["mlp"]
+    att = result["attention"]
     line = {
         "metric": METRIC,
         "value": round(tflops, 3),
@@ -292,18 +300,25 @@ def main() -> int:
                      "traffic": load_traffic("sgemm_4096_nt")},
         "gemv": gemv,
         "mlp_fused": {"tflops": round(mlp["flops"] / (mlp["event_ms"] * 1e-3) / 1e12, 3),
+                      "note": "bias + gelu-tanh in the epilogue; includes staging the odd-strided "
+                              "X and W into aligned copies",
                       "ms_per_call": round(mlp["event_ms"], 4),
+                      "traffic": load_traffic("sgemm_mlp"),
                       "frac": round(mlp["flops"] / (mlp["event_ms"] * 1e-3) / 1e12
                                     / PEAK_FP32_MFMA_TFLOPS, 4)},
         "attention": {
-            "ms_per_call": round(result["attention"]["total_ms"], 3),
-            "qk_gemm_tflops": round(result["attention"]["gemm_flops"]
-                                    / (result["attention"]["qk_ms"] * 1e-3) / 1e12, 2),
-            "pv_gemm_tflops": round(result["attention"]["gemm_flops"]
-                                    / (result["attention"]["pv_ms"] * 1e-3) / 1e12, 2),
-            "softmax_gbs": round(2 * result["attention"]["scores_bytes"]
-                                 / (result["attention"]["softmax_ms"] * 1e-3) / 1e9, 1),
-            "note": "reference composition: 2 batched GEMMs (4*B*H*S^2*D FLOP, dense), where "
+            "fused_ms_per_call": round(att["fused_ms"], 4),
+            "fused_tflops": round(att["causal_flops"] / (att["fused_ms"] * 1e-3) / 1e12, 2),
+            "fused_frac": round(att["causal_flops"] / (att["fused_ms"] * 1e-3) / 1e12
+                                / PEAK_FP32_MFMA_TFLOPS, 4),
+            "fused_traffic": load_traffic("attention_fused"),
+            "composed_ms_per_call": round(att["total_ms"], 3),
+            "composed_qk_gemm_tflops": round(att["gemm_flops"] / (att["qk_ms"] * 1e-3) / 1e12, 2),
+            "composed_pv_gemm_tflops": round(att["gemm_flops"] / (att["pv_ms"] * 1e-3) / 1e12, 2),
+            "composed_softmax_gbs": round(2 * att["scores_bytes"] / (att["softmax_ms"] * 1e-3)
+                                          / 1e9, 1),
+            "note": "fused: one kernel, online softmax, FLOP = 4*B*H*D*S(S+1)/2 (causal pairs); "
+                    "composed: the reference's 2 batched GEMMs (4*B*H*S^2*D FLOP, dense), where "
                     "with packed mask and -inf operands, softmax over materialized scores"},
         "copy_1gib": {"gbs": round(result["copy"]["bytes"] / (result["copy"]["event_ms"] * 1e-3)
                                    / 1e9, 1),

@@ -232,6 +232,69 @@ void gemm_batched_kernel(const OpArgs& args, Stream& stream) {
     }
 }
 
+// ---- attention ---------------------------------------------------------------------------------
+
+// OpId::Attention: q [batch..., lq, d], k and v [batch..., lk, dv] as views with the full batch
+// shape (stride 0 on broadcast dimensions), then the Bool mask [batch..., lq, lk] when has_mask;
+// out contiguous [batch..., lq, dv]; alpha is the scale. Batch dimensions of extent 1 are
+// dropped. A layout the fused kernel does not take throws NotImplemented, and the op composes.
+void attention_kernel(const OpArgs& args, Stream& stream) {
+    const Tensor& q = args.inputs[0];
+    const Tensor& k = args.inputs[1];
+    const Tensor& v = args.inputs[2];
+    const Tensor* mask = args.has_mask ? &args.inputs[3] : nullptr;
+    const Tensor& out = args.outputs[0];
+    const int nd = out.dim();
+    const auto row = static_cast<std::size_t>(nd - 2);
+    const auto col = static_cast<std::size_t>(nd - 1);
+    if (v.size(-1) != q.size(-1)) {
+        throw NotImplemented("attention: fused kernel needs v's width equal to d");
+    }
+    for (const Tensor* t : {&q, &k, &v}) {
+        if (t->strides()[col] != 1 && t->size(-1) != 1) {
+            throw NotImplemented("attention: fused kernel needs unit stride along d");
+        }
+    }
+    mfr_attention_desc d{};
+    d.lq = q.size(-2);
+    d.lk = k.size(-2);
+    d.d = q.size(-1);
+    int dims = 0;
+    for (std::size_t i = 0; i < row; ++i) {
+        if (out.shape()[i] == 1) {
+            continue;
+        }
+        if (dims == MFR_MAX_BATCH_DIMS) {
+            throw NotImplemented("attention: more than " + std::to_string(MFR_MAX_BATCH_DIMS) +
+                                 " batch dimensions for the fused kernel");
+        }
+        d.batch[dims] = out.shape()[i];
+        d.q_bs[dims] = q.strides()[i];
+        d.k_bs[dims] = k.strides()[i];
+        d.v_bs[dims] = v.strides()[i];
+        d.out_bs[dims] = out.strides()[i];
+        d.mask_bs[dims] = mask != nullptr ? mask->strides()[i] : 0;
+        ++dims;
+    }
+    d.batch_dims = dims;
+    d.q = ptr<float>(q);
+    d.q_rs = q.strides()[row];
+    d.k = ptr<float>(k);
+    d.k_rs = k.strides()[row];
+    d.v = ptr<float>(v);
+    d.v_rs = v.strides()[row];
+    d.out = ptr<float>(out);
+    d.out_rs = out.strides()[row];
+    if (mask != nullptr) {
+        d.mask = ptr<std::uint8_t>(*mask);
+        d.mask_rs = mask->strides()[row];
+        d.mask_cs = mask->strides()[col];
+    }
+    d.causal = args.causal ? 1 : 0;
+    d.scale = args.alpha;
+    check(mfr_attention(handle(stream), &d));
+}
+
 // ---- GEMV --------------------------------------------------------------------------------------
 
 // Inputs: a contiguous [rows, cols], x, and y0 when given; args.transpose = A^T.
@@ -351,6 +414,7 @@ class RocmBackend final : public Backend {
         };
         add(OpId::Matmul, matmul_kernel);
         add(OpId::Gemm, gemm_kernel);
+        add(OpId::Attention, attention_kernel);
         add(OpId::GemmBatched, gemm_batched_kernel);
         add(OpId::Gemv, gemv_kernel);
         add(OpId::Matvec, matvec_kernel);

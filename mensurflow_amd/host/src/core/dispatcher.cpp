@@ -26,6 +26,7 @@ const char* op_name(OpId op) {
     case OpId::Softmax: return "softmax";
     case OpId::Gemm: return "gemm";
     case OpId::StridedCopy: return "strided_copy";
+    case OpId::Attention: return "attention";
     }
     throw std::invalid_argument("invalid OpId");
 }
@@ -138,6 +139,15 @@ void dispatch(OpId op, const OpArgs& args, Execution execution) {
         }
     }
     run_on(op, args, execution_device(execution, data_device), data_device);
+}
+
+bool has_kernel_for(OpId op, Execution execution, Device data_device) {
+    try {
+        const Device target = execution_device(execution, data_device);
+        return Registry::instance().dispatcher().find({op, target.type, DType::F32}) != nullptr;
+    } catch (const std::exception&) {
+        return false;
+    }
 }
 
 } // namespace mensurflow::detail

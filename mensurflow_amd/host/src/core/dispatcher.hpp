@@ -40,7 +40,8 @@ enum class OpId {
     Normal,
     Softmax,
     Gemm,        // new: fused gemm (alpha, beta, bias, activation)
-    StridedCopy  // new: pack a strided view on its own device
+    StridedCopy, // new: pack a strided view on its own device
+    Attention    // new: fused scaled dot-product attention (mask, causal)
 };
 
 const char* op_name(OpId op);
@@ -79,6 +80,9 @@ struct OpArgs {
     // input is a bias vector.
     int activation = 0;
     bool has_bias = false;
+    // Attention only: causal masking, and whether the last input is a Bool mask.
+    bool causal = false;
+    bool has_mask = false;
     TuningConfig tuning{};
 };
 
@@ -137,5 +141,9 @@ Device execution_device(Execution execution, Device data_device);
 // elsewhere. Throws invalid_argument for mixed devices, runtime_error for an unavailable device,
 // NotImplemented for a missing kernel.
 void dispatch(OpId op, const OpArgs& args, Execution execution);
+
+// True when `op` has an F32 kernel on the device a call with these settings would run on (false
+// when that device cannot be resolved: the caller's unfused path then reports the error).
+bool has_kernel_for(OpId op, Execution execution, Device data_device);
 
 } // namespace mensurflow::detail

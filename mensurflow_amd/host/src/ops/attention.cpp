@@ -1,8 +1,11 @@
-// Naive scaled dot-product attention from existing ops (the reference's
-// src/ops/attention.cpp:48-98): a batched GEMM for the scaled scores, where() with -inf for
-// masked positions, softmax over the keys, a batched GEMM with v.
+// Scaled dot-product attention (the reference's src/ops/attention.cpp:48-98). Where the execution
+// device has a fused kernel (OpId::Attention) the op is one dispatch; a layout that kernel does
+// not take (it throws NotImplemented), or a device without one, gets the reference's
+// composition: a batched GEMM for the scaled scores, where() with -inf for masked positions,
+// softmax over the keys, a batched GEMM with v.
 #include "mensurflow/ops/attention.hpp"
 
+#include "core/dispatcher.hpp"
 #include "mensurflow/ops/blas.hpp"
 #include "mensurflow/ops/elementwise.hpp"
 #include "mensurflow/ops/softmax.hpp"
@@ -34,6 +37,38 @@ void require_operand(const Tensor& t, const char* name, const Tensor& q) {
     }
 }
 
+Shape batch_of(const Tensor& t) { return Shape(t.shape().begin(), t.shape().end() - 2); }
+
+Shape with_matrix(Shape batch, std::int64_t rows, std::int64_t cols) {
+    batch.push_back(rows);
+    batch.push_back(cols);
+    return batch;
+}
+
+// The fused kernel: q, k, v (and the mask) as views with the common batch shape. Returns an
+// undefined tensor when the kernel does not take this layout.
+Tensor fused_attention(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor* mask,
+                       bool causal, float scale, Execution execution) {
+    const Shape batch = broadcast_shapes(broadcast_shapes(batch_of(q), batch_of(k)), batch_of(v));
+    const std::int64_t lq = q.size(-2), lk = k.size(-2), d = q.size(-1), dv = v.size(-1);
+    detail::OpArgs args;
+    args.inputs = {q.expand(with_matrix(batch, lq, d)), k.expand(with_matrix(batch, lk, d)),
+                   v.expand(with_matrix(batch, lk, dv))};
+    if (mask != nullptr) {
+        args.inputs.push_back(mask->expand(with_matrix(batch, lq, lk)));
+        args.has_mask = true;
+    }
+    args.outputs = {Tensor::empty(with_matrix(batch, lq, dv), DType::F32, q.device())};
+    args.alpha = scale;
+    args.causal = causal;
+    try {
+        detail::dispatch(detail::OpId::Attention, args, execution);
+    } catch (const detail::NotImplemented&) {
+        return Tensor();
+    }
+    return args.outputs[0];
+}
+
 Tensor masked(const Tensor& scores, const Tensor& keep, Execution execution) {
     const Tensor minus_infinity =
         Tensor::full({}, -std::numeric_limits<double>::infinity(), DType::F32, scores.device());
@@ -61,7 +96,14 @@ Tensor attention(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor
     if (scale == 0.0f) {
         scale = depth > 0 ? static_cast<float>(1.0 / std::sqrt(static_cast<double>(depth))) : 1.0f;
     }
-    Tensor scores = gemm_strided_batched(q, k, scale, nullptr, 0.0f, false, true, execution);
+    Shape score_batch;
+    try {
+        score_batch = broadcast_shapes(batch_of(q), batch_of(k));
+    } catch (const std::invalid_argument&) {
+        throw std::invalid_argument("attention: batch shapes of q " + to_string(q.shape()) +
+                                    " and k " + to_string(k.shape()) + " do not broadcast");
+    }
+    const Shape score_shape = with_matrix(score_batch, queries, keys);
     if (mask != nullptr) {
         if (!mask->defined() || mask->dtype() != DType::Bool) {
             throw std::invalid_argument("attention: mask must be a defined Bool tensor");
@@ -69,11 +111,29 @@ Tensor attention(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor
         if (mask->device() != q.device()) {
             throw std::invalid_argument("attention: mask must be on the inputs' device");
         }
-        if (broadcast_shapes(mask->shape(), scores.shape()) != scores.shape()) {
+        bool fits = mask->dim() <= static_cast<int>(score_shape.size());
+        if (fits) {
+            try {
+                fits = broadcast_shapes(mask->shape(), score_shape) == score_shape;
+            } catch (const std::invalid_argument&) {
+                fits = false;
+            }
+        }
+        if (!fits) {
             throw std::invalid_argument("attention: mask " + to_string(mask->shape()) +
                                         " does not broadcast to the scores " +
-                                        to_string(scores.shape()));
+                                        to_string(score_shape));
         }
+    }
+    if (detail::has_kernel_for(detail::OpId::Attention, execution, q.device())) {
+        Tensor out = fused_attention(q, k, v, mask, causal, scale, execution);
+        if (out.defined()) {
+            return out;
+        }
+    }
+
+    Tensor scores = gemm_strided_batched(q, k, scale, nullptr, 0.0f, false, true, execution);
+    if (mask != nullptr) {
         scores = masked(scores, *mask, execution);
     }
     if (causal) {

@@ -45,17 +45,6 @@ bool reads_strides(Device device) {
     return device.type == DeviceType::CPU || device.type == DeviceType::ROCm;
 }
 
-// True when `op` has an F32 kernel on the device this call would run on.
-bool has_kernel_for(detail::OpId op, Execution execution, Device data_device) {
-    try {
-        const Device target = detail::execution_device(execution, data_device);
-        return detail::Registry::instance().dispatcher().find({op, target.type, DType::F32}) !=
-               nullptr;
-    } catch (const std::exception&) {
-        return false; // the unfused path reports the error
-    }
-}
-
 int activation_code(Activation activation) {
     switch (activation) {
     case Activation::None: return 0;
@@ -234,7 +223,7 @@ Tensor matmul(const Tensor& a, const Tensor& b, Execution execution) {
 Tensor gemm(const Tensor& a, const Tensor& b, float alpha, const Tensor* c, float beta,
             bool transpose_a, bool transpose_b, Execution execution) {
     const GemmOperands g = gemm_operands(a, b, c, beta, transpose_a, transpose_b, "gemm");
-    if (has_kernel_for(detail::OpId::Gemm, execution, a.device())) {
+    if (detail::has_kernel_for(detail::OpId::Gemm, execution, a.device())) {
         return fused_gemm(g, nullptr, 0, alpha, c, beta, execution);
     }
     // The reference's composition (src/ops/blas.cpp:244-261).
@@ -264,7 +253,7 @@ Tensor gemm_epilogue(const Tensor& a, const Tensor& b, const Tensor* bias, Activ
             throw std::invalid_argument("gemm_epilogue: bias dtype or device differs");
         }
     }
-    if (has_kernel_for(detail::OpId::Gemm, execution, a.device())) {
+    if (detail::has_kernel_for(detail::OpId::Gemm, execution, a.device())) {
         return fused_gemm(g, bias, act, alpha, c, beta, execution);
     }
     Tensor result = gemm(a, b, alpha, c, beta, transpose_a, transpose_b, execution);

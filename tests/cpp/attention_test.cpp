@@ -80,6 +80,58 @@ void test_attention(Device device) {
     }
 }
 
+// d = 64: the fused kernel on rocm (the composition elsewhere), with ragged lengths around its
+// 128-query / 64-key blocks, k and v shared over the batch dimension, a [batch, 1, lq, lk]
+// mask, and an explicit scale.
+void test_attention_fused_shapes(Device device) {
+    const Execution on = test::execution_on(device);
+    const std::int64_t batch = 2, heads = 2, lq = 150, lk = 170, d = 64;
+    const float scale = 0.2f;
+    const Tensor q = normal({batch, heads, lq, d}, 0.0f, 1.0f, 11, 0).to(device);
+    const Tensor k = normal({1, heads, lk, d}, 0.0f, 1.0f, 12, 0).to(device);
+    const Tensor v = normal({1, heads, lk, d}, 0.0f, 1.0f, 13, 0).to(device);
+    std::vector<std::uint8_t> keep(static_cast<std::size_t>(batch * lq * lk));
+    for (std::size_t i = 0; i < keep.size(); ++i) {
+        keep[i] = ((i * 2246822519u) >> 9) % 3 != 0 ? 1 : 0;
+    }
+    const Tensor mask = Tensor::from_host(keep.data(), {batch, 1, lq, lk}, DType::Bool, device);
+    const auto qv = q.to_vector<float>();
+    const auto kv = k.to_vector<float>();
+    const auto vv = v.to_vector<float>();
+    for (int variant = 0; variant < 4; ++variant) {
+        const bool use_mask = variant & 1;
+        const bool causal = variant & 2;
+        const Tensor result = attention(q, k, v, use_mask ? &mask : nullptr, causal, scale, on);
+        test::require(result.shape() == Shape{batch, heads, lq, d}, "fused attention shape");
+        const auto got = result.to_vector<float>();
+        for (std::int64_t bi = 0; bi < batch; ++bi) {
+            for (std::int64_t h = 0; h < heads; ++h) {
+                std::vector<bool> visible(static_cast<std::size_t>(lq * lk), true);
+                for (std::int64_t i = 0; i < lq; ++i) {
+                    for (std::int64_t j = 0; j < lk; ++j) {
+                        bool ok = !use_mask || keep[static_cast<std::size_t>((bi * lq + i) * lk +
+                                                                             j)] != 0;
+                        visible[static_cast<std::size_t>(i * lk + j)] = ok && !(causal && j > i);
+                    }
+                }
+                const std::size_t qo = static_cast<std::size_t>((bi * heads + h) * lq * d);
+                const std::size_t ko = static_cast<std::size_t>(h * lk * d);
+                const auto want = reference::attention(
+                    std::vector<float>(qv.begin() + qo, qv.begin() + qo + lq * d),
+                    std::vector<float>(kv.begin() + ko, kv.begin() + ko + lk * d),
+                    std::vector<float>(vv.begin() + ko, vv.begin() + ko + lk * d), lq, lk, d, d,
+                    scale, visible);
+                for (std::size_t i = 0; i < want.size(); ++i) {
+                    const double g = got[qo + i];
+                    test::require(std::fabs(g - want[i]) <= 1e-4 * (1.0 + std::fabs(want[i])),
+                                  "fused attention variant " + std::to_string(variant) + " at " +
+                                      std::to_string(qo + i));
+                }
+            }
+        }
+    }
+}
+
 void test_softmax_where_argmax(Device device) {
     const Execution on = test::execution_on(device);
     const float inf = std::numeric_limits<float>::infinity();
@@ -156,6 +208,7 @@ int main(int argc, char** argv) {
         for (Device device : test::devices()) {
             std::cout << "  attention and elementwise on " << to_string(device) << '\n';
             test_attention(device);
+            test_attention_fused_shapes(device);
             test_softmax_where_argmax(device);
             test_bias_gelu(device);
         }
