@@ -153,8 +153,9 @@ typedef struct mfr_gemm_desc {
  * unit-stride extent and its other strides to be multiples of 4 and its base 16-byte aligned
  * (X[4093,1023] row-major is not). Such an operand can first be copied, zero-padded to that
  * shape, into the stream's workspace (one extra pass over it). AUTO stages when the product is
- * large (>= 2^30 flops) and the copy is small next to it (<= 1 byte per 64 flops); the result
- * is the same either way. */
+ * large (>= 2^30 flops) and the copy is small next to it (<= 1 byte per 64 flops), or when the
+ * caller fixed the 256x256 tile, which only runs with 16-byte loads; the result is the same
+ * either way. */
 enum { MFR_STAGE_AUTO = 0, MFR_STAGE_NEVER = 1, MFR_STAGE_ALWAYS = 2 };
 
 /* Workgroup tile of mfr_sgemm (rows x cols x depth slice). AUTO picks one from the shape: a cost
@@ -172,6 +173,15 @@ enum {
 };
 
 int mfr_sgemm(mfr_stream_t stream, const mfr_gemm_desc* desc);
+
+/* What mfr_sgemm would run for desc on device `device`, without launching anything: the tile
+ * (an MFR_TILE_* other than AUTO; AUTO when there is nothing to compute) and whether operands
+ * are staged (MFR_STAGE_ALWAYS) or read in place (MFR_STAGE_NEVER). Validates desc as mfr_sgemm
+ * does and fails with the same status where mfr_sgemm would (MFR_E_UNSUPPORTED for a fixed
+ * 256x256 tile with staging off and operands 16-byte loads cannot read). For tuners: the default
+ * a search starts from, and whether a (tile, stage) point can run (the reference's
+ * TunableKernel::defaults / allowed, src/core/dispatcher.hpp:226-239). */
+int mfr_sgemm_plan(int device, const mfr_gemm_desc* desc, int32_t* tile, int32_t* stage);
 
 /* Plain row-major convenience form: C[m,n] = alpha*op(A)*op(B) + beta*C0 with leading
  * dimensions lda/ldb/ldc (BLAS-style trans flags, row-major storage). c0 may be NULL. */

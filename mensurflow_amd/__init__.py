@@ -26,7 +26,7 @@ __all__ = [
     "ACT_NONE", "ACT_GELU_TANH", "ACT_GELU_ERF", "GemmDesc", "device_count", "device_info",
     "Stream", "DeviceArray", "Event", "sgemm", "gemm", "gemm_batched", "sgemv", "matvec",
     "bias_act", "where", "softmax", "argmax", "strided_copy", "fill", "attention",
-    "attention_fused", "attention_composed",
+    "attention_fused", "attention_composed", "gemm_plan",
 ]
 
 
@@ -291,6 +291,22 @@ def gemm_batched(a: DeviceArray, b: DeviceArray, c: DeviceArray, *, alpha=1.0,
     must already agree (expand them first). tile is an abi.TILE_* value, stage an abi.STAGE_*
     value (copy operands that 16-byte loads cannot read into an aligned workspace first).
     """
+    sgemm(c.stream, _gemm_desc(a, b, c, alpha, c0, beta, bias, act, tile, stage))
+
+
+def gemm_plan(a: DeviceArray, b: DeviceArray, c: DeviceArray, *, tile=0, stage=0,
+              c0: DeviceArray | None = None, beta=0.0) -> tuple[int, int]:
+    """(tile, stage) that gemm_batched(a, b, c, ...) would run with (mfr_sgemm_plan): AUTO
+    resolved to a fixed tile, stage reported as STAGE_ALWAYS (operands copied first) or
+    STAGE_NEVER. Raises as gemm_batched would for a point that cannot run."""
+    d = _gemm_desc(a, b, c, 1.0, c0, beta, None, ACT_NONE, tile, stage)
+    t, st = ctypes.c_int32(), ctypes.c_int32()
+    abi.check(abi.load().mfr_sgemm_plan(c.stream.device, ctypes.byref(d), ctypes.byref(t),
+                                        ctypes.byref(st)), "mfr_sgemm_plan")
+    return t.value, st.value
+
+
+def _gemm_desc(a, b, c, alpha, c0, beta, bias, act, tile, stage) -> GemmDesc:
     m, k = a.shape[-2:]
     k2, n = b.shape[-2:]
     if k != k2:
@@ -327,7 +343,7 @@ def gemm_batched(a: DeviceArray, b: DeviceArray, c: DeviceArray, *, alpha=1.0,
     d.beta = beta
     d.tile = tile
     d.stage = stage
-    sgemm(c.stream, d)
+    return d
 
 
 def gemm(a: DeviceArray, b: DeviceArray, *, alpha=1.0, c0: DeviceArray | None = None, beta=0.0,

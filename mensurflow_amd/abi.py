@@ -105,6 +105,8 @@ SIGNATURES = {
     "mfr_event_record": (ctypes.c_int, [_vp, _vp]),
     "mfr_event_elapsed_ms": (ctypes.c_int, [_vp, _vp, ctypes.POINTER(_f32)]),
     "mfr_sgemm": (ctypes.c_int, [_vp, ctypes.POINTER(GemmDesc)]),
+    "mfr_sgemm_plan": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(GemmDesc),
+                                      ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
     "mfr_sgemm_rm": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _i64, _i64, _i64, _f32, _vp,
                                     _i64, _vp, _i64, _f32, _vp, _vp, _i64]),
     "mfr_sgemv": (ctypes.c_int, [_vp, ctypes.c_int, _i64, _i64, _f32, _vp, _i64, _vp, _f32, _vp,

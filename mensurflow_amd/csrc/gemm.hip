@@ -245,24 +245,57 @@ void* try_reserve(mfr_stream& s, size_t bytes) {
     }
 }
 
-void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
+// Everything mfr_sgemm decides before launching: the kernel parameters (strides of extent-1
+// dimensions normalised), each operand's layout and load width, which operands to stage, and the
+// tile. mfr_sgemm_plan reports it without launching.
+struct Plan {
+    GemmParams p{};
+    bool empty = false;        // nothing to compute (m, n or the batch is 0)
+    bool ak = true, bk = true; // K-major operands
+    int va = 4, vb = 4;        // load widths read in place
+    bool stage_a = false, stage_b = false;
+    int tile = MFR_TILE_AUTO;
+};
+
+Operand operand_a(GemmParams& p, bool ak) {
+    return Operand{p.a, ak ? p.m : p.k, ak ? p.k : p.m, ak ? &p.a_rs : &p.a_cs,
+                   ak ? &p.a_cs : &p.a_rs, p.a_bs};
+}
+
+Operand operand_b(GemmParams& p, bool bk) {
+    return Operand{p.b, bk ? p.n : p.k, bk ? p.k : p.n, bk ? &p.b_cs : &p.b_rs,
+                   bk ? &p.b_rs : &p.b_cs, p.b_bs};
+}
+
+int64_t staged_floats_padded(const Operand& o, const GemmParams& p) {
+    return (staged_floats(o, p) + 63) / 64 * 64; // 256-byte aligned parts of the workspace
+}
+
+// Validates d (the checks and error codes of mfr_sgemm) and makes the plan for a device with
+// `cus` compute units.
+Plan plan_sgemm(const mfr_gemm_desc& d, int cus) {
     using mfr::require;
     require(d.m >= 0 && d.n >= 0 && d.k >= 0, "sgemm: negative dimension");
     require(d.batch_dims >= 0 && d.batch_dims <= MFR_MAX_BATCH_DIMS,
             "sgemm: batch_dims out of range");
     require(d.act == MFR_ACT_NONE || d.act == MFR_ACT_GELU_TANH || d.act == MFR_ACT_GELU_ERF,
             "sgemm: unknown activation");
+    require(d.tile >= MFR_TILE_AUTO && d.tile < MFR_TILE_COUNT, "sgemm: unknown tile");
+    require(d.stage == MFR_STAGE_AUTO || d.stage == MFR_STAGE_NEVER || d.stage == MFR_STAGE_ALWAYS,
+            "sgemm: unknown stage mode");
+    Plan plan;
+    GemmParams& p = plan.p;
     int64_t batch_count = 1;
     for (int i = 0; i < d.batch_dims; ++i) {
         require(d.batch[i] >= 0, "sgemm: negative batch size");
         batch_count *= d.batch[i];
     }
     if (d.m == 0 || d.n == 0 || batch_count == 0) {
-        return;
+        plan.empty = true;
+        return plan;
     }
     require(d.c != nullptr, "sgemm: null c");
     require(d.m == 1 || d.c_rs >= d.n, "sgemm: c row stride smaller than n");
-    GemmParams p{};
     p.a = d.a;
     p.b = d.b;
     p.c = d.c;
@@ -289,11 +322,12 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
     p.alpha = d.alpha;
     p.beta = d.beta;
     p.batch_count = batch_count;
+    if (p.beta != 0.0f && p.c0 != nullptr) {
+        require(p.m == 1 || p.c0_rs >= p.n, "sgemm: c0 row stride smaller than n");
+    }
 
     // A dimension of extent 1 is never stepped along, so its stride is free: pick the one that
-    // gives the operand a unit stride.
-    bool ak = true, bk = true;
-    int va = 1, vb = 1;
+    // gives the operand a unit stride. With k == 0 nothing is loaded at all.
     if (d.k > 0) {
         require(d.a != nullptr && d.b != nullptr, "sgemm: null a or b");
         if (p.k == 1 && p.a_cs != 1) p.a_cs = 1;
@@ -301,73 +335,92 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
         if (p.k == 1 && p.b_rs != 1 && p.b_cs != 1) p.b_rs = 1;
         if (p.n == 1 && p.b_rs != 1) p.b_cs = 1;
         if (p.a_cs == 1) {
-            ak = true;
+            plan.ak = true;
         } else if (p.a_rs == 1) {
-            ak = false;
+            plan.ak = false;
         } else {
             throw mfr::Error(MFR_E_UNSUPPORTED, "sgemm: A needs a unit stride along a dimension");
         }
         if (p.b_rs == 1) {
-            bk = true;
+            plan.bk = true;
         } else if (p.b_cs == 1) {
-            bk = false;
+            plan.bk = false;
         } else {
             throw mfr::Error(MFR_E_UNSUPPORTED, "sgemm: B needs a unit stride along a dimension");
         }
-        va = ak ? vector_width(p.a, p.k, p.a_rs, p.m, p.a_bs, p.batch_dims)
-                : vector_width(p.a, p.m, p.a_cs, p.k, p.a_bs, p.batch_dims);
-        vb = bk ? vector_width(p.b, p.k, p.b_cs, p.n, p.b_bs, p.batch_dims)
-                : vector_width(p.b, p.n, p.b_rs, p.k, p.b_bs, p.batch_dims);
+        plan.va = plan.ak ? vector_width(p.a, p.k, p.a_rs, p.m, p.a_bs, p.batch_dims)
+                          : vector_width(p.a, p.m, p.a_cs, p.k, p.a_bs, p.batch_dims);
+        plan.vb = plan.bk ? vector_width(p.b, p.k, p.b_cs, p.n, p.b_bs, p.batch_dims)
+                          : vector_width(p.b, p.n, p.b_rs, p.k, p.b_bs, p.batch_dims);
     }
-    if (p.beta != 0.0f && p.c0 != nullptr) {
-        require(p.m == 1 || p.c0_rs >= p.n, "sgemm: c0 row stride smaller than n");
-    }
-    require(d.tile >= MFR_TILE_AUTO && d.tile < MFR_TILE_COUNT, "sgemm: unknown tile");
-    require(d.stage == MFR_STAGE_AUTO || d.stage == MFR_STAGE_NEVER || d.stage == MFR_STAGE_ALWAYS,
-            "sgemm: unknown stage mode");
 
-    // Stage the operands that would take 4-byte loads (see the design notes at the top).
-    if (d.k > 0 && (va == 1 || vb == 1) && d.stage != MFR_STAGE_NEVER) {
-        Operand oa{p.a, ak ? p.m : p.k, ak ? p.k : p.m, ak ? &p.a_rs : &p.a_cs,
-                   ak ? &p.a_cs : &p.a_rs, p.a_bs};
-        Operand ob{p.b, bk ? p.n : p.k, bk ? p.k : p.n, bk ? &p.b_cs : &p.b_rs,
-                   bk ? &p.b_rs : &p.b_cs, p.b_bs};
-        const int64_t fa = va == 1 ? (staged_floats(oa, p) + 63) / 64 * 64 : 0;
-        const int64_t fb = vb == 1 ? (staged_floats(ob, p) + 63) / 64 * 64 : 0;
+    // Staging (see the design notes at the top): ALWAYS, or AUTO when the product is large next
+    // to the copy, or when the caller fixed the 256x256 tile (which needs 16-byte loads).
+    if ((plan.va == 1 || plan.vb == 1) && d.stage != MFR_STAGE_NEVER) {
+        const Operand oa = operand_a(p, plan.ak);
+        const Operand ob = operand_b(p, plan.bk);
+        const int64_t fa = plan.va == 1 ? staged_floats_padded(oa, p) : 0;
+        const int64_t fb = plan.vb == 1 ? staged_floats_padded(ob, p) : 0;
         const double flops = 2.0 * static_cast<double>(p.m) * p.n * p.k * batch_count;
         const double staged_bytes = 4.0 * static_cast<double>(fa + fb);
         const bool worth = flops >= 1073741824.0 && staged_bytes * 64.0 <= flops &&
                            staged_bytes <= 4294967296.0;
-        if (d.stage == MFR_STAGE_ALWAYS || worth) {
-            float* ws = static_cast<float*>(try_reserve(s, static_cast<size_t>(staged_bytes)));
-            if (ws == nullptr && d.stage == MFR_STAGE_ALWAYS) {
+        if (d.stage == MFR_STAGE_ALWAYS || worth || d.tile == MFR_TILE_256x256) {
+            plan.stage_a = plan.va == 1;
+            plan.stage_b = plan.vb == 1;
+        }
+    }
+    const bool wide = (plan.va == 4 || plan.stage_a) && (plan.vb == 4 || plan.stage_b);
+    plan.tile = d.tile;
+    if (plan.tile == MFR_TILE_AUTO) {
+        plan.tile = choose_tile(p.m, p.n, p.k, batch_count, cus, wide);
+    } else if (plan.tile == MFR_TILE_256x256 && !wide) {
+        throw mfr::Error(MFR_E_UNSUPPORTED,
+                         "sgemm: the 256x256 tile needs 16-byte loads (staging is off)");
+    }
+    return plan;
+}
+
+void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
+    using mfr::require;
+    Plan plan = plan_sgemm(d, s.compute_units);
+    if (plan.empty) {
+        return;
+    }
+    GemmParams& p = plan.p;
+    int va = plan.va, vb = plan.vb;
+    if (plan.stage_a || plan.stage_b) {
+        Operand oa = operand_a(p, plan.ak);
+        Operand ob = operand_b(p, plan.bk);
+        const int64_t fa = plan.stage_a ? staged_floats_padded(oa, p) : 0;
+        const int64_t fb = plan.stage_b ? staged_floats_padded(ob, p) : 0;
+        float* ws = static_cast<float*>(try_reserve(s, 4 * static_cast<size_t>(fa + fb)));
+        if (ws == nullptr) {
+            if (d.stage == MFR_STAGE_ALWAYS || d.tile == MFR_TILE_256x256) {
                 throw mfr::Error(MFR_E_RUNTIME, "sgemm: no workspace for operand staging");
             }
-            if (ws != nullptr) {
-                if (fa > 0) {
-                    stage_operand(oa, ws, p, s.stream);
-                    p.a = oa.base;
-                    va = 4;
-                }
-                if (fb > 0) {
-                    stage_operand(ob, ws + fa, p, s.stream);
-                    p.b = ob.base;
-                    vb = 4;
-                }
+            // AUTO without the memory: read in place, and choose the tile for 4-byte loads.
+            if (d.tile == MFR_TILE_AUTO) {
+                plan.tile = choose_tile(p.m, p.n, p.k, p.batch_count, s.compute_units,
+                                        va == 4 && vb == 4);
+            }
+        } else {
+            if (plan.stage_a) {
+                stage_operand(oa, ws, p, s.stream);
+                p.a = oa.base;
+                va = 4;
+            }
+            if (plan.stage_b) {
+                stage_operand(ob, ws + fa, p, s.stream);
+                p.b = ob.base;
+                vb = 4;
             }
         }
     }
-    const bool wide = va == 4 && vb == 4;
-    int tile = d.tile;
-    if (tile == MFR_TILE_AUTO) {
-        tile = choose_tile(p.m, p.n, p.k, batch_count, s.compute_units, wide);
-    } else if (tile == MFR_TILE_256x256 && !wide) {
-        throw mfr::Error(MFR_E_UNSUPPORTED,
-                         "sgemm: the 256x256 tile needs 16-byte aligned operands");
-    }
+    const int tile = plan.tile;
     const int64_t tiles_m = (p.m + kTiles[tile].bm - 1) / kTiles[tile].bm;
     const int64_t tiles_n = (p.n + kTiles[tile].bn - 1) / kTiles[tile].bn;
-    const int64_t blocks = tiles_m * tiles_n * batch_count;
+    const int64_t blocks = tiles_m * tiles_n * p.batch_count;
     require(tiles_m < (int64_t{1} << 30) && tiles_n < (int64_t{1} << 30) &&
                 blocks < (int64_t{1} << 31),
             "sgemm: problem too large for one launch");
@@ -375,11 +428,11 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
     p.tiles_n = static_cast<int32_t>(tiles_n);
     p.group_m = kGroupM;
     const unsigned grid = static_cast<unsigned>(blocks);
-    if (ak && bk) {
+    if (plan.ak && plan.bk) {
         launch_layout<true, true>(tile, p, va, vb, grid, s.stream);
-    } else if (ak) {
+    } else if (plan.ak) {
         launch_layout<true, false>(tile, p, va, vb, grid, s.stream);
-    } else if (bk) {
+    } else if (plan.bk) {
         launch_layout<false, true>(tile, p, va, vb, grid, s.stream);
     } else {
         launch_layout<false, false>(tile, p, va, vb, grid, s.stream);
@@ -396,6 +449,21 @@ int mfr_sgemm(mfr_stream_t stream, const mfr_gemm_desc* desc) {
         auto& s = mfr::stream_of(stream);
         mfr::require(desc != nullptr, "sgemm: null descriptor");
         run_sgemm(s, *desc);
+    });
+}
+
+int mfr_sgemm_plan(int device, const mfr_gemm_desc* desc, int32_t* tile, int32_t* stage) {
+    return mfr::guarded([&] {
+        mfr::require(desc != nullptr && tile != nullptr && stage != nullptr,
+                     "sgemm_plan: null argument");
+        int cus = 0;
+        const int status = mfr_get_device_info(device, nullptr, 0, nullptr, &cus, nullptr);
+        if (status != MFR_OK) {
+            throw mfr::Error(status, mfr_last_error());
+        }
+        const Plan plan = plan_sgemm(*desc, cus);
+        *tile = plan.empty ? MFR_TILE_AUTO : plan.tile;
+        *stage = plan.stage_a || plan.stage_b ? MFR_STAGE_ALWAYS : MFR_STAGE_NEVER;
     });
 }
 

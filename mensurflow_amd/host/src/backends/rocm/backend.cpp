@@ -113,66 +113,86 @@ void fill_matrix(mfr_gemm_desc& d, const Tensor& a, const Tensor& b, const Tenso
     d.b_cs = b.strides()[b.dim() - 1];
     d.c = ptr<float>(out);
     d.c_rs = out.size(-1);
-}
-
-// Inputs: op(a) [m,k] and op(b) [k,n] as views; out contiguous [m,n].
-void matmul_kernel(const OpArgs& args, Stream& stream) {
-    const Tensor a = readable_matrix(args.inputs[0]);
-    const Tensor b = readable_matrix(args.inputs[1]);
-    mfr_gemm_desc d{};
-    fill_matrix(d, a, b, args.outputs[0]);
     d.alpha = 1.0f;
     d.beta = 0.0f;
     d.act = MFR_ACT_NONE;
-    check(mfr_sgemm(handle(stream), &d));
 }
 
-// OpId::Gemm: inputs op(a), op(b), then c0 [m,n] when beta != 0, then bias [n] when has_bias.
-void gemm_kernel(const OpArgs& args, Stream& stream) {
-    const Tensor a = readable_matrix(args.inputs[0]);
-    const Tensor b = readable_matrix(args.inputs[1]);
+// The tuner's choice for this call (TunableKernel params "tile", "stage"; none = AUTO).
+void apply_tuning(mfr_gemm_desc& d, const TuningConfig& tuning) {
+    if (tuning.size >= 2) {
+        d.tile = static_cast<std::int32_t>(tuning.values[0]);
+        d.stage = static_cast<std::int32_t>(tuning.values[1]);
+    }
+}
+
+// OpId::Matmul: op(a) [m,k] and op(b) [k,n] as views; out contiguous [m,n].
+// OpId::Gemm: the same, then c0 [m,n] when beta != 0, then bias [n] when has_bias.
+// `a` and `b` are the readable forms of inputs[0] and inputs[1].
+mfr_gemm_desc matrix_desc(OpId op, const OpArgs& args, const Tensor& a, const Tensor& b) {
     const Tensor& out = args.outputs[0];
     mfr_gemm_desc d{};
     fill_matrix(d, a, b, out);
-    d.alpha = args.alpha;
-    d.beta = args.beta;
-    std::size_t next = 2;
-    if (args.beta != 0.0f) {
-        const Tensor& c0 = args.inputs[next++];
-        d.c0 = ptr<float>(c0);
-        d.c0_rs = out.size(-1);
+    if (op == OpId::Gemm) {
+        d.alpha = args.alpha;
+        d.beta = args.beta;
+        std::size_t next = 2;
+        if (args.beta != 0.0f) {
+            d.c0 = ptr<float>(args.inputs[next++]);
+            d.c0_rs = out.size(-1);
+        }
+        if (args.has_bias) {
+            d.bias = ptr<float>(args.inputs[next]);
+        }
+        d.act = args.activation;
     }
-    if (args.has_bias) {
-        d.bias = ptr<float>(args.inputs[next]);
-    }
-    d.act = args.activation;
+    apply_tuning(d, args.tuning);
+    return d;
+}
+
+void matmul_kernel(const OpArgs& args, Stream& stream) {
+    const Tensor a = readable_matrix(args.inputs[0]);
+    const Tensor b = readable_matrix(args.inputs[1]);
+    const mfr_gemm_desc d = matrix_desc(OpId::Matmul, args, a, b);
+    check(mfr_sgemm(handle(stream), &d));
+}
+
+void gemm_kernel(const OpArgs& args, Stream& stream) {
+    const Tensor a = readable_matrix(args.inputs[0]);
+    const Tensor b = readable_matrix(args.inputs[1]);
+    const mfr_gemm_desc d = matrix_desc(OpId::Gemm, args, a, b);
     check(mfr_sgemm(handle(stream), &d));
 }
 
 // OpId::GemmBatched: a [batch..., m, k] and b [batch..., k, n] as views with the full batch shape
 // (stride 0 on broadcast dimensions), out contiguous, and c0 (contiguous, out's shape) when
 // beta != 0. Batch dimensions that step through memory together are merged, size-1 dimensions
-// dropped; more than MFR_MAX_BATCH_DIMS left are walked on the host, one launch per index.
-void gemm_batched_kernel(const OpArgs& args, Stream& stream) {
-    const Tensor a = readable_matrix(args.inputs[0]);
-    const Tensor b = readable_matrix(args.inputs[1]);
+// dropped; the innermost MFR_MAX_BATCH_DIMS go into one launch's descriptor, any left are
+// walked on the host, one launch per index (`outer`).
+struct BatchDim {
+    std::int64_t size, a, b, c, c0;
+};
+
+struct BatchedCall {
+    mfr_gemm_desc desc{};
+    std::vector<BatchDim> outer;
+};
+
+BatchedCall batched_desc(const OpArgs& args, const Tensor& a, const Tensor& b) {
     const Tensor& out = args.outputs[0];
     const bool with_c0 = args.inputs.size() > 2;
     const Tensor* c0 = with_c0 ? &args.inputs[2] : nullptr;
     const int batch_dims = out.dim() - 2;
-    struct Dim {
-        std::int64_t size, a, b, c, c0;
-    };
-    std::vector<Dim> dims;
+    std::vector<BatchDim> dims;
     for (int d = 0; d < batch_dims; ++d) {
         const auto du = static_cast<std::size_t>(d);
-        const Dim dim{out.size(d), a.strides()[du], b.strides()[du], out.strides()[du],
-                      c0 != nullptr ? c0->strides()[du] : 0};
+        const BatchDim dim{out.size(d), a.strides()[du], b.strides()[du], out.strides()[du],
+                           c0 != nullptr ? c0->strides()[du] : 0};
         if (dim.size == 1) {
             continue;
         }
         if (!dims.empty()) {
-            Dim& prev = dims.back();
+            BatchDim& prev = dims.back();
             if (prev.a == dim.size * dim.a && prev.b == dim.size * dim.b &&
                 prev.c == dim.size * dim.c && prev.c0 == dim.size * dim.c0) {
                 prev.size *= dim.size;
@@ -185,11 +205,11 @@ void gemm_batched_kernel(const OpArgs& args, Stream& stream) {
         }
         dims.push_back(dim);
     }
-    mfr_gemm_desc d{};
+    BatchedCall call;
+    mfr_gemm_desc& d = call.desc;
     fill_matrix(d, a, b, out);
     d.alpha = args.alpha;
     d.beta = with_c0 ? args.beta : 0.0f;
-    d.act = MFR_ACT_NONE;
     if (with_c0) {
         d.c0 = ptr<float>(*c0);
         d.c0_rs = out.size(-1);
@@ -198,17 +218,26 @@ void gemm_batched_kernel(const OpArgs& args, Stream& stream) {
     const std::size_t outer = dims.size() - inner;
     d.batch_dims = static_cast<std::int32_t>(inner);
     for (std::size_t i = 0; i < inner; ++i) {
-        const Dim& dim = dims[outer + i];
+        const BatchDim& dim = dims[outer + i];
         d.batch[i] = dim.size;
         d.a_bs[i] = dim.a;
         d.b_bs[i] = dim.b;
         d.c_bs[i] = dim.c;
         d.c0_bs[i] = dim.c0;
     }
-    // Host loop over the outermost dimensions beyond what one launch takes.
+    call.outer.assign(dims.begin(), dims.begin() + static_cast<std::ptrdiff_t>(outer));
+    apply_tuning(d, args.tuning);
+    return call;
+}
+
+void gemm_batched_kernel(const OpArgs& args, Stream& stream) {
+    const Tensor a = readable_matrix(args.inputs[0]);
+    const Tensor b = readable_matrix(args.inputs[1]);
+    BatchedCall call = batched_desc(args, a, b);
+    mfr_gemm_desc& d = call.desc;
     std::int64_t launches = 1;
-    for (std::size_t i = 0; i < outer; ++i) {
-        launches *= dims[i].size;
+    for (const BatchDim& dim : call.outer) {
+        launches *= dim.size;
     }
     const float* a0 = d.a;
     const float* b0 = d.b;
@@ -216,13 +245,13 @@ void gemm_batched_kernel(const OpArgs& args, Stream& stream) {
     const float* c0_base = d.c0;
     for (std::int64_t l = 0; l < launches; ++l) {
         std::int64_t rest = l, oa = 0, ob = 0, oc = 0, oc0 = 0;
-        for (std::size_t i = outer; i-- > 0;) {
-            const std::int64_t idx = rest % dims[i].size;
-            rest /= dims[i].size;
-            oa += idx * dims[i].a;
-            ob += idx * dims[i].b;
-            oc += idx * dims[i].c;
-            oc0 += idx * dims[i].c0;
+        for (std::size_t i = call.outer.size(); i-- > 0;) {
+            const std::int64_t idx = rest % call.outer[i].size;
+            rest /= call.outer[i].size;
+            oa += idx * call.outer[i].a;
+            ob += idx * call.outer[i].b;
+            oc += idx * call.outer[i].c;
+            oc0 += idx * call.outer[i].c0;
         }
         d.a = a0 + oa;
         d.b = b0 + ob;
@@ -230,6 +259,89 @@ void gemm_batched_kernel(const OpArgs& args, Stream& stream) {
         d.c0 = c0_base != nullptr ? c0_base + oc0 : nullptr;
         check(mfr_sgemm(handle(stream), &d));
     }
+}
+
+// ---- tuning ------------------------------------------------------------------------------------
+//
+// The GEMM kernels' settings a tuner may choose (the reference's TunableKernel,
+// src/core/dispatcher.hpp:226-239, registered as the Metal matmul is,
+// src/backends/metal/backend.mm:231-289): params {"tile", "stage"} = the workgroup tile
+// (MFR_TILE_*) and operand staging (MFR_STAGE_NEVER / MFR_STAGE_ALWAYS). The defaults {0, 0}
+// leave both to the kernel (AUTO). The space is one region whose start is what AUTO picks for
+// the call (mfr_sgemm_plan), with the tiles ordered by area, so neighbours on the axis are
+// neighbours in effect; a point is allowed when mfr_sgemm_plan accepts it.
+
+// The descriptor the kernel for `op` would launch with for these args.
+mfr_gemm_desc planned_desc(OpId op, const OpArgs& args) {
+    const Tensor a = readable_matrix(args.inputs[0]);
+    const Tensor b = readable_matrix(args.inputs[1]);
+    return op == OpId::GemmBatched ? batched_desc(args, a, b).desc : matrix_desc(op, args, a, b);
+}
+
+TuningConfig tuning_of(std::int64_t tile, std::int64_t stage) {
+    TuningConfig config;
+    config.values[0] = tile;
+    config.values[1] = stage;
+    config.size = 2;
+    return config;
+}
+
+template <OpId Op> std::vector<std::int64_t> gemm_key(const OpArgs& args) {
+    const Tensor& out = args.outputs[0];
+    std::int64_t batch = 1;
+    for (int d = 0; d + 2 < out.dim(); ++d) {
+        batch *= out.size(d);
+    }
+    const std::int64_t m = out.size(-2), n = out.size(-1), k = args.inputs[0].size(-1);
+    if (Op == OpId::GemmBatched) {
+        return {batch, m, n, k};
+    }
+    return {m, n, k};
+}
+
+template <OpId Op> std::vector<SearchRegion> gemm_space(const OpArgs& args) {
+    mfr_gemm_desc d = planned_desc(Op, args);
+    d.tile = MFR_TILE_AUTO;
+    d.stage = MFR_STAGE_AUTO;
+    std::int32_t tile = 0, stage = 0;
+    check(mfr_sgemm_plan(args.outputs[0].device().index, &d, &tile, &stage));
+    if (tile == MFR_TILE_AUTO) {
+        return {}; // nothing to compute: nothing to tune
+    }
+    SearchRegion region;
+    region.name = "mfma";
+    region.start = tuning_of(tile, stage);
+    region.axes = {{0, {MFR_TILE_64x64, MFR_TILE_128x64, MFR_TILE_64x128, MFR_TILE_128x128,
+                        MFR_TILE_256x256}},
+                   {1, {MFR_STAGE_NEVER, MFR_STAGE_ALWAYS}}};
+    return {region};
+}
+
+template <OpId Op> bool gemm_allowed(const OpArgs& args, const TuningConfig& config) {
+    if (config.size != 2 || config.values[0] <= MFR_TILE_AUTO ||
+        config.values[0] >= MFR_TILE_COUNT ||
+        (config.values[1] != MFR_STAGE_NEVER && config.values[1] != MFR_STAGE_ALWAYS)) {
+        return false;
+    }
+    OpArgs tuned = args;
+    tuned.tuning = config;
+    const mfr_gemm_desc d = planned_desc(Op, tuned);
+    std::int32_t tile = 0, stage = 0;
+    return mfr_sgemm_plan(args.outputs[0].device().index, &d, &tile, &stage) == MFR_OK;
+}
+
+template <OpId Op> TunableKernel gemm_tunable(const char* name) {
+    TunableKernel t;
+    t.name = name;
+    t.version = 1;
+    t.key_names = Op == OpId::GemmBatched ? std::vector<std::string>{"batch", "m", "n", "k"}
+                                          : std::vector<std::string>{"m", "n", "k"};
+    t.key = gemm_key<Op>;
+    t.params = {"tile", "stage"};
+    t.defaults = [] { return tuning_of(MFR_TILE_AUTO, MFR_STAGE_AUTO); };
+    t.space = gemm_space<Op>;
+    t.allowed = gemm_allowed<Op>;
+    return t;
 }
 
 // ---- attention ---------------------------------------------------------------------------------
@@ -426,6 +538,12 @@ class RocmBackend final : public Backend {
         add(OpId::Add, binary_kernel<MFR_EW_ADD>);
         add(OpId::Mul, binary_kernel<MFR_EW_MUL>);
         add(OpId::Scal, binary_kernel<MFR_EW_SCAL>);
+        dispatcher.register_tunable({OpId::Matmul, DeviceType::ROCm, DType::F32},
+                                    gemm_tunable<OpId::Matmul>("matmul"));
+        dispatcher.register_tunable({OpId::Gemm, DeviceType::ROCm, DType::F32},
+                                    gemm_tunable<OpId::Gemm>("gemm"));
+        dispatcher.register_tunable({OpId::GemmBatched, DeviceType::ROCm, DType::F32},
+                                    gemm_tunable<OpId::GemmBatched>("gemm_strided_batched"));
         for (DType type : {DType::F32, DType::I32, DType::I64, DType::U8, DType::Bool,
                            DType::F16, DType::BF16}) {
             dispatcher.register_kernel({OpId::StridedCopy, DeviceType::ROCm, type},

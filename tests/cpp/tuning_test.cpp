@@ -1,0 +1,219 @@
+// The rocm GEMM kernels' tunable settings (TunableKernel "matmul", "gemm" and
+// "gemm_strided_batched", as the reference's tuner sees them: src/core/dispatcher.hpp:226-239):
+// registration, key, defaults, the search space and `allowed`, and every allowed point of the
+// space run through the kernel the way the tuner runs it (args.tuning set), each bit-exact on
+// quarter-integer inputs, whose products sum exactly in any order. Without a rocm device there is
+// nothing registered to check.
+#include "core/dispatcher.hpp"
+#include "core/registry.hpp"
+#include "oracle_cpu.hpp"
+#include "test_util.hpp"
+
+#include "mfr_rocm.h"
+
+#include <string>
+#include <vector>
+
+using namespace mensurflow;
+using namespace mensurflow::detail;
+
+namespace {
+
+// C = alpha * A B + beta * C0 + bias, in double (exact for quarter-integer inputs), as float.
+std::vector<float> exact_gemm(const std::vector<float>& a, const std::vector<float>& b,
+                              std::int64_t m, std::int64_t n, std::int64_t k, double alpha,
+                              const std::vector<float>* c0, double beta,
+                              const std::vector<float>* bias) {
+    std::vector<float> out(static_cast<std::size_t>(m * n));
+    for (std::int64_t i = 0; i < m; ++i) {
+        for (std::int64_t j = 0; j < n; ++j) {
+            double sum = 0.0;
+            for (std::int64_t p = 0; p < k; ++p) {
+                sum += static_cast<double>(a[static_cast<std::size_t>(i * k + p)]) *
+                       b[static_cast<std::size_t>(p * n + j)];
+            }
+            double v = alpha * sum;
+            if (c0 != nullptr) {
+                v += beta * (*c0)[static_cast<std::size_t>(i * n + j)];
+            }
+            if (bias != nullptr) {
+                v += (*bias)[static_cast<std::size_t>(j)];
+            }
+            out[static_cast<std::size_t>(i * n + j)] = static_cast<float>(v);
+        }
+    }
+    return out;
+}
+
+TuningConfig point(std::int64_t tile, std::int64_t stage) {
+    TuningConfig c;
+    c.values[0] = tile;
+    c.values[1] = stage;
+    c.size = 2;
+    return c;
+}
+
+// Runs every point of `op`'s space that `allowed` accepts and checks the output each time.
+// Points refused are exactly the 256x256 tile with staging off when `narrow` (an operand that
+// 16-byte loads cannot read).
+void sweep(Device device, OpId op, OpArgs args, const std::vector<float>& want, bool narrow,
+           const std::string& what) {
+    Registry& registry = Registry::instance();
+    const TunableKernel& tunable = *registry.dispatcher().tunable({op, DeviceType::ROCm, DType::F32});
+    const KernelFn kernel = registry.dispatcher().lookup({op, DeviceType::ROCm, DType::F32});
+    Stream& stream = registry.get(device).stream(device.index);
+    const std::vector<SearchRegion> regions = tunable.space(args);
+    test::require(regions.size() == 1 && regions[0].axes.size() == 2, what + ": one region");
+    const SearchRegion& region = regions[0];
+    test::require(region.start.size == 2 && region.start.values[0] > MFR_TILE_AUTO &&
+                      region.start.values[0] < MFR_TILE_COUNT,
+                  what + ": the start is a fixed tile");
+    test::require(tunable.allowed(args, region.start), what + ": the start is allowed");
+    int ran = 0;
+    for (std::int64_t tile : region.axes[0].values) {
+        for (std::int64_t stage : region.axes[1].values) {
+            const TuningConfig config = point(tile, stage);
+            const bool allowed = tunable.allowed(args, config);
+            const bool expected = !(narrow && tile == MFR_TILE_256x256 && stage == MFR_STAGE_NEVER);
+            test::require(allowed == expected, what + ": allowed(tile " + std::to_string(tile) +
+                                                   ", stage " + std::to_string(stage) + ")");
+            if (!allowed) {
+                continue;
+            }
+            args.tuning = config;
+            kernel(args, stream);
+            test::require(test::same_bits(args.outputs[0].to_vector<float>(), want),
+                          what + ": tile " + std::to_string(tile) + " stage " +
+                              std::to_string(stage));
+            ++ran;
+        }
+    }
+    test::require(ran == (narrow ? 9 : 10), what + ": every allowed point ran");
+    // Not a point: AUTO is only the default, and unknown values are refused.
+    test::require(!tunable.allowed(args, point(MFR_TILE_AUTO, MFR_STAGE_NEVER)) &&
+                      !tunable.allowed(args, point(MFR_TILE_64x64, 7)),
+                  what + ": invalid points refused");
+}
+
+void test_registration() {
+    const Dispatcher& dispatcher = Registry::instance().dispatcher();
+    const std::pair<OpId, const char*> ops[] = {
+        {OpId::Matmul, "matmul"}, {OpId::Gemm, "gemm"}, {OpId::GemmBatched, "gemm_strided_batched"}};
+    for (const auto& [op, name] : ops) {
+        const TunableKernel* t = dispatcher.tunable({op, DeviceType::ROCm, DType::F32});
+        test::require(t != nullptr && t->name == name, std::string(name) + " is tunable on rocm");
+        test::require(t->params == std::vector<std::string>{"tile", "stage"}, "params");
+        const TuningConfig d = t->defaults();
+        test::require(d.size == 2 && d.values[0] == MFR_TILE_AUTO && d.values[1] == MFR_STAGE_AUTO,
+                      "defaults leave both settings to the kernel");
+    }
+}
+
+void test_matmul(Device device) {
+    const std::int64_t m = 300, n = 261, k = 1023; // odd k and n: 4-byte loads in place
+    const auto av = test::quarter_input(m * k, 61);
+    const auto bv = test::quarter_input(k * n, 62);
+    OpArgs args;
+    args.inputs = {Tensor::from_vector(av, {m, k}, device), Tensor::from_vector(bv, {k, n}, device)};
+    args.outputs = {Tensor::empty({m, n}, DType::F32, device)};
+    const TunableKernel& t =
+        *Registry::instance().dispatcher().tunable({OpId::Matmul, DeviceType::ROCm, DType::F32});
+    test::require(t.key(args) == std::vector<std::int64_t>{m, n, k}, "matmul key");
+    const auto want = exact_gemm(av, bv, m, n, k, 1.0, nullptr, 0.0, nullptr);
+    sweep(device, OpId::Matmul, args, want, true, "matmul 300x261x1023");
+}
+
+void test_gemm_fused(Device device) {
+    // B stored [n, k] and read transposed, as configs[2]; alpha, beta*C0 and a bias.
+    const std::int64_t m = 257, n = 200, k = 96; // aligned: every point runs
+    const auto av = test::quarter_input(m * k, 63);
+    const auto bt = test::quarter_input(n * k, 64);
+    const auto cv = test::quarter_input(m * n, 65);
+    const auto biasv = test::quarter_input(n, 66);
+    std::vector<float> bv(static_cast<std::size_t>(k * n));
+    for (std::int64_t p = 0; p < k; ++p) {
+        for (std::int64_t j = 0; j < n; ++j) {
+            bv[static_cast<std::size_t>(p * n + j)] = bt[static_cast<std::size_t>(j * k + p)];
+        }
+    }
+    OpArgs args;
+    args.inputs = {Tensor::from_vector(av, {m, k}, device),
+                   Tensor::from_vector(bt, {n, k}, device).transpose(0, 1),
+                   Tensor::from_vector(cv, {m, n}, device), Tensor::from_vector(biasv, {n}, device)};
+    args.outputs = {Tensor::empty({m, n}, DType::F32, device)};
+    args.alpha = 1.5f;
+    args.beta = 0.5f;
+    args.has_bias = true;
+    const auto want = exact_gemm(av, bv, m, n, k, 1.5, &cv, 0.5, &biasv);
+    sweep(device, OpId::Gemm, args, want, false, "gemm 257x200x96 NT");
+}
+
+void test_batched(Device device) {
+    // [2, 3] batch, B shared over the first dimension (stride 0), odd k.
+    const std::int64_t bs = 2, h = 3, m = 70, n = 45, k = 63;
+    const auto av = test::quarter_input(bs * h * m * k, 67);
+    const auto bv = test::quarter_input(h * k * n, 68);
+    OpArgs args;
+    args.inputs = {Tensor::from_vector(av, {bs, h, m, k}, device),
+                   Tensor::from_vector(bv, {1, h, k, n}, device).expand({bs, h, k, n})};
+    args.outputs = {Tensor::empty({bs, h, m, n}, DType::F32, device)};
+    args.alpha = 0.5f;
+    args.beta = 0.0f;
+    const TunableKernel& t = *Registry::instance().dispatcher().tunable(
+        {OpId::GemmBatched, DeviceType::ROCm, DType::F32});
+    test::require(t.key(args) == std::vector<std::int64_t>{bs * h, m, n, k}, "batched key");
+    std::vector<float> want;
+    for (std::int64_t i = 0; i < bs; ++i) {
+        for (std::int64_t j = 0; j < h; ++j) {
+            const auto off_a = static_cast<std::ptrdiff_t>((i * h + j) * m * k);
+            const auto off_b = static_cast<std::ptrdiff_t>(j * k * n);
+            const std::vector<float> a(av.begin() + off_a, av.begin() + off_a + m * k);
+            const std::vector<float> b(bv.begin() + off_b, bv.begin() + off_b + k * n);
+            const auto c = exact_gemm(a, b, m, n, k, 0.5, nullptr, 0.0, nullptr);
+            want.insert(want.end(), c.begin(), c.end());
+        }
+    }
+    sweep(device, OpId::GemmBatched, args, want, true, "batched 2x3x70x45x63");
+}
+
+void test_start_is_the_automatic_choice(Device device) {
+    // configs[3]'s shape: large and misaligned, so AUTO stages both operands.
+    const std::int64_t m = 2045, n = 2051, k = 1023;
+    OpArgs args;
+    args.inputs = {Tensor::zeros({m, k}, DType::F32, device), Tensor::zeros({k, n}, DType::F32, device)};
+    args.outputs = {Tensor::empty({m, n}, DType::F32, device)};
+    const TunableKernel& t =
+        *Registry::instance().dispatcher().tunable({OpId::Matmul, DeviceType::ROCm, DType::F32});
+    const auto regions = t.space(args);
+    test::require(regions.size() == 1 && regions[0].start.values[1] == MFR_STAGE_ALWAYS,
+                  "a large misaligned product starts staged");
+    // Nothing to compute: nothing to tune.
+    OpArgs empty;
+    empty.inputs = {Tensor::zeros({0, k}, DType::F32, device), Tensor::zeros({k, n}, DType::F32, device)};
+    empty.outputs = {Tensor::empty({0, n}, DType::F32, device)};
+    test::require(t.space(empty).empty(), "an empty product has no space");
+}
+
+} // namespace
+
+int main(int argc, char** argv) {
+    return test::run("tuning_test", argc, argv, [] {
+        test::register_oracle_cpu_kernels();
+        bool rocm = false;
+        for (Device device : test::devices()) {
+            if (device.type != DeviceType::ROCm) {
+                continue;
+            }
+            rocm = true;
+            std::cout << "  gemm tunables on " << to_string(device) << '\n';
+            test_registration();
+            test_matmul(device);
+            test_gemm_fused(device);
+            test_batched(device);
+            test_start_is_the_automatic_choice(device);
+        }
+        if (!rocm) {
+            std::cout << "  no rocm device: the backend registers no tunables to check\n";
+        }
+    });
+}

@@ -227,6 +227,35 @@ def test_stage_modes_agree_bitwise(stream, oracle):
     assert_gemm_parity(got, oracle.gemm(x, w), magnitude(oracle, x, w), k, "staged 256x256")
 
 
+def test_plan_on_baseline_shapes(stream):
+    """mfr_sgemm_plan reports what AUTO runs: the 256x256 tile in place for configs[2], staged
+    operands for configs[3], a short-depth tile for the attention scores; a fixed 256x256 tile
+    with staging off is refused on operands 16-byte loads cannot read, and staged otherwise."""
+    abi = mf.abi
+    big = mf.DeviceArray.empty((4096, 4096), stream)
+    assert mf.gemm_plan(big, big.T, big) == (abi.TILE_256x256, abi.STAGE_NEVER)
+    x = mf.DeviceArray.empty((4093, 1023), stream)
+    w = mf.DeviceArray.empty((1023, 4099), stream)
+    out = mf.DeviceArray.empty((4093, 4099), stream)
+    tile, stage = mf.gemm_plan(x, w, out)
+    assert stage == abi.STAGE_ALWAYS and tile != abi.TILE_AUTO
+    assert mf.gemm_plan(x, w, out, stage=abi.STAGE_NEVER)[1] == abi.STAGE_NEVER
+    q = mf.DeviceArray.empty((128, 1024, 64), stream)
+    scores = mf.DeviceArray.empty((128, 1024, 1024), stream)
+    assert mf.gemm_plan(q, q.transpose(-2, -1), scores)[0] in (abi.TILE_128x64, abi.TILE_64x128)
+    with pytest.raises(NotImplementedError):
+        mf.gemm_plan(x, w, out, tile=abi.TILE_256x256, stage=abi.STAGE_NEVER)
+    assert mf.gemm_plan(x, w, out, tile=abi.TILE_256x256) == (abi.TILE_256x256, abi.STAGE_ALWAYS)
+    empty = mf.DeviceArray.empty((0, 4099), stream)
+    assert mf.gemm_plan(mf.DeviceArray.empty((0, 1023), stream), w, empty)[0] == abi.TILE_AUTO
+    # The fixed 256x256 tile on odd operands runs staged, bit-exact.
+    m, n, k = 130, 75, 67
+    a = quarter_matrix(m, k, 97)
+    b = quarter_matrix(k, n, 98)
+    got = mf.gemm(dev(a, stream), dev(b, stream), tile=abi.TILE_256x256).numpy()
+    assert same_bits(got, exact_product(a, b))
+
+
 def test_unknown_stage_mode_is_invalid(stream):
     a = dev(np.ones((4, 4), np.float32), stream)
     with pytest.raises(ValueError):
