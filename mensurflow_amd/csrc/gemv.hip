@@ -7,25 +7,28 @@
 // fused multiply-add in double rounds exactly like the reference's multiply-then-add; only the
 // order of the additions differs, and it is fixed, so every call gives the same bits.
 //
-// N form (y has `rows` entries): one wavefront owns kRowsPerWave (4) rows and walks them with
-// 16-byte loads, kUnrollN loads per row in flight per lane; each x chunk is read once for all 4
+// N form (y has `rows` entries): one wavefront owns kRowsPerWave (8) rows and walks them with
+// 16-byte loads, kUnrollN loads per row in flight per lane; each x chunk is read once for all 8
 // rows. The partial sums are reduced across the wavefront with shuffles. Every byte of A is read
-// once, coalesced. At 16384 rows this is 4096 wavefronts: one full round of the chip at 4
-// wavefronts per SIMD, so no tail of half-empty rounds.
+// once, coalesced. Workgroups of 2 wavefronts stream 16 consecutive rows; at 16384 rows that is
+// 1024 workgroups (4 per CU), one round of the chip. Measured against 4 rows per wavefront in
+// workgroups of 4: 6.89 vs 6.52 TB/s, the read rate of a plain contiguous stream (6.92 TB/s).
 //
-// T form (y has `cols` entries): a workgroup owns a strip of 256 columns (64 lanes x 4) and a
-// chunk of rows; its four wavefronts split the chunk's rows, each lane keeps 4 column sums, and
-// the wavefronts are added in LDS in a fixed order. The chunk's partial sums go to the stream's
-// workspace ([chunks][cols] doubles) and a second kernel adds the chunks in order. A is again
-// read once, coalesced along the rows.
+// T form (y has `cols` entries): a workgroup of one wavefront owns a strip of 256 columns
+// (64 lanes x 4) and a chunk of rows, walks the rows in order with kUnrollT rows in flight, and
+// each lane keeps 4 column sums. The chunk's partial sums go to the stream's workspace
+// ([chunks][cols] doubles) and a second kernel adds the chunks in order. A is again read once,
+// coalesced along the rows. At 16384^2: 64 strips x 32 chunks = 2048 wavefronts. Measured
+// against four wavefronts splitting each chunk's rows (exchanging sums in LDS) with 8 rows in
+// flight: 6.96 vs 6.44 TB/s.
 #include "common.hpp"
 
 namespace {
 
 using mfr::dev::kWave;
 
-constexpr int kRowsPerWave = 4;
-constexpr int kWavesPerBlockN = 4;
+constexpr int kRowsPerWave = 8;
+constexpr int kWavesPerBlockN = 2;
 constexpr int kUnrollN = 4;
 
 // The reference's final rounding: (float)(alpha * sum + (beta == 0 ? 0 : (double)(beta * y0))),
@@ -35,31 +38,26 @@ __device__ inline float finish(double sum, float alpha, float beta, const float*
     return static_cast<float>(static_cast<double>(alpha) * sum + tail);
 }
 
-// VEC4: rows start 16-byte aligned and cols % 4 == 0 (checked on the host).
-template <bool VEC4>
-__global__ __launch_bounds__(kWave* kWavesPerBlockN) void gemv_n_kernel(
-    const float* __restrict__ a, int64_t lda, const float* __restrict__ x, int64_t rows,
-    int64_t cols, float alpha, float beta, const float* __restrict__ y0, float* __restrict__ y) {
-    const int lane = threadIdx.x % kWave;
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlockN + threadIdx.x / kWave;
-    const int64_t row0 = wave * kRowsPerWave;
-    if (row0 >= rows) {
-        return;
-    }
-    const int nrows = rows - row0 < kRowsPerWave ? static_cast<int>(rows - row0) : kRowsPerWave;
-    double sum[kRowsPerWave];
+// Per-lane sums of rows row0 .. row0 + kRowsPerWave - 1 of A times x. FULL: all kRowsPerWave
+// rows exist, so they are lda apart from row0 and the compiler walks them from one base (that
+// schedule streams faster); otherwise rows past the end repeat the last valid row, and their sums
+// are never stored. VEC4: rows start 16-byte aligned and cols % 4 == 0 (checked on the host).
+template <bool VEC4, bool FULL>
+__device__ inline void gemv_n_rows(const float* __restrict__ a, int64_t lda,
+                                   const float* __restrict__ x, int64_t cols, int64_t row0,
+                                   int nrows, int lane, double (&sum)[kRowsPerWave]) {
     const float* arow[kRowsPerWave];
 #pragma unroll
     for (int r = 0; r < kRowsPerWave; ++r) {
         sum[r] = 0.0;
-        // Rows past the end repeat the last valid row; their sums are never stored.
-        arow[r] = a + (row0 + (r < nrows ? r : nrows - 1)) * lda;
+        arow[r] = a + (row0 + (FULL || r < nrows ? r : nrows - 1)) * lda;
     }
     if constexpr (VEC4) {
-        const int64_t quads = cols / 4;                 // float4 per row
+        const int64_t quads = cols / 4;                              // float4 per row
         const int64_t step = static_cast<int64_t>(kWave) * kUnrollN; // quads per iteration
+        const int64_t main_quads = quads / step * step;
         int64_t q = lane;
-        for (; q + (kUnrollN - 1) * kWave < quads; q += step) {
+        for (; q < main_quads; q += step) {
             float4 xv[kUnrollN];
             float4 av[kRowsPerWave][kUnrollN];
 #pragma unroll
@@ -102,6 +100,25 @@ __global__ __launch_bounds__(kWave* kWavesPerBlockN) void gemv_n_kernel(
             }
         }
     }
+}
+
+template <bool VEC4>
+__global__ __launch_bounds__(kWave* kWavesPerBlockN) void gemv_n_kernel(
+    const float* __restrict__ a, int64_t lda, const float* __restrict__ x, int64_t rows,
+    int64_t cols, float alpha, float beta, const float* __restrict__ y0, float* __restrict__ y) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlockN + threadIdx.x / kWave;
+    const int64_t row0 = wave * kRowsPerWave;
+    if (row0 >= rows) {
+        return;
+    }
+    const int nrows = rows - row0 < kRowsPerWave ? static_cast<int>(rows - row0) : kRowsPerWave;
+    double sum[kRowsPerWave];
+    if (nrows == kRowsPerWave) {
+        gemv_n_rows<VEC4, true>(a, lda, x, cols, row0, nrows, lane, sum);
+    } else {
+        gemv_n_rows<VEC4, false>(a, lda, x, cols, row0, nrows, lane, sum);
+    }
 #pragma unroll
     for (int r = 0; r < kRowsPerWave; ++r) {
         sum[r] = mfr::dev::wave_sum(sum[r]);
@@ -114,49 +131,66 @@ __global__ __launch_bounds__(kWave* kWavesPerBlockN) void gemv_n_kernel(
 }
 
 constexpr int kStripCols = 256; // columns per workgroup in the T form: 64 lanes x 4
-constexpr int kWavesPerBlockT = 4;
-constexpr int kUnrollT = 8;
+constexpr int kUnrollT = 16;
 
-// Partial sums of one (column strip, row chunk) tile of A^T x: out[chunk][col], in double.
-// VEC4: lda % 4 == 0, cols % 4 == 0 and A 16-byte aligned, so a lane's 4 columns are one float4.
+// Partial sums of one (column strip, row chunk) tile of A^T x: out[chunk][col], in double; one
+// wavefront, rows in increasing order. VEC4: lda % 4 == 0, cols % 4 == 0 and A 16-byte aligned,
+// so a lane's 4 columns are one float4; otherwise its columns are 64 apart.
 template <bool VEC4>
-__global__ __launch_bounds__(kWave* kWavesPerBlockT) void gemv_t_partial_kernel(
+__global__ __launch_bounds__(kWave) void gemv_t_partial_kernel(
     const float* __restrict__ a, int64_t lda, const float* __restrict__ x, int64_t rows,
     int64_t cols, int64_t rows_per_chunk, double* __restrict__ partial) {
-    __shared__ double exchange[kWavesPerBlockT - 1][kStripCols];
-    const int lane = threadIdx.x % kWave;
-    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x;
     const int64_t strip = blockIdx.x;
     const int64_t chunk = blockIdx.y;
     const int64_t r_begin = chunk * rows_per_chunk;
     const int64_t r_end = r_begin + rows_per_chunk < rows ? r_begin + rows_per_chunk : rows;
     // Column of component c of this lane: VEC4 -> 4 adjacent columns, else 4 columns 64 apart.
-    const int64_t col_base = strip * kStripCols + (VEC4 ? 4 * lane : lane);
+    auto local_col = [&](int c) { return VEC4 ? 4 * lane + c : lane + c * kWave; };
+    const int64_t col_base = strip * kStripCols + local_col(0);
     double sum[4] = {0.0, 0.0, 0.0, 0.0};
     if constexpr (VEC4) {
         const bool active = col_base < cols;
-        int64_t r = r_begin + wave;
-        const int64_t row_step = kWavesPerBlockT;
-        for (; r + (kUnrollT - 1) * row_step < r_end; r += kUnrollT * row_step) {
-            float4 av[kUnrollT];
+        // A strip wholly inside the matrix (all but possibly the last) loads unconditionally;
+        // the condition is uniform across the wavefront.
+        const bool full_strip = (strip + 1) * kStripCols <= cols;
+        int64_t r = r_begin;
+        if (full_strip && r + kUnrollT <= r_end) {
+            // x[r .. r+15] is the same for every lane (a scalar load); it is fetched one
+            // iteration ahead (index clamped to the last row) so its latency overlaps the
+            // current iteration instead of stalling the stream of A loads.
             float xr[kUnrollT];
 #pragma unroll
             for (int u = 0; u < kUnrollT; ++u) {
-                const int64_t row = r + u * row_step;
-                xr[u] = x[row];
-                av[u] = active ? mfr::dev::load_streaming(a + row * lda + col_base)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
+                xr[u] = x[r + u];
             }
+            for (; r + kUnrollT <= r_end; r += kUnrollT) {
+                float4 av[kUnrollT];
 #pragma unroll
-            for (int u = 0; u < kUnrollT; ++u) {
-                const double xv = static_cast<double>(xr[u]);
-                sum[0] = fma(static_cast<double>(av[u].x), xv, sum[0]);
-                sum[1] = fma(static_cast<double>(av[u].y), xv, sum[1]);
-                sum[2] = fma(static_cast<double>(av[u].z), xv, sum[2]);
-                sum[3] = fma(static_cast<double>(av[u].w), xv, sum[3]);
+                for (int u = 0; u < kUnrollT; ++u) {
+                    av[u] = mfr::dev::load_streaming(a + (r + u) * lda + col_base);
+                }
+                float xn[kUnrollT];
+#pragma unroll
+                for (int u = 0; u < kUnrollT; ++u) {
+                    const int64_t next = r + kUnrollT + u;
+                    xn[u] = x[next < rows ? next : rows - 1];
+                }
+#pragma unroll
+                for (int u = 0; u < kUnrollT; ++u) {
+                    const double xv = static_cast<double>(xr[u]);
+                    sum[0] = fma(static_cast<double>(av[u].x), xv, sum[0]);
+                    sum[1] = fma(static_cast<double>(av[u].y), xv, sum[1]);
+                    sum[2] = fma(static_cast<double>(av[u].z), xv, sum[2]);
+                    sum[3] = fma(static_cast<double>(av[u].w), xv, sum[3]);
+                }
+#pragma unroll
+                for (int u = 0; u < kUnrollT; ++u) {
+                    xr[u] = xn[u];
+                }
             }
         }
-        for (; r < r_end; r += row_step) {
+        for (; r < r_end; ++r) {
             const double xv = static_cast<double>(x[r]);
             if (active) {
                 const float4 av = *reinterpret_cast<const float4*>(a + r * lda + col_base);
@@ -167,39 +201,23 @@ __global__ __launch_bounds__(kWave* kWavesPerBlockT) void gemv_t_partial_kernel(
             }
         }
     } else {
-        for (int64_t r = r_begin + wave; r < r_end; r += kWavesPerBlockT) {
+        for (int64_t r = r_begin; r < r_end; ++r) {
             const double xv = static_cast<double>(x[r]);
             const float* row = a + r * lda;
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const int64_t col = col_base + c * kWave;
+                const int64_t col = strip * kStripCols + local_col(c);
                 if (col < cols) {
                     sum[c] = fma(static_cast<double>(row[col]), xv, sum[c]);
                 }
             }
         }
     }
-    // Wavefronts 1..3 hand their sums to wavefront 0, which adds them in order 0, 1, 2, 3.
-    auto local_col = [&](int c) { return VEC4 ? 4 * lane + c : lane + c * kWave; };
-    if (wave > 0) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            exchange[wave - 1][local_col(c)] = sum[c];
-        }
-    }
-    __syncthreads();
-    if (wave == 0) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            double total = sum[c];
-#pragma unroll
-            for (int w = 0; w < kWavesPerBlockT - 1; ++w) {
-                total += exchange[w][local_col(c)];
-            }
-            const int64_t col = strip * kStripCols + local_col(c);
-            if (col < cols) {
-                partial[chunk * cols + col] = total;
-            }
+    for (int c = 0; c < 4; ++c) {
+        const int64_t col = strip * kStripCols + local_col(c);
+        if (col < cols) {
+            partial[chunk * cols + col] = sum[c];
         }
     }
 }
@@ -219,18 +237,17 @@ __global__ void gemv_t_finish_kernel(const double* __restrict__ partial, int64_t
     y[j] = finish(sum, alpha, beta, y0, j);
 }
 
-// Rows per chunk of the T form: enough (strip, chunk) tiles to cover the chip several times
-// (256 CUs), each chunk a multiple of the unrolled row step, at least 64 rows.
+// Rows per chunk of the T form: about 2048 (strip, chunk) wavefronts (2 per SIMD of 256 CUs,
+// each with kUnrollT rows in flight), each chunk a multiple of the unrolled row step and at least
+// 64 rows.
 int64_t t_rows_per_chunk(int64_t rows, int64_t strips) {
-    // 1024 workgroups of 4 wavefronts: one full round of 256 CUs x 4 SIMDs x 4 wavefronts.
-    const int64_t target_tiles = 1024;
+    const int64_t target_tiles = 2048;
     int64_t chunks = (target_tiles + strips - 1) / strips;
     if (chunks < 1) {
         chunks = 1;
     }
     int64_t per = (rows + chunks - 1) / chunks;
-    const int64_t step = static_cast<int64_t>(kWavesPerBlockT) * kUnrollT;
-    per = (per + step - 1) / step * step;
+    per = (per + kUnrollT - 1) / kUnrollT * kUnrollT;
     return per < 64 ? 64 : per;
 }
 
@@ -273,10 +290,10 @@ void launch_gemv(mfr_stream& s, bool trans, int64_t rows, int64_t cols, float al
             s.reserve(static_cast<size_t>(chunks) * static_cast<size_t>(cols) * sizeof(double)));
         const dim3 grid(static_cast<unsigned>(strips), static_cast<unsigned>(chunks));
         if (vec4) {
-            gemv_t_partial_kernel<true><<<grid, kWave * kWavesPerBlockT, 0, s.stream>>>(
+            gemv_t_partial_kernel<true><<<grid, kWave, 0, s.stream>>>(
                 a, lda, x, rows, cols, per, partial);
         } else {
-            gemv_t_partial_kernel<false><<<grid, kWave * kWavesPerBlockT, 0, s.stream>>>(
+            gemv_t_partial_kernel<false><<<grid, kWave, 0, s.stream>>>(
                 a, lda, x, rows, cols, per, partial);
         }
         mfr::check_launch("gemv_t_partial_kernel");

@@ -54,8 +54,12 @@ def test_config2_full_size(stream, oracle, trans):
     assert same > 0.999
 
 
+# 16-byte paths too (cols % 4 == 0): a partial last 256-column strip of the T form, row counts
+# around its 16-row step and chunking, and a partial last group of 8 rows in the N form.
 @pytest.mark.parametrize("rows,cols", [(1, 1), (1, 1000), (1000, 1), (37, 53), (255, 257),
-                                       (513, 4099), (4093, 130), (3, 70000)])
+                                       (513, 4099), (4093, 130), (3, 70000), (1029, 1024),
+                                       (300, 260), (2050, 772), (17, 4096), (5, 4096),
+                                       (4111, 516)])
 @pytest.mark.parametrize("trans", [False, True])
 def test_exact_shapes(stream, oracle, rows, cols, trans):
     a = quarter_matrix(rows, cols, rows + cols)
