@@ -8,9 +8,12 @@ A step is one call of the hot path on inputs already resident in HBM:
   * gemv: configs[1] -- y = 2 * op(A) * x + 0.5 * y0 with A [16384, 16384], for A and A^T.
 Inputs are synthetic (seeded numpy uniform[-1,1] / N(0,1)), as the configs describe.
 
-Timing: W untimed warmup steps, then K steps bracketed by stream synchronisation; the
-per-launch duration of the dominant kernel comes from HIP events recorded on the stream the
-kernel runs on. The CPU baseline (rank 0, N=1 only) times the reference's own packed
+Timing: W untimed warmup steps (continued until at least MIN_WARMUP_MS of GPU work has run,
+because every leg starts after host-side setup with the GPU idle, and the first ~10 ms after
+idle run slower while the clocks ramp: the MLP leg measured 446 us per call over its first 20
+calls and 377 us after), then K steps bracketed by stream synchronisation; the per-launch
+duration of the dominant kernel comes from HIP events recorded on the stream the kernel runs
+on. The CPU baseline (rank 0, N=1 only) times the reference's own packed
 AVX2/OpenMP GEMM (oracle/_ref, compiled from the reference sources) on a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
@@ -31,6 +34,7 @@ sys.path.insert(0, ROOT)
 METRIC = "fp32 GEMM TFLOP/s at 4096^3 (% MFMA peak); gemv HBM GB/s (% peak)"
 PEAK_FP32_MFMA_TFLOPS = 157.3   # MI355X dense fp32 matrix peak (AMD published)
 PEAK_HBM_GBS = 8000.0           # MI355X HBM3E peak (AMD published)
+MIN_WARMUP_MS = 50.0            # warm-up per leg, at least (see the module docstring)
 GEMM_N = 4096
 GEMV_N = 16384
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
@@ -53,8 +57,17 @@ def load_traffic(kernel: str):
 
 
 def time_launches(mf, stream, launch, steps: int, warmup: int):
-    """(ms per step from host-synchronised wall clock, ms per step from HIP events)."""
-    for _ in range(warmup):
+    """(ms per step from host-synchronised wall clock, ms per step from HIP events), after
+    `warmup` untimed steps and then more until MIN_WARMUP_MS of them have run."""
+    t0 = time.perf_counter()
+    done = 0
+    while done < max(warmup, 1):
+        launch()
+        done += 1
+    stream.synchronize()
+    per_call = (time.perf_counter() - t0) * 1e3 / done
+    extra = int(max(0.0, MIN_WARMUP_MS - per_call * done) / max(per_call, 1e-3))
+    for _ in range(extra):
         launch()
     stream.synchronize()
     start, end = mf.Event(), mf.Event()
