@@ -8,7 +8,7 @@ import pytest
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CPP = os.path.join(HERE, "cpp")
-TESTS = ["core_test", "blas_test", "attention_test", "tuning_test"]
+TESTS = ["core_test", "blas_test", "attention_test", "tuning_test", "reference_cases_test"]
 
 
 def binary(name):
