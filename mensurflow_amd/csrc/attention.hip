@@ -3,7 +3,7 @@
 // [.., lq, lk] scores to memory; the reference composes the same op from a batched GEMM, where(),
 // softmax and a second batched GEMM (src/ops/attention.cpp:48-98).
 //
-// Design (a workgroup of 4 wavefronts, 32 queries each; keys in blocks of BK):
+// Design (a workgroup of 8 wavefronts for d = 64, else 4, 32 queries each; keys in blocks of BK):
 //   - Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x2_f32: the accumulator
 //     of a 32-key x 32-query block puts one query in each lane column (lanes l and l+32 hold
 //     query l % 32, 16 keys each). Every per-query quantity of the softmax (running maximum,
@@ -31,9 +31,12 @@ namespace {
 using mfr::gemm::floatx16;
 using mfr::gemm::SliceLoader;
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
-constexpr int kBlockQ = kWaves * 32; // queries per workgroup
+constexpr int kWaves = 4; // wavefronts of 32 queries per workgroup, by default
+
+// Wavefronts per workgroup by head size: 8 for d = 64, where one K/V tile then serves 256
+// queries (configs[4]: 189-191 us against 199-205 us with 4), 4 otherwise (d = 32 measured
+// slower with 8; d = 128 needs its LDS for 4).
+constexpr int waves_for(int64_t d) { return d == 64 ? 8 : kWaves; }
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnParams {
@@ -62,18 +65,23 @@ __device__ inline float weight(float x, float m) {
 }
 
 // MASKED: a mask tensor is given (read for every score). Without it only the key count and the
-// causal diagonal remove scores, and only blocks that reach past either are checked.
-template <int D, int BK, bool MASKED>
-__global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnParams p) {
+// causal diagonal remove scores, and only blocks that reach past either are checked. WAVES
+// wavefronts of 32 queries per workgroup; MIN_WAVES is the occupancy the compiler must allow
+// (wavefronts per SIMD).
+template <int D, int BK, bool MASKED, int WAVES = kWaves, int MIN_WAVES = 2>
+__global__ __launch_bounds__(WAVES * 64, MIN_WAVES) void attention_kernel(AttnParams p) {
+    constexpr int THREADS = WAVES * 64;
+    constexpr int BLOCK_Q = WAVES * 32;
     constexpr int SUB = BK / 32; // 32-key sub-blocks per key block
     constexpr int DB = D / 32;   // 32-wide output column blocks
     constexpr int G = D / 8;     // depth groups of q . k
     constexpr int kStagePitch = D + 4;
-    using LoadK = SliceLoader<BK, D, true, 4, kThreads>;  // rows = keys, depth = d
-    using LoadV = SliceLoader<D, BK, false, 4, kThreads>; // rows = d, depth = keys
-    __shared__ float smem[2 * (LoadK::kFloats + LoadV::kFloats)];
-    static_assert(kWaves * 32 * kStagePitch <= 2 * (LoadK::kFloats + LoadV::kFloats),
-                  "output staging must fit in the tile buffers");
+    using LoadK = SliceLoader<BK, D, true, 4, THREADS>;  // rows = keys, depth = d
+    using LoadV = SliceLoader<D, BK, false, 4, THREADS>; // rows = d, depth = keys
+    // Double-buffered K and V tiles; after the key loop the same memory stages the output.
+    constexpr int kTileFloats = 2 * (LoadK::kFloats + LoadV::kFloats);
+    constexpr int kStageFloats = WAVES * 32 * kStagePitch;
+    __shared__ float smem[kTileFloats > kStageFloats ? kTileFloats : kStageFloats];
     auto lds_k = [&](int which) { return smem + which * LoadK::kFloats; };
     auto lds_v = [&](int which) { return smem + 2 * LoadK::kFloats + which * LoadV::kFloats; };
 
@@ -98,7 +106,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / 64));
     const int half = lane / 32;
     const int r32 = lane % 32;
-    const int64_t q0 = qb * kBlockQ;
+    const int64_t q0 = qb * BLOCK_Q;
     const int64_t wq0 = q0 + wave * 32; // first query of this wavefront
     const int64_t query = wq0 + r32;    // this lane's query
     const bool wave_live = wq0 < p.lq;
@@ -127,7 +135,7 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnParams p) {
     // Keys this workgroup needs: all of them, or (causal) up to its last query.
     int64_t k_end = p.lk;
     if (p.causal) {
-        const int64_t last_query = (q0 + kBlockQ < p.lq ? q0 + kBlockQ : p.lq) - 1;
+        const int64_t last_query = (q0 + BLOCK_Q < p.lq ? q0 + BLOCK_Q : p.lq) - 1;
         k_end = last_query + 1 < k_end ? last_query + 1 : k_end;
     }
     const int64_t blocks = (k_end + BK - 1) / BK;
@@ -331,13 +339,14 @@ __global__ __launch_bounds__(kThreads, 2) void attention_kernel(AttnParams p) {
 template <bool MASKED> void launch(int64_t d, const AttnParams& p, unsigned grid, hipStream_t st) {
     switch (d) {
     case 32:
-        attention_kernel<32, 64, MASKED><<<grid, kThreads, 0, st>>>(p);
+        attention_kernel<32, 64, MASKED, waves_for(32)><<<grid, waves_for(32) * 64, 0, st>>>(p);
         break;
     case 64:
-        attention_kernel<64, 64, MASKED><<<grid, kThreads, 0, st>>>(p);
+        attention_kernel<64, 64, MASKED, waves_for(64)><<<grid, waves_for(64) * 64, 0, st>>>(p);
         break;
     default:
-        attention_kernel<128, 32, MASKED><<<grid, kThreads, 0, st>>>(p);
+        attention_kernel<128, 32, MASKED, waves_for(128)><<<grid, waves_for(128) * 64, 0, st>>>(
+            p);
         break;
     }
 }
@@ -409,7 +418,8 @@ void run_attention(mfr_stream& s, const mfr_attention_desc& d) {
     p.causal = d.causal != 0;
     p.scale = d.scale != 0.0f ? d.scale
                               : static_cast<float>(1.0 / std::sqrt(static_cast<double>(d.d)));
-    const int64_t q_blocks = (d.lq + kBlockQ - 1) / kBlockQ;
+    const int64_t block_q = 32 * waves_for(d.d); // queries per workgroup
+    const int64_t q_blocks = (d.lq + block_q - 1) / block_q;
     const int64_t blocks = q_blocks * batch_count;
     require(blocks < (int64_t{1} << 31), "attention: problem too large for one launch");
     p.q_blocks = static_cast<int32_t>(q_blocks);
