@@ -153,151 +153,163 @@ __global__ __launch_bounds__(WAVES * 64, MIN_WAVES) void attention_kernel(AttnPa
 
     const float* k_base = p.k + off_k;
     const float* v_base = p.v + off_v;
-    LoadK lk_;
-    LoadV lv_;
-    if (blocks > 0) {
-        const int keys = p.lk < BK ? static_cast<int>(p.lk) : BK;
-        lk_.load(k_base, p.k_rs, 1, keys, D);
-        lv_.load(v_base, 1, p.v_rs, D, keys);
-        lk_.store(lds_k(0));
-        lv_.store(lds_v(0));
-        __syncthreads();
-    }
-    for (int64_t kb = 0; kb < blocks; ++kb) {
-        const int cur = static_cast<int>(kb & 1);
-        const bool more = kb + 1 < blocks;
-        const int64_t k0 = kb * BK;
-        if (more) {
-            const int64_t left = p.lk - (k0 + BK);
-            const int keys = left < BK ? static_cast<int>(left) : BK;
-            lk_.load(k_base + (k0 + BK) * p.k_rs, p.k_rs, 1, keys, D);
-            lv_.load(v_base + (k0 + BK) * p.v_rs, 1, p.v_rs, D, keys);
-        }
-        const float* sk = lds_k(cur);
-        const float* sv = lds_v(cur);
 
-        // Whether this wavefront needs the block at all (uniform across the wavefront): causal
-        // attention skips blocks lying wholly above its queries' diagonal. Inside, every MFMA
-        // runs unconditionally (masking removes what is not wanted), which keeps the
-        // accumulators in place.
-        if (wave_live && (!p.causal || k0 <= wq0 + 31)) {
-            // ---- S^T = K Q^T, the sub-blocks' accumulator chains interleaved ----
-            floatx16 sacc[SUB];
+    // Keys of block `blk` inside the matrix, and whether this wavefront needs the block at all
+    // (uniform across the wavefront: causal attention skips blocks lying wholly above its
+    // queries' diagonal). Inside a needed block every MFMA runs unconditionally (masking removes
+    // what is not wanted), which keeps the accumulators in place.
+    auto keys_in = [&](int64_t blk) {
+        const int64_t left = p.lk - blk * BK;
+        return left < BK ? static_cast<int>(left) : BK;
+    };
+    auto needed = [&](int64_t blk) { return wave_live && (!p.causal || blk * BK <= wq0 + 31); };
+
+    // ---- S^T = K Q^T for one block, the sub-blocks' accumulator chains interleaved ----
+    auto scores = [&](const float* sk, floatx16(&sacc)[SUB]) {
+#pragma unroll
+        for (int sb = 0; sb < SUB; ++sb) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                sacc[sb][e] = 0.0f;
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float kf[SUB][4];
+#pragma unroll
+            for (int sb = 0; sb < SUB; ++sb) {
+                LoadK::fragment(sk, 32 * sb + r32, g, half, kf[sb]);
+            }
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+#pragma unroll
+                for (int sb = 0; sb < SUB; ++sb) {
+                    sacc[sb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[sb][st], qf[g][st],
+                                                                     sacc[sb], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // ---- scale, mask and the online softmax of the block starting at key k0: sacc becomes
+    //      the weights exp(s - m) (per lane: query `query`, 16 keys per sub-block) ----
+    auto softmax = [&](int64_t k0, floatx16(&sacc)[SUB]) {
+        // Key of element e of sub-block sb, relative to k0: 32*sb + 8*(e/4) + e%4 + 4*half.
+        // A block needs checking when it reaches past the last key or (causal) past the
+        // wavefront's first query; both tests are uniform across the wavefront.
+        const bool edge = k0 + BK > p.lk || (p.causal && k0 + BK - 1 > wq0);
+        if (MASKED || edge) {
+            const int64_t keys_left = p.lk - k0;
+            const int64_t diag = query - k0; // causal keeps relative keys <= diag
+            const int lim_k = static_cast<int>(keys_left < BK ? keys_left : BK) - 4 * half;
+            const int lim_q = static_cast<int>(!p.causal || diag >= BK ? BK
+                                               : diag < -1 ? -1
+                                                           : diag) -
+                              4 * half;
 #pragma unroll
             for (int sb = 0; sb < SUB; ++sb) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    sacc[sb][e] = 0.0f;
+                    const int rel = 32 * sb + 8 * (e / 4) + e % 4; // minus 4*half (above)
+                    bool keep = rel < lim_k && rel <= lim_q;
+                    if constexpr (MASKED) {
+                        if (keep) {
+                            keep = mask_row[(k0 + rel + 4 * half) * p.mask_cs] != 0;
+                        }
+                    }
+                    sacc[sb][e] = keep ? p.scale * sacc[sb][e] : -INFINITY;
                 }
             }
+        } else {
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float kf[SUB][4];
+            for (int sb = 0; sb < SUB; ++sb) {
 #pragma unroll
-                for (int sb = 0; sb < SUB; ++sb) {
-                    LoadK::fragment(sk, 32 * sb + r32, g, half, kf[sb]);
+                for (int e = 0; e < 16; ++e) {
+                    sacc[sb][e] = p.scale * sacc[sb][e];
+                }
+            }
+        }
+        float block_max = -INFINITY;
+#pragma unroll
+        for (int sb = 0; sb < SUB; ++sb) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                block_max = fmaxf(block_max, sacc[sb][e]);
+            }
+        }
+        block_max = fmaxf(block_max, __shfl_xor(block_max, 32, 64));
+        const float m_new = fmaxf(m_run, block_max);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float rescale = weight(m_run, m_use); // exactly 1 where the maximum stayed
+        m_run = m_new;
+        l_run *= rescale;
+#pragma unroll
+        for (int b = 0; b < DB; ++b) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                oacc[b][e] *= rescale;
+            }
+        }
+#pragma unroll
+        for (int sb = 0; sb < SUB; ++sb) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float w = weight(sacc[sb][e], m_use);
+                sacc[sb][e] = w;
+                l_run += w;
+            }
+        }
+    };
+
+    // ---- O^T += V^T P^T: P^T's fragments are the S^T accumulators themselves ----
+    auto accumulate = [&](const float* sv, const floatx16(&sacc)[SUB]) {
+#pragma unroll
+        for (int sb = 0; sb < SUB; ++sb) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                float vf[DB][4];
+#pragma unroll
+                for (int b = 0; b < DB; ++b) {
+                    LoadV::fragment(sv, 32 * b + r32, 4 * sb + g, half, vf[b]);
                 }
 #pragma unroll
                 for (int st = 0; st < 4; ++st) {
 #pragma unroll
-                    for (int sb = 0; sb < SUB; ++sb) {
-                        sacc[sb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[sb][st], qf[g][st],
-                                                                         sacc[sb], 0, 0, 0);
-                    }
-                }
-            }
-
-            // ---- scale and mask (per lane: query `query`, 16 keys per sub-block) ----
-            // Key of element e of sub-block sb, relative to k0: 32*sb + 8*(e/4) + e%4 + 4*half.
-            // A block needs checking when it reaches past the last key or (causal) past the
-            // wavefront's first query; both tests are uniform across the wavefront.
-            const bool edge = k0 + BK > p.lk || (p.causal && k0 + BK - 1 > wq0);
-            if (MASKED || edge) {
-                const int64_t keys_left = p.lk - k0;
-                const int64_t diag = query - k0; // causal keeps relative keys <= diag
-                const int lim_k = static_cast<int>(keys_left < BK ? keys_left : BK) - 4 * half;
-                const int lim_q = static_cast<int>(!p.causal || diag >= BK ? BK
-                                                   : diag < -1 ? -1
-                                                               : diag) -
-                                  4 * half;
-#pragma unroll
-                for (int sb = 0; sb < SUB; ++sb) {
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        const int rel = 32 * sb + 8 * (e / 4) + e % 4; // minus 4*half (above)
-                        bool keep = rel < lim_k && rel <= lim_q;
-                        if constexpr (MASKED) {
-                            if (keep) {
-                                keep = mask_row[(k0 + rel + 4 * half) * p.mask_cs] != 0;
-                            }
-                        }
-                        sacc[sb][e] = keep ? p.scale * sacc[sb][e] : -INFINITY;
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int sb = 0; sb < SUB; ++sb) {
-#pragma unroll
-                    for (int e = 0; e < 16; ++e) {
-                        sacc[sb][e] = p.scale * sacc[sb][e];
-                    }
-                }
-            }
-
-            // ---- online softmax: running maximum, rescale, weights ----
-            float block_max = -INFINITY;
-#pragma unroll
-            for (int sb = 0; sb < SUB; ++sb) {
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    block_max = fmaxf(block_max, sacc[sb][e]);
-                }
-            }
-            block_max = fmaxf(block_max, __shfl_xor(block_max, 32, 64));
-            const float m_new = fmaxf(m_run, block_max);
-            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-            const float rescale = weight(m_run, m_use); // exactly 1 where the maximum stayed
-            m_run = m_new;
-            l_run *= rescale;
-#pragma unroll
-            for (int b = 0; b < DB; ++b) {
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    oacc[b][e] *= rescale;
-                }
-            }
-#pragma unroll
-            for (int sb = 0; sb < SUB; ++sb) {
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const float w = weight(sacc[sb][e], m_use);
-                    sacc[sb][e] = w;
-                    l_run += w;
-                }
-            }
-
-            // ---- O^T += V^T P^T: P^T's fragments are the S^T accumulators themselves ----
-#pragma unroll
-            for (int sb = 0; sb < SUB; ++sb) {
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    float vf[DB][4];
-#pragma unroll
                     for (int b = 0; b < DB; ++b) {
-                        LoadV::fragment(sv, 32 * b + r32, 4 * sb + g, half, vf[b]);
-                    }
-#pragma unroll
-                    for (int st = 0; st < 4; ++st) {
-#pragma unroll
-                        for (int b = 0; b < DB; ++b) {
-                            oacc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                                vf[b][st], sacc[sb][4 * g + st], oacc[b], 0, 0, 0);
-                        }
+                        oacc[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                            vf[b][st], sacc[sb][4 * g + st], oacc[b], 0, 0, 0);
                     }
                 }
             }
         }
+    };
 
+    LoadK lk_;
+    LoadV lv_;
+    if (blocks > 0) {
+        lk_.load(k_base, p.k_rs, 1, keys_in(0), D);
+        lv_.load(v_base, 1, p.v_rs, D, keys_in(0));
+        lk_.store(lds_k(0));
+        lv_.store(lds_v(0));
+        __syncthreads();
+    }
+    // One barrier per block: the next block's tiles are loaded into registers while this one is
+    // computed, then written to the other buffers. (A software-pipelined form, K one block
+    // ahead so the next scores' MFMAs overlap this block's softmax, gave the same bits but ran
+    // 198-202 us against 183-186 us at configs[4].)
+    for (int64_t kb = 0; kb < blocks; ++kb) {
+        const int cur = static_cast<int>(kb & 1);
+        const bool more = kb + 1 < blocks;
+        if (more) {
+            lk_.load(k_base + (kb + 1) * BK * p.k_rs, p.k_rs, 1, keys_in(kb + 1), D);
+            lv_.load(v_base + (kb + 1) * BK * p.v_rs, 1, p.v_rs, D, keys_in(kb + 1));
+        }
+        if (needed(kb)) {
+            floatx16 sacc[SUB];
+            scores(lds_k(cur), sacc);
+            softmax(kb * BK, sacc);
+            accumulate(lds_v(cur), sacc);
+        }
         if (more) {
             lk_.store(lds_k(cur ^ 1));
             lv_.store(lds_v(cur ^ 1));
