@@ -125,6 +125,21 @@ def test_strided_copy_views(stream, oracle):
                                                    (2, 3, 5, 5)).copy())
 
 
+@pytest.mark.parametrize("count", [4, 1000, 2048 * 4 + 4, 4096 * 2048 * 4 + 12, 3, 8191])
+def test_contiguous_copy_sizes(stream, count):
+    """The contiguous fast path (16-byte units, one chunk per workgroup): a single unit, tails
+    after the unrolled steps, more chunks than workgroups, and byte counts that are not
+    multiples of 16 (the runtime's copy); output between guard bands."""
+    src = np.arange(count, dtype=np.float32) * np.float32(0.5) - np.float32(7.0)
+    buf = mf.DeviceArray.empty((count + 64,), stream)
+    mf.fill(buf, 99.0)
+    out = buf.slice(0, 32, 32 + count)
+    mf.strided_copy(dev(src, stream), out=out)
+    host = buf.numpy()
+    assert same_bits(host[32:32 + count], src)
+    assert np.all(host[:32] == 99.0) and np.all(host[32 + count:] == 99.0)
+
+
 def test_fill(stream):
     buf = mf.DeviceArray.empty((1001,), stream)
     mf.fill(buf, -np.inf)
