@@ -179,9 +179,11 @@ class DeviceArray:
         return True
 
     def upload(self, host: np.ndarray) -> None:
-        assert self.is_contiguous(), "upload needs a contiguous view"
+        if not self.is_contiguous():
+            raise ValueError("upload needs a contiguous view")
         host = np.ascontiguousarray(host, dtype=self.dtype)
-        assert host.shape == self.shape, (host.shape, self.shape)
+        if host.shape != self.shape:
+            raise ValueError(f"upload: host shape {host.shape} differs from {self.shape}")
         abi.check(abi.load().mfr_memcpy_h2d(self.stream.handle, self.ptr, host.ctypes.data,
                                             host.nbytes), "mfr_memcpy_h2d")
 
@@ -217,13 +219,15 @@ class DeviceArray:
         return self.transpose(-2, -1)
 
     def view(self, shape) -> "DeviceArray":
-        assert self.is_contiguous()
+        if not self.is_contiguous():
+            raise ValueError("view: the array is not contiguous")
         shape = list(shape)
         if -1 in shape:
             i = shape.index(-1)
             rest = int(np.prod([s for j, s in enumerate(shape) if j != i], dtype=np.int64))
             shape[i] = self.size // rest
-        assert int(np.prod(shape, dtype=np.int64)) == self.size
+        if int(np.prod(shape, dtype=np.int64)) != self.size:
+            raise ValueError(f"view: cannot view {self.shape} as {tuple(shape)}")
         strides, step = [], 1
         for s in reversed(shape):
             strides.append(step)

@@ -133,6 +133,91 @@ __global__ __launch_bounds__(kCopyThreads) void copy16_kernel(const u32x4* __res
     }
 }
 
+// dst[i] = src[0] for i < n (a source whose strides are all 0): one load per thread, then
+// stores only.
+template <typename T>
+__global__ __launch_bounds__(256) void broadcast_kernel(const T* __restrict__ src,
+                                                        T* __restrict__ dst, int64_t n) {
+    const T value = src[0];
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += stride) {
+        dst[i] = value;
+    }
+}
+
+// A view whose last dimension has unit stride: `rows` rows of `row_units` units (elements, or
+// 16-byte groups of them when every row start and length allow it), row r of dst at
+// r * row_units, row r of src at the offset of index r in `outer` (the other dimensions, strides
+// in units). Each work item copies `chunk` units of one row, so the index is decomposed once per
+// item rather than per element.
+template <typename U>
+__global__ __launch_bounds__(256) void copy_rows_kernel(const U* __restrict__ src,
+                                                        U* __restrict__ dst, int64_t rows,
+                                                        int64_t row_units, int64_t chunks_per_row,
+                                                        int64_t chunk, CopyShape outer) {
+    const int64_t items = rows * chunks_per_row;
+    for (int64_t w = blockIdx.x; w < items; w += gridDim.x) {
+        const int64_t row = w / chunks_per_row;
+        const int64_t begin = (w - row * chunks_per_row) * chunk;
+        const int64_t end = begin + chunk < row_units ? begin + chunk : row_units;
+        int64_t rest = row;
+        int64_t offset = 0;
+        for (int d = outer.ndim - 1; d >= 0; --d) {
+            const int64_t index = rest % outer.shape[d];
+            rest /= outer.shape[d];
+            offset += index * outer.strides[d];
+        }
+        const U* in = src + offset;
+        U* out = dst + row * row_units;
+        for (int64_t j = begin + threadIdx.x; j < end; j += blockDim.x) {
+            out[j] = in[j];
+        }
+    }
+}
+
+template <typename T>
+void launch_copy_rows(const void* src, void* dst, const CopyShape& cs, int elem_size,
+                      hipStream_t stream) {
+    const int last = cs.ndim - 1;
+    const int64_t row_len = cs.shape[last];
+    CopyShape outer{};
+    outer.ndim = last;
+    int64_t rows = 1;
+    bool wide = mfr::aligned16(src) && mfr::aligned16(dst) && (row_len * elem_size) % 16 == 0;
+    for (int d = 0; d < last; ++d) {
+        outer.shape[d] = cs.shape[d];
+        outer.strides[d] = cs.strides[d];
+        rows *= cs.shape[d];
+        wide = wide && (cs.strides[d] * elem_size) % 16 == 0;
+    }
+    const int per = wide ? 16 / elem_size : 1; // elements per unit
+    for (int d = 0; d < last; ++d) {
+        outer.strides[d] /= per;
+    }
+    const int64_t row_units = row_len / per;
+    const int64_t chunk = 2048;
+    const int64_t chunks_per_row = (row_units + chunk - 1) / chunk;
+    const unsigned blocks = mfr::grid_blocks(rows * chunks_per_row, 1, 65536);
+    if (wide) {
+        copy_rows_kernel<<<blocks, 256, 0, stream>>>(static_cast<const u32x4*>(src),
+                                                     static_cast<u32x4*>(dst), rows, row_units,
+                                                     chunks_per_row, chunk, outer);
+    } else {
+        copy_rows_kernel<<<blocks, 256, 0, stream>>>(static_cast<const T*>(src),
+                                                     static_cast<T*>(dst), rows, row_units,
+                                                     chunks_per_row, chunk, outer);
+    }
+    mfr::check_launch("copy_rows_kernel");
+}
+
+template <typename T>
+void launch_broadcast(const void* src, void* dst, int64_t n, hipStream_t stream) {
+    broadcast_kernel<<<mfr::grid_blocks(n, 256 * 4, 8192), 256, 0, stream>>>(
+        static_cast<const T*>(src), static_cast<T*>(dst), n);
+    mfr::check_launch("broadcast_kernel");
+}
+
 // Drops size-1 dimensions and merges neighbours that are contiguous with each other
 // (stride[d] == shape[d+1] * stride[d+1]), so a packed view becomes one dimension of stride 1.
 void collapse(CopyShape& s) {
@@ -424,6 +509,42 @@ int mfr_strided_copy(mfr_stream_t stream, const void* src, void* dst, int32_t el
             } else {
                 check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s.stream),
                       "hipMemcpyAsync");
+            }
+            return;
+        }
+        if (cs.ndim == 1 && cs.strides[0] == 0) {
+            // One element repeated (a broadcast scalar, e.g. -inf expanded to a score tensor).
+            switch (elem_size) {
+            case 1:
+                launch_broadcast<uint8_t>(src, dst, n, s.stream);
+                break;
+            case 2:
+                launch_broadcast<uint16_t>(src, dst, n, s.stream);
+                break;
+            case 4:
+                launch_broadcast<uint32_t>(src, dst, n, s.stream);
+                break;
+            default:
+                launch_broadcast<uint64_t>(src, dst, n, s.stream);
+                break;
+            }
+            return;
+        }
+        if (cs.strides[cs.ndim - 1] == 1 && cs.shape[cs.ndim - 1] >= 64) {
+            // Rows with a unit stride (sliced, broadcast or strided outer dimensions).
+            switch (elem_size) {
+            case 1:
+                launch_copy_rows<uint8_t>(src, dst, cs, elem_size, s.stream);
+                break;
+            case 2:
+                launch_copy_rows<uint16_t>(src, dst, cs, elem_size, s.stream);
+                break;
+            case 4:
+                launch_copy_rows<uint32_t>(src, dst, cs, elem_size, s.stream);
+                break;
+            default:
+                launch_copy_rows<uint64_t>(src, dst, cs, elem_size, s.stream);
+                break;
             }
             return;
         }

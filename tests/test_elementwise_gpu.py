@@ -125,6 +125,30 @@ def test_strided_copy_views(stream, oracle):
                                                    (2, 3, 5, 5)).copy())
 
 
+def test_strided_copy_fast_paths(stream, oracle):
+    """The two fast paths of the strided copy, against numpy: a source whose strides are all 0
+    (a broadcast scalar), and rows with a unit stride, copied in 16-byte units when every row
+    start and length allow it (a slice of a 304-wide matrix, an expanded byte mask) and element
+    by element otherwise (odd strides and lengths, a middle broadcast dimension)."""
+    for value, dtype in ((3.5, np.float32), (7, np.uint8), (-2, np.int64)):
+        scalar = dev(np.array([value], dtype), stream)
+        got = scalar.view((1, 1)).expand((3, 1000)).numpy()
+        assert got.dtype == dtype and np.all(got == dtype(value))
+    base = uniform(oracle, (50, 304), -1.0, 1.0, 91, 0)
+    d = dev(base, stream)
+    assert same_bits(d.slice(1, 4, 260).numpy(), np.ascontiguousarray(base[:, 4:260]))
+    assert same_bits(d.slice(1, 3, 259).numpy(), np.ascontiguousarray(base[:, 3:259]))
+    mask = (np.arange(100 * 100).reshape(100, 100) % 3 == 0).astype(np.uint8)
+    expanded = dev(mask, stream).expand((2, 3, 100, 100)).numpy()
+    assert same_bits(expanded, np.broadcast_to(mask, (2, 3, 100, 100)).copy())
+    wide_bytes = (np.arange(7 * 2000) % 251).astype(np.uint8).reshape(7, 2000)
+    assert same_bits(dev(wide_bytes, stream).slice(1, 5, 1006).numpy(),
+                     np.ascontiguousarray(wide_bytes[:, 5:1006]))
+    x = uniform(oracle, (4, 1, 300), -1.0, 1.0, 92, 0)
+    assert same_bits(dev(x, stream).expand((4, 5, 300)).numpy(),
+                     np.broadcast_to(x, (4, 5, 300)).copy())
+
+
 @pytest.mark.parametrize("count", [4, 1000, 2048 * 4 + 4, 4096 * 2048 * 4 + 12, 3, 8191])
 def test_contiguous_copy_sizes(stream, count):
     """The contiguous fast path (16-byte units, one chunk per workgroup): a single unit, tails
