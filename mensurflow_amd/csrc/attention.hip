@@ -3,7 +3,7 @@
 // [.., lq, lk] scores to memory; the reference composes the same op from a batched GEMM, where(),
 // softmax and a second batched GEMM (src/ops/attention.cpp:48-98).
 //
-// Design (a workgroup of 8 wavefronts for d = 64, else 4, 32 queries each; keys in blocks of BK):
+// Design (a workgroup of 8 wavefronts, 4 for d = 32, 32 queries each; keys in blocks of BK):
 //   - Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x2_f32: the accumulator
 //     of a 32-key x 32-query block puts one query in each lane column (lanes l and l+32 hold
 //     query l % 32, 16 keys each). Every per-query quantity of the softmax (running maximum,
@@ -33,10 +33,10 @@ using mfr::gemm::SliceLoader;
 
 constexpr int kWaves = 4; // wavefronts of 32 queries per workgroup, by default
 
-// Wavefronts per workgroup by head size: 8 for d = 64, where one K/V tile then serves 256
-// queries (configs[4]: 189-191 us against 199-205 us with 4), 4 otherwise (d = 32 measured
-// slower with 8; d = 128 needs its LDS for 4).
-constexpr int waves_for(int64_t d) { return d == 64 ? 8 : kWaves; }
+// Wavefronts per workgroup by head size: 8 for d = 64 and 128, where one K/V tile then serves
+// 256 queries (8 x 16 x 1024, causal: d = 64 189-191 us against 199-205 us with 4; d = 128
+// 346 us against 373-376 us), 4 for d = 32 (109 us with 8 against 105 us).
+constexpr int waves_for(int64_t d) { return d == 32 ? kWaves : 8; }
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnParams {
@@ -351,7 +351,10 @@ __global__ __launch_bounds__(WAVES * 64, MIN_WAVES) void attention_kernel(AttnPa
 template <bool MASKED> void launch(int64_t d, const AttnParams& p, unsigned grid, hipStream_t st) {
     switch (d) {
     case 32:
-        attention_kernel<32, 64, MASKED, waves_for(32)><<<grid, waves_for(32) * 64, 0, st>>>(p);
+        // 3 wavefronts per SIMD where the registers allow it (148 VGPRs without a mask):
+        // 102.9 us against 105.3 us with 2.
+        attention_kernel<32, 64, MASKED, waves_for(32), MASKED ? 2 : 3>
+            <<<grid, waves_for(32) * 64, 0, st>>>(p);
         break;
     case 64:
         attention_kernel<64, 64, MASKED, waves_for(64)><<<grid, waves_for(64) * 64, 0, st>>>(p);
