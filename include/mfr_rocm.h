@@ -147,6 +147,8 @@ typedef struct mfr_gemm_desc {
     float alpha, beta;
     int32_t tile;                             /* MFR_TILE_AUTO or a fixed MFR_TILE_* */
     int32_t stage;                            /* MFR_STAGE_* */
+    int32_t splits;                           /* 0 = AUTO, or 1 .. MFR_MAX_SPLITS depth ranges */
+    int32_t reserved;                         /* must be 0 */
 } mfr_gemm_desc;
 
 /* Operand staging of mfr_sgemm. The fast loads read 4 floats at once, which needs an operand's
@@ -158,9 +160,11 @@ typedef struct mfr_gemm_desc {
  * either way. */
 enum { MFR_STAGE_AUTO = 0, MFR_STAGE_NEVER = 1, MFR_STAGE_ALWAYS = 2 };
 
-/* Workgroup tile of mfr_sgemm (rows x cols x depth slice). AUTO picks one from the shape: a cost
- * model of ceil(tiles / CUs) * tile area / measured efficiency, and the high-occupancy tiles for
- * a short depth. A fixed tile is what a tuner sets (the reference's TuningConfig,
+/* Workgroup tile of mfr_sgemm (rows x cols x depth slice). AUTO picks one from the shape (with
+ * the split count): a time model of the busiest CU's tiles (ceil(tiles / CUs) of them, each its
+ * area x (depth + a fixed per-tile overhead) at the tile's measured rate, slower when a SIMD holds
+ * fewer than 3 wavefronts), and the high-occupancy tiles for a depth <= 128. A fixed tile is what
+ * a tuner sets (the reference's TuningConfig,
  * src/core/dispatcher.hpp:145-149). Every tile gives the same results up to summation order. */
 enum {
     MFR_TILE_AUTO = 0,
@@ -172,16 +176,29 @@ enum {
     MFR_TILE_COUNT = 6
 };
 
+/* Split-K of mfr_sgemm. A product with few output tiles and a long depth (256 x 256 x 16384)
+ * would leave most compute units idle, so its depth may be cut into `splits` ranges (each a
+ * multiple of 32 deep; fewer ranges than asked when the depth is short): each range's raw sums go
+ * to the stream's workspace (splits * m * n * batch floats), and a second pass adds the ranges in
+ * order and applies the epilogue with the same roundings. AUTO picks the tile and the count
+ * together from a time model (no split when the output fills the device, ranges >= 256 deep,
+ * partial sums <= 1 GiB) and falls back to no split when the workspace cannot be had; a fixed
+ * count fails with MFR_E_RUNTIME then. Results are deterministic; the summation order, hence
+ * the rounding, depends on the count. */
+#define MFR_MAX_SPLITS 64
+
 int mfr_sgemm(mfr_stream_t stream, const mfr_gemm_desc* desc);
 
 /* What mfr_sgemm would run for desc on device `device`, without launching anything: the tile
- * (an MFR_TILE_* other than AUTO; AUTO when there is nothing to compute) and whether operands
- * are staged (MFR_STAGE_ALWAYS) or read in place (MFR_STAGE_NEVER). Validates desc as mfr_sgemm
+ * (an MFR_TILE_* other than AUTO; AUTO when there is nothing to compute), whether operands
+ * are staged (MFR_STAGE_ALWAYS) or read in place (MFR_STAGE_NEVER), and the depth ranges
+ * (1 = no split; 0 when there is nothing to compute). Validates desc as mfr_sgemm
  * does and fails with the same status where mfr_sgemm would (MFR_E_UNSUPPORTED for a fixed
  * 256x256 tile with staging off and operands 16-byte loads cannot read). For tuners: the default
  * a search starts from, and whether a (tile, stage) point can run (the reference's
  * TunableKernel::defaults / allowed, src/core/dispatcher.hpp:226-239). */
-int mfr_sgemm_plan(int device, const mfr_gemm_desc* desc, int32_t* tile, int32_t* stage);
+int mfr_sgemm_plan(int device, const mfr_gemm_desc* desc, int32_t* tile, int32_t* stage,
+                   int32_t* splits);
 
 /* Plain row-major convenience form: C[m,n] = alpha*op(A)*op(B) + beta*C0 with leading
  * dimensions lda/ldb/ldc (BLAS-style trans flags, row-major storage). c0 may be NULL. */

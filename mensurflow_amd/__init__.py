@@ -287,30 +287,32 @@ def _fill_batch(field, values, dims):
 
 def gemm_batched(a: DeviceArray, b: DeviceArray, c: DeviceArray, *, alpha=1.0,
                  c0: DeviceArray | None = None, beta=0.0, bias: DeviceArray | None = None,
-                 act=ACT_NONE, tile=0, stage=0) -> None:
+                 act=ACT_NONE, tile=0, stage=0, splits=0) -> None:
     """c[...] = act(alpha*a@b + beta*c0 + bias) over the leading (batch) dimensions.
 
     a is [..., m, k], b is [..., k, n] (any strides with a unit stride in one matrix dimension;
     batch strides may be 0), c and c0 are [..., m, n] with unit column stride. The batch shapes
     must already agree (expand them first). tile is an abi.TILE_* value, stage an abi.STAGE_*
-    value (copy operands that 16-byte loads cannot read into an aligned workspace first).
+    value (copy operands that 16-byte loads cannot read into an aligned workspace first), splits
+    the number of depth ranges (0 = automatic, 1 = none; split-K, abi.MAX_SPLITS at most).
     """
-    sgemm(c.stream, _gemm_desc(a, b, c, alpha, c0, beta, bias, act, tile, stage))
+    sgemm(c.stream, _gemm_desc(a, b, c, alpha, c0, beta, bias, act, tile, stage, splits))
 
 
-def gemm_plan(a: DeviceArray, b: DeviceArray, c: DeviceArray, *, tile=0, stage=0,
-              c0: DeviceArray | None = None, beta=0.0) -> tuple[int, int]:
-    """(tile, stage) that gemm_batched(a, b, c, ...) would run with (mfr_sgemm_plan): AUTO
-    resolved to a fixed tile, stage reported as STAGE_ALWAYS (operands copied first) or
-    STAGE_NEVER. Raises as gemm_batched would for a point that cannot run."""
-    d = _gemm_desc(a, b, c, 1.0, c0, beta, None, ACT_NONE, tile, stage)
-    t, st = ctypes.c_int32(), ctypes.c_int32()
+def gemm_plan(a: DeviceArray, b: DeviceArray, c: DeviceArray, *, tile=0, stage=0, splits=0,
+              c0: DeviceArray | None = None, beta=0.0) -> tuple[int, int, int]:
+    """(tile, stage, splits) that gemm_batched(a, b, c, ...) would run with (mfr_sgemm_plan):
+    AUTO resolved to a fixed tile, stage reported as STAGE_ALWAYS (operands copied first) or
+    STAGE_NEVER, splits the depth ranges (1 = no split). Raises as gemm_batched would for a point
+    that cannot run."""
+    d = _gemm_desc(a, b, c, 1.0, c0, beta, None, ACT_NONE, tile, stage, splits)
+    t, st, sp = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
     abi.check(abi.load().mfr_sgemm_plan(c.stream.device, ctypes.byref(d), ctypes.byref(t),
-                                        ctypes.byref(st)), "mfr_sgemm_plan")
-    return t.value, st.value
+                                        ctypes.byref(st), ctypes.byref(sp)), "mfr_sgemm_plan")
+    return t.value, st.value, sp.value
 
 
-def _gemm_desc(a, b, c, alpha, c0, beta, bias, act, tile, stage) -> GemmDesc:
+def _gemm_desc(a, b, c, alpha, c0, beta, bias, act, tile, stage, splits=0) -> GemmDesc:
     m, k = a.shape[-2:]
     k2, n = b.shape[-2:]
     if k != k2:
@@ -347,12 +349,13 @@ def _gemm_desc(a, b, c, alpha, c0, beta, bias, act, tile, stage) -> GemmDesc:
     d.beta = beta
     d.tile = tile
     d.stage = stage
+    d.splits = splits
     return d
 
 
 def gemm(a: DeviceArray, b: DeviceArray, *, alpha=1.0, c0: DeviceArray | None = None, beta=0.0,
          trans_a=False, trans_b=False, bias: DeviceArray | None = None, act=ACT_NONE,
-         out: DeviceArray | None = None, tile=0, stage=0) -> DeviceArray:
+         out: DeviceArray | None = None, tile=0, stage=0, splits=0) -> DeviceArray:
     """mensurflow::gemm's semantics (plus the fused bias/activation): a new [m, n] result."""
     left = a.T if trans_a else a
     right = b.T if trans_b else b
@@ -360,7 +363,7 @@ def gemm(a: DeviceArray, b: DeviceArray, *, alpha=1.0, c0: DeviceArray | None = 
     if out is None:
         out = DeviceArray.empty((m, n), a.stream)
     gemm_batched(left, right, out, alpha=alpha, c0=c0, beta=beta, bias=bias, act=act, tile=tile,
-                 stage=stage)
+                 stage=stage, splits=splits)
     return out
 
 

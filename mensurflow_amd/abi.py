@@ -37,6 +37,7 @@ TILE_COUNT = 6
 STAGE_AUTO = 0
 STAGE_NEVER = 1
 STAGE_ALWAYS = 2
+MAX_SPLITS = 64
 
 MAX_BATCH_DIMS = 4
 MAX_COPY_DIMS = 8
@@ -61,7 +62,7 @@ class GemmDesc(ctypes.Structure):
         ("c0", _vp), ("c0_rs", _i64), ("c0_bs", _i64 * MAX_BATCH_DIMS),
         ("bias", _vp),
         ("alpha", _f32), ("beta", _f32),
-        ("tile", _i32), ("stage", _i32),
+        ("tile", _i32), ("stage", _i32), ("splits", _i32), ("reserved", _i32),
     ]
 
 
@@ -106,7 +107,8 @@ SIGNATURES = {
     "mfr_event_elapsed_ms": (ctypes.c_int, [_vp, _vp, ctypes.POINTER(_f32)]),
     "mfr_sgemm": (ctypes.c_int, [_vp, ctypes.POINTER(GemmDesc)]),
     "mfr_sgemm_plan": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(GemmDesc),
-                                      ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
+                                      ctypes.POINTER(_i32), ctypes.POINTER(_i32),
+                                      ctypes.POINTER(_i32)]),
     "mfr_sgemm_rm": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _i64, _i64, _i64, _f32, _vp,
                                     _i64, _vp, _i64, _f32, _vp, _vp, _i64]),
     "mfr_sgemv": (ctypes.c_int, [_vp, ctypes.c_int, _i64, _i64, _f32, _vp, _i64, _vp, _f32, _vp,

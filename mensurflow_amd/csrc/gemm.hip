@@ -58,34 +58,172 @@ int64_t tile_count(int tile, int64_t m, int64_t n, int64_t batch) {
            ((n + kTiles[tile].bn - 1) / kTiles[tile].bn) * batch;
 }
 
-// The automatic tile. A short depth (K <= 128) is latency-bound per tile, so it takes the
-// high-occupancy 128x64 / 64x128 tiles (the one padding the output less). Otherwise the cost of a
-// tile is the work of the busiest CU, ceil(tiles / CUs) * tile area, at the tile's measured rate,
-// 15% slower when that CU runs fewer than 2 wavefronts per SIMD (nothing hides the latencies of
-// a lone wavefront). The 256x256 tile needs 16-byte loads on both operands.
-int choose_tile(int64_t m, int64_t n, int64_t k, int64_t batch, int cus, bool wide_loads) {
-    if (k <= 128) {
+// ---- split-K ------------------------------------------------------------------------------------
+//
+// A product with few output tiles and a long depth (256 x 256 x 16384) leaves most CUs idle. It
+// is cut along the depth into `splits` ranges, each range a workgroup of its own writing raw sums
+// to the workspace; split_reduce_kernel adds them in order and applies the epilogue.
+
+constexpr int kMaxSplits = MFR_MAX_SPLITS;
+constexpr int64_t kMinAutoDepth = 256;           // AUTO never cuts a range shorter than this
+constexpr double kMaxPartialBytes = 1073741824.0; // AUTO keeps the partial sums under 1 GiB
+constexpr double kReduceBytesPerUs = 4.0e6;       // split_reduce_kernel's HBM rate (bytes/us)
+constexpr double kReduceLaunchUs = 4.0;           // its launch and ramp
+// A tile's fixed cost (first slice's load latency, writing the tile out), in depth-equivalents
+// of its MFMA work, shared among the workgroups a CU runs at once. Fit to the measured times of
+// every tile and split count on 14 shapes (64^2 x 65536 .. 8192^2 x 1024): it is why a depth of
+// 256 on 4096^2 runs faster in 64x64 tiles (4 per CU) than in 256x256 ones (1 per CU).
+constexpr double kTileOverheadDepth = 192.0;
+
+// Depth of each range when `splits` are asked for: a multiple of 32, which every tile's depth
+// slice divides, so no range starts inside a slice.
+int64_t depth_per_split(int64_t k, int splits) {
+    const int64_t per = (k + splits - 1) / splits;
+    return (per + 31) / 32 * 32;
+}
+
+int splits_for(int64_t k, int64_t per) { return static_cast<int>((k + per - 1) / per); }
+
+// Relative rate of a CU by how many wavefronts each SIMD holds: one alone hides no latency.
+double simd_efficiency(int64_t waves_per_simd) {
+    return waves_per_simd >= 3 ? 1.0 : waves_per_simd == 2 ? 0.9 : 0.8;
+}
+
+// Modelled time (us) of tile t with `splits` depth ranges of `per` each: the busiest CU's share
+// of the tiles, each its depth plus the fixed overhead, at the tile's rate on 4096^3 (with the
+// overhead taken out), scaled by its wavefronts per SIMD relative to that measurement; plus the
+// reduce pass when split.
+double modelled_us(int t, int64_t m, int64_t n, int64_t k, int64_t batch, int cus, int splits,
+                   int64_t per, bool c0) {
+    const TileInfo& info = kTiles[t];
+    const int64_t per_cu = (tile_count(t, m, n, batch) * splits + cus - 1) / cus;
+    const int64_t concurrent = per_cu < info.occupancy ? per_cu : info.occupancy;
+    const int64_t reference_waves = (4096 / info.bm) * (4096 / info.bn) / 256;
+    const int64_t ref_concurrent =
+        reference_waves < info.occupancy ? reference_waves : info.occupancy;
+    const double efficiency = simd_efficiency(concurrent * info.waves / 4) /
+                              simd_efficiency(ref_concurrent * info.waves / 4);
+    const double depth = static_cast<double>(splits > 1 ? per : k);
+    const double overhead = kTileOverheadDepth / static_cast<double>(concurrent);
+    const double cu_flops_per_us = info.tflops * 1e6 / 256.0 *
+                                   (4096.0 + kTileOverheadDepth / ref_concurrent) / 4096.0;
+    double us = static_cast<double>(per_cu) * 2.0 * info.bm * info.bn * (depth + overhead) /
+                (cu_flops_per_us * efficiency);
+    if (splits > 1) {
+        const double outputs = static_cast<double>(m) * n * batch;
+        us += outputs * 4.0 * (2.0 * splits + (c0 ? 2.0 : 1.0)) / kReduceBytesPerUs +
+              kReduceLaunchUs;
+    }
+    return us;
+}
+
+struct Choice {
+    int tile = MFR_TILE_128x128;
+    int splits = 1;      // depth ranges
+    int64_t per = 0;     // depth of each (the last may be shorter); k when not split
+};
+
+// The automatic tile and split count (either may be fixed by the caller: tile != AUTO, splits !=
+// 0). A short depth (K <= 128) is latency-bound per tile, so it takes the high-occupancy 128x64 /
+// 64x128 tiles (the one padding the output less). Otherwise the pair with the least modelled
+// time. The 256x256 tile needs 16-byte loads on both operands.
+Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int cus, bool wide_loads,
+              int fixed_tile, int fixed_splits, bool c0) {
+    Choice best;
+    best.per = k;
+    if (fixed_splits > 0 && k > 0) {
+        best.per = depth_per_split(k, fixed_splits);
+        best.splits = splits_for(k, best.per);
+        if (best.splits == 1) {
+            best.per = k;
+        }
+    }
+    if (fixed_tile == MFR_TILE_AUTO && best.splits == 1 && k <= 128) {
         const int64_t a = tile_count(MFR_TILE_128x64, m, n, batch) * 128 * 64;
         const int64_t b = tile_count(MFR_TILE_64x128, m, n, batch) * 64 * 128;
-        return b < a ? MFR_TILE_64x128 : MFR_TILE_128x64;
+        best.tile = b < a ? MFR_TILE_64x128 : MFR_TILE_128x64;
+        return best;
     }
-    int best = MFR_TILE_128x128;
-    double best_cost = 1e300;
+    double best_us = 1e300;
     for (int t = 1; t < MFR_TILE_COUNT; ++t) {
-        if (t == MFR_TILE_256x256 && !wide_loads) {
+        if ((fixed_tile != MFR_TILE_AUTO && t != fixed_tile) ||
+            (fixed_tile == MFR_TILE_AUTO && t == MFR_TILE_256x256 && !wide_loads)) {
             continue;
         }
-        const int64_t per_cu = (tile_count(t, m, n, batch) + cus - 1) / cus;
-        const int64_t concurrent = per_cu < kTiles[t].occupancy ? per_cu : kTiles[t].occupancy;
-        const int64_t waves_per_simd = concurrent * kTiles[t].waves / 4;
-        const double cost = static_cast<double>(per_cu) * kTiles[t].bm * kTiles[t].bn /
-                            kTiles[t].tflops / (waves_per_simd >= 2 ? 1.0 : 0.85);
-        if (cost < best_cost) {
-            best_cost = cost;
-            best = t;
+        if (fixed_splits > 0) {
+            // Only the tile is open.
+            const double us = modelled_us(t, m, n, k, batch, cus, best.splits, best.per, c0);
+            if (us < best_us) {
+                best_us = us;
+                best.tile = t;
+            }
+            continue;
+        }
+        int prev = 0;
+        for (int want = 1; want <= kMaxSplits; ++want) {
+            const int64_t per = want == 1 || k == 0 ? k : depth_per_split(k, want);
+            const int splits = want == 1 || k == 0 ? 1 : splits_for(k, per);
+            if (splits == prev) {
+                continue;
+            }
+            prev = splits;
+            if (splits > 1 &&
+                (per < kMinAutoDepth ||
+                 4.0 * splits * static_cast<double>(m) * n * batch > kMaxPartialBytes)) {
+                break;
+            }
+            const double us = modelled_us(t, m, n, k, batch, cus, splits, per, c0);
+            if (us < best_us) {
+                best_us = us;
+                best.tile = t;
+                best.splits = splits;
+                best.per = per;
+            }
         }
     }
     return best;
+}
+
+// C[b](i, j) = act(fl(fl(fl(alpha * sum_s partial[s][b](i, j)) + fl(beta * C0[b](i, j))) +
+// bias[j])) for every output of a split-K product: the splits are added in order in fp32, then
+// the epilogue of sgemm_kernel, with its roundings. Lines (batch, row) go over blockIdx.y,
+// columns over blockIdx.x and the threads.
+__global__ __launch_bounds__(256) void split_reduce_kernel(GemmParams p) {
+    const int64_t lines = p.m * p.batch_count;
+    const int64_t split_stride = lines * p.n;
+    for (int64_t line = blockIdx.y; line < lines; line += gridDim.y) {
+        const int64_t b = line / p.m;
+        const int64_t row = line - b * p.m;
+        int64_t rest = b, off_c = 0, off_c0 = 0;
+        for (int d = p.batch_dims - 1; d >= 0; --d) {
+            const int64_t index = rest % p.batch[d];
+            rest /= p.batch[d];
+            off_c += index * p.c_bs[d];
+            off_c0 += index * p.c0_bs[d];
+        }
+        const float* part = p.partial + line * p.n;
+        float* c_row = p.c + off_c + row * p.c_rs;
+        const float* c0_row =
+            p.c0 != nullptr && p.beta != 0.0f ? p.c0 + off_c0 + row * p.c0_rs : nullptr;
+        for (int64_t col = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+             col < p.n; col += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+            float v = part[col];
+            for (int32_t s = 1; s < p.splits; ++s) {
+                v += part[s * split_stride + col];
+            }
+            if (p.alpha != 1.0f) {
+                v = p.alpha * v;
+            }
+            if (c0_row != nullptr) {
+                const float scaled = p.beta * c0_row[col];
+                v = v + scaled;
+            }
+            if (p.bias != nullptr) {
+                v = v + p.bias[col];
+            }
+            c_row[col] = mfr::dev::activate(v, p.act);
+        }
+    }
 }
 
 template <int BM, int BN, int KT, int WAVES_M, int WAVES_N, bool AK, bool BK>
@@ -254,7 +392,10 @@ struct Plan {
     bool ak = true, bk = true; // K-major operands
     int va = 4, vb = 4;        // load widths read in place
     bool stage_a = false, stage_b = false;
+    bool c0 = false;           // beta * C0 is read
     int tile = MFR_TILE_AUTO;
+    int splits = 1;            // depth ranges (split-K when > 1)
+    int64_t per = 0;           // depth of each range
 };
 
 Operand operand_a(GemmParams& p, bool ak) {
@@ -283,6 +424,8 @@ Plan plan_sgemm(const mfr_gemm_desc& d, int cus) {
     require(d.tile >= MFR_TILE_AUTO && d.tile < MFR_TILE_COUNT, "sgemm: unknown tile");
     require(d.stage == MFR_STAGE_AUTO || d.stage == MFR_STAGE_NEVER || d.stage == MFR_STAGE_ALWAYS,
             "sgemm: unknown stage mode");
+    require(d.splits >= 0 && d.splits <= kMaxSplits, "sgemm: splits out of range");
+    require(d.reserved == 0, "sgemm: reserved field not 0");
     Plan plan;
     GemmParams& p = plan.p;
     int64_t batch_count = 1;
@@ -371,14 +514,28 @@ Plan plan_sgemm(const mfr_gemm_desc& d, int cus) {
         }
     }
     const bool wide = (plan.va == 4 || plan.stage_a) && (plan.vb == 4 || plan.stage_b);
-    plan.tile = d.tile;
-    if (plan.tile == MFR_TILE_AUTO) {
-        plan.tile = choose_tile(p.m, p.n, p.k, batch_count, cus, wide);
-    } else if (plan.tile == MFR_TILE_256x256 && !wide) {
+    if (d.tile == MFR_TILE_256x256 && !wide) {
         throw mfr::Error(MFR_E_UNSUPPORTED,
                          "sgemm: the 256x256 tile needs 16-byte loads (staging is off)");
     }
+    plan.c0 = p.c0 != nullptr && p.beta != 0.0f;
+    const Choice choice = choose(p.m, p.n, p.k, batch_count, cus, wide, d.tile, d.splits, plan.c0);
+    plan.tile = choice.tile;
+    plan.splits = choice.splits;
+    plan.per = choice.per;
+    if (plan.splits > 1) {
+        require(4.0 * plan.splits * static_cast<double>(p.m) * p.n * batch_count <= 17179869184.0,
+                "sgemm: split-K partial sums over 16 GiB");
+    }
     return plan;
+}
+
+// Floats of workspace for the split-K partial sums of `plan` (256-byte aligned).
+int64_t partial_floats(const Plan& plan) {
+    if (plan.splits <= 1) {
+        return 0;
+    }
+    return (plan.splits * plan.p.m * plan.p.n * plan.p.batch_count + 63) / 64 * 64;
 }
 
 void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
@@ -389,44 +546,70 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
     }
     GemmParams& p = plan.p;
     int va = plan.va, vb = plan.vb;
-    if (plan.stage_a || plan.stage_b) {
-        Operand oa = operand_a(p, plan.ak);
-        Operand ob = operand_b(p, plan.bk);
-        const int64_t fa = plan.stage_a ? staged_floats_padded(oa, p) : 0;
-        const int64_t fb = plan.stage_b ? staged_floats_padded(ob, p) : 0;
-        float* ws = static_cast<float*>(try_reserve(s, 4 * static_cast<size_t>(fa + fb)));
-        if (ws == nullptr) {
+    Operand oa = operand_a(p, plan.ak);
+    Operand ob = operand_b(p, plan.bk);
+    int64_t fa = plan.stage_a ? staged_floats_padded(oa, p) : 0;
+    int64_t fb = plan.stage_b ? staged_floats_padded(ob, p) : 0;
+    // One workspace: [split-K partial sums][staged A][staged B].
+    float* ws = nullptr;
+    if (partial_floats(plan) + fa + fb > 0) {
+        ws = static_cast<float*>(
+            try_reserve(s, 4 * static_cast<size_t>(partial_floats(plan) + fa + fb)));
+        if (ws == nullptr && plan.splits > 1 && d.splits == 0) {
+            // An automatic split without the memory: one range.
+            plan.splits = 1;
+            plan.per = p.k;
+            if (d.tile == MFR_TILE_AUTO) {
+                plan.tile = choose(p.m, p.n, p.k, p.batch_count, s.compute_units,
+                                   (va == 4 || plan.stage_a) && (vb == 4 || plan.stage_b),
+                                   MFR_TILE_AUTO, 1, plan.c0)
+                                .tile;
+            }
+            if (fa + fb > 0) {
+                ws = static_cast<float*>(try_reserve(s, 4 * static_cast<size_t>(fa + fb)));
+            }
+        }
+        if (ws == nullptr && partial_floats(plan) + fa + fb > 0) {
+            if (plan.splits > 1) {
+                throw mfr::Error(MFR_E_RUNTIME, "sgemm: no workspace for split-K partial sums");
+            }
             if (d.stage == MFR_STAGE_ALWAYS || d.tile == MFR_TILE_256x256) {
                 throw mfr::Error(MFR_E_RUNTIME, "sgemm: no workspace for operand staging");
             }
             // AUTO without the memory: read in place, and choose the tile for 4-byte loads.
+            plan.stage_a = plan.stage_b = false;
+            fa = fb = 0;
             if (d.tile == MFR_TILE_AUTO) {
-                plan.tile = choose_tile(p.m, p.n, p.k, p.batch_count, s.compute_units,
-                                        va == 4 && vb == 4);
-            }
-        } else {
-            if (plan.stage_a) {
-                stage_operand(oa, ws, p, s.stream);
-                p.a = oa.base;
-                va = 4;
-            }
-            if (plan.stage_b) {
-                stage_operand(ob, ws + fa, p, s.stream);
-                p.b = ob.base;
-                vb = 4;
+                plan.tile = choose(p.m, p.n, p.k, p.batch_count, s.compute_units,
+                                   va == 4 && vb == 4, MFR_TILE_AUTO, 1, plan.c0)
+                                .tile;
             }
         }
+    }
+    float* partial = plan.splits > 1 ? ws : nullptr;
+    if (plan.stage_a) {
+        stage_operand(oa, ws + partial_floats(plan), p, s.stream);
+        p.a = oa.base;
+        va = 4;
+    }
+    if (plan.stage_b) {
+        stage_operand(ob, ws + partial_floats(plan) + fa, p, s.stream);
+        p.b = ob.base;
+        vb = 4;
     }
     const int tile = plan.tile;
     const int64_t tiles_m = (p.m + kTiles[tile].bm - 1) / kTiles[tile].bm;
     const int64_t tiles_n = (p.n + kTiles[tile].bn - 1) / kTiles[tile].bn;
-    const int64_t blocks = tiles_m * tiles_n * p.batch_count;
+    const int64_t blocks = tiles_m * tiles_n * p.batch_count * plan.splits;
     require(tiles_m < (int64_t{1} << 30) && tiles_n < (int64_t{1} << 30) &&
                 blocks < (int64_t{1} << 31),
             "sgemm: problem too large for one launch");
     p.tiles_m = static_cast<int32_t>(tiles_m);
     p.tiles_n = static_cast<int32_t>(tiles_n);
     p.group_m = kGroupM;
+    p.splits = plan.splits;
+    p.k_per_split = plan.splits > 1 ? plan.per : p.k;
+    p.partial = partial;
     const unsigned grid = static_cast<unsigned>(blocks);
     if (plan.ak && plan.bk) {
         launch_layout<true, true>(tile, p, va, vb, grid, s.stream);
@@ -438,6 +621,13 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
         launch_layout<false, false>(tile, p, va, vb, grid, s.stream);
     }
     mfr::check_launch("sgemm_kernel");
+    if (partial != nullptr) {
+        const int64_t lines = p.m * p.batch_count;
+        const dim3 grid(mfr::grid_blocks(p.n, 256, 64),
+                        static_cast<unsigned>(lines < 65535 ? lines : 65535));
+        split_reduce_kernel<<<grid, 256, 0, s.stream>>>(p);
+        mfr::check_launch("split_reduce_kernel");
+    }
 }
 
 } // namespace
@@ -452,9 +642,10 @@ int mfr_sgemm(mfr_stream_t stream, const mfr_gemm_desc* desc) {
     });
 }
 
-int mfr_sgemm_plan(int device, const mfr_gemm_desc* desc, int32_t* tile, int32_t* stage) {
+int mfr_sgemm_plan(int device, const mfr_gemm_desc* desc, int32_t* tile, int32_t* stage,
+                   int32_t* splits) {
     return mfr::guarded([&] {
-        mfr::require(desc != nullptr && tile != nullptr && stage != nullptr,
+        mfr::require(desc != nullptr && tile != nullptr && stage != nullptr && splits != nullptr,
                      "sgemm_plan: null argument");
         int cus = 0;
         const int status = mfr_get_device_info(device, nullptr, 0, nullptr, &cus, nullptr);
@@ -464,6 +655,7 @@ int mfr_sgemm_plan(int device, const mfr_gemm_desc* desc, int32_t* tile, int32_t
         const Plan plan = plan_sgemm(*desc, cus);
         *tile = plan.empty ? MFR_TILE_AUTO : plan.tile;
         *stage = plan.stage_a || plan.stage_b ? MFR_STAGE_ALWAYS : MFR_STAGE_NEVER;
+        *splits = plan.empty ? 0 : plan.splits;
     });
 }
 

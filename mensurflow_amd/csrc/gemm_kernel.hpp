@@ -27,6 +27,13 @@ struct GemmParams {
     int32_t tiles_m, tiles_n;
     int32_t group_m;
     float alpha, beta;
+    // Split-K: the depth is cut into `splits` ranges of k_per_split (a multiple of the depth
+    // slice; the last may be shorter). With splits > 1 each workgroup writes its raw fp32 sums to
+    // partial[split][batch][m][n] (dense, batch in linear order) instead of running the
+    // epilogue; split_reduce_kernel then adds the splits and applies it.
+    int64_t k_per_split;
+    int32_t splits;
+    float* partial;
 };
 
 // Global -> register -> LDS copy of one operand slice: ROWS rows (M for A, N for B) by KT depth.
@@ -132,13 +139,18 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_kernel(GemmParam
     auto lds_a = [&](int which) { return smem + which * LoadA::kFloats; };
     auto lds_b = [&](int which) { return smem + 2 * LoadA::kFloats + which * LoadB::kFloats; };
 
-    // ---- which tile: XCD-aware remap, then grouped row-major order within the batch ----
+    // ---- which tile: XCD-aware remap, then grouped row-major order within the batch; the
+    //      depth split is the outermost index ----
     const int64_t tiles_per_batch = static_cast<int64_t>(p.tiles_m) * p.tiles_n;
-    const int64_t total = tiles_per_batch * p.batch_count;
+    const int64_t tiles_per_split = tiles_per_batch * p.batch_count;
+    const int64_t total = tiles_per_split * p.splits;
     const int64_t hw = blockIdx.x;
     const int64_t per_xcd = total / 8;
-    const int64_t logical = hw < per_xcd * 8 ? (hw % 8) * per_xcd + hw / 8 : hw;
-    int64_t batch_index = logical / tiles_per_batch;
+    const int64_t logical_all = hw < per_xcd * 8 ? (hw % 8) * per_xcd + hw / 8 : hw;
+    const int64_t split = logical_all / tiles_per_split;
+    const int64_t logical = logical_all - split * tiles_per_split;
+    const int64_t batch_linear = logical / tiles_per_batch;
+    int64_t batch_index = batch_linear;
     const int64_t t = logical % tiles_per_batch;
     const int64_t group_tiles = static_cast<int64_t>(p.group_m) * p.tiles_n;
     const int64_t group = t / group_tiles;
@@ -163,8 +175,11 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_kernel(GemmParam
     const int rows_a = p.m - m0 < BM ? static_cast<int>(p.m - m0) : BM;
     const int rows_b = p.n - n0 < BN ? static_cast<int>(p.n - n0) : BN;
 
-    const float* a_base = p.a + off_a + m0 * p.a_rs;
-    const float* b_base = p.b + off_b + n0 * p.b_cs;
+    // This workgroup's depth range [k_begin, k_begin + kk).
+    const int64_t k_begin = split * p.k_per_split;
+    const int64_t kk = p.k - k_begin < p.k_per_split ? p.k - k_begin : p.k_per_split;
+    const float* a_base = p.a + off_a + m0 * p.a_rs + k_begin * p.a_cs;
+    const float* b_base = p.b + off_b + n0 * p.b_cs + k_begin * p.b_rs;
     // Per slice the bases advance by KT depths.
     const int64_t a_step = KT * p.a_cs;
     const int64_t b_step = KT * p.b_rs;
@@ -188,11 +203,11 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_kernel(GemmParam
         }
     }
 
-    const int64_t slices = (p.k + KT - 1) / KT;
+    const int64_t slices = kk > 0 ? (kk + KT - 1) / KT : 0;
     LoadA la;
     LoadB lb;
     if (slices > 0) {
-        const int k_left = p.k < KT ? static_cast<int>(p.k) : KT;
+        const int k_left = kk < KT ? static_cast<int>(kk) : KT;
         la.load(a_base, p.a_rs, p.a_cs, rows_a, k_left);
         lb.load(b_base, p.b_cs, p.b_rs, rows_b, k_left);
         la.store(lds_a(0));
@@ -204,7 +219,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_kernel(GemmParam
         const bool more = s + 1 < slices;
         if (more) {
             const int64_t k_next = (s + 1) * KT;
-            const int k_left = p.k - k_next < KT ? static_cast<int>(p.k - k_next) : KT;
+            const int k_left = kk - k_next < KT ? static_cast<int>(kk - k_next) : KT;
             la.load(a_base + (s + 1) * a_step, p.a_rs, p.a_cs, rows_a, k_left);
             lb.load(b_base + (s + 1) * b_step, p.b_cs, p.b_rs, rows_b, k_left);
         }
@@ -243,6 +258,29 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_kernel(GemmParam
 
     // ---- epilogue: accumulator e of block (i, j) is C(row, col) with
     //      row = 32i + 8(e/4) + 4*half + e%4, col = 32j + lane%32 (v_mfma_f32_32x32x2_f32 layout)
+    if (p.partial != nullptr) {
+        // Split-K: raw sums only (uniform branch).
+        float* part = p.partial + (split * p.batch_count + batch_linear) * p.m * p.n;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+                const int64_t col = n0 + wave_n * WN + j * 32 + r32;
+                if (col >= p.n) {
+                    continue;
+                }
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int64_t row =
+                        m0 + wave_m * WM + i * 32 + 8 * (e / 4) + 4 * half + e % 4;
+                    if (row < p.m) {
+                        part[row * p.n + col] = acc[i][j][e];
+                    }
+                }
+            }
+        }
+        return;
+    }
     float* c_base = p.c + off_c;
     const float* c0_base = p.c0 != nullptr ? p.c0 + off_c0 : nullptr;
     const bool use_c0 = c0_base != nullptr && p.beta != 0.0f;

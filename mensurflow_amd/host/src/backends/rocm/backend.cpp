@@ -118,11 +118,13 @@ void fill_matrix(mfr_gemm_desc& d, const Tensor& a, const Tensor& b, const Tenso
     d.act = MFR_ACT_NONE;
 }
 
-// The tuner's choice for this call (TunableKernel params "tile", "stage"; none = AUTO).
+// The tuner's choice for this call (TunableKernel params "tile", "stage", "splits"; none =
+// AUTO).
 void apply_tuning(mfr_gemm_desc& d, const TuningConfig& tuning) {
-    if (tuning.size >= 2) {
+    if (tuning.size >= 3) {
         d.tile = static_cast<std::int32_t>(tuning.values[0]);
         d.stage = static_cast<std::int32_t>(tuning.values[1]);
+        d.splits = static_cast<std::int32_t>(tuning.values[2]);
     }
 }
 
@@ -265,11 +267,13 @@ void gemm_batched_kernel(const OpArgs& args, Stream& stream) {
 //
 // The GEMM kernels' settings a tuner may choose (the reference's TunableKernel,
 // src/core/dispatcher.hpp:226-239, registered as the Metal matmul is,
-// src/backends/metal/backend.mm:231-289): params {"tile", "stage"} = the workgroup tile
-// (MFR_TILE_*) and operand staging (MFR_STAGE_NEVER / MFR_STAGE_ALWAYS). The defaults {0, 0}
-// leave both to the kernel (AUTO). The space is one region whose start is what AUTO picks for
-// the call (mfr_sgemm_plan), with the tiles ordered by area, so neighbours on the axis are
-// neighbours in effect; a point is allowed when mfr_sgemm_plan accepts it.
+// src/backends/metal/backend.mm:231-289): params {"tile", "stage", "splits"} = the workgroup
+// tile (MFR_TILE_*), operand staging (MFR_STAGE_NEVER / MFR_STAGE_ALWAYS) and the depth ranges
+// of split-K (1 = none). The defaults {0, 0, 0} leave all three to the kernel (AUTO). The space
+// is one region whose start is what AUTO picks for the call (mfr_sgemm_plan), with the tiles
+// ordered by area and the split counts by size, so neighbours on an axis are neighbours in
+// effect; a point is allowed when mfr_sgemm_plan accepts it and runs that many ranges (a count
+// the depth is too short for runs fewer, the same as a smaller point).
 
 // The descriptor the kernel for `op` would launch with for these args.
 mfr_gemm_desc planned_desc(OpId op, const OpArgs& args) {
@@ -278,11 +282,12 @@ mfr_gemm_desc planned_desc(OpId op, const OpArgs& args) {
     return op == OpId::GemmBatched ? batched_desc(args, a, b).desc : matrix_desc(op, args, a, b);
 }
 
-TuningConfig tuning_of(std::int64_t tile, std::int64_t stage) {
+TuningConfig tuning_of(std::int64_t tile, std::int64_t stage, std::int64_t splits) {
     TuningConfig config;
     config.values[0] = tile;
     config.values[1] = stage;
-    config.size = 2;
+    config.values[2] = splits;
+    config.size = 3;
     return config;
 }
 
@@ -303,42 +308,46 @@ template <OpId Op> std::vector<SearchRegion> gemm_space(const OpArgs& args) {
     mfr_gemm_desc d = planned_desc(Op, args);
     d.tile = MFR_TILE_AUTO;
     d.stage = MFR_STAGE_AUTO;
-    std::int32_t tile = 0, stage = 0;
-    check(mfr_sgemm_plan(args.outputs[0].device().index, &d, &tile, &stage));
+    d.splits = 0;
+    std::int32_t tile = 0, stage = 0, splits = 0;
+    check(mfr_sgemm_plan(args.outputs[0].device().index, &d, &tile, &stage, &splits));
     if (tile == MFR_TILE_AUTO) {
         return {}; // nothing to compute: nothing to tune
     }
     SearchRegion region;
     region.name = "mfma";
-    region.start = tuning_of(tile, stage);
+    region.start = tuning_of(tile, stage, splits);
     region.axes = {{0, {MFR_TILE_64x64, MFR_TILE_128x64, MFR_TILE_64x128, MFR_TILE_128x128,
                         MFR_TILE_256x256}},
-                   {1, {MFR_STAGE_NEVER, MFR_STAGE_ALWAYS}}};
+                   {1, {MFR_STAGE_NEVER, MFR_STAGE_ALWAYS}},
+                   {2, {1, 2, 4, 8, 16, 32}}};
     return {region};
 }
 
 template <OpId Op> bool gemm_allowed(const OpArgs& args, const TuningConfig& config) {
-    if (config.size != 2 || config.values[0] <= MFR_TILE_AUTO ||
+    if (config.size != 3 || config.values[0] <= MFR_TILE_AUTO ||
         config.values[0] >= MFR_TILE_COUNT ||
-        (config.values[1] != MFR_STAGE_NEVER && config.values[1] != MFR_STAGE_ALWAYS)) {
+        (config.values[1] != MFR_STAGE_NEVER && config.values[1] != MFR_STAGE_ALWAYS) ||
+        config.values[2] < 1 || config.values[2] > MFR_MAX_SPLITS) {
         return false;
     }
     OpArgs tuned = args;
     tuned.tuning = config;
     const mfr_gemm_desc d = planned_desc(Op, tuned);
-    std::int32_t tile = 0, stage = 0;
-    return mfr_sgemm_plan(args.outputs[0].device().index, &d, &tile, &stage) == MFR_OK;
+    std::int32_t tile = 0, stage = 0, splits = 0;
+    return mfr_sgemm_plan(args.outputs[0].device().index, &d, &tile, &stage, &splits) == MFR_OK &&
+           splits == config.values[2];
 }
 
 template <OpId Op> TunableKernel gemm_tunable(const char* name) {
     TunableKernel t;
     t.name = name;
-    t.version = 1;
+    t.version = 2;
     t.key_names = Op == OpId::GemmBatched ? std::vector<std::string>{"batch", "m", "n", "k"}
                                           : std::vector<std::string>{"m", "n", "k"};
     t.key = gemm_key<Op>;
-    t.params = {"tile", "stage"};
-    t.defaults = [] { return tuning_of(MFR_TILE_AUTO, MFR_STAGE_AUTO); };
+    t.params = {"tile", "stage", "splits"};
+    t.defaults = [] { return tuning_of(MFR_TILE_AUTO, MFR_STAGE_AUTO, 0); };
     t.space = gemm_space<Op>;
     t.allowed = gemm_allowed<Op>;
     return t;

@@ -2,8 +2,8 @@
 // "gemm_strided_batched", as the reference's tuner sees them: src/core/dispatcher.hpp:226-239):
 // registration, key, defaults, the search space and `allowed`, and every allowed point of the
 // space run through the kernel the way the tuner runs it (args.tuning set), each bit-exact on
-// quarter-integer inputs, whose products sum exactly in any order. Without a rocm device there is
-// nothing registered to check.
+// quarter-integer inputs, whose products sum exactly in any order (split-K included). Without a
+// rocm device there is nothing registered to check.
 #include "core/dispatcher.hpp"
 #include "core/registry.hpp"
 #include "oracle_cpu.hpp"
@@ -45,53 +45,70 @@ std::vector<float> exact_gemm(const std::vector<float>& a, const std::vector<flo
     return out;
 }
 
-TuningConfig point(std::int64_t tile, std::int64_t stage) {
+TuningConfig point(std::int64_t tile, std::int64_t stage, std::int64_t splits) {
     TuningConfig c;
     c.values[0] = tile;
     c.values[1] = stage;
-    c.size = 2;
+    c.values[2] = splits;
+    c.size = 3;
     return c;
+}
+
+// Depth ranges mfr_sgemm runs when `splits` are asked for at depth k: ranges a multiple of 32
+// deep, so fewer when the depth is short.
+std::int64_t ranges_run(std::int64_t k, std::int64_t splits) {
+    const std::int64_t per = ((k + splits - 1) / splits + 31) / 32 * 32;
+    return splits == 1 ? 1 : (k + per - 1) / per;
 }
 
 // Runs every point of `op`'s space that `allowed` accepts and checks the output each time.
 // Points refused are exactly the 256x256 tile with staging off when `narrow` (an operand that
-// 16-byte loads cannot read).
+// 16-byte loads cannot read) and split counts the depth k is too short for.
 void sweep(Device device, OpId op, OpArgs args, const std::vector<float>& want, bool narrow,
-           const std::string& what) {
+           std::int64_t k, const std::string& what) {
     Registry& registry = Registry::instance();
     const TunableKernel& tunable = *registry.dispatcher().tunable({op, DeviceType::ROCm, DType::F32});
     const KernelFn kernel = registry.dispatcher().lookup({op, DeviceType::ROCm, DType::F32});
     Stream& stream = registry.get(device).stream(device.index);
     const std::vector<SearchRegion> regions = tunable.space(args);
-    test::require(regions.size() == 1 && regions[0].axes.size() == 2, what + ": one region");
+    test::require(regions.size() == 1 && regions[0].axes.size() == 3, what + ": one region");
     const SearchRegion& region = regions[0];
-    test::require(region.start.size == 2 && region.start.values[0] > MFR_TILE_AUTO &&
-                      region.start.values[0] < MFR_TILE_COUNT,
-                  what + ": the start is a fixed tile");
+    test::require(region.start.size == 3 && region.start.values[0] > MFR_TILE_AUTO &&
+                      region.start.values[0] < MFR_TILE_COUNT && region.start.values[2] >= 1,
+                  what + ": the start is a fixed tile and split count");
     test::require(tunable.allowed(args, region.start), what + ": the start is allowed");
-    int ran = 0;
-    for (std::int64_t tile : region.axes[0].values) {
-        for (std::int64_t stage : region.axes[1].values) {
-            const TuningConfig config = point(tile, stage);
-            const bool allowed = tunable.allowed(args, config);
-            const bool expected = !(narrow && tile == MFR_TILE_256x256 && stage == MFR_STAGE_NEVER);
-            test::require(allowed == expected, what + ": allowed(tile " + std::to_string(tile) +
-                                                   ", stage " + std::to_string(stage) + ")");
-            if (!allowed) {
-                continue;
+    int ran = 0, counts = 0;
+    for (std::int64_t splits : region.axes[2].values) {
+        counts += ranges_run(k, splits) == splits;
+        for (std::int64_t tile : region.axes[0].values) {
+            for (std::int64_t stage : region.axes[1].values) {
+                const TuningConfig config = point(tile, stage, splits);
+                const bool allowed = tunable.allowed(args, config);
+                const bool expected =
+                    !(narrow && tile == MFR_TILE_256x256 && stage == MFR_STAGE_NEVER) &&
+                    ranges_run(k, splits) == splits;
+                const std::string name = "tile " + std::to_string(tile) + " stage " +
+                                         std::to_string(stage) + " splits " +
+                                         std::to_string(splits);
+                test::require(allowed == expected, what + ": allowed(" + name + ")");
+                if (!allowed) {
+                    continue;
+                }
+                args.tuning = config;
+                kernel(args, stream);
+                test::require(test::same_bits(args.outputs[0].to_vector<float>(), want),
+                              what + ": " + name);
+                ++ran;
             }
-            args.tuning = config;
-            kernel(args, stream);
-            test::require(test::same_bits(args.outputs[0].to_vector<float>(), want),
-                          what + ": tile " + std::to_string(tile) + " stage " +
-                              std::to_string(stage));
-            ++ran;
         }
     }
-    test::require(ran == (narrow ? 9 : 10), what + ": every allowed point ran");
+    test::require(counts >= 2 && ran == (narrow ? 9 : 10) * counts,
+                  what + ": every allowed point ran");
     // Not a point: AUTO is only the default, and unknown values are refused.
-    test::require(!tunable.allowed(args, point(MFR_TILE_AUTO, MFR_STAGE_NEVER)) &&
-                      !tunable.allowed(args, point(MFR_TILE_64x64, 7)),
+    test::require(!tunable.allowed(args, point(MFR_TILE_AUTO, MFR_STAGE_NEVER, 1)) &&
+                      !tunable.allowed(args, point(MFR_TILE_64x64, 7, 1)) &&
+                      !tunable.allowed(args, point(MFR_TILE_64x64, MFR_STAGE_NEVER, 0)) &&
+                      !tunable.allowed(args, point(MFR_TILE_64x64, MFR_STAGE_NEVER, 65)),
                   what + ": invalid points refused");
 }
 
@@ -102,10 +119,11 @@ void test_registration() {
     for (const auto& [op, name] : ops) {
         const TunableKernel* t = dispatcher.tunable({op, DeviceType::ROCm, DType::F32});
         test::require(t != nullptr && t->name == name, std::string(name) + " is tunable on rocm");
-        test::require(t->params == std::vector<std::string>{"tile", "stage"}, "params");
+        test::require(t->params == std::vector<std::string>{"tile", "stage", "splits"}, "params");
         const TuningConfig d = t->defaults();
-        test::require(d.size == 2 && d.values[0] == MFR_TILE_AUTO && d.values[1] == MFR_STAGE_AUTO,
-                      "defaults leave both settings to the kernel");
+        test::require(d.size == 3 && d.values[0] == MFR_TILE_AUTO &&
+                          d.values[1] == MFR_STAGE_AUTO && d.values[2] == 0,
+                      "defaults leave every setting to the kernel");
     }
 }
 
@@ -120,7 +138,7 @@ void test_matmul(Device device) {
         *Registry::instance().dispatcher().tunable({OpId::Matmul, DeviceType::ROCm, DType::F32});
     test::require(t.key(args) == std::vector<std::int64_t>{m, n, k}, "matmul key");
     const auto want = exact_gemm(av, bv, m, n, k, 1.0, nullptr, 0.0, nullptr);
-    sweep(device, OpId::Matmul, args, want, true, "matmul 300x261x1023");
+    sweep(device, OpId::Matmul, args, want, true, k, "matmul 300x261x1023");
 }
 
 void test_gemm_fused(Device device) {
@@ -145,7 +163,7 @@ void test_gemm_fused(Device device) {
     args.beta = 0.5f;
     args.has_bias = true;
     const auto want = exact_gemm(av, bv, m, n, k, 1.5, &cv, 0.5, &biasv);
-    sweep(device, OpId::Gemm, args, want, false, "gemm 257x200x96 NT");
+    sweep(device, OpId::Gemm, args, want, false, k, "gemm 257x200x96 NT");
 }
 
 void test_batched(Device device) {
@@ -173,7 +191,7 @@ void test_batched(Device device) {
             want.insert(want.end(), c.begin(), c.end());
         }
     }
-    sweep(device, OpId::GemmBatched, args, want, true, "batched 2x3x70x45x63");
+    sweep(device, OpId::GemmBatched, args, want, true, k, "batched 2x3x70x45x63");
 }
 
 void test_start_is_the_automatic_choice(Device device) {

@@ -233,11 +233,12 @@ def test_plan_on_baseline_shapes(stream):
     with staging off is refused on operands 16-byte loads cannot read, and staged otherwise."""
     abi = mf.abi
     big = mf.DeviceArray.empty((4096, 4096), stream)
-    assert mf.gemm_plan(big, big.T, big) == (abi.TILE_256x256, abi.STAGE_NEVER)
+    assert mf.gemm_plan(big, big.T, big) == (abi.TILE_256x256, abi.STAGE_NEVER, 1)
     x = mf.DeviceArray.empty((4093, 1023), stream)
     w = mf.DeviceArray.empty((1023, 4099), stream)
     out = mf.DeviceArray.empty((4093, 4099), stream)
-    tile, stage = mf.gemm_plan(x, w, out)
+    tile, stage, splits = mf.gemm_plan(x, w, out)
+    assert splits == 1
     assert stage == abi.STAGE_ALWAYS and tile != abi.TILE_AUTO
     assert mf.gemm_plan(x, w, out, stage=abi.STAGE_NEVER)[1] == abi.STAGE_NEVER
     q = mf.DeviceArray.empty((128, 1024, 64), stream)
@@ -245,7 +246,8 @@ def test_plan_on_baseline_shapes(stream):
     assert mf.gemm_plan(q, q.transpose(-2, -1), scores)[0] in (abi.TILE_128x64, abi.TILE_64x128)
     with pytest.raises(NotImplementedError):
         mf.gemm_plan(x, w, out, tile=abi.TILE_256x256, stage=abi.STAGE_NEVER)
-    assert mf.gemm_plan(x, w, out, tile=abi.TILE_256x256) == (abi.TILE_256x256, abi.STAGE_ALWAYS)
+    assert mf.gemm_plan(x, w, out, tile=abi.TILE_256x256)[:2] == (abi.TILE_256x256,
+                                                                  abi.STAGE_ALWAYS)
     empty = mf.DeviceArray.empty((0, 4099), stream)
     assert mf.gemm_plan(mf.DeviceArray.empty((0, 1023), stream), w, empty)[0] == abi.TILE_AUTO
     # The fixed 256x256 tile on odd operands runs staged, bit-exact.
@@ -254,6 +256,138 @@ def test_plan_on_baseline_shapes(stream):
     b = quarter_matrix(k, n, 98)
     got = mf.gemm(dev(a, stream), dev(b, stream), tile=abi.TILE_256x256).numpy()
     assert same_bits(got, exact_product(a, b))
+
+
+# ---- split-K -----------------------------------------------------------------------------------
+
+def ranges_run(k, splits):
+    """Depth ranges mfr_sgemm runs when `splits` are asked for: each a multiple of 32 deep."""
+    if splits <= 1 or k == 0:
+        return 1
+    per = -(-k // splits)           # ceil(k / splits)
+    per = -(-per // 32) * 32        # rounded up to a multiple of 32
+    return -(-k // per)
+
+
+@pytest.mark.parametrize("splits", [2, 3, 5, 8, 64])
+@pytest.mark.parametrize("tile", TILES)
+def test_exact_split_k_every_tile(stream, tile, splits):
+    """Split-K on every tile and all four layouts, with alpha, beta*C0 and a bias: the ranges'
+    raw sums and their reduction are exact on quarter integers, so the bits equal the exact
+    product. n is odd, so the fixed 256x256 tile also stages its operands into the same
+    workspace as the partial sums."""
+    m, n, k = 130, 97, 1000
+    a = quarter_matrix(m, k, 171)
+    b = quarter_matrix(k, n, 172)
+    c0 = quarter_matrix(m, n, 173)
+    bias = quarter_matrix(1, n, 174)[0]
+    want = (np.float32(1.5) * exact_product(a, b)) + np.float32(0.5) * c0
+    want = (want + bias).astype(np.float32)
+    for trans_a in (False, True):
+        for trans_b in (False, True):
+            a_d = dev(np.ascontiguousarray(a.T) if trans_a else a, stream)
+            b_d = dev(np.ascontiguousarray(b.T) if trans_b else b, stream)
+            left = a_d.T if trans_a else a_d
+            right = b_d.T if trans_b else b_d
+            c, buf = guarded_output(stream, (m, n))
+            plan = mf.gemm_plan(left, right, c, tile=tile, splits=splits)
+            assert plan[0] == tile and plan[2] == ranges_run(k, splits), plan
+            mf.gemm(left, right, alpha=1.5, c0=dev(c0, stream), beta=0.5,
+                    bias=dev(bias, stream), out=c, tile=tile, splits=splits)
+            assert same_bits(c.numpy(), want), (tile, splits, trans_a, trans_b)
+            check_guards(buf)
+
+
+def test_exact_split_k_batched_broadcast_in_place(stream):
+    """Split-K over a [2,3] batch with B broadcast over the first dimension (stride 0) and read
+    transposed, and C0 == C (the reduction reads and writes each element in place)."""
+    bsz, heads, m, n, k = 2, 3, 70, 45, 777
+    a = quarter_matrix(bsz * heads * m, k, 181).reshape(bsz, heads, m, k)
+    bt = quarter_matrix(heads * n, k, 182).reshape(1, heads, n, k)
+    c0 = quarter_matrix(bsz * heads * m, n, 183).reshape(bsz, heads, m, n)
+    b_d = dev(bt, stream).expand((bsz, heads, n, k)).transpose(-2, -1)
+    for splits in (4, 7):
+        c = dev(c0, stream)
+        mf.gemm_batched(dev(a, stream), b_d, c, alpha=0.25, c0=c, beta=-2.0, splits=splits)
+        got = c.numpy()
+        for i in range(bsz):
+            for h in range(heads):
+                prod = exact_product(a[i, h], bt[0, h].T)
+                want = (np.float32(0.25) * prod) + (np.float32(-2.0) * c0[i, h])
+                assert same_bits(got[i, h], want.astype(np.float32)), (splits, i, h)
+
+
+def test_split_k_short_depths(stream):
+    """More ranges asked for than the depth allows runs fewer (ranges are 32 deep at least);
+    k == 0 runs no split and gives the epilogue of a zero product."""
+    m, n = 33, 65
+    for k in (1, 31, 33, 40, 95):
+        a = quarter_matrix(m, k, 191 + k)
+        b = quarter_matrix(k, n, 192 + k)
+        a_d, b_d = dev(a, stream), dev(b, stream)
+        c, buf = guarded_output(stream, (m, n))
+        assert mf.gemm_plan(a_d, b_d, c, splits=8)[2] == ranges_run(k, 8)
+        mf.gemm(a_d, b_d, out=c, splits=8)
+        assert same_bits(c.numpy(), exact_product(a, b)), k
+        check_guards(buf)
+    c0 = quarter_matrix(m, n, 199)
+    a = mf.DeviceArray.empty((m, 0), stream)
+    b = mf.DeviceArray.empty((0, n), stream)
+    c, _ = guarded_output(stream, (m, n))
+    assert mf.gemm_plan(a, b, c, splits=4)[2] == 1
+    mf.gemm(a, b, alpha=2.0, c0=dev(c0, stream), beta=0.5, out=c, splits=4)
+    assert same_bits(c.numpy(), (np.float32(0.5) * c0).astype(np.float32))
+
+
+def test_split_k_invalid_counts(stream):
+    a = dev(np.ones((8, 64), np.float32), stream)
+    b = dev(np.ones((64, 8), np.float32), stream)
+    for splits in (-1, mf.abi.MAX_SPLITS + 1):
+        with pytest.raises(ValueError):
+            mf.gemm(a, b, splits=splits)
+    assert np.all(mf.gemm(a, b, splits=mf.abi.MAX_SPLITS).numpy() == 64.0)
+
+
+def test_split_k_gelu_same_bits_as_unsplit(stream):
+    """The activation sees the same pre-activation value split or not (exact inputs), so the
+    outputs agree in every bit."""
+    m, n, k = 96, 200, 2048
+    a = dev(quarter_matrix(m, k, 201), stream)
+    b = dev(quarter_matrix(k, n, 202), stream)
+    bias = dev(quarter_matrix(1, n, 203)[0], stream)
+    one = mf.gemm(a, b, bias=bias, act=mf.ACT_GELU_TANH, splits=1).numpy()
+    for splits in (2, 16):
+        got = mf.gemm(a, b, bias=bias, act=mf.ACT_GELU_TANH, splits=splits).numpy()
+        assert same_bits(got, one), splits
+
+
+def test_split_k_automatic_choice(stream):
+    """AUTO splits a product with few output tiles and a long depth, and leaves products that
+    fill the device (4096^3, the MLP) or have a short depth unsplit."""
+    def plan(m, n, k):
+        return mf.gemm_plan(mf.DeviceArray.empty((m, k), stream),
+                            mf.DeviceArray.empty((k, n), stream),
+                            mf.DeviceArray.empty((m, n), stream))
+    assert plan(256, 256, 16384)[2] > 1
+    assert plan(512, 512, 8192)[2] > 1
+    assert plan(4096, 4096, 4096)[2] == 1
+    assert plan(4093, 4099, 1023)[2] == 1
+    assert plan(256, 256, 256)[2] == 1
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 16384), (128, 4096, 4096), (1000, 1000, 3000)])
+def test_split_k_realistic(stream, oracle, m, n, k):
+    """Split-K (as AUTO picks it, and fixed at 8) on normal inputs against the packed CPU GEMM,
+    to the 1e-5*sqrt(K) bar; deterministic from call to call."""
+    a = normal(oracle, (m, k), 0.0, 1.0, 11, 0)
+    b = normal(oracle, (k, n), 0.0, 1.0, 12, 0)
+    a_d, b_d = dev(a, stream), dev(b, stream)
+    want = oracle.matmul(a, b)
+    scale = magnitude(oracle, a, b)
+    for splits in (0, 8):
+        got = mf.gemm(a_d, b_d, splits=splits).numpy()
+        assert_gemm_parity(got, want, scale, k, f"split {splits}")
+        assert same_bits(got, mf.gemm(a_d, b_d, splits=splits).numpy())
 
 
 def test_unknown_stage_mode_is_invalid(stream):
