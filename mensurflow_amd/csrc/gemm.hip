@@ -45,11 +45,11 @@ struct TileInfo {
 };
 constexpr TileInfo kTiles[MFR_TILE_COUNT] = {
     {0, 0, 0, 0, 0.0},         // AUTO
-    {256, 256, 1, 8, 127.8},   // 8 wavefronts of 128x64, depth slice 32
-    {128, 128, 2, 4, 122.0},   // 4 wavefronts of 64x64, depth slice 32
-    {128, 64, 5, 4, 110.9},    // 4 wavefronts of 64x32, depth slice 16
-    {64, 128, 5, 4, 114.7},    // 4 wavefronts of 32x64, depth slice 16
-    {64, 64, 4, 4, 112.9},     // 4 wavefronts of 32x32, depth slice 32
+    {256, 256, 1, 8, 133.4},   // 8 wavefronts of 128x64, depth slice 32
+    {128, 128, 2, 4, 127.3},   // 4 wavefronts of 64x64, depth slice 32
+    {128, 64, 5, 4, 114.9},    // 4 wavefronts of 64x32, depth slice 16
+    {64, 128, 5, 4, 116.0},    // 4 wavefronts of 32x64, depth slice 16
+    {64, 64, 4, 4, 111.4},     // 4 wavefronts of 32x32, depth slice 32
 };
 constexpr int kGroupM = 8;
 
@@ -70,10 +70,9 @@ constexpr double kMaxPartialBytes = 1073741824.0; // AUTO keeps the partial sums
 constexpr double kReduceBytesPerUs = 4.0e6;       // split_reduce_kernel's HBM rate (bytes/us)
 constexpr double kReduceLaunchUs = 4.0;           // its launch and ramp
 // A tile's fixed cost (first slice's load latency, writing the tile out), in depth-equivalents
-// of its MFMA work, shared among the workgroups a CU runs at once. Fit to the measured times of
-// every tile and split count on 14 shapes (64^2 x 65536 .. 8192^2 x 1024): it is why a depth of
-// 256 on 4096^2 runs faster in 64x64 tiles (4 per CU) than in 256x256 ones (1 per CU).
-constexpr double kTileOverheadDepth = 192.0;
+// of its MFMA work, shared among the workgroups a CU runs at once. Fit, with simd_efficiency, to
+// the measured times of every tile and split count on 14 shapes (64^2 x 65536 .. 8192^2 x 1024).
+constexpr double kTileOverheadDepth = 96.0;
 
 // Depth of each range when `splits` are asked for: a multiple of 32, which every tile's depth
 // slice divides, so no range starts inside a slice.
@@ -86,7 +85,7 @@ int splits_for(int64_t k, int64_t per) { return static_cast<int>((k + per - 1) /
 
 // Relative rate of a CU by how many wavefronts each SIMD holds: one alone hides no latency.
 double simd_efficiency(int64_t waves_per_simd) {
-    return waves_per_simd >= 3 ? 1.0 : waves_per_simd == 2 ? 0.9 : 0.8;
+    return waves_per_simd >= 3 ? 1.0 : waves_per_simd == 2 ? 0.9 : 0.85;
 }
 
 // Modelled time (us) of tile t with `splits` depth ranges of `per` each: the busiest CU's share

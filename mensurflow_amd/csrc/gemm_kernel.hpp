@@ -53,7 +53,7 @@ template <int ROWS, int KT, bool KMAJ, int V, int THREADS> struct SliceLoader {
     Vec reg[kPerThread];
 
     // (row, depth) of this thread's i-th load, in elements.
-    __device__ static void coords(int i, int& r, int& p) {
+    __device__ __forceinline__ static void coords(int i, int& r, int& p) {
         const int u = static_cast<int>(threadIdx.x) + i * THREADS;
         if constexpr (KMAJ) {
             constexpr int per_row = KT / V;
@@ -68,8 +68,8 @@ template <int ROWS, int KT, bool KMAJ, int V, int THREADS> struct SliceLoader {
 
     // base points at element (row 0, depth k0) of the slice. rows_left / k_left: how many rows
     // and depths of the slice are inside the matrix (>= ROWS / KT for an interior slice).
-    __device__ void load(const float* base, int64_t row_stride, int64_t k_stride, int rows_left,
-                         int k_left) {
+    __device__ __forceinline__ void load(const float* base, int64_t row_stride, int64_t k_stride,
+                                         int rows_left, int k_left) {
         const bool full = rows_left >= ROWS && k_left >= KT;
 #pragma unroll
         for (int i = 0; i < kPerThread; ++i) {
@@ -92,7 +92,7 @@ template <int ROWS, int KT, bool KMAJ, int V, int THREADS> struct SliceLoader {
         }
     }
 
-    __device__ void store(float* lds) const {
+    __device__ __forceinline__ void store(float* lds) const {
 #pragma unroll
         for (int i = 0; i < kPerThread; ++i) {
             int r, p;
@@ -108,7 +108,8 @@ template <int ROWS, int KT, bool KMAJ, int V, int THREADS> struct SliceLoader {
 
     // The four MFMA-step values of fragment row `row` (0..ROWS-1) for depth group g (8 depths):
     // lanes 0-31 (half 0) take depths 8g+0..3, lanes 32-63 (half 1) depths 8g+4..7.
-    __device__ static void fragment(const float* lds, int row, int g, int half, float out[4]) {
+    __device__ __forceinline__ static void fragment(const float* lds, int row, int g, int half,
+                                                    float out[4]) {
         if constexpr (KMAJ) {
             const float4 v = *reinterpret_cast<const float4*>(lds + row * kPitch + 8 * g + 4 * half);
             out[0] = v.x;
@@ -123,6 +124,100 @@ template <int ROWS, int KT, bool KMAJ, int V, int THREADS> struct SliceLoader {
         }
     }
 };
+
+// Writes a wavefront's accumulators: block (i, j), element e is C(row0 + 32i + 8(e/4) + e%4,
+// col0 + 32j), as
+//   C = act(fl(fl(fl(alpha * acc) + fl(beta * C0)) + bias))      (RAW: C = acc),
+// the C0 term only when c0 is non-null and the bias only when p.bias is non-null, so the roundings
+// are the reference's. alpha * acc is exact for alpha == 1. INTERIOR: every row and column is
+// inside C (no checks). C0 == kC0Batched: c0 is non-null and a row-block's C0 values are all
+// loaded before any is used, so the loads overlap; kC0None: no C0; kC0Checked: c0 checked per
+// element (one copy of the code for both cases).
+enum { kC0None = 0, kC0Batched = 1, kC0Checked = 2 };
+template <int FM, int FN, int ACT, bool INTERIOR, bool RAW, int C0>
+__device__ __forceinline__ void write_tile(const floatx16 (&acc)[FM][FN], float* c, int64_t c_rs,
+                                           const float* c0, int64_t c0_rs, const GemmParams& p,
+                                           int64_t row0, int64_t col0) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const int64_t row_i = row0 + 32 * i;
+        float* c_i = c + row_i * c_rs + col0;
+        float c0v[FN][16];
+        if constexpr (C0 == kC0Batched) {
+            const float* c0_i = c0 + row_i * c0_rs + col0;
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int dr = 8 * (e / 4) + e % 4;
+                    const bool inside = INTERIOR || (col0 + 32 * j < p.n && row_i + dr < p.m);
+                    c0v[j][e] = inside ? c0_i[dr * c0_rs + 32 * j] : 0.0f;
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int64_t col = col0 + 32 * j;
+            if (!INTERIOR && col >= p.n) {
+                continue;
+            }
+            const float bias = !RAW && p.bias != nullptr ? p.bias[col] : 0.0f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int dr = 8 * (e / 4) + e % 4;
+                if (!INTERIOR && row_i + dr >= p.m) {
+                    continue;
+                }
+                float v = acc[i][j][e];
+                if constexpr (!RAW) {
+                    v = p.alpha * v;
+                    if constexpr (C0 == kC0Batched) {
+                        const float scaled = p.beta * c0v[j][e];
+                        v = v + scaled;
+                    } else if constexpr (C0 == kC0Checked) {
+                        if (c0 != nullptr) {
+                            const float scaled = p.beta * c0[(row_i + dr) * c0_rs + col];
+                            v = v + scaled;
+                        }
+                    }
+                    if (p.bias != nullptr) {
+                        v = v + bias;
+                    }
+                    if constexpr (ACT != MFR_ACT_NONE) {
+                        v = mfr::dev::gelu(v, ACT);
+                    }
+                }
+                c_i[dr * c_rs + 32 * j] = v;
+            }
+        }
+    }
+}
+
+// The epilogue for activation ACT. Without one it is dispatched on C0 and on whether the tile is
+// interior; a gelu epilogue is one copy (its transcendental work outweighs the checks).
+template <int FM, int FN, int ACT>
+__device__ __forceinline__ void epilogue(const floatx16 (&acc)[FM][FN], float* c, int64_t c_rs,
+                                         const float* c0, int64_t c0_rs, const GemmParams& p,
+                                         int64_t row0, int64_t col0, bool interior) {
+    if constexpr (ACT != MFR_ACT_NONE) {
+        write_tile<FM, FN, ACT, false, false, kC0Checked>(acc, c, c_rs, c0, c0_rs, p, row0, col0);
+    } else if (c0 != nullptr) {
+        if (interior) {
+            write_tile<FM, FN, ACT, true, false, kC0Batched>(acc, c, c_rs, c0, c0_rs, p, row0,
+                                                             col0);
+        } else {
+            write_tile<FM, FN, ACT, false, false, kC0Batched>(acc, c, c_rs, c0, c0_rs, p, row0,
+                                                              col0);
+        }
+    } else {
+        if (interior) {
+            write_tile<FM, FN, ACT, true, false, kC0None>(acc, c, c_rs, c0, c0_rs, p, row0, col0);
+        } else {
+            write_tile<FM, FN, ACT, false, false, kC0None>(acc, c, c_rs, c0, c0_rs, p, row0,
+                                                           col0);
+        }
+    }
+}
 
 template <int BM, int BN, int KT, int WAVES_M, int WAVES_N, bool AK, bool BK, int VA, int VB>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_kernel(GemmParams p) {
@@ -258,61 +353,34 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_kernel(GemmParam
 
     // ---- epilogue: accumulator e of block (i, j) is C(row, col) with
     //      row = 32i + 8(e/4) + 4*half + e%4, col = 32j + lane%32 (v_mfma_f32_32x32x2_f32 layout)
+    const int64_t row0 = m0 + wave_m * WM + 4 * half;
+    const int64_t col0 = n0 + wave_n * WN + r32;
+    const bool interior = m0 + BM <= p.m && n0 + BN <= p.n;
     if (p.partial != nullptr) {
-        // Split-K: raw sums only (uniform branch).
+        // Split-K: raw sums only, to partial[split][batch] (dense m x n).
         float* part = p.partial + (split * p.batch_count + batch_linear) * p.m * p.n;
-#pragma unroll
-        for (int i = 0; i < FM; ++i) {
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                const int64_t col = n0 + wave_n * WN + j * 32 + r32;
-                if (col >= p.n) {
-                    continue;
-                }
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int64_t row =
-                        m0 + wave_m * WM + i * 32 + 8 * (e / 4) + 4 * half + e % 4;
-                    if (row < p.m) {
-                        part[row * p.n + col] = acc[i][j][e];
-                    }
-                }
-            }
+        if (interior) {
+            write_tile<FM, FN, MFR_ACT_NONE, true, true, kC0None>(acc, part, p.n, nullptr, 0, p,
+                                                                  row0, col0);
+        } else {
+            write_tile<FM, FN, MFR_ACT_NONE, false, true, kC0None>(acc, part, p.n, nullptr, 0, p,
+                                                                   row0, col0);
         }
         return;
     }
     float* c_base = p.c + off_c;
-    const float* c0_base = p.c0 != nullptr ? p.c0 + off_c0 : nullptr;
-    const bool use_c0 = c0_base != nullptr && p.beta != 0.0f;
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-            const int64_t col = n0 + wave_n * WN + j * 32 + r32;
-            if (col >= p.n) {
-                continue;
-            }
-            const float bias = p.bias != nullptr ? p.bias[col] : 0.0f;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int64_t row = m0 + wave_m * WM + i * 32 + 8 * (e / 4) + 4 * half + e % 4;
-                if (row >= p.m) {
-                    continue;
-                }
-                float v = acc[i][j][e];
-                if (p.alpha != 1.0f) {
-                    v = p.alpha * v;
-                }
-                if (use_c0) {
-                    const float scaled = p.beta * c0_base[row * p.c0_rs + col];
-                    v = v + scaled;
-                }
-                if (p.bias != nullptr) {
-                    v = v + bias;
-                }
-                c_base[row * p.c_rs + col] = mfr::dev::activate(v, p.act);
-            }
-        }
+    const float* c0_base = p.c0 != nullptr && p.beta != 0.0f ? p.c0 + off_c0 : nullptr;
+    // One activation per branch (uniform), so each epilogue is straight-line code: unrolled
+    // over every accumulator, the three would not fit the instruction cache together.
+    if (p.act == MFR_ACT_NONE) {
+        epilogue<FM, FN, MFR_ACT_NONE>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
+                                       interior);
+    } else if (p.act == MFR_ACT_GELU_TANH) {
+        epilogue<FM, FN, MFR_ACT_GELU_TANH>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
+                                            interior);
+    } else {
+        epilogue<FM, FN, MFR_ACT_GELU_ERF>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
+                                           interior);
     }
 }
 
