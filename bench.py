@@ -176,6 +176,28 @@ def bench_copy(mf, stream, steps, warmup):
     return {"event_ms": event_ms, "bytes": 8.0 * n}
 
 
+def host_description() -> str:
+    """CPU model, hardware threads and physical cores of this host (from /proc/cpuinfo)."""
+    model, cores = "unknown CPU", set()
+    physical = core = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key, _, value = line.partition(":")
+                key, value = key.strip(), value.strip()
+                if key == "model name":
+                    model = value
+                elif key == "physical id":
+                    physical = value
+                elif key == "core id":
+                    core = value
+                    cores.add((physical, core))
+    except OSError:
+        pass
+    physical_cores = f"{len(cores)} physical cores" if cores else "physical cores unknown"
+    return f"{model}, {os.cpu_count()} hardware threads, {physical_cores}"
+
+
 def cpu_baseline(seconds: float = 12.0):
     """The reference's packed AVX2/OpenMP GEMM (oracle/_ref) on the box's host cores: the
     matmul of configs[2] (4096^3, B read transposed), repeated for about `seconds`."""
@@ -218,7 +240,7 @@ def cpu_baseline(seconds: float = 12.0):
         "kind": kind,
         "sample": (f"{len(times)} calls of the packed CPU GEMM at 4096^3 (A * B^T, fp32), median "
                    f"{median * 1e3:.1f} ms; the alpha/beta passes (memory-bound, <1% of the "
-                   f"work) not included"),
+                   f"work) not included; host: {host_description()}, {threads} threads used"),
     }
 
 

@@ -173,8 +173,14 @@ enum {
     MFR_TILE_128x64 = 3,  /* 4 wavefronts of 64x32, depth slice 16, up to 5 per CU */
     MFR_TILE_64x128 = 4,  /* 4 wavefronts of 32x64, depth slice 16 */
     MFR_TILE_64x64 = 5,   /* 4 wavefronts of 32x32, 4 per CU */
-    MFR_TILE_COUNT = 6
+    MFR_TILE_THIN = 6,    /* no MFMA: at most 8 output columns (or rows) as dot products */
+    MFR_TILE_COUNT = 7
 };
+
+/* The thin path (MFR_TILE_THIN) streams the long operand once and keeps the other, at most 8
+ * columns wide, in LDS: for n <= 8 with A read along k (unit stride along K), or m <= 8 with B
+ * read along k. Elsewhere a fixed THIN fails with MFR_E_UNSUPPORTED; it runs no split. AUTO
+ * prices it against the MFMA tiles. */
 
 /* Split-K of mfr_sgemm. A product with few output tiles and a long depth (256 x 256 x 16384)
  * would leave most compute units idle, so its depth may be cut into `splits` ranges (each a
@@ -189,16 +195,24 @@ enum {
 
 int mfr_sgemm(mfr_stream_t stream, const mfr_gemm_desc* desc);
 
+/* Edge peeling (tile and splits both AUTO): a dimension a few rows past a multiple of a big tile
+ * (N = 4099 = 16 x 256 + 3) would cost that tile a whole extra wave of tiles for a sliver of work,
+ * so such a remainder (at most a quarter of the tile) may run as a separate launch with its own
+ * tile and split count, when the time model prices that at least 5% lower. Up to 4 launches: the main
+ * rectangle, the right strip, the bottom strip, the corner. */
+
 /* What mfr_sgemm would run for desc on device `device`, without launching anything: the tile
  * (an MFR_TILE_* other than AUTO; AUTO when there is nothing to compute), whether operands
  * are staged (MFR_STAGE_ALWAYS) or read in place (MFR_STAGE_NEVER), and the depth ranges
- * (1 = no split; 0 when there is nothing to compute). Validates desc as mfr_sgemm
+ * (1 = no split; 0 when there is nothing to compute), each of the main region, and the number of
+ * output regions launched separately (1, or 2-4 with edge peeling; 0 when there is nothing to
+ * compute). Validates desc as mfr_sgemm
  * does and fails with the same status where mfr_sgemm would (MFR_E_UNSUPPORTED for a fixed
  * 256x256 tile with staging off and operands 16-byte loads cannot read). For tuners: the default
  * a search starts from, and whether a (tile, stage) point can run (the reference's
  * TunableKernel::defaults / allowed, src/core/dispatcher.hpp:226-239). */
 int mfr_sgemm_plan(int device, const mfr_gemm_desc* desc, int32_t* tile, int32_t* stage,
-                   int32_t* splits);
+                   int32_t* splits, int32_t* regions);
 
 /* Plain row-major convenience form: C[m,n] = alpha*op(A)*op(B) + beta*C0 with leading
  * dimensions lda/ldb/ldc (BLAS-style trans flags, row-major storage). c0 may be NULL. */

@@ -300,16 +300,18 @@ def gemm_batched(a: DeviceArray, b: DeviceArray, c: DeviceArray, *, alpha=1.0,
 
 
 def gemm_plan(a: DeviceArray, b: DeviceArray, c: DeviceArray, *, tile=0, stage=0, splits=0,
-              c0: DeviceArray | None = None, beta=0.0) -> tuple[int, int, int]:
-    """(tile, stage, splits) that gemm_batched(a, b, c, ...) would run with (mfr_sgemm_plan):
-    AUTO resolved to a fixed tile, stage reported as STAGE_ALWAYS (operands copied first) or
-    STAGE_NEVER, splits the depth ranges (1 = no split). Raises as gemm_batched would for a point
-    that cannot run."""
+              c0: DeviceArray | None = None, beta=0.0) -> tuple[int, int, int, int]:
+    """(tile, stage, splits, regions) that gemm_batched(a, b, c, ...) would run with
+    (mfr_sgemm_plan): AUTO resolved to a fixed tile, stage reported as STAGE_ALWAYS (operands
+    copied first) or STAGE_NEVER, splits the depth ranges (1 = no split) -- both of the main
+    region -- and regions the output rectangles launched separately (more than 1 when AUTO peels
+    edge strips). Raises as gemm_batched would for a point that cannot run."""
     d = _gemm_desc(a, b, c, 1.0, c0, beta, None, ACT_NONE, tile, stage, splits)
-    t, st, sp = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    t, st, sp, rg = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
     abi.check(abi.load().mfr_sgemm_plan(c.stream.device, ctypes.byref(d), ctypes.byref(t),
-                                        ctypes.byref(st), ctypes.byref(sp)), "mfr_sgemm_plan")
-    return t.value, st.value, sp.value
+                                        ctypes.byref(st), ctypes.byref(sp), ctypes.byref(rg)),
+              "mfr_sgemm_plan")
+    return t.value, st.value, sp.value, rg.value
 
 
 def _gemm_desc(a, b, c, alpha, c0, beta, bias, act, tile, stage, splits=0) -> GemmDesc:

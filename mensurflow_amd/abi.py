@@ -33,7 +33,8 @@ TILE_128x128 = 2
 TILE_128x64 = 3
 TILE_64x128 = 4
 TILE_64x64 = 5
-TILE_COUNT = 6
+TILE_THIN = 6
+TILE_COUNT = 7
 STAGE_AUTO = 0
 STAGE_NEVER = 1
 STAGE_ALWAYS = 2
@@ -108,7 +109,7 @@ SIGNATURES = {
     "mfr_sgemm": (ctypes.c_int, [_vp, ctypes.POINTER(GemmDesc)]),
     "mfr_sgemm_plan": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(GemmDesc),
                                       ctypes.POINTER(_i32), ctypes.POINTER(_i32),
-                                      ctypes.POINTER(_i32)]),
+                                      ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
     "mfr_sgemm_rm": (ctypes.c_int, [_vp, ctypes.c_int, ctypes.c_int, _i64, _i64, _i64, _f32, _vp,
                                     _i64, _vp, _i64, _f32, _vp, _vp, _i64]),
     "mfr_sgemv": (ctypes.c_int, [_vp, ctypes.c_int, _i64, _i64, _f32, _vp, _i64, _vp, _f32, _vp,

@@ -29,6 +29,10 @@
 //     to a multiple of 4 by zeros (stage_kernel); vector loads that reach past the end of a line
 //     then read zeros of its own line, and the zeros add nothing to any sum.
 #include "gemm_kernel.hpp"
+#include "thin_kernel.hpp"
+
+#include <algorithm>
+#include <cmath>
 
 namespace {
 
@@ -50,6 +54,7 @@ constexpr TileInfo kTiles[MFR_TILE_COUNT] = {
     {128, 64, 5, 4, 114.9},    // 4 wavefronts of 64x32, depth slice 16
     {64, 128, 5, 4, 116.0},    // 4 wavefronts of 32x64, depth slice 16
     {64, 64, 4, 4, 111.4},     // 4 wavefronts of 32x32, depth slice 32
+    {0, 0, 0, 0, 0.0},         // THIN (no tile; priced by thin_us)
 };
 constexpr int kGroupM = 8;
 
@@ -116,20 +121,62 @@ double modelled_us(int t, int64_t m, int64_t n, int64_t k, int64_t batch, int cu
     return us;
 }
 
+// ---- the thin path ---------------------------------------------------------------------------
+
+constexpr double kThinBytesPerUs = 6.0e6; // its streaming rate (bytes/us) for one column
+constexpr double kThinLaunchUs = 3.0;
+
+// Whether the thin path takes an m x n product: n <= 8 with A read along k (ak), or m <= 8 with
+// B read along k (bk). along_n: the first (C = A B row by row), else the transposed form.
+bool thin_possible(int64_t m, int64_t n, bool ak, bool bk, bool* along_n = nullptr) {
+    const bool by_rows = n <= kThinCols && ak;
+    if (along_n != nullptr) {
+        *along_n = by_rows;
+    }
+    return by_rows || (m <= kThinCols && bk);
+}
+
+// Modelled time (us): every byte read or written once, at kThinBytesPerUs for one column and
+// slower by half that per further column (each B' value is a load of its own), and slower in
+// proportion with fewer than 512 workgroups. Fit to measured times of 1-8 columns.
+double thin_us(int64_t m, int64_t n, int64_t k, int64_t batch, bool c0, bool ak, bool bk) {
+    bool along_n = true;
+    thin_possible(m, n, ak, bk, &along_n);
+    const double rows = static_cast<double>(along_n ? m : n);
+    const double cols = static_cast<double>(along_n ? n : m);
+    const double bytes = 4.0 * batch * (rows * k + k * cols + rows * cols * (c0 ? 2.0 : 1.0));
+    const double blocks = batch * std::ceil(rows / kThinDotRows);
+    return bytes / kThinBytesPerUs * (1.0 + 0.5 * cols) * std::max(1.0, 512.0 / blocks) +
+           kThinLaunchUs;
+}
+
 struct Choice {
     int tile = MFR_TILE_128x128;
     int splits = 1;      // depth ranges
     int64_t per = 0;     // depth of each (the last may be shorter); k when not split
+    double us = 0.0;     // modelled time
 };
 
 // The automatic tile and split count (either may be fixed by the caller: tile != AUTO, splits !=
 // 0). A short depth (K <= 128) is latency-bound per tile, so it takes the high-occupancy 128x64 /
 // 64x128 tiles (the one padding the output less). Otherwise the pair with the least modelled
-// time. The 256x256 tile needs 16-byte loads on both operands.
+// time. The 256x256 tile needs 16-byte loads on both operands. The thin path competes where it
+// can take the product (ak, bk: whether A and B are read along k) and no split is fixed.
 Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int cus, bool wide_loads,
-              int fixed_tile, int fixed_splits, bool c0) {
+              int fixed_tile, int fixed_splits, bool c0, bool ak, bool bk) {
     Choice best;
     best.per = k;
+    const bool thin = thin_possible(m, n, ak, bk) && fixed_splits <= 1;
+    if (fixed_tile == MFR_TILE_THIN) {
+        if (!thin) {
+            throw mfr::Error(MFR_E_UNSUPPORTED,
+                             "sgemm: the thin path takes n <= 8 with A read along k, or m <= 8 "
+                             "with B read along k, and no split");
+        }
+        best.tile = MFR_TILE_THIN;
+        best.us = thin_us(m, n, k, batch, c0, ak, bk);
+        return best;
+    }
     if (fixed_splits > 0 && k > 0) {
         best.per = depth_per_split(k, fixed_splits);
         best.splits = splits_for(k, best.per);
@@ -141,43 +188,55 @@ Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int cus, bool wide
         const int64_t a = tile_count(MFR_TILE_128x64, m, n, batch) * 128 * 64;
         const int64_t b = tile_count(MFR_TILE_64x128, m, n, batch) * 64 * 128;
         best.tile = b < a ? MFR_TILE_64x128 : MFR_TILE_128x64;
-        return best;
-    }
-    double best_us = 1e300;
-    for (int t = 1; t < MFR_TILE_COUNT; ++t) {
-        if ((fixed_tile != MFR_TILE_AUTO && t != fixed_tile) ||
-            (fixed_tile == MFR_TILE_AUTO && t == MFR_TILE_256x256 && !wide_loads)) {
-            continue;
-        }
-        if (fixed_splits > 0) {
-            // Only the tile is open.
-            const double us = modelled_us(t, m, n, k, batch, cus, best.splits, best.per, c0);
-            if (us < best_us) {
-                best_us = us;
-                best.tile = t;
-            }
-            continue;
-        }
-        int prev = 0;
-        for (int want = 1; want <= kMaxSplits; ++want) {
-            const int64_t per = want == 1 || k == 0 ? k : depth_per_split(k, want);
-            const int splits = want == 1 || k == 0 ? 1 : splits_for(k, per);
-            if (splits == prev) {
+        best.us = modelled_us(best.tile, m, n, k, batch, cus, 1, k, c0);
+    } else {
+        double best_us = 1e300;
+        for (int t = 1; t < MFR_TILE_THIN; ++t) {
+            if ((fixed_tile != MFR_TILE_AUTO && t != fixed_tile) ||
+                (fixed_tile == MFR_TILE_AUTO && t == MFR_TILE_256x256 && !wide_loads)) {
                 continue;
             }
-            prev = splits;
-            if (splits > 1 &&
-                (per < kMinAutoDepth ||
-                 4.0 * splits * static_cast<double>(m) * n * batch > kMaxPartialBytes)) {
-                break;
+            if (fixed_splits > 0) {
+                // Only the tile is open.
+                const double us = modelled_us(t, m, n, k, batch, cus, best.splits, best.per, c0);
+                if (us < best_us) {
+                    best_us = us;
+                    best.tile = t;
+                    best.us = us;
+                }
+                continue;
             }
-            const double us = modelled_us(t, m, n, k, batch, cus, splits, per, c0);
-            if (us < best_us) {
-                best_us = us;
-                best.tile = t;
-                best.splits = splits;
-                best.per = per;
+            int prev = 0;
+            for (int want = 1; want <= kMaxSplits; ++want) {
+                const int64_t per = want == 1 || k == 0 ? k : depth_per_split(k, want);
+                const int splits = want == 1 || k == 0 ? 1 : splits_for(k, per);
+                if (splits == prev) {
+                    continue;
+                }
+                prev = splits;
+                if (splits > 1 &&
+                    (per < kMinAutoDepth ||
+                     4.0 * splits * static_cast<double>(m) * n * batch > kMaxPartialBytes)) {
+                    break;
+                }
+                const double us = modelled_us(t, m, n, k, batch, cus, splits, per, c0);
+                if (us < best_us) {
+                    best_us = us;
+                    best.tile = t;
+                    best.splits = splits;
+                    best.per = per;
+                    best.us = us;
+                }
             }
+        }
+    }
+    if (fixed_tile == MFR_TILE_AUTO && thin) {
+        const double us = thin_us(m, n, k, batch, c0, ak, bk);
+        if (us < best.us) {
+            best.tile = MFR_TILE_THIN;
+            best.splits = 1;
+            best.per = k;
+            best.us = us;
         }
     }
     return best;
@@ -385,6 +444,14 @@ void* try_reserve(mfr_stream& s, size_t bytes) {
 // Everything mfr_sgemm decides before launching: the kernel parameters (strides of extent-1
 // dimensions normalised), each operand's layout and load width, which operands to stage, and the
 // tile. mfr_sgemm_plan reports it without launching.
+// A rectangle of the output run as one launch (plus its reduce when split).
+struct Region {
+    int64_t m_off = 0, n_off = 0, m = 0, n = 0;
+    int tile = MFR_TILE_AUTO;
+    int splits = 1;  // depth ranges (split-K when > 1)
+    int64_t per = 0; // depth of each range
+};
+
 struct Plan {
     GemmParams p{};
     bool empty = false;        // nothing to compute (m, n or the batch is 0)
@@ -392,10 +459,72 @@ struct Plan {
     int va = 4, vb = 4;        // load widths read in place
     bool stage_a = false, stage_b = false;
     bool c0 = false;           // beta * C0 is read
-    int tile = MFR_TILE_AUTO;
-    int splits = 1;            // depth ranges (split-K when > 1)
-    int64_t per = 0;           // depth of each range
+    Region regions[4];         // [0] is the main one; the rest are peeled edge strips
+    int region_count = 1;
 };
+
+// The plan's output as one region with `choice`.
+void single_region(Plan& plan, const Choice& choice) {
+    plan.region_count = 1;
+    plan.regions[0] = Region{0, 0, plan.p.m, plan.p.n, choice.tile, choice.splits, choice.per};
+}
+
+// ---- edge peeling ----------------------------------------------------------------------------
+//
+// A dimension a few rows past a multiple of a big tile (N = 4099 = 16 x 256 + 3) costs that tile a
+// whole extra wave of tiles for a sliver of work. In AUTO, such a remainder (at most a quarter of
+// the tile) may be peeled off: the main rectangle runs on the big tile, and each edge strip runs
+// as a launch of its own, with its own tile and split count. The peeled plan is kept when the
+// model prices it (plus kLaunchUs per extra launch) at least 5% below the best single launch.
+constexpr double kLaunchUs = 5.0;
+constexpr double kPeelMargin = 0.95;
+
+void consider_peeling(Plan& plan, int64_t batch, int cus, bool wide, double single_us) {
+    const GemmParams& p = plan.p;
+    double best_us = single_us * kPeelMargin;
+    for (int t = 1; t < MFR_TILE_THIN; ++t) {
+        if (t == MFR_TILE_256x256 && !wide) {
+            continue;
+        }
+        const int64_t bm = kTiles[t].bm, bn = kTiles[t].bn;
+        const int64_t rem_m = p.m % bm, rem_n = p.n % bn;
+        const bool peel_m = p.m > bm && rem_m > 0 && rem_m * 4 <= bm;
+        const bool peel_n = p.n > bn && rem_n > 0 && rem_n * 4 <= bn;
+        if (!peel_m && !peel_n) {
+            continue;
+        }
+        const int64_t main_m = peel_m ? p.m - rem_m : p.m;
+        const int64_t main_n = peel_n ? p.n - rem_n : p.n;
+        Region regions[4];
+        int count = 0;
+        const Choice main =
+            choose(main_m, main_n, p.k, batch, cus, wide, t, 1, plan.c0, plan.ak, plan.bk);
+        regions[count++] = Region{0, 0, main_m, main_n, main.tile, main.splits, main.per};
+        double us = main.us;
+        auto strip = [&](int64_t m_off, int64_t n_off, int64_t m, int64_t n) {
+            const Choice c =
+                choose(m, n, p.k, batch, cus, wide, MFR_TILE_AUTO, 0, plan.c0, plan.ak, plan.bk);
+            regions[count++] = Region{m_off, n_off, m, n, c.tile, c.splits, c.per};
+            us += c.us + kLaunchUs;
+        };
+        if (peel_n) {
+            strip(0, main_n, main_m, rem_n);
+        }
+        if (peel_m) {
+            strip(main_m, 0, rem_m, main_n);
+        }
+        if (peel_m && peel_n) {
+            strip(main_m, main_n, rem_m, rem_n);
+        }
+        if (us < best_us) {
+            best_us = us;
+            plan.region_count = count;
+            for (int i = 0; i < count; ++i) {
+                plan.regions[i] = regions[i];
+            }
+        }
+    }
+}
 
 Operand operand_a(GemmParams& p, bool ak) {
     return Operand{p.a, ak ? p.m : p.k, ak ? p.k : p.m, ak ? &p.a_rs : &p.a_cs,
@@ -518,27 +647,156 @@ Plan plan_sgemm(const mfr_gemm_desc& d, int cus) {
                          "sgemm: the 256x256 tile needs 16-byte loads (staging is off)");
     }
     plan.c0 = p.c0 != nullptr && p.beta != 0.0f;
-    const Choice choice = choose(p.m, p.n, p.k, batch_count, cus, wide, d.tile, d.splits, plan.c0);
-    plan.tile = choice.tile;
-    plan.splits = choice.splits;
-    plan.per = choice.per;
-    if (plan.splits > 1) {
-        require(4.0 * plan.splits * static_cast<double>(p.m) * p.n * batch_count <= 17179869184.0,
+    const Choice choice = choose(p.m, p.n, p.k, batch_count, cus, wide, d.tile, d.splits, plan.c0,
+                                 plan.ak, plan.bk);
+    single_region(plan, choice);
+    if (d.tile == MFR_TILE_AUTO && d.splits == 0) {
+        consider_peeling(plan, batch_count, cus, wide, choice.us);
+    }
+    for (int i = 0; i < plan.region_count; ++i) {
+        const Region& r = plan.regions[i];
+        require(r.splits <= 1 ||
+                    4.0 * r.splits * static_cast<double>(r.m) * r.n * batch_count <= 17179869184.0,
                 "sgemm: split-K partial sums over 16 GiB");
     }
     return plan;
 }
 
-// Floats of workspace for the split-K partial sums of `plan` (256-byte aligned).
+// Floats of workspace for the split-K partial sums of `plan` (256-byte aligned): the largest any
+// region needs, since regions run one after another on the stream.
 int64_t partial_floats(const Plan& plan) {
-    if (plan.splits <= 1) {
-        return 0;
+    int64_t most = 0;
+    for (int i = 0; i < plan.region_count; ++i) {
+        const Region& r = plan.regions[i];
+        if (r.splits > 1) {
+            const int64_t f = (r.splits * r.m * r.n * plan.p.batch_count + 63) / 64 * 64;
+            most = f > most ? f : most;
+        }
     }
-    return (plan.splits * plan.p.m * plan.p.n * plan.p.batch_count + 63) / 64 * 64;
+    return most;
+}
+
+// The thin path on the product q describes (thin_possible holds): C = A B by rows of A when
+// n <= 8 and A is read along k, else C^T = B^T A^T by rows of B^T.
+void launch_thin(const Plan& plan, const GemmParams& q, int va, int vb, hipStream_t stream) {
+    ThinParams t{};
+    bool along_n = true;
+    thin_possible(q.m, q.n, plan.ak, plan.bk, &along_n);
+    const float* c0 = q.c0 != nullptr && q.beta != 0.0f ? q.c0 : nullptr;
+    const int64_t* a_bs = q.a_bs;
+    const int64_t* b_bs = q.b_bs;
+    int width = va;
+    if (along_n) {
+        t.a = q.a;
+        t.a_rs = q.a_rs;
+        t.a_cs = q.a_cs;
+        t.b = q.b;
+        t.b_rs = q.b_rs;
+        t.b_cs = q.b_cs;
+        t.rows = q.m;
+        t.cols = q.n;
+        t.c_rs = q.c_rs;
+        t.c_cs = 1;
+        t.c0_rs = q.c0_rs;
+        t.c0_cs = 1;
+        t.bias_rs = 0;
+        t.bias_cs = 1;
+    } else {
+        // A'(j, p) = B(p, j), B'(p, i) = A(i, p), C'(j, i) = C(i, j), bias'(j, i) = bias[j].
+        t.a = q.b;
+        t.a_rs = q.b_cs;
+        t.a_cs = q.b_rs;
+        t.b = q.a;
+        t.b_rs = q.a_cs;
+        t.b_cs = q.a_rs;
+        t.rows = q.n;
+        t.cols = q.m;
+        t.c_rs = 1;
+        t.c_cs = q.c_rs;
+        t.c0_rs = 1;
+        t.c0_cs = q.c0_rs;
+        t.bias_rs = 1;
+        t.bias_cs = 0;
+        a_bs = q.b_bs;
+        b_bs = q.a_bs;
+        width = vb;
+    }
+    t.c = q.c;
+    t.c0 = c0;
+    t.bias = q.bias;
+    t.k = q.k;
+    t.batch_dims = q.batch_dims;
+    for (int d = 0; d < q.batch_dims; ++d) {
+        t.batch[d] = q.batch[d];
+        t.a_bs[d] = a_bs[d];
+        t.b_bs[d] = b_bs[d];
+        t.c_bs[d] = q.c_bs[d];
+        t.c0_bs[d] = q.c0_bs[d];
+    }
+    t.act = q.act;
+    t.alpha = q.alpha;
+    t.beta = q.beta;
+    t.blocks_per_batch = (t.rows + kThinDotRows - 1) / kThinDotRows;
+    const int64_t blocks = t.blocks_per_batch * q.batch_count;
+    mfr::require(blocks < (int64_t{1} << 31), "sgemm: problem too large for one launch");
+    if (width == 4) {
+        thin_dot_kernel<4><<<static_cast<unsigned>(blocks), kThinThreads, 0, stream>>>(t);
+    } else {
+        thin_dot_kernel<1><<<static_cast<unsigned>(blocks), kThinThreads, 0, stream>>>(t);
+    }
+    mfr::check_launch("thin_dot_kernel");
+}
+
+// Launches the kernel (and the reduce, when split) for region r of the product p describes.
+void launch_region(const Plan& plan, const GemmParams& p, const Region& r, int va, int vb,
+                   float* partial, hipStream_t stream) {
+    using mfr::require;
+    GemmParams q = p;
+    q.m = r.m;
+    q.n = r.n;
+    q.a = p.a + r.m_off * p.a_rs;
+    q.b = p.b + r.n_off * p.b_cs;
+    q.c = p.c + r.m_off * p.c_rs + r.n_off;
+    q.c0 = p.c0 != nullptr ? p.c0 + r.m_off * p.c0_rs + r.n_off : nullptr;
+    q.bias = p.bias != nullptr ? p.bias + r.n_off : nullptr;
+    if (r.tile == MFR_TILE_THIN) {
+        launch_thin(plan, q, va, vb, stream);
+        return;
+    }
+    const int tile = r.tile;
+    const int64_t tiles_m = (q.m + kTiles[tile].bm - 1) / kTiles[tile].bm;
+    const int64_t tiles_n = (q.n + kTiles[tile].bn - 1) / kTiles[tile].bn;
+    const int64_t blocks = tiles_m * tiles_n * q.batch_count * r.splits;
+    require(tiles_m < (int64_t{1} << 30) && tiles_n < (int64_t{1} << 30) &&
+                blocks < (int64_t{1} << 31),
+            "sgemm: problem too large for one launch");
+    q.tiles_m = static_cast<int32_t>(tiles_m);
+    q.tiles_n = static_cast<int32_t>(tiles_n);
+    q.group_m = kGroupM;
+    q.splits = r.splits;
+    q.k_per_split = r.splits > 1 ? r.per : q.k;
+    q.partial = r.splits > 1 ? partial : nullptr;
+    const unsigned grid = static_cast<unsigned>(blocks);
+    if (plan.ak && plan.bk) {
+        launch_layout<true, true>(tile, q, va, vb, grid, stream);
+    } else if (plan.ak) {
+        launch_layout<true, false>(tile, q, va, vb, grid, stream);
+    } else if (plan.bk) {
+        launch_layout<false, true>(tile, q, va, vb, grid, stream);
+    } else {
+        launch_layout<false, false>(tile, q, va, vb, grid, stream);
+    }
+    mfr::check_launch("sgemm_kernel");
+    if (q.partial != nullptr) {
+        const int64_t lines = q.m * q.batch_count;
+        const dim3 reduce_grid(mfr::grid_blocks(q.n, 256, 64),
+                               static_cast<unsigned>(lines < 65535 ? lines : 65535));
+        split_reduce_kernel<<<reduce_grid, 256, 0, stream>>>(q);
+        mfr::check_launch("split_reduce_kernel");
+    }
 }
 
 void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
-    using mfr::require;
     Plan plan = plan_sgemm(d, s.compute_units);
     if (plan.empty) {
         return;
@@ -554,22 +812,17 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
     if (partial_floats(plan) + fa + fb > 0) {
         ws = static_cast<float*>(
             try_reserve(s, 4 * static_cast<size_t>(partial_floats(plan) + fa + fb)));
-        if (ws == nullptr && plan.splits > 1 && d.splits == 0) {
-            // An automatic split without the memory: one range.
-            plan.splits = 1;
-            plan.per = p.k;
-            if (d.tile == MFR_TILE_AUTO) {
-                plan.tile = choose(p.m, p.n, p.k, p.batch_count, s.compute_units,
-                                   (va == 4 || plan.stage_a) && (vb == 4 || plan.stage_b),
-                                   MFR_TILE_AUTO, 1, plan.c0)
-                                .tile;
-            }
+        if (ws == nullptr && partial_floats(plan) > 0 && d.splits == 0) {
+            // Automatic splits without the memory: one region, one range.
+            single_region(plan, choose(p.m, p.n, p.k, p.batch_count, s.compute_units,
+                                       (va == 4 || plan.stage_a) && (vb == 4 || plan.stage_b),
+                                       d.tile, 1, plan.c0, plan.ak, plan.bk));
             if (fa + fb > 0) {
                 ws = static_cast<float*>(try_reserve(s, 4 * static_cast<size_t>(fa + fb)));
             }
         }
         if (ws == nullptr && partial_floats(plan) + fa + fb > 0) {
-            if (plan.splits > 1) {
+            if (partial_floats(plan) > 0) {
                 throw mfr::Error(MFR_E_RUNTIME, "sgemm: no workspace for split-K partial sums");
             }
             if (d.stage == MFR_STAGE_ALWAYS || d.tile == MFR_TILE_256x256) {
@@ -579,13 +832,13 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
             plan.stage_a = plan.stage_b = false;
             fa = fb = 0;
             if (d.tile == MFR_TILE_AUTO) {
-                plan.tile = choose(p.m, p.n, p.k, p.batch_count, s.compute_units,
-                                   va == 4 && vb == 4, MFR_TILE_AUTO, 1, plan.c0)
-                                .tile;
+                single_region(plan, choose(p.m, p.n, p.k, p.batch_count, s.compute_units,
+                                           va == 4 && vb == 4, MFR_TILE_AUTO, 1, plan.c0,
+                                           plan.ak, plan.bk));
             }
         }
     }
-    float* partial = plan.splits > 1 ? ws : nullptr;
+    float* partial = partial_floats(plan) > 0 ? ws : nullptr;
     if (plan.stage_a) {
         stage_operand(oa, ws + partial_floats(plan), p, s.stream);
         p.a = oa.base;
@@ -596,36 +849,8 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
         p.b = ob.base;
         vb = 4;
     }
-    const int tile = plan.tile;
-    const int64_t tiles_m = (p.m + kTiles[tile].bm - 1) / kTiles[tile].bm;
-    const int64_t tiles_n = (p.n + kTiles[tile].bn - 1) / kTiles[tile].bn;
-    const int64_t blocks = tiles_m * tiles_n * p.batch_count * plan.splits;
-    require(tiles_m < (int64_t{1} << 30) && tiles_n < (int64_t{1} << 30) &&
-                blocks < (int64_t{1} << 31),
-            "sgemm: problem too large for one launch");
-    p.tiles_m = static_cast<int32_t>(tiles_m);
-    p.tiles_n = static_cast<int32_t>(tiles_n);
-    p.group_m = kGroupM;
-    p.splits = plan.splits;
-    p.k_per_split = plan.splits > 1 ? plan.per : p.k;
-    p.partial = partial;
-    const unsigned grid = static_cast<unsigned>(blocks);
-    if (plan.ak && plan.bk) {
-        launch_layout<true, true>(tile, p, va, vb, grid, s.stream);
-    } else if (plan.ak) {
-        launch_layout<true, false>(tile, p, va, vb, grid, s.stream);
-    } else if (plan.bk) {
-        launch_layout<false, true>(tile, p, va, vb, grid, s.stream);
-    } else {
-        launch_layout<false, false>(tile, p, va, vb, grid, s.stream);
-    }
-    mfr::check_launch("sgemm_kernel");
-    if (partial != nullptr) {
-        const int64_t lines = p.m * p.batch_count;
-        const dim3 grid(mfr::grid_blocks(p.n, 256, 64),
-                        static_cast<unsigned>(lines < 65535 ? lines : 65535));
-        split_reduce_kernel<<<grid, 256, 0, s.stream>>>(p);
-        mfr::check_launch("split_reduce_kernel");
+    for (int i = 0; i < plan.region_count; ++i) {
+        launch_region(plan, p, plan.regions[i], va, vb, partial, s.stream);
     }
 }
 
@@ -642,9 +867,10 @@ int mfr_sgemm(mfr_stream_t stream, const mfr_gemm_desc* desc) {
 }
 
 int mfr_sgemm_plan(int device, const mfr_gemm_desc* desc, int32_t* tile, int32_t* stage,
-                   int32_t* splits) {
+                   int32_t* splits, int32_t* regions) {
     return mfr::guarded([&] {
-        mfr::require(desc != nullptr && tile != nullptr && stage != nullptr && splits != nullptr,
+        mfr::require(desc != nullptr && tile != nullptr && stage != nullptr && splits != nullptr &&
+                         regions != nullptr,
                      "sgemm_plan: null argument");
         int cus = 0;
         const int status = mfr_get_device_info(device, nullptr, 0, nullptr, &cus, nullptr);
@@ -652,9 +878,10 @@ int mfr_sgemm_plan(int device, const mfr_gemm_desc* desc, int32_t* tile, int32_t
             throw mfr::Error(status, mfr_last_error());
         }
         const Plan plan = plan_sgemm(*desc, cus);
-        *tile = plan.empty ? MFR_TILE_AUTO : plan.tile;
+        *tile = plan.empty ? MFR_TILE_AUTO : plan.regions[0].tile;
         *stage = plan.stage_a || plan.stage_b ? MFR_STAGE_ALWAYS : MFR_STAGE_NEVER;
-        *splits = plan.empty ? 0 : plan.splits;
+        *splits = plan.empty ? 0 : plan.regions[0].splits;
+        *regions = plan.empty ? 0 : plan.region_count;
     });
 }
 

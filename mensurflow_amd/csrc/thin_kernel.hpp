@@ -1,0 +1,172 @@
+// Device code of the thin GEMM path: products with at most 8 output columns (or, transposed, 8
+// output rows), which the MFMA tiles would pad to 64 and more. Included by gemm.hip, which picks
+// the path and sets up the parameters.
+//
+// The product is C'[rows, cols] = A'[rows, k] B'[k, cols] with cols <= 8, in general strides, so
+// one kernel serves both orientations: C = A B with n <= 8 (A' = A, B' = B), and C^T = B^T A^T
+// with m <= 8 (A' = B^T, B' = A^T, C' = C^T). The work is streaming A' from HBM once (as the gemv
+// kernels stream their matrix); B' (at most 8 columns) is read through the caches by every row.
+// A' rows must run along k (unit stride along k): each wavefront takes kThinRowsPerWave rows, its
+// lanes stride through k (16-byte loads when the rows allow), and the wavefront sums its lanes at
+// the end.
+// Each output is act(fl(fl(fl(alpha * sum) + fl(beta * C0)) + bias)), the MFMA epilogue's
+// roundings; the sum is fp32 in an order of its own (exact, in any order, on quarter integers).
+#pragma once
+
+#include "common.hpp"
+
+namespace mfr::gemm {
+
+constexpr int kThinCols = 8;        // most output columns (rows, transposed) the path takes
+constexpr int kThinRowsPerWave = 4;
+constexpr int kThinWaves = 2;
+constexpr int kThinThreads = 64 * kThinWaves;
+constexpr int kThinDotRows = kThinRowsPerWave * kThinWaves; // rows per workgroup
+constexpr int kThinUnroll = 2;
+
+struct ThinParams {
+    const float* a;
+    const float* b;
+    float* c;
+    const float* c0;   // null when beta * C0 is not added
+    const float* bias; // may be null
+    int64_t rows, cols, k;
+    int64_t a_rs, a_cs; // A'(r, p) at a + r*a_rs + p*a_cs
+    int64_t b_rs, b_cs; // B'(p, j) at b + p*b_rs + j*b_cs
+    int64_t c_rs, c_cs, c0_rs, c0_cs;
+    int64_t bias_rs, bias_cs; // bias'(r, j) at bias + r*bias_rs + j*bias_cs
+    int64_t batch[MFR_MAX_BATCH_DIMS];
+    int64_t a_bs[MFR_MAX_BATCH_DIMS], b_bs[MFR_MAX_BATCH_DIMS];
+    int64_t c_bs[MFR_MAX_BATCH_DIMS], c0_bs[MFR_MAX_BATCH_DIMS];
+    int32_t batch_dims;
+    int32_t act;
+    int64_t blocks_per_batch;
+    float alpha, beta;
+};
+
+// Offsets of batch matrix `index` (linear order) into A', B', C' and C0'.
+struct ThinBatch {
+    const float* a;
+    const float* b;
+    float* c;
+    const float* c0;
+};
+
+__device__ inline ThinBatch thin_batch(const ThinParams& p, int64_t index) {
+    int64_t off_a = 0, off_b = 0, off_c = 0, off_c0 = 0;
+    for (int d = p.batch_dims - 1; d >= 0; --d) {
+        const int64_t i = index % p.batch[d];
+        index /= p.batch[d];
+        off_a += i * p.a_bs[d];
+        off_b += i * p.b_bs[d];
+        off_c += i * p.c_bs[d];
+        off_c0 += i * p.c0_bs[d];
+    }
+    return ThinBatch{p.a + off_a, p.b + off_b, p.c + off_c,
+                     p.c0 != nullptr ? p.c0 + off_c0 : nullptr};
+}
+
+__device__ inline void thin_store(const ThinParams& p, const ThinBatch& t, int64_t r, int64_t j,
+                                  float sum) {
+    float v = p.alpha * sum;
+    if (t.c0 != nullptr) {
+        const float scaled = p.beta * t.c0[r * p.c0_rs + j * p.c0_cs];
+        v = v + scaled;
+    }
+    if (p.bias != nullptr) {
+        v = v + p.bias[r * p.bias_rs + j * p.bias_cs];
+    }
+    t.c[r * p.c_rs + j * p.c_cs] = mfr::dev::activate(v, p.act);
+}
+
+// VA = 4: 16-byte loads of A' (a_rs and the batch strides multiples of 4, a 16-byte aligned, and
+// either k % 4 == 0 or A' staged with its lines zero-padded to a multiple of 4).
+// B' values come from the caches (at most 8 columns, shared by every row).
+template <int VA>
+__global__ __launch_bounds__(kThinThreads) void thin_dot_kernel(ThinParams p) {
+    const int64_t batch_index = blockIdx.x / p.blocks_per_batch;
+    const ThinBatch t = thin_batch(p, batch_index);
+    const int lane = threadIdx.x % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int64_t row0 =
+        (blockIdx.x % p.blocks_per_batch) * kThinDotRows + wave * kThinRowsPerWave;
+    const int cols = static_cast<int>(p.cols);
+    float acc[kThinRowsPerWave][kThinCols] = {};
+    const float* a_row[kThinRowsPerWave];
+    bool valid[kThinRowsPerWave];
+#pragma unroll
+    for (int r = 0; r < kThinRowsPerWave; ++r) {
+        valid[r] = row0 + r < p.rows;
+        a_row[r] = t.a + (valid[r] ? row0 + r : 0) * p.a_rs;
+    }
+    constexpr int kStep = 64 * VA * kThinUnroll; // depths per group
+    // kThinUnroll steps of 64 * VA depths: every load of a group is issued before any is used;
+    // steps past k load nothing and add nothing.
+    for (int64_t base = static_cast<int64_t>(lane) * VA; base < p.k; base += kStep) {
+        float a[kThinUnroll][kThinRowsPerWave][VA];
+        float b[kThinUnroll][VA][kThinCols];
+#pragma unroll
+        for (int u = 0; u < kThinUnroll; ++u) {
+            const int64_t kk = base + u * 64 * VA;
+            const bool in_k = kk < p.k;
+#pragma unroll
+            for (int r = 0; r < kThinRowsPerWave; ++r) {
+                const bool ok = valid[r] && in_k;
+                if constexpr (VA == 4) {
+                    const float4 v =
+                        ok ? mfr::dev::load_streaming(a_row[r] + kk) : make_float4(0.f, 0.f, 0.f, 0.f);
+                    a[u][r][0] = v.x;
+                    a[u][r][1] = v.y;
+                    a[u][r][2] = v.z;
+                    a[u][r][3] = v.w;
+                } else {
+                    a[u][r][0] = ok ? a_row[r][kk] : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < VA; ++v) {
+                // A staged operand's lines are padded to a multiple of 4 (the A' values past k
+                // read its zeros), but B' has no depth kk + v >= k: those are not read.
+                const bool depth = kk + v < p.k;
+#pragma unroll
+                for (int j = 0; j < kThinCols; ++j) {
+                    b[u][v][j] = depth && j < cols ? t.b[(kk + v) * p.b_rs + j * p.b_cs] : 0.0f;
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kThinUnroll; ++u) {
+#pragma unroll
+            for (int v = 0; v < VA; ++v) {
+#pragma unroll
+                for (int r = 0; r < kThinRowsPerWave; ++r) {
+#pragma unroll
+                    for (int j = 0; j < kThinCols; ++j) {
+                        acc[r][j] = __builtin_fmaf(a[u][r][v], b[u][v][j], acc[r][j]);
+                    }
+                }
+            }
+        }
+    }
+    // Wavefront sums: every lane ends with every total; lane r*8 + j stores output (r, j).
+    float mine = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kThinRowsPerWave; ++r) {
+#pragma unroll
+        for (int j = 0; j < kThinCols; ++j) {
+            float v = acc[r][j];
+#pragma unroll
+            for (int offset = 32; offset > 0; offset >>= 1) {
+                v += __shfl_xor(v, offset, 64);
+            }
+            mine = lane == r * kThinCols + j ? v : mine;
+        }
+    }
+    const int r = lane / kThinCols;
+    const int j = lane % kThinCols;
+    if (r < kThinRowsPerWave && row0 + r < p.rows && j < cols) {
+        thin_store(p, t, row0 + r, j, mine);
+    }
+}
+
+} // namespace mfr::gemm

@@ -268,12 +268,13 @@ void gemm_batched_kernel(const OpArgs& args, Stream& stream) {
 // The GEMM kernels' settings a tuner may choose (the reference's TunableKernel,
 // src/core/dispatcher.hpp:226-239, registered as the Metal matmul is,
 // src/backends/metal/backend.mm:231-289): params {"tile", "stage", "splits"} = the workgroup
-// tile (MFR_TILE_*), operand staging (MFR_STAGE_NEVER / MFR_STAGE_ALWAYS) and the depth ranges
-// of split-K (1 = none). The defaults {0, 0, 0} leave all three to the kernel (AUTO). The space
-// is one region whose start is what AUTO picks for the call (mfr_sgemm_plan), with the tiles
-// ordered by area and the split counts by size, so neighbours on an axis are neighbours in
-// effect; a point is allowed when mfr_sgemm_plan accepts it and runs that many ranges (a count
-// the depth is too short for runs fewer, the same as a smaller point).
+// tile (MFR_TILE_*, the thin path included), operand staging (MFR_STAGE_NEVER /
+// MFR_STAGE_ALWAYS) and the depth ranges of split-K (1 = none). The defaults {0, 0, 0} leave all
+// three to the kernel (AUTO). The space is one region whose start is what AUTO picks for the
+// call (mfr_sgemm_plan), with the tiles ordered by area (the thin path first) and the split
+// counts by size, so neighbours on an axis are neighbours in effect; a point is allowed when
+// mfr_sgemm_plan accepts it and runs that many ranges (a count the depth is too short for runs
+// fewer, the same as a smaller point; the thin path only where it takes the product, unsplit).
 
 // The descriptor the kernel for `op` would launch with for these args.
 mfr_gemm_desc planned_desc(OpId op, const OpArgs& args) {
@@ -309,16 +310,16 @@ template <OpId Op> std::vector<SearchRegion> gemm_space(const OpArgs& args) {
     d.tile = MFR_TILE_AUTO;
     d.stage = MFR_STAGE_AUTO;
     d.splits = 0;
-    std::int32_t tile = 0, stage = 0, splits = 0;
-    check(mfr_sgemm_plan(args.outputs[0].device().index, &d, &tile, &stage, &splits));
+    std::int32_t tile = 0, stage = 0, splits = 0, regions = 0;
+    check(mfr_sgemm_plan(args.outputs[0].device().index, &d, &tile, &stage, &splits, &regions));
     if (tile == MFR_TILE_AUTO) {
         return {}; // nothing to compute: nothing to tune
     }
     SearchRegion region;
     region.name = "mfma";
     region.start = tuning_of(tile, stage, splits);
-    region.axes = {{0, {MFR_TILE_64x64, MFR_TILE_128x64, MFR_TILE_64x128, MFR_TILE_128x128,
-                        MFR_TILE_256x256}},
+    region.axes = {{0, {MFR_TILE_THIN, MFR_TILE_64x64, MFR_TILE_128x64, MFR_TILE_64x128,
+                        MFR_TILE_128x128, MFR_TILE_256x256}},
                    {1, {MFR_STAGE_NEVER, MFR_STAGE_ALWAYS}},
                    {2, {1, 2, 4, 8, 16, 32}}};
     return {region};
@@ -334,8 +335,9 @@ template <OpId Op> bool gemm_allowed(const OpArgs& args, const TuningConfig& con
     OpArgs tuned = args;
     tuned.tuning = config;
     const mfr_gemm_desc d = planned_desc(Op, tuned);
-    std::int32_t tile = 0, stage = 0, splits = 0;
-    return mfr_sgemm_plan(args.outputs[0].device().index, &d, &tile, &stage, &splits) == MFR_OK &&
+    std::int32_t tile = 0, stage = 0, splits = 0, regions = 0;
+    return mfr_sgemm_plan(args.outputs[0].device().index, &d, &tile, &stage, &splits,
+                          &regions) == MFR_OK &&
            splits == config.values[2];
 }
 

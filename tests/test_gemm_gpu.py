@@ -114,7 +114,7 @@ def test_exact_alpha_beta_in_place(stream, trans_a, trans_b):
     assert same_bits(c.numpy(), want.astype(np.float32))
 
 
-TILES = list(range(1, mf.abi.TILE_COUNT))
+TILES = list(range(1, mf.abi.TILE_THIN))  # the MFMA tiles
 
 
 def wide_loads_possible(a_stored, b_stored):
@@ -233,11 +233,11 @@ def test_plan_on_baseline_shapes(stream):
     with staging off is refused on operands 16-byte loads cannot read, and staged otherwise."""
     abi = mf.abi
     big = mf.DeviceArray.empty((4096, 4096), stream)
-    assert mf.gemm_plan(big, big.T, big) == (abi.TILE_256x256, abi.STAGE_NEVER, 1)
+    assert mf.gemm_plan(big, big.T, big) == (abi.TILE_256x256, abi.STAGE_NEVER, 1, 1)
     x = mf.DeviceArray.empty((4093, 1023), stream)
     w = mf.DeviceArray.empty((1023, 4099), stream)
     out = mf.DeviceArray.empty((4093, 4099), stream)
-    tile, stage, splits = mf.gemm_plan(x, w, out)
+    tile, stage, splits, regions = mf.gemm_plan(x, w, out)
     assert splits == 1
     assert stage == abi.STAGE_ALWAYS and tile != abi.TILE_AUTO
     assert mf.gemm_plan(x, w, out, stage=abi.STAGE_NEVER)[1] == abi.STAGE_NEVER
@@ -388,6 +388,129 @@ def test_split_k_realistic(stream, oracle, m, n, k):
         got = mf.gemm(a_d, b_d, splits=splits).numpy()
         assert_gemm_parity(got, want, scale, k, f"split {splits}")
         assert same_bits(got, mf.gemm(a_d, b_d, splits=splits).numpy())
+
+
+@pytest.mark.parametrize("m,n,k,regions", [(4093, 4099, 1023, 2), (4099, 4093, 1023, 2),
+                                           (4099, 4099, 2048, 4)])
+def test_peeled_edges_exact(stream, m, n, k, regions):
+    """AUTO peels edge strips a big tile would waste a wave on into launches of their own: the
+    MLP's 3 extra columns, 3 extra rows, and both (main, right strip, bottom strip, corner).
+    Quarter-integer inputs with alpha, beta*C0 and a bias: every region's bits equal the exact
+    product, which pins each strip's offsets into A, B, C, C0 and the bias; no stray writes."""
+    a = quarter_matrix(m, k, 211)
+    b = quarter_matrix(k, n, 212)
+    c0 = quarter_matrix(m, n, 213)
+    bias = quarter_matrix(1, n, 214)[0]
+    want = (np.float32(1.5) * exact_product(a, b)) + np.float32(0.5) * c0
+    want = (want + bias).astype(np.float32)
+    a_d, b_d, c0_d = dev(a, stream), dev(b, stream), dev(c0, stream)
+    c, buf = guarded_output(stream, (m, n))
+    assert mf.gemm_plan(a_d, b_d, c, c0=c0_d, beta=0.5)[3] == regions
+    mf.gemm(a_d, b_d, alpha=1.5, c0=c0_d, beta=0.5, bias=dev(bias, stream), out=c)
+    assert same_bits(c.numpy(), want)
+    check_guards(buf)
+    # A fixed tile or split count runs one region.
+    assert mf.gemm_plan(a_d, b_d, c, tile=mf.abi.TILE_64x64)[3] == 1
+    assert mf.gemm_plan(a_d, b_d, c, splits=1)[3] == 1
+
+
+# ---- the thin path ------------------------------------------------------------------------------
+
+THIN = mf.abi.TILE_THIN
+
+
+@pytest.mark.parametrize("m,n,k", [(4093, 3, 1023), (4096, 8, 1024), (300, 1, 77), (17, 5, 2500),
+                                   (1, 1, 1), (9, 8, 3)])
+def test_thin_exact_rows(stream, m, n, k):
+    """n <= 8 with A read along k (4-byte loads for odd k, 16-byte for k % 4 == 0), with alpha,
+    beta*C0 and a bias: the thin path's bits equal the exact product; no stray writes."""
+    a = quarter_matrix(m, k, 221)
+    b = quarter_matrix(k, n, 222)
+    c0 = quarter_matrix(m, n, 223)
+    bias = quarter_matrix(1, n, 224)[0]
+    want = (np.float32(1.5) * exact_product(a, b)) + np.float32(0.5) * c0
+    want = (want + bias).astype(np.float32)
+    for b_stored_t in (False, True):
+        for stage in (mf.abi.STAGE_AUTO, mf.abi.STAGE_ALWAYS):
+            # Staged, A's lines are padded to a multiple of 4 and read with 16-byte loads even
+            # for odd k; B has no depth past k, which must not be read.
+            b_d = dev(np.ascontiguousarray(b.T), stream).T if b_stored_t else dev(b, stream)
+            c, buf = guarded_output(stream, (m, n))
+            mf.gemm(dev(a, stream), b_d, alpha=1.5, c0=dev(c0, stream), beta=0.5,
+                    bias=dev(bias, stream), out=c, tile=THIN, stage=stage)
+            assert same_bits(c.numpy(), want), (b_stored_t, stage)
+            check_guards(buf)
+
+
+@pytest.mark.parametrize("m,n,k", [(3, 4099, 1023), (8, 4096, 1024), (1, 300, 77), (5, 17, 2500)])
+def test_thin_exact_transposed(stream, m, n, k):
+    """m <= 8 with B read along k (B stored [n, k], read transposed): the thin path computes
+    C^T = B^T A^T row by row of B^T; bits equal the exact product, bias per column of C."""
+    a = quarter_matrix(m, k, 231)
+    b_stored = quarter_matrix(n, k, 232)
+    c0 = quarter_matrix(m, n, 233)
+    bias = quarter_matrix(1, n, 234)[0]
+    want = (np.float32(0.25) * exact_product(a, b_stored.T)) + np.float32(-2.0) * c0
+    want = (want + bias).astype(np.float32)
+    for a_stored_t in (False, True):
+        a_d = dev(np.ascontiguousarray(a.T), stream).T if a_stored_t else dev(a, stream)
+        c, buf = guarded_output(stream, (m, n))
+        mf.gemm(a_d, dev(b_stored, stream), trans_b=True, alpha=0.25, c0=dev(c0, stream),
+                beta=-2.0, bias=dev(bias, stream), out=c, tile=THIN)
+        assert same_bits(c.numpy(), want), a_stored_t
+        check_guards(buf)
+
+
+def test_thin_batched_broadcast_gelu(stream):
+    """A [2,3] batch with B broadcast over the first dimension; gelu on the thin path gives the
+    bits an MFMA tile gives (the same exact pre-activation values)."""
+    bsz, heads, m, n, k = 2, 3, 70, 5, 300
+    a = quarter_matrix(bsz * heads * m, k, 241).reshape(bsz, heads, m, k)
+    bv = quarter_matrix(heads * k, n, 242).reshape(1, heads, k, n)
+    b_d = dev(bv, stream).expand((bsz, heads, k, n))
+    bias = dev(quarter_matrix(1, n, 243)[0], stream)
+    thin = mf.DeviceArray.empty((bsz, heads, m, n), stream)
+    tiled = mf.DeviceArray.empty((bsz, heads, m, n), stream)
+    mf.gemm_batched(dev(a, stream), b_d, thin, bias=bias, act=mf.ACT_GELU_TANH, tile=THIN)
+    mf.gemm_batched(dev(a, stream), b_d, tiled, bias=bias, act=mf.ACT_GELU_TANH,
+                    tile=mf.abi.TILE_64x64)
+    assert same_bits(thin.numpy(), tiled.numpy())
+    plain = mf.DeviceArray.empty((bsz, heads, m, n), stream)
+    mf.gemm_batched(dev(a, stream), b_d, plain, tile=THIN)
+    got = plain.numpy()
+    for i in range(bsz):
+        for h in range(heads):
+            assert same_bits(got[i, h], exact_product(a[i, h], bv[0, h])), (i, h)
+
+
+def test_thin_k_zero_and_refusals(stream):
+    m, n = 33, 4
+    c0 = quarter_matrix(m, n, 251)
+    c, _ = guarded_output(stream, (m, n))
+    mf.gemm(mf.DeviceArray.empty((m, 0), stream), mf.DeviceArray.empty((0, n), stream),
+            alpha=2.0, c0=dev(c0, stream), beta=0.5, out=c, tile=THIN)
+    assert same_bits(c.numpy(), (np.float32(0.5) * c0).astype(np.float32))
+    wide = dev(np.ones((64, 64), np.float32), stream)
+    with pytest.raises(NotImplementedError):        # n > 8 and m > 8
+        mf.gemm(wide, wide, tile=THIN)
+    a_t = dev(np.ones((64, 300), np.float32), stream).T  # [300, 64], unit stride along m
+    with pytest.raises(NotImplementedError):        # n <= 8 but A not read along k
+        mf.gemm(a_t, dev(np.ones((64, 3), np.float32), stream), tile=THIN)
+    with pytest.raises(NotImplementedError):        # no split on the thin path
+        mf.gemm(dev(np.ones((300, 64), np.float32), stream),
+                dev(np.ones((64, 3), np.float32), stream), tile=THIN, splits=2)
+
+
+def test_thin_automatic_choice(stream):
+    """AUTO takes the thin path for a long product with a few columns (the MLP's 3-column edge
+    strip), and the MFMA tiles where the output fills them."""
+    def plan(m, n, k, **kw):
+        return mf.gemm_plan(mf.DeviceArray.empty((m, k), stream),
+                            mf.DeviceArray.empty((k, n), stream),
+                            mf.DeviceArray.empty((m, n), stream), **kw)
+    assert plan(4093, 3, 1023)[0] == THIN
+    assert plan(16384, 1, 16384)[0] == THIN
+    assert plan(4096, 4096, 4096)[0] == mf.abi.TILE_256x256
 
 
 def test_unknown_stage_mode_is_invalid(stream):
