@@ -25,7 +25,7 @@ from .abi import ACT_GELU_ERF, ACT_GELU_TANH, ACT_NONE, GemmDesc  # noqa: F401
 __all__ = [
     "ACT_NONE", "ACT_GELU_TANH", "ACT_GELU_ERF", "GemmDesc", "device_count", "device_info",
     "Stream", "DeviceArray", "Event", "sgemm", "gemm", "gemm_batched", "sgemv", "matvec",
-    "bias_act", "where", "softmax", "argmax", "strided_copy", "fill", "attention",
+    "bias_act", "where", "elementwise", "softmax", "argmax", "strided_copy", "fill", "attention",
     "attention_fused", "attention_composed", "gemm_plan",
 ]
 
@@ -408,6 +408,18 @@ def where(cond: DeviceArray, x: DeviceArray, y: DeviceArray,
         out = DeviceArray.empty(x.shape, x.stream)
     abi.check(abi.load().mfr_where(x.stream.handle, cond.ptr, x.ptr, y.ptr, out.ptr, x.size),
               "mfr_where")
+    return out
+
+
+def elementwise(op: int, a: DeviceArray, b: DeviceArray | None = None, alpha=1.0,
+                out: DeviceArray | None = None) -> DeviceArray:
+    """out = a + b (abi.EW_ADD), a * b (abi.EW_MUL) or alpha * a (abi.EW_SCAL, b unused) over
+    contiguous arrays of a's size (mfr_elementwise)."""
+    if out is None:
+        out = DeviceArray.empty(a.shape, a.stream)
+    b_ptr = None if b is None else b.ptr
+    abi.check(abi.load().mfr_elementwise(a.stream.handle, op, a.ptr, b_ptr, alpha, out.ptr,
+                                         a.size), "mfr_elementwise")
     return out
 
 

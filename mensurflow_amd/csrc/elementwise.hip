@@ -63,6 +63,101 @@ __global__ void where_kernel(const uint8_t* __restrict__ cond, const float* __re
     }
 }
 
+// ---- 16-byte streaming forms (every pointer 16-byte aligned; cond 4-byte aligned) ----------
+//
+// Each workgroup streams one contiguous chunk of `chunk` quads (4 elements), its threads kStreamUnroll
+// quads apart per step with every load of a step issued before any is used, non-temporal (each
+// element is read once), as the device copy streams. The last n % 4 elements go to the scalar
+// kernels.
+constexpr int kStreamThreads = 256;
+constexpr int kStreamUnroll = 4;
+
+inline bool aligned_to(const void* p, uintptr_t bytes) {
+    return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0;
+}
+
+// Workgroups and quads per workgroup for `quads` quads (at most 4096 workgroups).
+inline void stream_shape(int64_t quads, unsigned* blocks, int64_t* chunk) {
+    const int64_t per_step = static_cast<int64_t>(kStreamThreads) * kStreamUnroll;
+    int64_t b = (quads + per_step - 1) / per_step;
+    b = b < 1 ? 1 : (b > 4096 ? 4096 : b);
+    *chunk = (quads + b - 1) / b;
+    *blocks = static_cast<unsigned>((quads + *chunk - 1) / *chunk);
+}
+
+__global__ __launch_bounds__(kStreamThreads) void where4_kernel(
+    const uint32_t* __restrict__ cond, const float4* __restrict__ x, const float4* __restrict__ y,
+    float4* __restrict__ out, int64_t quads, int64_t chunk) {
+    const int64_t begin = static_cast<int64_t>(blockIdx.x) * chunk;
+    const int64_t end = begin + chunk < quads ? begin + chunk : quads;
+    for (int64_t i = begin + threadIdx.x; i < end; i += kStreamThreads * kStreamUnroll) {
+        uint32_t c[kStreamUnroll];
+        float4 xv[kStreamUnroll], yv[kStreamUnroll];
+#pragma unroll
+        for (int u = 0; u < kStreamUnroll; ++u) {
+            const int64_t j = i + u * kStreamThreads;
+            if (j < end) {
+                c[u] = __builtin_nontemporal_load(cond + j);
+                xv[u] = mfr::dev::load_streaming(reinterpret_cast<const float*>(x + j));
+                yv[u] = mfr::dev::load_streaming(reinterpret_cast<const float*>(y + j));
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kStreamUnroll; ++u) {
+            const int64_t j = i + u * kStreamThreads;
+            if (j < end) {
+                float4 v;
+                v.x = (c[u] & 0xffu) != 0 ? xv[u].x : yv[u].x;
+                v.y = (c[u] & 0xff00u) != 0 ? xv[u].y : yv[u].y;
+                v.z = (c[u] & 0xff0000u) != 0 ? xv[u].z : yv[u].z;
+                v.w = (c[u] & 0xff000000u) != 0 ? xv[u].w : yv[u].w;
+                out[j] = v;
+            }
+        }
+    }
+}
+
+template <int OP>
+__global__ __launch_bounds__(kStreamThreads) void binary4_kernel(const float4* __restrict__ a,
+                                                                 const float4* __restrict__ b,
+                                                                 float alpha,
+                                                                 float4* __restrict__ out,
+                                                                 int64_t quads, int64_t chunk) {
+    const int64_t begin = static_cast<int64_t>(blockIdx.x) * chunk;
+    const int64_t end = begin + chunk < quads ? begin + chunk : quads;
+    for (int64_t i = begin + threadIdx.x; i < end; i += kStreamThreads * kStreamUnroll) {
+        float4 av[kStreamUnroll], bv[kStreamUnroll];
+#pragma unroll
+        for (int u = 0; u < kStreamUnroll; ++u) {
+            const int64_t j = i + u * kStreamThreads;
+            if (j < end) {
+                av[u] = mfr::dev::load_streaming(reinterpret_cast<const float*>(a + j));
+                if constexpr (OP != MFR_EW_SCAL) {
+                    bv[u] = mfr::dev::load_streaming(reinterpret_cast<const float*>(b + j));
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kStreamUnroll; ++u) {
+            const int64_t j = i + u * kStreamThreads;
+            if (j < end) {
+                float4 v;
+                if constexpr (OP == MFR_EW_ADD) {
+                    v = make_float4(av[u].x + bv[u].x, av[u].y + bv[u].y, av[u].z + bv[u].z,
+                                    av[u].w + bv[u].w);
+                } else if constexpr (OP == MFR_EW_MUL) {
+                    v = make_float4(av[u].x * bv[u].x, av[u].y * bv[u].y, av[u].z * bv[u].z,
+                                    av[u].w * bv[u].w);
+                } else {
+                    v = make_float4(alpha * av[u].x, alpha * av[u].y, alpha * av[u].z,
+                                    alpha * av[u].w);
+                }
+                out[j] = v;
+            }
+        }
+    }
+}
+
 // The reference's line maximum: a NaN anywhere makes it NaN (the scan stops at the first NaN),
 // otherwise the largest value (-inf for an empty or all -inf line).
 __device__ inline float line_max(float m, int has_nan) { return has_nan ? NAN : m; }
@@ -240,9 +335,35 @@ int mfr_elementwise(mfr_stream_t stream, int op, const float* a, const float* b,
         }
         mfr::require(a != nullptr && out != nullptr && (op == MFR_EW_SCAL || b != nullptr),
                      "elementwise: null pointer");
-        binary_kernel<<<mfr::grid_blocks(n, 256, 16384), 256, 0, s.stream>>>(op, a, b, alpha, out,
-                                                                             n);
-        mfr::check_launch("binary_kernel");
+        int64_t done = 0;
+        if (aligned_to(a, 16) && aligned_to(out, 16) && (op == MFR_EW_SCAL || aligned_to(b, 16)) &&
+            n >= 4) {
+            const int64_t quads = n / 4;
+            unsigned blocks = 0;
+            int64_t chunk = 0;
+            stream_shape(quads, &blocks, &chunk);
+            const auto* a4 = reinterpret_cast<const float4*>(a);
+            const auto* b4 = reinterpret_cast<const float4*>(b);
+            auto* o4 = reinterpret_cast<float4*>(out);
+            if (op == MFR_EW_ADD) {
+                binary4_kernel<MFR_EW_ADD><<<blocks, kStreamThreads, 0, s.stream>>>(
+                    a4, b4, alpha, o4, quads, chunk);
+            } else if (op == MFR_EW_MUL) {
+                binary4_kernel<MFR_EW_MUL><<<blocks, kStreamThreads, 0, s.stream>>>(
+                    a4, b4, alpha, o4, quads, chunk);
+            } else {
+                binary4_kernel<MFR_EW_SCAL><<<blocks, kStreamThreads, 0, s.stream>>>(
+                    a4, b4, alpha, o4, quads, chunk);
+            }
+            mfr::check_launch("binary4_kernel");
+            done = 4 * quads;
+        }
+        if (done < n) {
+            const int64_t rest = n - done;
+            binary_kernel<<<mfr::grid_blocks(rest, 256, 16384), 256, 0, s.stream>>>(
+                op, a + done, op == MFR_EW_SCAL ? b : b + done, alpha, out + done, rest);
+            mfr::check_launch("binary_kernel");
+        }
     });
 }
 
@@ -281,8 +402,25 @@ int mfr_where(mfr_stream_t stream, const uint8_t* cond, const float* x, const fl
         }
         mfr::require(cond != nullptr && x != nullptr && y != nullptr && out != nullptr,
                      "where: null pointer");
-        where_kernel<<<mfr::grid_blocks(n, 256, 16384), 256, 0, s.stream>>>(cond, x, y, out, n);
-        mfr::check_launch("where_kernel");
+        int64_t done = 0;
+        if (aligned_to(cond, 4) && aligned_to(x, 16) && aligned_to(y, 16) && aligned_to(out, 16) &&
+            n >= 4) {
+            const int64_t quads = n / 4;
+            unsigned blocks = 0;
+            int64_t chunk = 0;
+            stream_shape(quads, &blocks, &chunk);
+            where4_kernel<<<blocks, kStreamThreads, 0, s.stream>>>(
+                reinterpret_cast<const uint32_t*>(cond), reinterpret_cast<const float4*>(x),
+                reinterpret_cast<const float4*>(y), reinterpret_cast<float4*>(out), quads, chunk);
+            mfr::check_launch("where4_kernel");
+            done = 4 * quads;
+        }
+        if (done < n) {
+            const int64_t rest = n - done;
+            where_kernel<<<mfr::grid_blocks(rest, 256, 16384), 256, 0, s.stream>>>(
+                cond + done, x + done, y + done, out + done, rest);
+            mfr::check_launch("where_kernel");
+        }
     });
 }
 

@@ -113,6 +113,27 @@ def test_argmax_bit_exact(stream, vectors, oracle):
     assert mf.argmax(dev(x, stream)).numpy().tolist() == oracle.argmax(x).tolist()
 
 
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 8, 1023, 4096, 4099, (1 << 20) + 3])
+@pytest.mark.parametrize("offset", [0, 1, 3])
+def test_where_and_binary_sizes_and_alignment(stream, n, offset):
+    """where, add, mul and scal bit for bit against numpy on every size class (multiples of 4 go
+    through the 16-byte streaming kernels, the rest of n through the scalar ones) and on views
+    starting 1 or 3 elements into their buffers (misaligned: the scalar kernels only)."""
+    rng = np.random.default_rng(n + offset)
+    xs = rng.standard_normal(n + offset).astype(np.float32)
+    ys = rng.standard_normal(n + offset).astype(np.float32)
+    cs = (rng.random(n + offset) < 0.5).astype(np.uint8)
+    x = dev(xs, stream).slice(0, offset, offset + n)
+    y = dev(ys, stream).slice(0, offset, offset + n)
+    c = dev(cs, stream).slice(0, offset, offset + n)
+    xv, yv, cv = xs[offset:], ys[offset:], cs[offset:]
+    assert same_bits(mf.where(c, x, y).numpy(), np.where(cv != 0, xv, yv))
+    abi = mf.abi
+    assert same_bits(mf.elementwise(abi.EW_ADD, x, y).numpy(), xv + yv)
+    assert same_bits(mf.elementwise(abi.EW_MUL, x, y).numpy(), xv * yv)
+    assert same_bits(mf.elementwise(abi.EW_SCAL, x, alpha=-1.5).numpy(), np.float32(-1.5) * xv)
+
+
 def test_strided_copy_views(stream, oracle):
     base = uniform(oracle, (6, 7, 9), -1.0, 1.0, 88, 0)
     d = dev(base, stream)
