@@ -168,7 +168,7 @@ enum { MFR_STAGE_AUTO = 0, MFR_STAGE_NEVER = 1, MFR_STAGE_ALWAYS = 2 };
  * src/core/dispatcher.hpp:145-149). Every tile gives the same results up to summation order. */
 enum {
     MFR_TILE_AUTO = 0,
-    MFR_TILE_256x256 = 1, /* 8 wavefronts of 128x64, 1 workgroup per CU */
+    MFR_TILE_256x256 = 1, /* 16 wavefronts of 64x64, 1 workgroup per CU */
     MFR_TILE_128x128 = 2, /* 4 wavefronts of 64x64, 2 per CU */
     MFR_TILE_128x64 = 3,  /* 4 wavefronts of 64x32, depth slice 16, up to 5 per CU */
     MFR_TILE_64x128 = 4,  /* 4 wavefronts of 32x64, depth slice 16 */

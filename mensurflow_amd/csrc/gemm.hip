@@ -3,7 +3,7 @@
 //
 //   C[b] = act( fl( fl( fl(alpha * op(A[b]) op(B[b])) + fl(beta * C0[b]) ) + bias ) )
 //
-// Design (a workgroup of 4 or 8 wavefronts of 64 lanes; five tile shapes, chosen per call):
+// Design (a workgroup of 4 or 16 wavefronts of 64 lanes; five tile shapes, chosen per call):
 //   - The workgroup computes a BM x BN tile of C; its wavefronts form a WAVES_M x WAVES_N grid,
 //     each owning a (BM/WAVES_M) x (BN/WAVES_N) sub-tile held in 32x32 accumulator blocks of
 //     v_mfma_f32_32x32x2_f32 (16 fp32 accumulators per lane per block).
@@ -49,7 +49,7 @@ struct TileInfo {
 };
 constexpr TileInfo kTiles[MFR_TILE_COUNT] = {
     {0, 0, 0, 0, 0.0},         // AUTO
-    {256, 256, 1, 8, 133.4},   // 8 wavefronts of 128x64, depth slice 32
+    {256, 256, 1, 16, 135.3},  // 16 wavefronts of 64x64, depth slice 32
     {128, 128, 2, 4, 127.3},   // 4 wavefronts of 64x64, depth slice 32
     {128, 64, 5, 4, 114.9},    // 4 wavefronts of 64x32, depth slice 16
     {64, 128, 5, 4, 116.0},    // 4 wavefronts of 32x64, depth slice 16
@@ -303,7 +303,7 @@ void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned block
                    hipStream_t stream) {
     switch (tile) {
     case MFR_TILE_256x256: // 16-byte loads only (checked by the caller)
-        sgemm_kernel<256, 256, 32, 2, 4, AK, BK, 4, 4><<<blocks, 512, 0, stream>>>(p);
+        sgemm_kernel<256, 256, 32, 4, 4, AK, BK, 4, 4><<<blocks, 1024, 0, stream>>>(p);
         break;
     case MFR_TILE_128x64:
         launch_vec<128, 64, 16, 2, 2, AK, BK>(p, va, vb, blocks, stream);
