@@ -414,6 +414,26 @@ def test_peeled_edges_exact(stream, m, n, k, regions):
     assert mf.gemm_plan(a_d, b_d, c, splits=1)[3] == 1
 
 
+@pytest.mark.parametrize("bsz,m,n,k", [(2, 4093, 2051, 1023), (3, 2049, 2047, 2048)])
+def test_peeled_edges_batched_broadcast_exact(stream, bsz, m, n, k):
+    """Peeling on a batch, B broadcast over it (batch stride 0), with alpha, beta*C0 and a bias:
+    the strips' offsets combine with every matrix's batch offsets."""
+    a = quarter_matrix(bsz * m, k, 261).reshape(bsz, m, k)
+    b = quarter_matrix(k, n, 262)
+    c0 = quarter_matrix(bsz * m, n, 263).reshape(bsz, m, n)
+    bias = quarter_matrix(1, n, 264)[0]
+    a_d = dev(a, stream)
+    b_d = dev(b.reshape(1, k, n), stream).expand((bsz, k, n))
+    c0_d = dev(c0, stream)
+    out = mf.DeviceArray.empty((bsz, m, n), stream)
+    assert mf.gemm_plan(a_d, b_d, out, c0=c0_d, beta=0.5)[3] == 2
+    mf.gemm_batched(a_d, b_d, out, alpha=1.5, c0=c0_d, beta=0.5, bias=dev(bias, stream))
+    got = out.numpy()
+    for i in range(bsz):
+        want = (np.float32(1.5) * exact_product(a[i], b)) + np.float32(0.5) * c0[i]
+        assert same_bits(got[i], (want + bias).astype(np.float32)), i
+
+
 # ---- the thin path ------------------------------------------------------------------------------
 
 THIN = mf.abi.TILE_THIN
