@@ -3,7 +3,8 @@
 //
 //   C[b] = act( fl( fl( fl(alpha * op(A[b]) op(B[b])) + fl(beta * C0[b]) ) + bias ) )
 //
-// Design (a workgroup of 4 or 16 wavefronts of 64 lanes; five tile shapes, chosen per call):
+// Design (a workgroup of 4 or 16 wavefronts of 64 lanes; five MFMA tile shapes and a thin path,
+// chosen per call with the split-K count and edge peeling, below):
 //   - The workgroup computes a BM x BN tile of C; its wavefronts form a WAVES_M x WAVES_N grid,
 //     each owning a (BM/WAVES_M) x (BN/WAVES_N) sub-tile held in 32x32 accumulator blocks of
 //     v_mfma_f32_32x32x2_f32 (16 fp32 accumulators per lane per block).
@@ -28,6 +29,11 @@
 //     (X[4093,1023] row-major) is copied first into the stream's workspace with its lines padded
 //     to a multiple of 4 by zeros (stage_kernel); vector loads that reach past the end of a line
 //     then read zeros of its own line, and the zeros add nothing to any sum.
+//   - The epilogue applies the activation chosen once per workgroup, with copies for interior
+//     tiles and for C0, so each copy is straight-line code (gemm_kernel.hpp, write_tile).
+//   - Split-K cuts a long depth into ranges run as workgroups of their own, reduced in order by
+//     split_reduce_kernel; edge peeling runs a thin remainder of the output as launches of its
+//     own; the thin path (thin_kernel.hpp) takes products with at most 8 output columns or rows.
 #include "gemm_kernel.hpp"
 #include "thin_kernel.hpp"
 
