@@ -106,12 +106,15 @@ double simd_efficiency(int64_t waves_per_simd) {
 double modelled_us(int t, int64_t m, int64_t n, int64_t k, int64_t batch, int cus, int splits,
                    int64_t per, bool c0) {
     const TileInfo& info = kTiles[t];
-    const int64_t per_cu = (tile_count(t, m, n, batch) * splits + cus - 1) / cus;
+    const int64_t count = tile_count(t, m, n, batch) * splits;
+    const int64_t per_cu = (count + cus - 1) / cus;
     const int64_t concurrent = per_cu < info.occupancy ? per_cu : info.occupancy;
+    // The 128x128 tile runs 8 wavefronts when no CU gets two (launch_layout).
+    const int64_t waves = t == MFR_TILE_128x128 && count <= cus ? 8 : info.waves;
     const int64_t reference_waves = (4096 / info.bm) * (4096 / info.bn) / 256;
     const int64_t ref_concurrent =
         reference_waves < info.occupancy ? reference_waves : info.occupancy;
-    const double efficiency = simd_efficiency(concurrent * info.waves / 4) /
+    const double efficiency = simd_efficiency(concurrent * waves / 4) /
                               simd_efficiency(ref_concurrent * info.waves / 4);
     const double depth = static_cast<double>(splits > 1 ? per : k);
     const double overhead = kTileOverheadDepth / static_cast<double>(concurrent);
@@ -304,8 +307,11 @@ void launch_vec(const GemmParams& p, int va, int vb, unsigned blocks, hipStream_
     }
 }
 
+// one_per_cu: no CU gets more than one workgroup. The 128x128 tile then runs 8 wavefronts of
+// 64x32 (2 per SIMD) instead of 4 of 64x64: 2048^3 145 against 155 us. With two workgroups per
+// CU the 4 wavefronts are faster (4096^3 1075 against 1105 us).
 template <bool AK, bool BK>
-void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned blocks,
+void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned blocks, bool one_per_cu,
                    hipStream_t stream) {
     switch (tile) {
     case MFR_TILE_256x256: // 16-byte loads only (checked by the caller)
@@ -321,7 +327,11 @@ void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned block
         launch_vec<64, 64, 32, 2, 2, AK, BK>(p, va, vb, blocks, stream);
         break;
     default:
-        launch_vec<128, 128, 32, 2, 2, AK, BK>(p, va, vb, blocks, stream);
+        if (one_per_cu) {
+            launch_vec<128, 128, 32, 2, 4, AK, BK>(p, va, vb, blocks, stream);
+        } else {
+            launch_vec<128, 128, 32, 2, 2, AK, BK>(p, va, vb, blocks, stream);
+        }
         break;
     }
 }
@@ -755,7 +765,7 @@ void launch_thin(const Plan& plan, const GemmParams& q, int va, int vb, hipStrea
 
 // Launches the kernel (and the reduce, when split) for region r of the product p describes.
 void launch_region(const Plan& plan, const GemmParams& p, const Region& r, int va, int vb,
-                   float* partial, hipStream_t stream) {
+                   float* partial, int cus, hipStream_t stream) {
     using mfr::require;
     GemmParams q = p;
     q.m = r.m;
@@ -783,14 +793,15 @@ void launch_region(const Plan& plan, const GemmParams& p, const Region& r, int v
     q.k_per_split = r.splits > 1 ? r.per : q.k;
     q.partial = r.splits > 1 ? partial : nullptr;
     const unsigned grid = static_cast<unsigned>(blocks);
+    const bool one_per_cu = blocks <= cus;
     if (plan.ak && plan.bk) {
-        launch_layout<true, true>(tile, q, va, vb, grid, stream);
+        launch_layout<true, true>(tile, q, va, vb, grid, one_per_cu, stream);
     } else if (plan.ak) {
-        launch_layout<true, false>(tile, q, va, vb, grid, stream);
+        launch_layout<true, false>(tile, q, va, vb, grid, one_per_cu, stream);
     } else if (plan.bk) {
-        launch_layout<false, true>(tile, q, va, vb, grid, stream);
+        launch_layout<false, true>(tile, q, va, vb, grid, one_per_cu, stream);
     } else {
-        launch_layout<false, false>(tile, q, va, vb, grid, stream);
+        launch_layout<false, false>(tile, q, va, vb, grid, one_per_cu, stream);
     }
     mfr::check_launch("sgemm_kernel");
     if (q.partial != nullptr) {
@@ -856,7 +867,7 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
         vb = 4;
     }
     for (int i = 0; i < plan.region_count; ++i) {
-        launch_region(plan, p, plan.regions[i], va, vb, partial, s.stream);
+        launch_region(plan, p, plan.regions[i], va, vb, partial, s.compute_units, s.stream);
     }
 }
 

@@ -125,9 +125,11 @@ def wide_loads_possible(a_stored, b_stored):
 
 @pytest.mark.parametrize("tile", TILES)
 @pytest.mark.parametrize("m,n,k", [(300, 260, 1000), (257, 129, 257), (1, 300, 64),
-                                   (513, 7, 96), (64, 64, 2000), (129, 65, 36)])
+                                   (513, 7, 96), (64, 64, 2000), (129, 65, 36), (2100, 2100, 64)])
 def test_exact_every_tile(stream, tile, m, n, k):
-    """Every workgroup tile on edge shapes and all four layouts: bits equal the exact product."""
+    """Every workgroup tile on edge shapes and all four layouts: bits equal the exact product.
+    2100^2 has more tiles than CUs for the 128x128 tile, so both of its launch forms (8
+    wavefronts at one workgroup per CU, 4 beyond) are covered."""
     a = quarter_matrix(m, k, 71)
     b = quarter_matrix(k, n, 72)
     c0 = quarter_matrix(m, n, 73)
