@@ -37,6 +37,21 @@ constexpr int kWaves = 4; // wavefronts of 32 queries per workgroup, by default
 // 256 queries (8 x 16 x 1024, causal: d = 64 189-191 us against 199-205 us with 4; d = 128
 // 346 us against 373-376 us), 4 for d = 32 (109 us with 8 against 105 us).
 constexpr int waves_for(int64_t d) { return d == 32 ? kWaves : 8; }
+
+// Wavefronts per workgroup for one launch: waves_for(d), except 4 for d = 64 and 128 when
+// workgroups of 8 would leave fewer than two per CU (causal) or idle CUs. Causal work grows with
+// the query block, and with that few workgroups the longest decides the time (1 x 16 x 4096 x 64:
+// 16 heads x 16 query blocks of 256, 1 to 16 units of work, one workgroup per CU). With 4, twice
+// as many half-size workgroups, two resident per CU, are issued paired (see AttnParams::paired),
+// so each CU's pair sums to about the average.
+int waves_used(int64_t d, int64_t lq, int64_t batch_count, bool causal, int cus) {
+    const int w = waves_for(d);
+    if (w == 4) {
+        return 4;
+    }
+    const int64_t blocks = batch_count * ((lq + 32 * w - 1) / (32 * w));
+    return blocks < (causal ? 2 : 1) * static_cast<int64_t>(cus) ? 4 : w;
+}
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnParams {
@@ -54,6 +69,9 @@ struct AttnParams {
     int32_t batch_dims;
     int32_t causal;
     int32_t q_blocks;
+    // Issue order of the query blocks: longest first, or (paired) the longer half longest first,
+    // then the shorter half shortest first.
+    int32_t paired;
     float scale;
 };
 
@@ -87,7 +105,9 @@ __global__ __launch_bounds__(WAVES * 64, MIN_WAVES) void attention_kernel(AttnPa
 
     // ---- which (batch entry, query block): the longest (last) query blocks first ----
     const int64_t bid = blockIdx.x;
-    const int64_t qb = p.q_blocks - 1 - bid / p.batch_count;
+    const int64_t level = bid / p.batch_count;
+    const int64_t longer = (p.q_blocks + 1) / 2; // levels issued longest first when paired
+    const int64_t qb = !p.paired || level < longer ? p.q_blocks - 1 - level : level - longer;
     int64_t bi = bid % p.batch_count;
     int64_t off_q = 0, off_k = 0, off_v = 0, off_o = 0, off_m = 0;
     for (int d = p.batch_dims - 1; d >= 0; --d) {
@@ -348,7 +368,8 @@ __global__ __launch_bounds__(WAVES * 64, MIN_WAVES) void attention_kernel(AttnPa
     }
 }
 
-template <bool MASKED> void launch(int64_t d, const AttnParams& p, unsigned grid, hipStream_t st) {
+template <bool MASKED>
+void launch(int64_t d, int waves, const AttnParams& p, unsigned grid, hipStream_t st) {
     switch (d) {
     case 32:
         // 3 wavefronts per SIMD where the registers allow it (148 VGPRs without a mask):
@@ -357,11 +378,20 @@ template <bool MASKED> void launch(int64_t d, const AttnParams& p, unsigned grid
             <<<grid, waves_for(32) * 64, 0, st>>>(p);
         break;
     case 64:
-        attention_kernel<64, 64, MASKED, waves_for(64)><<<grid, waves_for(64) * 64, 0, st>>>(p);
+        if (waves == 4) {
+            attention_kernel<64, 64, MASKED, 4><<<grid, 4 * 64, 0, st>>>(p);
+        } else {
+            attention_kernel<64, 64, MASKED, waves_for(64)><<<grid, waves_for(64) * 64, 0, st>>>(
+                p);
+        }
         break;
     default:
-        attention_kernel<128, 32, MASKED, waves_for(128)><<<grid, waves_for(128) * 64, 0, st>>>(
-            p);
+        if (waves == 4) {
+            attention_kernel<128, 32, MASKED, 4><<<grid, 4 * 64, 0, st>>>(p);
+        } else {
+            attention_kernel<128, 32, MASKED, waves_for(128)>
+                <<<grid, waves_for(128) * 64, 0, st>>>(p);
+        }
         break;
     }
 }
@@ -433,16 +463,21 @@ void run_attention(mfr_stream& s, const mfr_attention_desc& d) {
     p.causal = d.causal != 0;
     p.scale = d.scale != 0.0f ? d.scale
                               : static_cast<float>(1.0 / std::sqrt(static_cast<double>(d.d)));
-    const int64_t block_q = 32 * waves_for(d.d); // queries per workgroup
+    const int waves = waves_used(d.d, d.lq, batch_count, d.causal != 0, s.compute_units);
+    const int64_t block_q = 32 * waves; // queries per workgroup
     const int64_t q_blocks = (d.lq + block_q - 1) / block_q;
     const int64_t blocks = q_blocks * batch_count;
     require(blocks < (int64_t{1} << 31), "attention: problem too large for one launch");
     p.q_blocks = static_cast<int32_t>(q_blocks);
+    // Every workgroup resident at once (two per CU): the CU holding the j-th issued also holds
+    // the (j + CUs)-th, so pair long with short. Otherwise CUs take the next as they free up,
+    // and longest first balances.
+    p.paired = p.causal && waves == 4 && waves_for(d.d) == 8 && blocks <= 2 * s.compute_units;
     const unsigned grid = static_cast<unsigned>(blocks);
     if (d.mask != nullptr) {
-        launch<true>(d.d, p, grid, s.stream);
+        launch<true>(d.d, waves, p, grid, s.stream);
     } else {
-        launch<false>(d.d, p, grid, s.stream);
+        launch<false>(d.d, waves, p, grid, s.stream);
     }
     mfr::check_launch("attention_kernel");
 }

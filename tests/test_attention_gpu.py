@@ -94,6 +94,23 @@ def test_fused_shapes(stream, oracle, d, lq, lk, causal):
     assert_gemm_parity(got, want, mag + 1e-6, lk, f"fused d={d} lq={lq} lk={lk}")
 
 
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_fused_many_batch_entries(stream, oracle, d, causal):
+    """Enough batch entries for two workgroups of 8 wavefronts per CU (512 entries of 100
+    queries), the form config 5 runs; smaller grids (test_fused_shapes) run 4 per workgroup."""
+    b, h, lq, lk = 32, 16, 100, 100
+    q = normal(oracle, (b, h, lq, d), 0.0, 1.0, 31)
+    k = normal(oracle, (b, h, lk, d), 0.0, 1.0, 32)
+    v = normal(oracle, (b, h, lk, d), 0.0, 1.0, 33)
+    keep = np.tril(np.ones((lq, lk), np.uint8)) if causal else None
+    got = mf.attention_fused(dev(q, stream), dev(k, stream), dev(v, stream),
+                             causal=causal).numpy()
+    scale = np.float32(1.0 / np.sqrt(d))
+    want, mag = oracle_attention(oracle, q, k, v, keep, scale)
+    assert_gemm_parity(got, want, mag + 1e-6, lk, f"fused d={d} many entries")
+
+
 def test_fused_broadcast_batch_and_batched_mask(stream, oracle):
     """k and v shared over the first batch dimension (stride 0), a [B, 1, Lq, Lk] mask, an
     explicit scale."""
