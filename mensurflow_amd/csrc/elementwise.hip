@@ -63,6 +63,30 @@ __global__ void where_kernel(const uint8_t* __restrict__ cond, const float* __re
     }
 }
 
+// Rows that 16-byte accesses cannot take (cols % 4 != 0 or unaligned: X W + b at 4099
+// columns), cols >= 64: workgroups take rows in turn, threads the columns of a row (coalesced
+// 4-byte accesses, no division per element), ACT fixed per instantiation.
+template <int ACT>
+__global__ __launch_bounds__(256) void bias_act_rows_kernel(const float* __restrict__ x,
+                                                            const float* __restrict__ bias,
+                                                            float* y, int64_t rows,
+                                                            int64_t cols) {
+    for (int64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const float* xr = x + r * cols;
+        float* yr = y + r * cols;
+        for (int64_t c = threadIdx.x; c < cols; c += 256) {
+            float v = xr[c];
+            if (bias != nullptr) {
+                v = v + bias[c];
+            }
+            if constexpr (ACT != MFR_ACT_NONE) {
+                v = mfr::dev::gelu(v, ACT);
+            }
+            yr[c] = v;
+        }
+    }
+}
+
 // ---- 16-byte streaming forms (every pointer 16-byte aligned; cond 4-byte aligned) ----------
 //
 // Each workgroup streams one contiguous chunk of `chunk` quads (4 elements), its threads kStreamUnroll
@@ -384,6 +408,18 @@ int mfr_bias_act(mfr_stream_t stream, const float* x, const float* bias, float* 
         if (vec4) {
             bias_act_kernel<true><<<mfr::grid_blocks(n / 4, 256, 16384), 256, 0, s.stream>>>(
                 x, bias, y, rows, cols, act);
+        } else if (cols >= 64) {
+            const unsigned grid = static_cast<unsigned>(rows < 16384 ? rows : 16384);
+            if (act == MFR_ACT_NONE) {
+                bias_act_rows_kernel<MFR_ACT_NONE><<<grid, 256, 0, s.stream>>>(x, bias, y, rows,
+                                                                               cols);
+            } else if (act == MFR_ACT_GELU_TANH) {
+                bias_act_rows_kernel<MFR_ACT_GELU_TANH><<<grid, 256, 0, s.stream>>>(x, bias, y,
+                                                                                    rows, cols);
+            } else {
+                bias_act_rows_kernel<MFR_ACT_GELU_ERF><<<grid, 256, 0, s.stream>>>(x, bias, y,
+                                                                                   rows, cols);
+            }
         } else {
             bias_act_kernel<false><<<mfr::grid_blocks(n, 256, 16384), 256, 0, s.stream>>>(
                 x, bias, y, rows, cols, act);
