@@ -220,6 +220,112 @@ void launch_broadcast(const void* src, void* dst, int64_t n, hipStream_t stream)
 
 // Drops size-1 dimensions and merges neighbours that are contiguous with each other
 // (stride[d] == shape[d+1] * stride[d+1]), so a packed view becomes one dimension of stride 1.
+// ---- transposed views ---------------------------------------------------------------------
+//
+// dst (packed row-major over cs.shape) from a source whose last dimension is strided but whose
+// dimension `da` is contiguous (a transposed matrix, or a batch of them): 64 x 64 tiles through
+// LDS, read along da (coalesced in the source) and written along the last dimension (coalesced
+// in dst). The padded row keeps the column reads free of bank conflicts.
+constexpr int kTransposeTile = 64;
+constexpr int kTransposeThreads = 256; // 64 x 4
+
+struct TransposeShape {
+    CopyShape cs;
+    int da;                // the dimension with unit source stride
+    int64_t tiles_a;       // tiles along da
+    int64_t tiles_b;       // tiles along the last dimension
+    int64_t jobs;          // tiles_a * tiles_b * (product of the other dimensions)
+    int64_t dst_stride_a;  // dst elements between consecutive indices of da
+};
+
+template <typename T>
+__global__ __launch_bounds__(kTransposeThreads) void transpose_kernel(const T* __restrict__ src,
+                                                                      T* __restrict__ dst,
+                                                                      TransposeShape t) {
+    __shared__ T tile[kTransposeTile][kTransposeTile + 1];
+    const int last = t.cs.ndim - 1;
+    const int64_t size_a = t.cs.shape[t.da];
+    const int64_t size_b = t.cs.shape[last];
+    const int64_t stride_b = t.cs.strides[last];
+    const int tx = threadIdx.x % kTransposeTile;
+    const int ty = threadIdx.x / kTransposeTile;
+    const int64_t per_rest = t.tiles_a * t.tiles_b;
+    for (int64_t job = blockIdx.x; job < t.jobs; job += gridDim.x) {
+        int64_t rest = job / per_rest;
+        const int64_t within = job - rest * per_rest;
+        const int64_t a0 = (within / t.tiles_b) * kTransposeTile;
+        const int64_t b0 = (within % t.tiles_b) * kTransposeTile;
+        // Offsets of the other dimensions, in the source and in dst.
+        int64_t src_off = 0, dst_off = 0, dst_stride = 1;
+        for (int d = last; d >= 0; --d) {
+            if (d != t.da && d != last) {
+                const int64_t index = rest % t.cs.shape[d];
+                rest /= t.cs.shape[d];
+                src_off += index * t.cs.strides[d];
+                dst_off += index * dst_stride;
+            }
+            dst_stride *= t.cs.shape[d];
+        }
+        for (int i = ty; i < kTransposeTile; i += kTransposeThreads / kTransposeTile) {
+            const int64_t a = a0 + tx, b = b0 + i;
+            if (a < size_a && b < size_b) {
+                tile[i][tx] = src[src_off + a + b * stride_b];
+            }
+        }
+        __syncthreads();
+        for (int i = ty; i < kTransposeTile; i += kTransposeThreads / kTransposeTile) {
+            const int64_t a = a0 + i, b = b0 + tx;
+            if (a < size_a && b < size_b) {
+                dst[dst_off + a * t.dst_stride_a + b] = tile[tx][i];
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// The transposed form of cs, if it has one: a strided last dimension and an earlier dimension
+// with unit stride, both at least 16 long.
+bool transpose_shape(const CopyShape& cs, TransposeShape* t) {
+    const int last = cs.ndim - 1;
+    if (cs.ndim < 2 || cs.strides[last] == 1 || cs.shape[last] < 16) {
+        return false;
+    }
+    int da = -1;
+    for (int d = last - 1; d >= 0; --d) {
+        if (cs.strides[d] == 1) {
+            da = d;
+            break;
+        }
+    }
+    if (da < 0 || cs.shape[da] < 16) {
+        return false;
+    }
+    t->cs = cs;
+    t->da = da;
+    t->tiles_a = (cs.shape[da] + kTransposeTile - 1) / kTransposeTile;
+    t->tiles_b = (cs.shape[last] + kTransposeTile - 1) / kTransposeTile;
+    int64_t rest = 1, stride_a = 1;
+    for (int d = 0; d < cs.ndim; ++d) {
+        if (d != da && d != last) {
+            rest *= cs.shape[d];
+        }
+        if (d > da) {
+            stride_a *= cs.shape[d];
+        }
+    }
+    t->jobs = t->tiles_a * t->tiles_b * rest;
+    t->dst_stride_a = stride_a;
+    return true;
+}
+
+template <typename T>
+void launch_transpose(const void* src, void* dst, const TransposeShape& t, hipStream_t stream) {
+    const unsigned blocks = static_cast<unsigned>(t.jobs < 65536 ? t.jobs : 65536);
+    transpose_kernel<T><<<blocks, kTransposeThreads, 0, stream>>>(static_cast<const T*>(src),
+                                                                  static_cast<T*>(dst), t);
+    mfr::check_launch("transpose_kernel");
+}
+
 void collapse(CopyShape& s) {
     CopyShape out{};
     out.ndim = 0;
@@ -544,6 +650,24 @@ int mfr_strided_copy(mfr_stream_t stream, const void* src, void* dst, int32_t el
                 break;
             default:
                 launch_copy_rows<uint64_t>(src, dst, cs, elem_size, s.stream);
+                break;
+            }
+            return;
+        }
+        TransposeShape ts;
+        if (transpose_shape(cs, &ts)) {
+            switch (elem_size) {
+            case 1:
+                launch_transpose<uint8_t>(src, dst, ts, s.stream);
+                break;
+            case 2:
+                launch_transpose<uint16_t>(src, dst, ts, s.stream);
+                break;
+            case 4:
+                launch_transpose<uint32_t>(src, dst, ts, s.stream);
+                break;
+            default:
+                launch_transpose<uint64_t>(src, dst, ts, s.stream);
                 break;
             }
             return;

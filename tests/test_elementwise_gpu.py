@@ -170,6 +170,30 @@ def test_strided_copy_fast_paths(stream, oracle):
                      np.broadcast_to(x, (4, 5, 300)).copy())
 
 
+def test_strided_copy_transposes(stream, oracle):
+    """Transposed views (a strided last dimension, an earlier one contiguous) go through LDS
+    tiles: 2-D with ragged edges, a batch of transposes, a transpose of a slice, one-byte,
+    four-byte and eight-byte elements, and a broadcast last dimension; all against numpy."""
+    base = uniform(oracle, (1000, 777), -1.0, 1.0, 93, 0)
+    assert same_bits(dev(base, stream).T.numpy(), np.ascontiguousarray(base.T))
+    batch = uniform(oracle, (3, 67, 130), -1.0, 1.0, 94, 0)
+    got = dev(batch, stream).transpose(-2, -1).numpy()
+    assert same_bits(got, np.ascontiguousarray(batch.transpose(0, 2, 1)))
+    got = dev(batch, stream).transpose(0, 2).numpy()          # (130, 67, 3) from (3, 67, 130)
+    assert same_bits(got, np.ascontiguousarray(batch.transpose(2, 1, 0)))
+    wide = uniform(oracle, (90, 300), -1.0, 1.0, 95, 0)
+    got = dev(wide, stream).slice(1, 17, 281).T.numpy()      # a slice, then transposed
+    assert same_bits(got, np.ascontiguousarray(wide[:, 17:281].T))
+    mask = (np.arange(300 * 200).reshape(300, 200) % 7 == 0).astype(np.uint8)
+    assert same_bits(dev(mask, stream).T.numpy(), np.ascontiguousarray(mask.T))
+    ints = np.arange(64 * 100, dtype=np.int64).reshape(64, 100)
+    got = dev(ints, stream).T.numpy()
+    assert got.dtype == np.int64 and np.array_equal(got, np.ascontiguousarray(ints.T))
+    col = uniform(oracle, (200, 1), -1.0, 1.0, 96, 0)
+    got = dev(col, stream).expand((200, 40)).numpy()           # last dimension broadcast
+    assert same_bits(got, np.broadcast_to(col, (200, 40)).copy())
+
+
 @pytest.mark.parametrize("count", [4, 1000, 2048 * 4 + 4, 4096 * 2048 * 4 + 12, 3, 8191])
 def test_contiguous_copy_sizes(stream, count):
     """The contiguous fast path (16-byte units, one chunk per workgroup): a single unit, tails
