@@ -132,7 +132,7 @@ double modelled_us(int t, int64_t m, int64_t n, int64_t k, int64_t batch, int cu
 
 // ---- the thin path ---------------------------------------------------------------------------
 
-constexpr double kThinBytesPerUs = 6.0e6; // its streaming rate (bytes/us) for one column
+constexpr double kThinBytesPerUs = 6.5e6; // its streaming rate (bytes/us) for one column
 constexpr double kThinLaunchUs = 3.0;
 
 // Whether the thin path takes an m x n product: n <= 8 with A read along k (ak), or m <= 8 with
@@ -145,17 +145,21 @@ bool thin_possible(int64_t m, int64_t n, bool ak, bool bk, bool* along_n = nullp
     return by_rows || (m <= kThinCols && bk);
 }
 
-// Modelled time (us): every byte read or written once, at kThinBytesPerUs for one column and
-// slower by half that per further column (each B' value is a load of its own), and slower in
-// proportion with fewer than 512 workgroups. Fit to measured times of 1-8 columns.
+// Modelled time (us): every byte read or written once, at kThinBytesPerUs for one column; the
+// kernel computes the columns rounded up to C = 1, 2, 4 or 8, and each B' value is a load of its
+// own, so C > 1 costs 0.75 * C times as much; slower in proportion with fewer than 512
+// workgroups. Fit to measured times (16384^2 x 1: 168 us; 16384 x 4 x 4096: 125 us; 4096 x 8 x
+// 1024: 22 us).
 double thin_us(int64_t m, int64_t n, int64_t k, int64_t batch, bool c0, bool ak, bool bk) {
     bool along_n = true;
     thin_possible(m, n, ak, bk, &along_n);
     const double rows = static_cast<double>(along_n ? m : n);
     const double cols = static_cast<double>(along_n ? n : m);
+    const double rounded = cols <= 1 ? 1.0 : cols <= 2 ? 2.0 : cols <= 4 ? 4.0 : 8.0;
     const double bytes = 4.0 * batch * (rows * k + k * cols + rows * cols * (c0 ? 2.0 : 1.0));
     const double blocks = batch * std::ceil(rows / kThinDotRows);
-    return bytes / kThinBytesPerUs * (1.0 + 0.5 * cols) * std::max(1.0, 512.0 / blocks) +
+    return bytes / kThinBytesPerUs * (rounded == 1.0 ? 1.0 : 0.75 * rounded) *
+               std::max(1.0, 512.0 / blocks) +
            kThinLaunchUs;
 }
 
@@ -755,10 +759,23 @@ void launch_thin(const Plan& plan, const GemmParams& q, int va, int vb, hipStrea
     t.blocks_per_batch = (t.rows + kThinDotRows - 1) / kThinDotRows;
     const int64_t blocks = t.blocks_per_batch * q.batch_count;
     mfr::require(blocks < (int64_t{1} << 31), "sgemm: problem too large for one launch");
+    const unsigned grid = static_cast<unsigned>(blocks);
+    // The column count rounded up to 1, 2, 4 or 8 (kThinCols).
+    const int c = t.cols <= 1 ? 1 : t.cols <= 2 ? 2 : t.cols <= 4 ? 4 : kThinCols;
     if (width == 4) {
-        thin_dot_kernel<4><<<static_cast<unsigned>(blocks), kThinThreads, 0, stream>>>(t);
+        switch (c) {
+        case 1: thin_dot_kernel<4, 1><<<grid, kThinThreads, 0, stream>>>(t); break;
+        case 2: thin_dot_kernel<4, 2><<<grid, kThinThreads, 0, stream>>>(t); break;
+        case 4: thin_dot_kernel<4, 4><<<grid, kThinThreads, 0, stream>>>(t); break;
+        default: thin_dot_kernel<4, kThinCols><<<grid, kThinThreads, 0, stream>>>(t); break;
+        }
     } else {
-        thin_dot_kernel<1><<<static_cast<unsigned>(blocks), kThinThreads, 0, stream>>>(t);
+        switch (c) {
+        case 1: thin_dot_kernel<1, 1><<<grid, kThinThreads, 0, stream>>>(t); break;
+        case 2: thin_dot_kernel<1, 2><<<grid, kThinThreads, 0, stream>>>(t); break;
+        case 4: thin_dot_kernel<1, 4><<<grid, kThinThreads, 0, stream>>>(t); break;
+        default: thin_dot_kernel<1, kThinCols><<<grid, kThinThreads, 0, stream>>>(t); break;
+        }
     }
     mfr::check_launch("thin_dot_kernel");
 }

@@ -81,9 +81,11 @@ __device__ inline void thin_store(const ThinParams& p, const ThinBatch& t, int64
 
 // VA = 4: 16-byte loads of A' (a_rs and the batch strides multiples of 4, a 16-byte aligned, and
 // either k % 4 == 0 or A' staged with its lines zero-padded to a multiple of 4).
-// B' values come from the caches (at most 8 columns, shared by every row).
-template <int VA>
+// C: the column count rounded up to 1, 2, 4 or 8; columns from p.cols to C are neither loaded
+// nor stored. B' values come from the caches (shared by every row).
+template <int VA, int C>
 __global__ __launch_bounds__(kThinThreads) void thin_dot_kernel(ThinParams p) {
+    static_assert(C == 1 || C == 2 || C == 4 || C == kThinCols, "C is 1, 2, 4 or 8");
     const int64_t batch_index = blockIdx.x / p.blocks_per_batch;
     const ThinBatch t = thin_batch(p, batch_index);
     const int lane = threadIdx.x % 64;
@@ -91,7 +93,7 @@ __global__ __launch_bounds__(kThinThreads) void thin_dot_kernel(ThinParams p) {
     const int64_t row0 =
         (blockIdx.x % p.blocks_per_batch) * kThinDotRows + wave * kThinRowsPerWave;
     const int cols = static_cast<int>(p.cols);
-    float acc[kThinRowsPerWave][kThinCols] = {};
+    float acc[kThinRowsPerWave][C] = {};
     const float* a_row[kThinRowsPerWave];
     bool valid[kThinRowsPerWave];
 #pragma unroll
@@ -104,7 +106,7 @@ __global__ __launch_bounds__(kThinThreads) void thin_dot_kernel(ThinParams p) {
     // steps past k load nothing and add nothing.
     for (int64_t base = static_cast<int64_t>(lane) * VA; base < p.k; base += kStep) {
         float a[kThinUnroll][kThinRowsPerWave][VA];
-        float b[kThinUnroll][VA][kThinCols];
+        float b[kThinUnroll][VA][C];
 #pragma unroll
         for (int u = 0; u < kThinUnroll; ++u) {
             const int64_t kk = base + u * 64 * VA;
@@ -129,7 +131,7 @@ __global__ __launch_bounds__(kThinThreads) void thin_dot_kernel(ThinParams p) {
                 // read its zeros), but B' has no depth kk + v >= k: those are not read.
                 const bool depth = kk + v < p.k;
 #pragma unroll
-                for (int j = 0; j < kThinCols; ++j) {
+                for (int j = 0; j < C; ++j) {
                     b[u][v][j] = depth && j < cols ? t.b[(kk + v) * p.b_rs + j * p.b_cs] : 0.0f;
                 }
             }
@@ -141,29 +143,31 @@ __global__ __launch_bounds__(kThinThreads) void thin_dot_kernel(ThinParams p) {
 #pragma unroll
                 for (int r = 0; r < kThinRowsPerWave; ++r) {
 #pragma unroll
-                    for (int j = 0; j < kThinCols; ++j) {
+                    for (int j = 0; j < C; ++j) {
                         acc[r][j] = __builtin_fmaf(a[u][r][v], b[u][v][j], acc[r][j]);
                     }
                 }
             }
         }
     }
-    // Wavefront sums: every lane ends with every total; lane r*8 + j stores output (r, j).
+    // Wavefront sums: every lane ends with every total; lane r*C + j stores output (r, j).
+    // (A halving exchange, each lane keeping half of its values per step, ran slower: 10.2
+    // against 7.9 us on 4093 x 3 x 1023.)
     float mine = 0.0f;
 #pragma unroll
     for (int r = 0; r < kThinRowsPerWave; ++r) {
 #pragma unroll
-        for (int j = 0; j < kThinCols; ++j) {
+        for (int j = 0; j < C; ++j) {
             float v = acc[r][j];
 #pragma unroll
             for (int offset = 32; offset > 0; offset >>= 1) {
                 v += __shfl_xor(v, offset, 64);
             }
-            mine = lane == r * kThinCols + j ? v : mine;
+            mine = lane == r * C + j ? v : mine;
         }
     }
-    const int r = lane / kThinCols;
-    const int j = lane % kThinCols;
+    const int r = lane / C;
+    const int j = lane % C;
     if (r < kThinRowsPerWave && row0 + r < p.rows && j < cols) {
         thin_store(p, t, row0 + r, j, mine);
     }

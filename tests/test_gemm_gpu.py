@@ -442,10 +442,11 @@ THIN = mf.abi.TILE_THIN
 
 
 @pytest.mark.parametrize("m,n,k", [(4093, 3, 1023), (4096, 8, 1024), (300, 1, 77), (17, 5, 2500),
-                                   (1, 1, 1), (9, 8, 3)])
+                                   (1, 1, 1), (9, 8, 3), (257, 2, 515), (100, 4, 64), (33, 7, 9)])
 def test_thin_exact_rows(stream, m, n, k):
     """n <= 8 with A read along k (4-byte loads for odd k, 16-byte for k % 4 == 0), with alpha,
-    beta*C0 and a bias: the thin path's bits equal the exact product; no stray writes."""
+    beta*C0 and a bias: the thin path's bits equal the exact product; no stray writes. The
+    column counts cover every kernel width (1, 2, 4, 8 computed columns)."""
     a = quarter_matrix(m, k, 221)
     b = quarter_matrix(k, n, 222)
     c0 = quarter_matrix(m, n, 223)
@@ -464,7 +465,8 @@ def test_thin_exact_rows(stream, m, n, k):
             check_guards(buf)
 
 
-@pytest.mark.parametrize("m,n,k", [(3, 4099, 1023), (8, 4096, 1024), (1, 300, 77), (5, 17, 2500)])
+@pytest.mark.parametrize("m,n,k", [(3, 4099, 1023), (8, 4096, 1024), (1, 300, 77), (5, 17, 2500),
+                                   (2, 600, 130)])
 def test_thin_exact_transposed(stream, m, n, k):
     """m <= 8 with B read along k (B stored [n, k], read transposed): the thin path computes
     C^T = B^T A^T row by row of B^T; bits equal the exact product, bias per column of C."""
