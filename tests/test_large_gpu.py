@@ -1,6 +1,7 @@
 """Index arithmetic past 2^31 elements: element offsets that overflow int32 and byte offsets past
-2^32, in gemv N and T over A [3, 2^30 + 4] (3.2 G elements, 12.9 GB) and in a GEMM whose output
-has more than 2^31 elements. Inputs are built on the device (row-wise constants, quarter
+2^32, in gemv N and T over A [3, 2^30 + 4] (3.2 G elements, 12.9 GB), in a GEMM whose output
+has more than 2^31 elements, and with a 2.4 G-element operand (GEMM tiles in both orientations,
+the thin path, argmax, broadcast strided copies, elementwise add). Inputs are built on the device (row-wise constants, quarter
 integers), so every expected value has a closed form and is exact in double before the one
 rounding to fp32."""
 import numpy as np
@@ -50,3 +51,42 @@ def test_gemm_output_past_2_31_elements(stream):
                 .astype(np.float32))
         assert same_bits(c.slice(0, lo, lo + 4).numpy(), want), lo
     c.close()
+
+
+def test_operands_past_2_31_elements(stream):
+    """A[60000, 40000] (2.4 G elements, 9.6 GB) as an operand: A(i, j) = r[i] + c[j] with small
+    integers, built on the device by two broadcast strided copies and an elementwise add over
+    2.4 G elements. Then A B and A^T B2 on the MFMA tiles, A x on the thin path and a row argmax,
+    each against its closed form (integer sums below 2^24: exact in fp32 in any order)."""
+    m, k, n = 60000, 40000, 64
+    rng = np.random.default_rng(7)
+    r = rng.integers(0, 4, m).astype(np.float32)
+    c = rng.integers(0, 4, k).astype(np.float32)
+    c[rng.integers(0, k)] = 5.0  # a single column maximum: every row's argmax
+    rows = mf.strided_copy(dev(r, stream).view((m, 1)).expand((m, k)))
+    cols = mf.strided_copy(dev(c, stream).view((1, k)).expand((m, k)))
+    a = mf.elementwise(mf.abi.EW_ADD, rows, cols)
+    rows.close()
+    cols.close()
+    # Spot checks of the built matrix, including its last elements (offset > 2^31).
+    for lo in (0, m // 2, m - 2):
+        assert np.array_equal(a.slice(0, lo, lo + 2).numpy(), r[lo:lo + 2, None] + c[None, :]), lo
+
+    b = rng.integers(0, 2, (k, n)).astype(np.float32)
+    want = (r.astype(np.float64)[:, None] * b.sum(0)[None, :] + (c.astype(np.float64) @ b))
+    got = mf.gemm(a, dev(b, stream)).numpy()
+    assert same_bits(got, want.astype(np.float32))
+
+    b2 = rng.integers(0, 2, (m, n)).astype(np.float32)
+    want_t = ((r.astype(np.float64) @ b2)[None, :] + c.astype(np.float64)[:, None] * b2.sum(0))
+    got_t = mf.gemm(a.T, dev(b2, stream)).numpy()
+    assert same_bits(got_t, want_t.astype(np.float32))
+
+    x = rng.integers(0, 2, (k, 1)).astype(np.float32)
+    plan = mf.gemm_plan(a, dev(x, stream), mf.DeviceArray.empty((m, 1), stream))
+    assert plan[0] == mf.abi.TILE_THIN
+    want_x = r.astype(np.float64) * x.sum() + float(c.astype(np.float64) @ x[:, 0])
+    assert same_bits(mf.gemm(a, dev(x, stream)).numpy()[:, 0], want_x.astype(np.float32))
+
+    assert np.all(mf.argmax(a).numpy() == int(np.argmax(c)))
+    a.close()
