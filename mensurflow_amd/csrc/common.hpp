@@ -6,6 +6,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include "gelu_tanh.hpp"
+
 #include <cstdint>
 #include <stdexcept>
 #include <string>
@@ -155,24 +157,17 @@ __device__ inline int wave_or(int v) {
     return v;
 }
 
-// exp(-|v|) form of the logistic function (the reference's stable_sigmoid,
-// src/backends/cpu/ops/elementwise/elementwise.cpp:24-27).
-__device__ inline double stable_sigmoid(double value) {
-    const double z = exp(-fabs(value));
-    return value < 0.0 ? z / (1.0 + z) : 1.0 / (1.0 + z);
-}
-
-// mensurflow::gelu in double, rounded once to float (elementwise.cpp:173-194). The library is
-// compiled with -ffp-contract=off, so the products and sums round as in the reference.
+// mensurflow::gelu in double, rounded once to float (elementwise.cpp:173-194): the tanh form in
+// gelu_tanh.hpp; the erf form 0.5 v erfc(-v / sqrt(2)) with the device library's erfc. The
+// library is compiled with -ffp-contract=off, so the products and sums round as in the reference.
 __device__ inline float gelu(float value, int act) {
+    if (act == MFR_ACT_GELU_TANH) {
+        return gelu_math::gelu_tanh(value);
+    }
     if (__builtin_isinf(value)) {
         return value < 0.0f ? -0.0f : value;
     }
     const double v = static_cast<double>(value);
-    if (act == MFR_ACT_GELU_TANH) {
-        const double u = 0.79788456080286535588 * v * (1.0 + 0.044715 * v * v);
-        return static_cast<float>(v * stable_sigmoid(2.0 * u));
-    }
     return static_cast<float>(0.5 * v * erfc(-v * 0.70710678118654752440));
 }
 

@@ -350,17 +350,33 @@ def test_split_k_invalid_counts(stream):
     assert np.all(mf.gemm(a, b, splits=mf.abi.MAX_SPLITS).numpy() == 64.0)
 
 
-def test_split_k_gelu_same_bits_as_unsplit(stream):
+def test_split_k_gelu_same_bits_as_unsplit(stream, oracle):
     """The activation sees the same pre-activation value split or not (exact inputs), so the
-    outputs agree in every bit."""
+    outputs agree in every bit, and equal the oracle's gelu of the exact pre-activation."""
     m, n, k = 96, 200, 2048
-    a = dev(quarter_matrix(m, k, 201), stream)
-    b = dev(quarter_matrix(k, n, 202), stream)
-    bias = dev(quarter_matrix(1, n, 203)[0], stream)
+    av, bv = quarter_matrix(m, k, 201), quarter_matrix(k, n, 202)
+    biasv = quarter_matrix(1, n, 203)[0]
+    a, b, bias = dev(av, stream), dev(bv, stream), dev(biasv, stream)
     one = mf.gemm(a, b, bias=bias, act=mf.ACT_GELU_TANH, splits=1).numpy()
+    want = oracle.gelu((exact_product(av, bv) + biasv).astype(np.float32), approximate=True)
+    assert same_bits(one, want)
     for splits in (2, 16):
         got = mf.gemm(a, b, bias=bias, act=mf.ACT_GELU_TANH, splits=splits).numpy()
         assert same_bits(got, one), splits
+
+
+@pytest.mark.parametrize("tile", TILES + [mf.abi.TILE_THIN])
+def test_epilogue_gelu_bits_equal_oracle(stream, oracle, tile):
+    """gelu-tanh in every tile's epilogue (and the thin path's) on exact pre-activation values
+    (quarter integers, widely spread by alpha): the oracle's bits, element for element."""
+    m, n, k = (300, 8, 77) if tile == mf.abi.TILE_THIN else (300, 260, 96)
+    av, bv = quarter_matrix(m, k, 211), quarter_matrix(k, n, 212)
+    biasv = quarter_matrix(1, n, 213)[0]
+    for alpha in (0.03125, 1.0, 0.125):
+        pre = (np.float32(alpha) * exact_product(av, bv) + biasv).astype(np.float32)
+        got = mf.gemm(dev(av, stream), dev(bv, stream), alpha=alpha, bias=dev(biasv, stream),
+                      act=mf.ACT_GELU_TANH, tile=tile).numpy()
+        assert same_bits(got, oracle.gelu(pre, approximate=True)), alpha
 
 
 def test_split_k_automatic_choice(stream):
