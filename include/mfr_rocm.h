@@ -224,7 +224,9 @@ int mfr_sgemm_rm(mfr_stream_t stream, int trans_a, int trans_b, int64_t m, int64
 
 /* y = alpha * op(A) * x + beta * y0, A row-major [rows, cols] with row stride lda >= cols,
  * op(A) = A (trans == 0, y has `rows` entries) or A^T (trans != 0, y has `cols` entries).
- * y0 may be NULL (then beta is ignored). Accumulates in double and rounds once, as
+ * y0 may be NULL only when beta == 0; beta != 0 without y0 is MFR_E_INVALID, the reference's
+ * "gemv: beta requires an output vector" (src/ops/blas.cpp:155-157). Accumulates in double and
+ * rounds once, as
  * mensurflow::cpu::gemv_f32 (src/backends/cpu/ops/blas/blas.cpp:66-79):
  *   y[i] = (float)( (double)alpha * sum + (double)(float)(beta * y0[i]) ).
  * Deterministic: the same inputs give the same bits on every call (fixed reduction order, no
