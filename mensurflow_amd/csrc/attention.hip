@@ -22,6 +22,8 @@
 //     the tail.
 //   - The result is scaled by the reciprocal of the row sum, staged through LDS and stored as
 //     16-byte rows.
+//   - attention16_kernel (below) is the same op with 16 queries per wavefront on the 16x16x4
+//     MFMA, at 4 wavefronts per SIMD; it takes causal d = 64 on large grids.
 #include "gemm_kernel.hpp"
 
 #include <cmath>
@@ -368,6 +370,318 @@ __global__ __launch_bounds__(WAVES * 64, MIN_WAVES) void attention_kernel(AttnPa
     }
 }
 
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// Wavefronts per workgroup of attention16_kernel: 16 (256 queries, one workgroup per CU, 4 per
+// SIMD). 8 (two workgroups per CU) measured 165.2 against 162.9 us at configs[4].
+constexpr int kWaves16 = 16;
+
+// The same op with 16 queries per wavefront on v_mfma_f32_16x16x4_f32 (4x4 accumulators per
+// lane per 16x16 block): a wavefront holds 16 scores, 16 output values and D/4 query values per
+// lane, a third of the 32-query form's registers, so 4 wavefronts fit on a SIMD.
+//   - S^T = K Q^T per 16-key block j: lane l supplies K(16j + l%16, d) and Q(l%16, d) at depth
+//     d = 16a + 4(l/16) + b on step (a, b) (both operands use that permutation, so the sum is
+//     unchanged), which makes each lane's K values for 4 steps one 16-byte LDS read. Lane l then
+//     holds the scores of query l%16 with keys 16j + 4(l/16) + r, r = 0..3: the four lanes
+//     l%16 + 16g share a query, and its maximum and sum take two exchanges.
+//   - O^T += V^T P^T over key steps (j, r): lane l's B value is its own score register
+//     sacc[j][r] (query l%16, key 16j + 4(l/16) + r), and its A value V(key, 16c + l%16), read
+//     from a transposed V tile [d][BK+4] as one 16-byte read per 4 steps.
+//   - K tiles are [keys][D+4]; V tiles are written transposed (each thread loads 4 adjacent d of
+//     one key and stores them down a column; adjacent lanes take adjacent keys, so the stores
+//     hit distinct banks). Both are double-buffered with one barrier per key block.
+template <int D, int BK, bool MASKED, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void attention16_kernel(AttnParams p) {
+    constexpr int THREADS = WAVES * 64;
+    constexpr int BLOCK_Q = WAVES * 16;
+    constexpr int KB = BK / 16;  // 16-key blocks per key block
+    constexpr int DB = D / 16;   // 16-wide output column blocks; 16-deep groups of q . k
+    constexpr int KP = D + 4;    // K tile pitch
+    constexpr int VP = BK + 4;   // V^T tile pitch
+    constexpr int kKFloats = BK * KP;
+    constexpr int kVFloats = D * VP;
+    constexpr int kTileFloats = 2 * (kKFloats + kVFloats);
+    constexpr int kStagePitch = D + 4;
+    constexpr int kStageFloats = BLOCK_Q * kStagePitch;
+    constexpr int kQuads = BK * (D / 4);                              // 16-byte pieces per tile
+    constexpr int kLoads = (kQuads + THREADS - 1) / THREADS;          // per thread per tile
+    __shared__ float smem[kTileFloats > kStageFloats ? kTileFloats : kStageFloats];
+    auto lds_k = [&](int which) { return smem + which * kKFloats; };
+    auto lds_v = [&](int which) { return smem + 2 * kKFloats + which * kVFloats; };
+
+    const int64_t bid = blockIdx.x;
+    const int64_t level = bid / p.batch_count;
+    const int64_t longer = (p.q_blocks + 1) / 2;
+    const int64_t qb = !p.paired || level < longer ? p.q_blocks - 1 - level : level - longer;
+    int64_t bi = bid % p.batch_count;
+    int64_t off_q = 0, off_k = 0, off_v = 0, off_o = 0, off_m = 0;
+    for (int d = p.batch_dims - 1; d >= 0; --d) {
+        const int64_t idx = bi % p.batch[d];
+        bi /= p.batch[d];
+        off_q += idx * p.q_bs[d];
+        off_k += idx * p.k_bs[d];
+        off_v += idx * p.v_bs[d];
+        off_o += idx * p.out_bs[d];
+        off_m += idx * p.mask_bs[d];
+    }
+
+    const int lane = threadIdx.x % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / 64));
+    const int g = lane / 16;   // which 4 of each 16 keys (and depths) this lane takes
+    const int col = lane % 16; // this lane's query within the wavefront's 16
+    const int64_t q0 = qb * BLOCK_Q;
+    const int64_t wq0 = q0 + wave * 16;
+    const int64_t query = wq0 + col;
+    const bool wave_live = wq0 < p.lq;
+
+    float qf[DB][4];
+    {
+        const float* qrow = p.q + off_q + query * p.q_rs + 4 * g;
+#pragma unroll
+        for (int a = 0; a < DB; ++a) {
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (query < p.lq) {
+                v = *reinterpret_cast<const float4*>(qrow + 16 * a);
+            }
+            qf[a][0] = v.x;
+            qf[a][1] = v.y;
+            qf[a][2] = v.z;
+            qf[a][3] = v.w;
+        }
+    }
+    const uint8_t* mask_row = nullptr;
+    if constexpr (MASKED) {
+        mask_row = p.mask + off_m + (query < p.lq ? query : 0) * p.mask_rs;
+    }
+
+    int64_t k_end = p.lk;
+    if (p.causal) {
+        const int64_t last_query = (q0 + BLOCK_Q < p.lq ? q0 + BLOCK_Q : p.lq) - 1;
+        k_end = last_query + 1 < k_end ? last_query + 1 : k_end;
+    }
+    const int64_t blocks = (k_end + BK - 1) / BK;
+
+    float m_run = -INFINITY;
+    float l_run = 0.0f;
+    floatx4 oacc[DB];
+#pragma unroll
+    for (int c = 0; c < DB; ++c) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            oacc[c][r] = 0.0f;
+        }
+    }
+
+    const float* k_base = p.k + off_k;
+    const float* v_base = p.v + off_v;
+    auto keys_in = [&](int64_t blk) {
+        const int64_t left = p.lk - blk * BK;
+        return left < BK ? static_cast<int>(left) : BK;
+    };
+    auto needed = [&](int64_t blk) { return wave_live && (!p.causal || blk * BK <= wq0 + 15); };
+
+    // Tile loads: piece u of K is (key u / (D/4), depths 4(u % (D/4))..+3); piece u of V is
+    // (key u % BK, depths 4(u / BK)..+3). Keys at or past `keys` read as zeros.
+    float4 kr[kLoads], vr[kLoads];
+    auto load_tiles = [&](int64_t blk) {
+        const int keys = keys_in(blk);
+        const float* kb = k_base + blk * BK * p.k_rs;
+        const float* vb = v_base + blk * BK * p.v_rs;
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) {
+            const int u = static_cast<int>(threadIdx.x) + i * THREADS;
+            const int kkey = u / (D / 4), kq = u % (D / 4);
+            const int vkey = u % BK, vq = u / BK;
+            const bool in = u < kQuads;
+            kr[i] = in && kkey < keys
+                        ? *reinterpret_cast<const float4*>(kb + kkey * p.k_rs + 4 * kq)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+            vr[i] = in && vkey < keys
+                        ? *reinterpret_cast<const float4*>(vb + vkey * p.v_rs + 4 * vq)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto store_tiles = [&](int which) {
+        float* sk = lds_k(which);
+        float* sv = lds_v(which);
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) {
+            const int u = static_cast<int>(threadIdx.x) + i * THREADS;
+            if (u < kQuads) {
+                const int kkey = u / (D / 4), kq = u % (D / 4);
+                const int vkey = u % BK, vq = u / BK;
+                *reinterpret_cast<float4*>(sk + kkey * KP + 4 * kq) = kr[i];
+                sv[(4 * vq + 0) * VP + vkey] = vr[i].x;
+                sv[(4 * vq + 1) * VP + vkey] = vr[i].y;
+                sv[(4 * vq + 2) * VP + vkey] = vr[i].z;
+                sv[(4 * vq + 3) * VP + vkey] = vr[i].w;
+            }
+        }
+    };
+
+    auto scores = [&](const float* sk, floatx4(&sacc)[KB]) {
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                sacc[j][r] = 0.0f;
+            }
+        }
+#pragma unroll
+        for (int a = 0; a < DB; ++a) {
+            float4 kf[KB];
+#pragma unroll
+            for (int j = 0; j < KB; ++j) {
+                kf[j] = *reinterpret_cast<const float4*>(sk + (16 * j + col) * KP + 16 * a + 4 * g);
+            }
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+#pragma unroll
+                for (int j = 0; j < KB; ++j) {
+                    const float kv = b == 0 ? kf[j].x : b == 1 ? kf[j].y : b == 2 ? kf[j].z : kf[j].w;
+                    sacc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv, qf[a][b], sacc[j], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // Scale, mask and the online softmax of the block at key k0 (element r of block j: relative
+    // key 16j + 4g + r).
+    auto softmax = [&](int64_t k0, floatx4(&sacc)[KB]) {
+        const bool edge = k0 + BK > p.lk || (p.causal && k0 + BK - 1 > wq0);
+        if (MASKED || edge) {
+            const int64_t keys_left = p.lk - k0;
+            const int64_t diag = query - k0;
+            const int lim_k = static_cast<int>(keys_left < BK ? keys_left : BK) - 4 * g;
+            const int lim_q = static_cast<int>(!p.causal || diag >= BK ? BK
+                                               : diag < -1 ? -1
+                                                           : diag) -
+                              4 * g;
+#pragma unroll
+            for (int j = 0; j < KB; ++j) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int rel = 16 * j + r; // minus 4g (above)
+                    bool keep = rel < lim_k && rel <= lim_q;
+                    if constexpr (MASKED) {
+                        if (keep) {
+                            keep = mask_row[(k0 + rel + 4 * g) * p.mask_cs] != 0;
+                        }
+                    }
+                    sacc[j][r] = keep ? p.scale * sacc[j][r] : -INFINITY;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < KB; ++j) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    sacc[j][r] = p.scale * sacc[j][r];
+                }
+            }
+        }
+        float block_max = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                block_max = fmaxf(block_max, sacc[j][r]);
+            }
+        }
+        block_max = fmaxf(block_max, __shfl_xor(block_max, 16, 64));
+        block_max = fmaxf(block_max, __shfl_xor(block_max, 32, 64));
+        const float m_new = fmaxf(m_run, block_max);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float rescale = weight(m_run, m_use);
+        m_run = m_new;
+        l_run *= rescale;
+#pragma unroll
+        for (int c = 0; c < DB; ++c) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                oacc[c][r] *= rescale;
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float w = weight(sacc[j][r], m_use);
+                sacc[j][r] = w;
+                l_run += w;
+            }
+        }
+    };
+
+    auto accumulate = [&](const float* sv, const floatx4(&sacc)[KB]) {
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+            float4 vf[DB];
+#pragma unroll
+            for (int c = 0; c < DB; ++c) {
+                vf[c] = *reinterpret_cast<const float4*>(sv + (16 * c + col) * VP + 16 * j + 4 * g);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+#pragma unroll
+                for (int c = 0; c < DB; ++c) {
+                    const float vv = r == 0 ? vf[c].x : r == 1 ? vf[c].y : r == 2 ? vf[c].z : vf[c].w;
+                    oacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv, sacc[j][r], oacc[c], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    if (blocks > 0) {
+        load_tiles(0);
+        store_tiles(0);
+        __syncthreads();
+    }
+    for (int64_t kb = 0; kb < blocks; ++kb) {
+        const int cur = static_cast<int>(kb & 1);
+        const bool more = kb + 1 < blocks;
+        if (more) {
+            load_tiles(kb + 1);
+        }
+        if (needed(kb)) {
+            floatx4 sacc[KB];
+            scores(lds_k(cur), sacc);
+            softmax(kb * BK, sacc);
+            accumulate(lds_v(cur), sacc);
+        }
+        if (more) {
+            store_tiles(cur ^ 1);
+        }
+        __syncthreads();
+    }
+
+    // ---- normalise, stage [16 queries][D] per wavefront in LDS, store 16-byte rows ----
+    float l_total = l_run + __shfl_xor(l_run, 16, 64);
+    l_total += __shfl_xor(l_total, 32, 64);
+    const float inv = l_total == 0.0f ? 0.0f : 1.0f / l_total;
+    float* stage = smem + wave * 16 * kStagePitch;
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < DB; ++c) {
+        *reinterpret_cast<float4*>(stage + col * kStagePitch + 16 * c + 4 * g) =
+            make_float4(oacc[c][0] * inv, oacc[c][1] * inv, oacc[c][2] * inv, oacc[c][3] * inv);
+    }
+    __syncthreads();
+    float* out_base = p.out + off_o;
+    constexpr int kRowUnits = D / 4;
+#pragma unroll
+    for (int i = 0; i < 16 * kRowUnits / 64; ++i) {
+        const int u = lane + 64 * i;
+        const int row = u / kRowUnits;
+        const int c4 = u % kRowUnits;
+        const int64_t qrow = wq0 + row;
+        if (qrow < p.lq) {
+            *reinterpret_cast<float4*>(out_base + qrow * p.out_rs + 4 * c4) =
+                *reinterpret_cast<const float4*>(stage + row * kStagePitch + 4 * c4);
+        }
+    }
+}
+
 template <bool MASKED>
 void launch(int64_t d, int waves, const AttnParams& p, unsigned grid, hipStream_t st) {
     switch (d) {
@@ -464,7 +778,12 @@ void run_attention(mfr_stream& s, const mfr_attention_desc& d) {
     p.scale = d.scale != 0.0f ? d.scale
                               : static_cast<float>(1.0 / std::sqrt(static_cast<double>(d.d)));
     const int waves = waves_used(d.d, d.lq, batch_count, d.causal != 0, s.compute_units);
-    const int64_t block_q = 32 * waves; // queries per workgroup
+    // d = 64, causal, no mask, a grid of 8-wavefront workgroups: the 16-query kernel, whose
+    // last diagonal key blocks keep every SIMD busy (configs[4]: 163.6 against 170.0 us).
+    // Non-causal it measured 291 against 288 us, at d = 32 96.9 against 93.5 us (causal) and
+    // 169.6 against 159.8 us, and its masked form spills; those keep the 32-query kernel.
+    const bool use16 = d.d == 64 && d.causal != 0 && d.mask == nullptr && waves == waves_for(64);
+    const int64_t block_q = use16 ? 16 * kWaves16 : 32 * waves; // queries per workgroup
     const int64_t q_blocks = (d.lq + block_q - 1) / block_q;
     const int64_t blocks = q_blocks * batch_count;
     require(blocks < (int64_t{1} << 31), "attention: problem too large for one launch");
@@ -474,7 +793,9 @@ void run_attention(mfr_stream& s, const mfr_attention_desc& d) {
     // and longest first balances.
     p.paired = p.causal && waves == 4 && waves_for(d.d) == 8 && blocks <= 2 * s.compute_units;
     const unsigned grid = static_cast<unsigned>(blocks);
-    if (d.mask != nullptr) {
+    if (use16) {
+        attention16_kernel<64, 64, false, kWaves16><<<grid, kWaves16 * 64, 0, s.stream>>>(p);
+    } else if (d.mask != nullptr) {
         launch<true>(d.d, waves, p, grid, s.stream);
     } else {
         launch<false>(d.d, waves, p, grid, s.stream);

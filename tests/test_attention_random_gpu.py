@@ -1,7 +1,8 @@
 """Seeded random sweep of the fused attention kernel (mfr_attention) against the oracle's
 restatement of the reference's composition (src/ops/attention.cpp:48-98: packed GEMM q k^T,
 alpha pass, where(-inf), softmax, packed GEMM with v): head sizes 32, 64 and 128, ragged and
-empty key counts, one or two batch dimensions with k and v broadcast, causal or not, no mask, a
+empty key counts, one or two batch dimensions with k and v broadcast (512 entries in every 15th
+case, which runs the 16-query kernel for causal d = 64), causal or not, no mask, a
 [Lq, Lk] mask or a batched mask broadcast over heads, the default or an explicit scale, and row
 strides wider than d (16-byte aligned) for q, k, v and the output. The bar is the GEMM's: max
 relative error 1e-5*sqrt(Lk) of sum_j |p_ij v_jc| per output entry; rows whose keys are all
@@ -40,6 +41,10 @@ def test_random_fused_attention(stream, oracle, index):
     causal = bool(rng.random() < 0.5)
     mask_kind = str(rng.choice(["none", "2d", "batched"]))
     scale = 0.0 if rng.random() < 0.5 else float(np.float32(rng.uniform(0.05, 0.5)))
+    if index % 15 == 14:
+        # 512 batch entries, causal, d = 64, no mask: a grid large enough for the 16-query
+        # kernel (one 256-query workgroup per CU, longest first).
+        d, batch, causal, mask_kind, lk = 64, (32, 16), True, "none", max(lk, 1)
     kv_lead = tuple(1 if rng.random() < 1 / 3 else s for s in batch)
     what = (f"case {index}: d={d} batch={batch} lq={lq} lk={lk} causal={causal} "
             f"mask={mask_kind} scale={scale} kv={kv_lead}")
