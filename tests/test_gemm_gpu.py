@@ -684,3 +684,36 @@ def test_unsupported_and_invalid(stream):
         mf.gemm(odd, a)
     with pytest.raises(ValueError):
         mf.gemm(a, dev(np.ones((7, 8), np.float32), stream))
+
+
+def test_repeated_shapes_with_new_operands(stream, oracle):
+    """The same shapes called again (mfr_sgemm reuses its plan for them) with other buffers, an
+    operand moved off a 16-byte boundary, other alpha/beta/bias/activation values and C0 present
+    or absent: every call equals its exact result."""
+    m, n, k = 300, 260, 516
+    rng = np.random.default_rng(77)
+    for trial in range(8):
+        av = quarter_matrix(m, k, 300 + trial)
+        bv = quarter_matrix(k, n, 400 + trial)
+        shift = trial % 2  # odd trials read A one float into its storage (4-byte loads)
+        store = np.zeros(m * k + shift, np.float32)
+        store[shift:] = av.ravel()
+        a_d = dev(store, stream).slice(0, shift, shift + m * k).view((m, k))
+        alpha = float(rng.choice([1.0, 0.5, -2.0]))
+        beta = float(rng.choice([0.0, 0.5]))
+        c0v = quarter_matrix(m, n, 500 + trial)
+        biasv = quarter_matrix(1, n, 600 + trial)[0]
+        use_c0, use_bias = trial % 3 != 0, trial % 4 < 2
+        act = [mf.ACT_NONE, mf.ACT_GELU_TANH][trial % 2]
+        c, buf = guarded_output(stream, (m, n))
+        mf.gemm(a_d, dev(bv, stream), alpha=alpha, c0=dev(c0v, stream) if use_c0 else None,
+                beta=beta, bias=dev(biasv, stream) if use_bias else None, act=act, out=c)
+        pre = np.float32(alpha) * exact_product(av, bv)
+        if use_c0 and beta != 0.0:
+            pre = pre + np.float32(beta) * c0v
+        if use_bias:
+            pre = pre + biasv
+        pre = pre.astype(np.float32)
+        want = oracle.gelu(pre, approximate=True) if act == mf.ACT_GELU_TANH else pre
+        assert same_bits(c.numpy(), want), trial
+        check_guards(buf)
