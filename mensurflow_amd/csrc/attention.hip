@@ -77,6 +77,34 @@ struct AttnParams {
     float scale;
 };
 
+// Which (batch entry, query block) workgroup blockIdx.x computes, and that entry's element
+// offsets into q, k, v, out and the mask. Query blocks are issued longest first (the last ones of
+// every batch entry), or, when paired, the longer half longest first and then the shorter half
+// shortest first.
+struct BlockWork {
+    int64_t qb;
+    int64_t off_q, off_k, off_v, off_o, off_m;
+};
+
+__device__ inline BlockWork block_work(const AttnParams& p) {
+    const int64_t bid = blockIdx.x;
+    const int64_t level = bid / p.batch_count;
+    const int64_t longer = (p.q_blocks + 1) / 2;
+    BlockWork w{};
+    w.qb = !p.paired || level < longer ? p.q_blocks - 1 - level : level - longer;
+    int64_t bi = bid % p.batch_count;
+    for (int d = p.batch_dims - 1; d >= 0; --d) {
+        const int64_t idx = bi % p.batch[d];
+        bi /= p.batch[d];
+        w.off_q += idx * p.q_bs[d];
+        w.off_k += idx * p.k_bs[d];
+        w.off_v += idx * p.v_bs[d];
+        w.off_o += idx * p.out_bs[d];
+        w.off_m += idx * p.mask_bs[d];
+    }
+    return w;
+}
+
 // exp(x - m) through the hardware's 2^x (v_exp_f32, 1 ulp; results below 2^-126 may flush to
 // zero, which is below the rounding of any row sum, whose largest term is exp(0) = 1). m is
 // never -inf here (the caller substitutes 0), so x = -inf gives exp2(-inf) = 0 without a NaN.
@@ -106,21 +134,10 @@ __global__ __launch_bounds__(WAVES * 64, MIN_WAVES) void attention_kernel(AttnPa
     auto lds_v = [&](int which) { return smem + 2 * LoadK::kFloats + which * LoadV::kFloats; };
 
     // ---- which (batch entry, query block): the longest (last) query blocks first ----
-    const int64_t bid = blockIdx.x;
-    const int64_t level = bid / p.batch_count;
-    const int64_t longer = (p.q_blocks + 1) / 2; // levels issued longest first when paired
-    const int64_t qb = !p.paired || level < longer ? p.q_blocks - 1 - level : level - longer;
-    int64_t bi = bid % p.batch_count;
-    int64_t off_q = 0, off_k = 0, off_v = 0, off_o = 0, off_m = 0;
-    for (int d = p.batch_dims - 1; d >= 0; --d) {
-        const int64_t idx = bi % p.batch[d];
-        bi /= p.batch[d];
-        off_q += idx * p.q_bs[d];
-        off_k += idx * p.k_bs[d];
-        off_v += idx * p.v_bs[d];
-        off_o += idx * p.out_bs[d];
-        off_m += idx * p.mask_bs[d];
-    }
+    const BlockWork work = block_work(p);
+    const int64_t qb = work.qb;
+    const int64_t off_q = work.off_q, off_k = work.off_k, off_v = work.off_v,
+                  off_o = work.off_o, off_m = work.off_m;
 
     const int lane = threadIdx.x % 64;
     // Uniform across the wavefront; read into a scalar register so that the branches on it
@@ -409,21 +426,10 @@ __global__ __launch_bounds__(WAVES * 64) void attention16_kernel(AttnParams p) {
     auto lds_k = [&](int which) { return smem + which * kKFloats; };
     auto lds_v = [&](int which) { return smem + 2 * kKFloats + which * kVFloats; };
 
-    const int64_t bid = blockIdx.x;
-    const int64_t level = bid / p.batch_count;
-    const int64_t longer = (p.q_blocks + 1) / 2;
-    const int64_t qb = !p.paired || level < longer ? p.q_blocks - 1 - level : level - longer;
-    int64_t bi = bid % p.batch_count;
-    int64_t off_q = 0, off_k = 0, off_v = 0, off_o = 0, off_m = 0;
-    for (int d = p.batch_dims - 1; d >= 0; --d) {
-        const int64_t idx = bi % p.batch[d];
-        bi /= p.batch[d];
-        off_q += idx * p.q_bs[d];
-        off_k += idx * p.k_bs[d];
-        off_v += idx * p.v_bs[d];
-        off_o += idx * p.out_bs[d];
-        off_m += idx * p.mask_bs[d];
-    }
+    const BlockWork work = block_work(p);
+    const int64_t qb = work.qb;
+    const int64_t off_q = work.off_q, off_k = work.off_k, off_v = work.off_v,
+                  off_o = work.off_o, off_m = work.off_m;
 
     const int lane = threadIdx.x % 64;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / 64));
