@@ -111,7 +111,10 @@ double modelled_us(int t, int64_t m, int64_t n, int64_t k, int64_t batch, int cu
     const int64_t count = tile_count(t, m, n, batch) * splits;
     const int64_t per_cu = (count + cus - 1) / cus;
     const int64_t concurrent = per_cu < info.occupancy ? per_cu : info.occupancy;
-    // The 128x128 tile runs 8 wavefronts when no CU gets two (launch_layout).
+    // The 128x128 tile runs 8 wavefronts when no CU gets two (launch_layout). (The 64x64 tile
+    // then runs 16, four sets sharing each depth slice, but is priced as its 4-wavefront form:
+    // priced at 4 per SIMD, AUTO took it over split-K and the thin path where it is slower, e.g.
+    // 512^3 16.2 against 14.1 us, the MLP's 4093 x 3 strip 19.1 against 7.9 us.)
     const int64_t waves = t == MFR_TILE_128x128 && count <= cus ? 8 : info.waves;
     const int64_t reference_waves = (4096 / info.bm) * (4096 / info.bn) / 256;
     const int64_t ref_concurrent =
@@ -299,23 +302,28 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(GemmParams p) {
     }
 }
 
-template <int BM, int BN, int KT, int WAVES_M, int WAVES_N, bool AK, bool BK>
+template <int BM, int BN, int KT, int WAVES_M, int WAVES_N, bool AK, bool BK, int WAVES_K = 1>
 void launch_vec(const GemmParams& p, int va, int vb, unsigned blocks, hipStream_t stream) {
-    constexpr int threads = WAVES_M * WAVES_N * 64;
+    constexpr int threads = WAVES_M * WAVES_N * WAVES_K * 64;
     if (va == 4 && vb == 4) {
-        sgemm_kernel<BM, BN, KT, WAVES_M, WAVES_N, AK, BK, 4, 4><<<blocks, threads, 0, stream>>>(p);
+        sgemm_kernel<BM, BN, KT, WAVES_M, WAVES_N, AK, BK, 4, 4, WAVES_K>
+            <<<blocks, threads, 0, stream>>>(p);
     } else if (va == 4) {
-        sgemm_kernel<BM, BN, KT, WAVES_M, WAVES_N, AK, BK, 4, 1><<<blocks, threads, 0, stream>>>(p);
+        sgemm_kernel<BM, BN, KT, WAVES_M, WAVES_N, AK, BK, 4, 1, WAVES_K>
+            <<<blocks, threads, 0, stream>>>(p);
     } else if (vb == 4) {
-        sgemm_kernel<BM, BN, KT, WAVES_M, WAVES_N, AK, BK, 1, 4><<<blocks, threads, 0, stream>>>(p);
+        sgemm_kernel<BM, BN, KT, WAVES_M, WAVES_N, AK, BK, 1, 4, WAVES_K>
+            <<<blocks, threads, 0, stream>>>(p);
     } else {
-        sgemm_kernel<BM, BN, KT, WAVES_M, WAVES_N, AK, BK, 1, 1><<<blocks, threads, 0, stream>>>(p);
+        sgemm_kernel<BM, BN, KT, WAVES_M, WAVES_N, AK, BK, 1, 1, WAVES_K>
+            <<<blocks, threads, 0, stream>>>(p);
     }
 }
 
 // one_per_cu: no CU gets more than one workgroup. The 128x128 tile then runs 8 wavefronts of
 // 64x32 (2 per SIMD) instead of 4 of 64x64: 2048^3 145 against 155 us. With two workgroups per
-// CU the 4 wavefronts are faster (4096^3 1075 against 1105 us).
+// CU the 4 wavefronts are faster (4096^3 1075 against 1105 us). The 64x64 tile, unsplit, then
+// runs 16 wavefronts in four sets that share each depth slice.
 template <bool AK, bool BK>
 void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned blocks, bool one_per_cu,
                    hipStream_t stream) {
@@ -330,7 +338,14 @@ void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned block
         launch_vec<64, 128, 16, 2, 2, AK, BK>(p, va, vb, blocks, stream);
         break;
     case MFR_TILE_64x64:
-        launch_vec<64, 64, 32, 2, 2, AK, BK>(p, va, vb, blocks, stream);
+        if (one_per_cu && p.splits == 1) {
+            // 16 wavefronts: four sets of 2x2 share each 64-deep slice (4 per SIMD). 1024^3:
+            // 31.0 -> 27.7 us; 16384 x 4 x 4096: 113.7 -> 94.2 us. Split depth ranges are
+            // short and keep the 4-wavefront form (512^3 in two: 14.5 against 14.1 us).
+            launch_vec<64, 64, 64, 2, 2, AK, BK, 4>(p, va, vb, blocks, stream);
+        } else {
+            launch_vec<64, 64, 32, 2, 2, AK, BK>(p, va, vb, blocks, stream);
+        }
         break;
     default:
         if (one_per_cu) {

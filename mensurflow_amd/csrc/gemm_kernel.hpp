@@ -219,14 +219,20 @@ __device__ __forceinline__ void epilogue(const floatx16 (&acc)[FM][FN], float* c
     }
 }
 
-template <int BM, int BN, int KT, int WAVES_M, int WAVES_N, bool AK, bool BK, int VA, int VB>
-__global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_kernel(GemmParams p) {
-    constexpr int THREADS = WAVES_M * WAVES_N * 64;
+// WAVES_K > 1: WAVES_K sets of WAVES_M x WAVES_N wavefronts share each depth slice, set w taking
+// its 8-deep groups w, w + WAVES_K, ...; the sets' accumulators are then added through LDS, in
+// set order, and set 0 runs the epilogue. It gives a small grid (a workgroup per CU) several
+// wavefronts per SIMD without splitting the depth across workgroups.
+template <int BM, int BN, int KT, int WAVES_M, int WAVES_N, bool AK, bool BK, int VA, int VB,
+          int WAVES_K = 1>
+__global__ __launch_bounds__(WAVES_M * WAVES_N * WAVES_K * 64) void sgemm_kernel(GemmParams p) {
+    constexpr int THREADS = WAVES_M * WAVES_N * WAVES_K * 64;
     constexpr int WM = BM / WAVES_M;
     constexpr int WN = BN / WAVES_N;
     constexpr int FM = WM / 32; // 32x32 accumulator blocks per wavefront, along M
     constexpr int FN = WN / 32;
     static_assert(KT % 8 == 0 && WM % 32 == 0 && WN % 32 == 0, "tile shape");
+    static_assert((KT / 8) % WAVES_K == 0, "each wavefront set takes whole 8-deep groups");
     using LoadA = SliceLoader<BM, KT, AK, VA, THREADS>;
     using LoadB = SliceLoader<BN, KT, BK, VB, THREADS>;
     __shared__ float smem[2 * (LoadA::kFloats + LoadB::kFloats)];
@@ -281,8 +287,13 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_kernel(GemmParam
 
     const int lane = threadIdx.x % 64;
     const int wave = threadIdx.x / 64;
-    const int wave_m = wave / WAVES_N;
-    const int wave_n = wave % WAVES_N;
+    // With one set, the set index is the constant 0, which keeps every fragment's LDS offset
+    // a compile-time constant (a run-time 0 cost 3 % at 3000^3 on the 64x64 tile).
+    const int wave_mn = WAVES_K == 1 ? wave : wave % (WAVES_M * WAVES_N);
+    const int wave_k =
+        WAVES_K == 1 ? 0 : __builtin_amdgcn_readfirstlane(wave / (WAVES_M * WAVES_N));
+    const int wave_m = wave_mn / WAVES_N;
+    const int wave_n = wave_mn % WAVES_N;
     const int half = lane / 32;
     const int r32 = lane % 32;
 
@@ -321,7 +332,8 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_kernel(GemmParam
         const float* sa = lds_a(cur);
         const float* sb = lds_b(cur);
 #pragma unroll
-        for (int g = 0; g < KT / 8; ++g) {
+        for (int gi = 0; gi < KT / 8 / WAVES_K; ++gi) {
+            const int g = gi * WAVES_K + wave_k;
             float fa[FM][4];
             float fb[FN][4];
 #pragma unroll
@@ -349,6 +361,46 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_kernel(GemmParam
             lb.store(lds_b(cur ^ 1));
         }
         __syncthreads();
+    }
+
+    if constexpr (WAVES_K > 1) {
+        // The depth loop ended with a barrier, so the LDS tiles are free: sets 1.. park their
+        // accumulators there (lane-contiguous), set 0 adds them in set order.
+        constexpr int kPerWave = FM * FN * 16 * 64;
+        static_assert((WAVES_K - 1) * WAVES_M * WAVES_N * kPerWave <=
+                          2 * (LoadA::kFloats + LoadB::kFloats),
+                      "the partial accumulators fit in the tiles' LDS");
+        if (wave_k > 0) {
+            float* mine = smem + ((wave_k - 1) * WAVES_M * WAVES_N + wave_mn) * kPerWave;
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        mine[((i * FN + j) * 16 + e) * 64 + lane] = acc[i][j][e];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        if (wave_k > 0) {
+            return;
+        }
+#pragma unroll
+        for (int w = 1; w < WAVES_K; ++w) {
+            const float* theirs = smem + ((w - 1) * WAVES_M * WAVES_N + wave_mn) * kPerWave;
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        acc[i][j][e] += theirs[((i * FN + j) * 16 + e) * 64 + lane];
+                    }
+                }
+            }
+        }
     }
 
     // ---- epilogue: accumulator e of block (i, j) is C(row, col) with
