@@ -717,3 +717,27 @@ def test_repeated_shapes_with_new_operands(stream, oracle):
         want = oracle.gelu(pre, approximate=True) if act == mf.ACT_GELU_TANH else pre
         assert same_bits(c.numpy(), want), trial
         check_guards(buf)
+
+
+@pytest.mark.parametrize("m,n,k", [(1000, 1000, 1000), (300, 260, 1023), (64, 64, 2000),
+                                   (37, 100, 65), (1024, 1024, 0)])
+def test_exact_64x64_sixteen_wave_form(stream, m, n, k):
+    """The 64x64 tile unsplit with at most one workgroup per CU runs 16 wavefronts in four sets
+    sharing each depth slice, their accumulators added through LDS: bits equal the exact result
+    in all four layouts (4-byte loads for odd k), with alpha, beta*C0, a bias and gelu."""
+    assert ((m + 63) // 64) * ((n + 63) // 64) <= mf.device_info(0).compute_units
+    a = quarter_matrix(m, k, 91)
+    b = quarter_matrix(k, n, 92)
+    c0 = quarter_matrix(m, n, 93)
+    bias = quarter_matrix(1, n, 94)[0]
+    pre = (np.float32(0.5) * exact_product(a, b) + np.float32(1.5) * c0 + bias).astype(np.float32)
+    for trans_a in (False, True):
+        for trans_b in (False, True):
+            a_st = np.ascontiguousarray(a.T) if trans_a else a
+            b_st = np.ascontiguousarray(b.T) if trans_b else b
+            c, buf = guarded_output(stream, (m, n))
+            mf.gemm(dev(a_st, stream), dev(b_st, stream), alpha=0.5, c0=dev(c0, stream), beta=1.5,
+                    trans_a=trans_a, trans_b=trans_b, bias=dev(bias, stream), out=c,
+                    tile=mf.abi.TILE_64x64, splits=1, stage=mf.abi.STAGE_NEVER)
+            assert same_bits(c.numpy(), pre), (trans_a, trans_b)
+            check_guards(buf)
