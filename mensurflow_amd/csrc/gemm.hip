@@ -322,8 +322,9 @@ void launch_vec(const GemmParams& p, int va, int vb, unsigned blocks, hipStream_
 
 // one_per_cu: no CU gets more than one workgroup. The 128x128 tile then runs 8 wavefronts of
 // 64x32 (2 per SIMD) instead of 4 of 64x64: 2048^3 145 against 155 us. With two workgroups per
-// CU the 4 wavefronts are faster (4096^3 1075 against 1105 us). The 64x64 tile, unsplit, then
-// runs 16 wavefronts in four sets that share each depth slice.
+// CU the 4 wavefronts are faster (4096^3 1075 against 1105 us). Unsplit, the 128x128 tile
+// then runs 16 wavefronts in two sets and the 64x64 tile 16 in four, the sets sharing each
+// depth slice.
 template <bool AK, bool BK>
 void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned blocks, bool one_per_cu,
                    hipStream_t stream) {
@@ -348,7 +349,12 @@ void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned block
         }
         break;
     default:
-        if (one_per_cu) {
+        if (one_per_cu && p.splits == 1) {
+            // 16 wavefronts: two sets of 2x4 share each 64-deep slice (4 per SIMD). 2048^3:
+            // 150.2 -> 145.6 us; 2048 x 2048 x 8192: 583.9 -> 560.9 us (32-deep slices: 149.3
+            // and 574.1 us).
+            launch_vec<128, 128, 64, 2, 4, AK, BK, 2>(p, va, vb, blocks, stream);
+        } else if (one_per_cu) {
             launch_vec<128, 128, 32, 2, 4, AK, BK>(p, va, vb, blocks, stream);
         } else {
             launch_vec<128, 128, 32, 2, 2, AK, BK>(p, va, vb, blocks, stream);

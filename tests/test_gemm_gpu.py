@@ -719,13 +719,18 @@ def test_repeated_shapes_with_new_operands(stream, oracle):
         check_guards(buf)
 
 
-@pytest.mark.parametrize("m,n,k", [(1000, 1000, 1000), (300, 260, 1023), (64, 64, 2000),
-                                   (37, 100, 65), (1024, 1024, 0)])
-def test_exact_64x64_sixteen_wave_form(stream, m, n, k):
-    """The 64x64 tile unsplit with at most one workgroup per CU runs 16 wavefronts in four sets
-    sharing each depth slice, their accumulators added through LDS: bits equal the exact result
-    in all four layouts (4-byte loads for odd k), with alpha, beta*C0, a bias and gelu."""
-    assert ((m + 63) // 64) * ((n + 63) // 64) <= mf.device_info(0).compute_units
+@pytest.mark.parametrize("tile,m,n,k", [
+    (mf.abi.TILE_64x64, 1000, 1000, 1000), (mf.abi.TILE_64x64, 300, 260, 1023),
+    (mf.abi.TILE_64x64, 64, 64, 2000), (mf.abi.TILE_64x64, 37, 100, 65),
+    (mf.abi.TILE_64x64, 1024, 1024, 0), (mf.abi.TILE_128x128, 2000, 2048, 300),
+    (mf.abi.TILE_128x128, 300, 260, 1023), (mf.abi.TILE_128x128, 129, 127, 70)])
+def test_exact_sixteen_wave_set_forms(stream, tile, m, n, k):
+    """Unsplit with at most one workgroup per CU, the 64x64 tile runs 16 wavefronts in four sets
+    and the 128x128 tile 16 in two, the sets sharing each depth slice and adding their
+    accumulators through LDS: bits equal the exact result in all four layouts (4-byte loads for
+    odd k), with alpha, beta*C0 and a bias."""
+    size = 64 if tile == mf.abi.TILE_64x64 else 128
+    assert ((m + size - 1) // size) * ((n + size - 1) // size) <= mf.device_info(0).compute_units
     a = quarter_matrix(m, k, 91)
     b = quarter_matrix(k, n, 92)
     c0 = quarter_matrix(m, n, 93)
@@ -738,6 +743,6 @@ def test_exact_64x64_sixteen_wave_form(stream, m, n, k):
             c, buf = guarded_output(stream, (m, n))
             mf.gemm(dev(a_st, stream), dev(b_st, stream), alpha=0.5, c0=dev(c0, stream), beta=1.5,
                     trans_a=trans_a, trans_b=trans_b, bias=dev(bias, stream), out=c,
-                    tile=mf.abi.TILE_64x64, splits=1, stage=mf.abi.STAGE_NEVER)
+                    tile=tile, splits=1, stage=mf.abi.STAGE_NEVER)
             assert same_bits(c.numpy(), pre), (trans_a, trans_b)
             check_guards(buf)
