@@ -34,6 +34,10 @@ struct GemmParams {
     int64_t k_per_split;
     int32_t splits;
     float* partial;
+    // Nonzero: C is written with non-temporal (streaming) stores on interior tiles without C0 or
+    // an activation. Set for outputs larger than the last-level cache whose rows all start on
+    // 128-byte lines (partial lines would be merged in L2 otherwise).
+    int32_t stream_c;
 };
 
 // Global -> register -> LDS copy of one operand slice: ROWS rows (M for A, N for B) by KT depth.
@@ -132,9 +136,9 @@ template <int ROWS, int KT, bool KMAJ, int V, int THREADS> struct SliceLoader {
 // are the reference's. alpha * acc is exact for alpha == 1. INTERIOR: every row and column is
 // inside C (no checks). C0 == kC0Batched: c0 is non-null and a row-block's C0 values are all
 // loaded before any is used, so the loads overlap; kC0None: no C0; kC0Checked: c0 checked per
-// element (one copy of the code for both cases).
+// element (one copy of the code for both cases). STREAM: non-temporal stores.
 enum { kC0None = 0, kC0Batched = 1, kC0Checked = 2 };
-template <int FM, int FN, int ACT, bool INTERIOR, bool RAW, int C0>
+template <int FM, int FN, int ACT, bool INTERIOR, bool RAW, int C0, bool STREAM = false>
 __device__ __forceinline__ void write_tile(const floatx16 (&acc)[FM][FN], float* c, int64_t c_rs,
                                            const float* c0, int64_t c0_rs, const GemmParams& p,
                                            int64_t row0, int64_t col0) {
@@ -187,7 +191,11 @@ __device__ __forceinline__ void write_tile(const floatx16 (&acc)[FM][FN], float*
                         v = mfr::dev::gelu(v, ACT);
                     }
                 }
-                c_i[dr * c_rs + 32 * j] = v;
+                if constexpr (STREAM) {
+                    __builtin_nontemporal_store(v, &c_i[dr * c_rs + 32 * j]);
+                } else {
+                    c_i[dr * c_rs + 32 * j] = v;
+                }
             }
         }
     }
@@ -210,7 +218,10 @@ __device__ __forceinline__ void epilogue(const floatx16 (&acc)[FM][FN], float* c
                                                               col0);
         }
     } else {
-        if (interior) {
+        if (interior && p.stream_c) {
+            write_tile<FM, FN, ACT, true, false, kC0None, true>(acc, c, c_rs, c0, c0_rs, p, row0,
+                                                                col0);
+        } else if (interior) {
             write_tile<FM, FN, ACT, true, false, kC0None>(acc, c, c_rs, c0, c0_rs, p, row0, col0);
         } else {
             write_tile<FM, FN, ACT, false, false, kC0None>(acc, c, c_rs, c0, c0_rs, p, row0,

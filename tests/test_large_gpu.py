@@ -90,3 +90,25 @@ def test_operands_past_2_31_elements(stream):
 
     assert np.all(mf.argmax(a).numpy() == int(np.argmax(c)))
     a.close()
+
+
+def test_streamed_output_past_last_level_cache(stream):
+    """An output over 256 MiB whose rows start on 128-byte lines is written with non-temporal
+    stores (8192 x 8448 floats, 277 MB): sampled rows equal the exact product; a padded row
+    stride (off the lines) takes ordinary stores and gives the same bits."""
+    m, n, k = 8192, 8448, 12
+    av = quarter_matrix(m, k, 111)
+    bv = quarter_matrix(k, n, 112)
+    a_d, b_d = dev(av, stream), dev(bv, stream)
+    c = mf.DeviceArray.empty((m, n), stream)
+    mf.gemm(a_d, b_d, alpha=0.5, out=c)
+    wide = mf.DeviceArray.empty((m, n + 1), stream)
+    mf.gemm(a_d, b_d, alpha=0.5, out=wide.slice(1, 0, n))
+    for lo in (0, 4096, m - 3):
+        rows = slice(lo, lo + 3)
+        want = (np.float32(0.5) * (av[rows].astype(np.float64) @ bv.astype(np.float64))
+                .astype(np.float32))
+        assert same_bits(c.slice(0, lo, lo + 3).numpy(), want), lo
+        assert same_bits(wide.slice(0, lo, lo + 3).numpy()[:, :n], want), lo
+    c.close()
+    wide.close()
