@@ -705,6 +705,14 @@ void launch(int64_t d, int waves, const AttnParams& p, unsigned grid, hipStream_
                 p);
         }
         break;
+    case 96:
+        if (waves == 4) {
+            attention_kernel<96, 32, MASKED, 4><<<grid, 4 * 64, 0, st>>>(p);
+        } else {
+            attention_kernel<96, 64, MASKED, waves_for(96)><<<grid, waves_for(96) * 64, 0, st>>>(
+                p);
+        }
+        break;
     default:
         if (waves == 4) {
             attention_kernel<128, 32, MASKED, 4><<<grid, 4 * 64, 0, st>>>(p);
@@ -741,8 +749,8 @@ void run_attention(mfr_stream& s, const mfr_attention_desc& d) {
     if (d.lq == 0 || batch_count == 0) {
         return;
     }
-    if (d.d != 32 && d.d != 64 && d.d != 128) {
-        throw mfr::Error(MFR_E_UNSUPPORTED, "attention: fused kernel takes d = 32, 64 or 128");
+    if (d.d != 32 && d.d != 64 && d.d != 96 && d.d != 128) {
+        throw mfr::Error(MFR_E_UNSUPPORTED, "attention: fused kernel takes d = 32, 64, 96 or 128");
     }
     require(d.q != nullptr && d.out != nullptr, "attention: null q or out");
     require(d.lk == 0 || (d.k != nullptr && d.v != nullptr), "attention: null k or v");

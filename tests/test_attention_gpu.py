@@ -76,7 +76,7 @@ def test_config5_attention_full(stream, oracle):
             assert np.max(np.abs(got[bi, hi] - ref) / (1.0 + np.abs(ref))) < 1e-4
 
 
-@pytest.mark.parametrize("d", [32, 64, 128])
+@pytest.mark.parametrize("d", [32, 64, 96, 128])
 @pytest.mark.parametrize("lq,lk", [(100, 130), (300, 200), (129, 1), (1, 257)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_fused_shapes(stream, oracle, d, lq, lk, causal):
@@ -94,7 +94,7 @@ def test_fused_shapes(stream, oracle, d, lq, lk, causal):
     assert_gemm_parity(got, want, mag + 1e-6, lk, f"fused d={d} lq={lq} lk={lk}")
 
 
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [64, 96, 128])
 @pytest.mark.parametrize("causal", [False, True])
 def test_fused_many_batch_entries(stream, oracle, d, causal):
     """Enough batch entries for two workgroups of 8 wavefronts per CU (512 entries of 100
