@@ -285,8 +285,8 @@ int mfr_elementwise(mfr_stream_t stream, int op, const float* a, const float* b,
  * sums by exp(m_old - m_new), and the output is divided by the row's sum once at the end; a row
  * with every key removed gives zeros, a NaN score gives a NaN row. q [.., lq, d], k [.., lk, d],
  * v [.., lk, d] and out [.., lq, d] have unit stride along d, row strides and batch strides
- * (0 = broadcast) that are multiples of 4 floats and 16-byte aligned bases; d is 32, 64, 96 or
- * 128.
+ * (0 = broadcast) that are multiples of 4 floats and 16-byte aligned bases; d is a multiple of 16,
+ * at most 128.
  * Anything else is MFR_E_UNSUPPORTED (the caller composes the op instead). The mask (NULL, or
  * 1 byte per element: nonzero keeps) has any strides, 0 for broadcast dimensions. scale 0 means
  * fl(1/sqrt(d)).

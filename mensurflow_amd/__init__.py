@@ -467,7 +467,8 @@ def attention_fused(q: DeviceArray, k: DeviceArray, v: DeviceArray,
                     mask: DeviceArray | None = None, causal: bool = False, scale: float = 0.0,
                     out: DeviceArray | None = None) -> DeviceArray:
     """mfr_attention: the whole op in one kernel (online softmax, no score matrix). q [..., Lq, D],
-    k and v [..., Lk, D] with equal batch shapes (stride 0 for broadcast), D in {32, 64, 96, 128};
+    k and v [..., Lk, D] with equal batch shapes (stride 0 for broadcast), D a multiple of 16 up to
+    128;
     mask a uint8 array broadcastable to [..., Lq, Lk]. Raises NotImplementedError for layouts
     the kernel does not take."""
     lq, depth = q.shape[-2:]

@@ -38,7 +38,7 @@ constexpr int kWaves = 4; // wavefronts of 32 queries per workgroup, by default
 // Wavefronts per workgroup by head size: 8 for d = 64 and 128, where one K/V tile then serves
 // 256 queries (8 x 16 x 1024, causal: d = 64 189-191 us against 199-205 us with 4; d = 128
 // 346 us against 373-376 us), 4 for d = 32 (109 us with 8 against 105 us).
-constexpr int waves_for(int64_t d) { return d == 32 ? kWaves : 8; }
+constexpr int waves_for(int64_t d) { return d == 32 || d % 32 != 0 ? kWaves : 8; }
 
 // Wavefronts per workgroup for one launch: waves_for(d), except 4 for d = 64 and 128 when
 // workgroups of 8 would leave fewer than two per CU (causal) or idle CUs. Causal work grows with
@@ -121,11 +121,15 @@ __global__ __launch_bounds__(WAVES * 64, MIN_WAVES) void attention_kernel(AttnPa
     constexpr int THREADS = WAVES * 64;
     constexpr int BLOCK_Q = WAVES * 32;
     constexpr int SUB = BK / 32; // 32-key sub-blocks per key block
-    constexpr int DB = D / 32;   // 32-wide output column blocks
+    // d need not be a multiple of 32: the output side runs on DP = d rounded up to 32, whose V
+    // rows past d load as zeros, so those output columns are zero and never stored.
+    static_assert(D % 16 == 0, "d is a multiple of 16");
+    constexpr int DP = (D + 31) / 32 * 32;
+    constexpr int DB = DP / 32;  // 32-wide output column blocks
     constexpr int G = D / 8;     // depth groups of q . k
-    constexpr int kStagePitch = D + 4;
-    using LoadK = SliceLoader<BK, D, true, 4, THREADS>;  // rows = keys, depth = d
-    using LoadV = SliceLoader<D, BK, false, 4, THREADS>; // rows = d, depth = keys
+    constexpr int kStagePitch = DP + 4;
+    using LoadK = SliceLoader<BK, D, true, 4, THREADS>;   // rows = keys, depth = d
+    using LoadV = SliceLoader<DP, BK, false, 4, THREADS>; // rows = d (DP), depth = keys
     // Double-buffered K and V tiles; after the key loop the same memory stages the output.
     constexpr int kTileFloats = 2 * (LoadK::kFloats + LoadV::kFloats);
     constexpr int kStageFloats = WAVES * 32 * kStagePitch;
@@ -705,6 +709,18 @@ void launch(int64_t d, int waves, const AttnParams& p, unsigned grid, hipStream_
                 p);
         }
         break;
+    case 16:
+        attention_kernel<16, 64, MASKED, 4><<<grid, 4 * 64, 0, st>>>(p);
+        break;
+    case 48:
+        attention_kernel<48, 64, MASKED, 4><<<grid, 4 * 64, 0, st>>>(p);
+        break;
+    case 80:
+        attention_kernel<80, 64, MASKED, 4><<<grid, 4 * 64, 0, st>>>(p);
+        break;
+    case 112:
+        attention_kernel<112, 64, MASKED, 4><<<grid, 4 * 64, 0, st>>>(p);
+        break;
     case 96:
         if (waves == 4) {
             attention_kernel<96, 32, MASKED, 4><<<grid, 4 * 64, 0, st>>>(p);
@@ -749,8 +765,9 @@ void run_attention(mfr_stream& s, const mfr_attention_desc& d) {
     if (d.lq == 0 || batch_count == 0) {
         return;
     }
-    if (d.d != 32 && d.d != 64 && d.d != 96 && d.d != 128) {
-        throw mfr::Error(MFR_E_UNSUPPORTED, "attention: fused kernel takes d = 32, 64, 96 or 128");
+    if (d.d <= 0 || d.d > 128 || d.d % 16 != 0) {
+        throw mfr::Error(MFR_E_UNSUPPORTED,
+                         "attention: fused kernel takes d = 16, 32, ..., 128 (a multiple of 16)");
     }
     require(d.q != nullptr && d.out != nullptr, "attention: null q or out");
     require(d.lk == 0 || (d.k != nullptr && d.v != nullptr), "attention: null k or v");

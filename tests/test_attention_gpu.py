@@ -76,7 +76,7 @@ def test_config5_attention_full(stream, oracle):
             assert np.max(np.abs(got[bi, hi] - ref) / (1.0 + np.abs(ref))) < 1e-4
 
 
-@pytest.mark.parametrize("d", [32, 64, 96, 128])
+@pytest.mark.parametrize("d", [16, 32, 48, 64, 80, 96, 112, 128])
 @pytest.mark.parametrize("lq,lk", [(100, 130), (300, 200), (129, 1), (1, 257)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_fused_shapes(stream, oracle, d, lq, lk, causal):
@@ -153,10 +153,10 @@ def test_fused_nan_row_and_empty_keys(stream, oracle):
 
 
 def test_fused_unsupported_falls_back(stream, oracle):
-    """d = 48 and a q view starting off a 16-byte boundary are not the fused kernel's: fused=True
-    raises NotImplementedError, the default composes the op instead."""
+    """d = 40 (not a multiple of 16) and a q view starting off a 16-byte boundary are not the
+    fused kernel's: fused=True raises NotImplementedError, the default composes the op instead."""
     lq, lk = 33, 47
-    for d, offset in ((48, 0), (64, 1)):
+    for d, offset in ((40, 0), (64, 1)):
         store = normal(oracle, (lq * d + offset,), 0.0, 1.0, 51)
         q = store[offset:].reshape(1, lq, d)
         k = normal(oracle, (1, lk, d), 0.0, 1.0, 52)
