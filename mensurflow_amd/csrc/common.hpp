@@ -120,6 +120,14 @@ inline void check_launch(const char* what) { check(hipGetLastError(), what); }
 
 // ---- device helpers --------------------------------------------------------------------------
 
+namespace mfr {
+
+// MI355X's last-level cache (Infinity Cache). An output larger than this is written with
+// non-temporal stores: no later kernel would find it cached anyway.
+constexpr double kLastLevelCacheBytes = 256.0 * 1024 * 1024;
+
+} // namespace mfr
+
 namespace mfr::dev {
 
 constexpr int kWave = 64;
@@ -128,6 +136,13 @@ typedef float native_float4 __attribute__((ext_vector_type(4)));
 
 // 16-byte load marked non-temporal: streamed data that is read once should not displace
 // reused data (x, C0) from the caches. p must be 16-byte aligned.
+// A 16-byte non-temporal store (not kept in the caches), for outputs written once and too large
+// for the last-level cache.
+__device__ inline void store_streaming(float* p, float4 v) {
+    const native_float4 n = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(n, reinterpret_cast<native_float4*>(p));
+}
+
 __device__ inline float4 load_streaming(const float* p) {
     const native_float4 v = __builtin_nontemporal_load(reinterpret_cast<const native_float4*>(p));
     return make_float4(v.x, v.y, v.z, v.w);

@@ -7,6 +7,8 @@
 //   argmax            src/backends/cpu/ops/reduction/reduction.cpp:284-296
 #include "common.hpp"
 
+#include <type_traits>
+
 #include <cmath>
 
 namespace {
@@ -109,6 +111,8 @@ inline void stream_shape(int64_t quads, unsigned* blocks, int64_t* chunk) {
     *blocks = static_cast<unsigned>((quads + *chunk - 1) / *chunk);
 }
 
+// STREAM: non-temporal stores (outputs larger than the last-level cache).
+template <bool STREAM>
 __global__ __launch_bounds__(kStreamThreads) void where4_kernel(
     const uint32_t* __restrict__ cond, const float4* __restrict__ x, const float4* __restrict__ y,
     float4* __restrict__ out, int64_t quads, int64_t chunk) {
@@ -135,13 +139,17 @@ __global__ __launch_bounds__(kStreamThreads) void where4_kernel(
                 v.y = (c[u] & 0xff00u) != 0 ? xv[u].y : yv[u].y;
                 v.z = (c[u] & 0xff0000u) != 0 ? xv[u].z : yv[u].z;
                 v.w = (c[u] & 0xff000000u) != 0 ? xv[u].w : yv[u].w;
-                out[j] = v;
+                if constexpr (STREAM) {
+                    mfr::dev::store_streaming(reinterpret_cast<float*>(out + j), v);
+                } else {
+                    out[j] = v;
+                }
             }
         }
     }
 }
 
-template <int OP>
+template <int OP, bool STREAM>
 __global__ __launch_bounds__(kStreamThreads) void binary4_kernel(const float4* __restrict__ a,
                                                                  const float4* __restrict__ b,
                                                                  float alpha,
@@ -176,7 +184,11 @@ __global__ __launch_bounds__(kStreamThreads) void binary4_kernel(const float4* _
                     v = make_float4(alpha * av[u].x, alpha * av[u].y, alpha * av[u].z,
                                     alpha * av[u].w);
                 }
-                out[j] = v;
+                if constexpr (STREAM) {
+                    mfr::dev::store_streaming(reinterpret_cast<float*>(out + j), v);
+                } else {
+                    out[j] = v;
+                }
             }
         }
     }
@@ -188,7 +200,7 @@ __device__ inline float line_max(float m, int has_nan) { return has_nan ? NAN : 
 
 // Softmax of contiguous lines (inner == 1), one wavefront per line, the line held in registers:
 // each lane keeps kPer values at positions lane + 64*i.
-template <int kPer>
+template <int kPer, bool STREAM>
 __global__ __launch_bounds__(256) void softmax_rows_reg_kernel(const float* __restrict__ x,
                                                                float* __restrict__ y,
                                                                int64_t lines, int64_t length) {
@@ -236,7 +248,11 @@ __global__ __launch_bounds__(256) void softmax_rows_reg_kernel(const float* __re
     for (int i = 0; i < kPer; ++i) {
         const int64_t j = lane + static_cast<int64_t>(kWave) * i;
         if (j < length) {
-            out[j] = v[i] * scale;
+            if constexpr (STREAM) {
+                __builtin_nontemporal_store(v[i] * scale, out + j);
+            } else {
+                out[j] = v[i] * scale;
+            }
         }
     }
 }
@@ -369,15 +385,31 @@ int mfr_elementwise(mfr_stream_t stream, int op, const float* a, const float* b,
             const auto* a4 = reinterpret_cast<const float4*>(a);
             const auto* b4 = reinterpret_cast<const float4*>(b);
             auto* o4 = reinterpret_cast<float4*>(out);
-            if (op == MFR_EW_ADD) {
-                binary4_kernel<MFR_EW_ADD><<<blocks, kStreamThreads, 0, s.stream>>>(
-                    a4, b4, alpha, o4, quads, chunk);
-            } else if (op == MFR_EW_MUL) {
-                binary4_kernel<MFR_EW_MUL><<<blocks, kStreamThreads, 0, s.stream>>>(
-                    a4, b4, alpha, o4, quads, chunk);
+            // Outputs past the last-level cache stream (512 MiB add: 300 -> 290 us).
+            const bool stream_out = 4.0 * static_cast<double>(n) > mfr::kLastLevelCacheBytes;
+            auto run = [&](auto op_tag, auto stream_tag) {
+                binary4_kernel<decltype(op_tag)::value, decltype(stream_tag)::value>
+                    <<<blocks, kStreamThreads, 0, s.stream>>>(a4, b4, alpha, o4, quads, chunk);
+            };
+            using Add = std::integral_constant<int, MFR_EW_ADD>;
+            using Mul = std::integral_constant<int, MFR_EW_MUL>;
+            using Scal = std::integral_constant<int, MFR_EW_SCAL>;
+            if (stream_out) {
+                if (op == MFR_EW_ADD) {
+                    run(Add{}, std::true_type{});
+                } else if (op == MFR_EW_MUL) {
+                    run(Mul{}, std::true_type{});
+                } else {
+                    run(Scal{}, std::true_type{});
+                }
             } else {
-                binary4_kernel<MFR_EW_SCAL><<<blocks, kStreamThreads, 0, s.stream>>>(
-                    a4, b4, alpha, o4, quads, chunk);
+                if (op == MFR_EW_ADD) {
+                    run(Add{}, std::false_type{});
+                } else if (op == MFR_EW_MUL) {
+                    run(Mul{}, std::false_type{});
+                } else {
+                    run(Scal{}, std::false_type{});
+                }
             }
             mfr::check_launch("binary4_kernel");
             done = 4 * quads;
@@ -445,9 +477,19 @@ int mfr_where(mfr_stream_t stream, const uint8_t* cond, const float* x, const fl
             unsigned blocks = 0;
             int64_t chunk = 0;
             stream_shape(quads, &blocks, &chunk);
-            where4_kernel<<<blocks, kStreamThreads, 0, s.stream>>>(
-                reinterpret_cast<const uint32_t*>(cond), reinterpret_cast<const float4*>(x),
-                reinterpret_cast<const float4*>(y), reinterpret_cast<float4*>(out), quads, chunk);
+            // Outputs past the last-level cache stream (512 MiB: 327 -> 314 us).
+            const bool stream_out = 4.0 * static_cast<double>(n) > mfr::kLastLevelCacheBytes;
+            const auto* c4 = reinterpret_cast<const uint32_t*>(cond);
+            const auto* x4 = reinterpret_cast<const float4*>(x);
+            const auto* y4 = reinterpret_cast<const float4*>(y);
+            auto* o4 = reinterpret_cast<float4*>(out);
+            if (stream_out) {
+                where4_kernel<true><<<blocks, kStreamThreads, 0, s.stream>>>(c4, x4, y4, o4, quads,
+                                                                             chunk);
+            } else {
+                where4_kernel<false><<<blocks, kStreamThreads, 0, s.stream>>>(c4, x4, y4, o4,
+                                                                              quads, chunk);
+            }
             mfr::check_launch("where4_kernel");
             done = 4 * quads;
         }
@@ -471,12 +513,19 @@ int mfr_softmax(mfr_stream_t stream, const float* x, float* y, int64_t outer, in
         }
         mfr::require(x != nullptr && y != nullptr, "softmax: null pointer");
         const unsigned blocks = mfr::grid_blocks(lines, 4);
+        // Outputs past the last-level cache stream (512 MiB: 182 -> 178 us).
+        const bool stream_out =
+            4.0 * static_cast<double>(lines) * length > mfr::kLastLevelCacheBytes;
         if (inner == 1 && length <= 64 * 4) {
-            softmax_rows_reg_kernel<4><<<blocks, 256, 0, s.stream>>>(x, y, lines, length);
+            softmax_rows_reg_kernel<4, false><<<blocks, 256, 0, s.stream>>>(x, y, lines, length);
+        } else if (inner == 1 && length <= 64 * 16 && stream_out) {
+            softmax_rows_reg_kernel<16, true><<<blocks, 256, 0, s.stream>>>(x, y, lines, length);
         } else if (inner == 1 && length <= 64 * 16) {
-            softmax_rows_reg_kernel<16><<<blocks, 256, 0, s.stream>>>(x, y, lines, length);
+            softmax_rows_reg_kernel<16, false><<<blocks, 256, 0, s.stream>>>(x, y, lines, length);
+        } else if (inner == 1 && length <= 64 * 32 && stream_out) {
+            softmax_rows_reg_kernel<32, true><<<blocks, 256, 0, s.stream>>>(x, y, lines, length);
         } else if (inner == 1 && length <= 64 * 32) {
-            softmax_rows_reg_kernel<32><<<blocks, 256, 0, s.stream>>>(x, y, lines, length);
+            softmax_rows_reg_kernel<32, false><<<blocks, 256, 0, s.stream>>>(x, y, lines, length);
         } else {
             softmax_lines_kernel<<<blocks, 256, 0, s.stream>>>(x, y, outer, length, inner);
         }

@@ -810,8 +810,7 @@ void launch_thin(const Plan& plan, const GemmParams& q, int va, int vb, hipStrea
 // slower streamed (the MLP's 4099-float rows, whose tile edges write partial lines: 321.5 ->
 // 334.5 us); 4096^3 and 2048^3 are unchanged either way.
 bool streamed_output(const GemmParams& q) {
-    constexpr double kLastLevelCacheBytes = 256.0 * 1024 * 1024;
-    if (4.0 * static_cast<double>(q.m) * q.n * q.batch_count <= kLastLevelCacheBytes) {
+    if (4.0 * static_cast<double>(q.m) * q.n * q.batch_count <= mfr::kLastLevelCacheBytes) {
         return false;
     }
     if (reinterpret_cast<uintptr_t>(q.c) % 128 != 0 || q.c_rs % 32 != 0) {
