@@ -19,6 +19,8 @@
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <unordered_map>
+#include <utility>
 #include <vector>
 
 namespace mensurflow::detail {
@@ -40,20 +42,117 @@ void check(int status) {
     throw std::runtime_error(message);
 }
 
+// Device memory blocks of one device kept for reuse. Every kernel and copy of a device runs on
+// that device's one stream (RocmBackend::stream), in order, so a block a Buffer releases can serve
+// the next allocation at once: work on the new tensor is queued after the work that used the old
+// one. Without the pool each released tensor would reach hipFree, which waits for the whole
+// device, so dropping a temporary would stall the host until the GPU is idle.
+// Blocks come in size classes (powers of two below 1 MiB, at least 512 B; multiples of 2 MiB
+// above). Idle blocks are kept up to 1/8 of the device's memory; past that a released block is
+// freed. An allocation that fails frees every idle block and tries again.
+class BlockPool {
+  public:
+    explicit BlockPool(int device) : device_(device) {
+        std::size_t bytes = 0;
+        if (mfr_get_device_info(device, nullptr, 0, &bytes, nullptr, nullptr) == MFR_OK) {
+            limit_ = std::max<std::size_t>(bytes / 8, std::size_t{1} << 30);
+        }
+    }
+    ~BlockPool() { release_idle(); }
+    BlockPool(const BlockPool&) = delete;
+    BlockPool& operator=(const BlockPool&) = delete;
+
+    static std::size_t size_class(std::size_t bytes) {
+        constexpr std::size_t kSmall = std::size_t{1} << 20;
+        constexpr std::size_t kLargeStep = std::size_t{2} << 20;
+        if (bytes >= kSmall) {
+            return (bytes + kLargeStep - 1) / kLargeStep * kLargeStep;
+        }
+        std::size_t size = 512;
+        while (size < bytes) {
+            size *= 2;
+        }
+        return size;
+    }
+
+    // A block of `size` bytes (a size class): an idle one, else a new allocation.
+    void* take(std::size_t size) {
+        {
+            std::lock_guard<std::mutex> lock(mutex_);
+            auto found = idle_.find(size);
+            if (found != idle_.end() && !found->second.empty()) {
+                void* block = found->second.back();
+                found->second.pop_back();
+                idle_bytes_ -= size;
+                return block;
+            }
+        }
+        void* block = nullptr;
+        if (mfr_malloc(device_, size, &block) != MFR_OK) {
+            release_idle();
+            check(mfr_malloc(device_, size, &block));
+        }
+        return block;
+    }
+
+    void give(std::size_t size, void* block) {
+        {
+            std::lock_guard<std::mutex> lock(mutex_);
+            if (idle_bytes_ + size <= limit_) {
+                idle_[size].push_back(block);
+                idle_bytes_ += size;
+                return;
+            }
+        }
+        (void)mfr_free(device_, block); // errors ignored, as the reference's buffer destructor
+    }
+
+    void release_idle() {
+        std::unordered_map<std::size_t, std::vector<void*>> blocks;
+        {
+            std::lock_guard<std::mutex> lock(mutex_);
+            blocks.swap(idle_);
+            idle_bytes_ = 0;
+        }
+        for (auto& [size, list] : blocks) {
+            for (void* block : list) {
+                (void)mfr_free(device_, block);
+            }
+        }
+    }
+
+  private:
+    int device_;
+    std::size_t limit_ = std::size_t{1} << 30;
+    std::mutex mutex_;
+    std::unordered_map<std::size_t, std::vector<void*>> idle_;
+    std::size_t idle_bytes_ = 0;
+};
+
+// A tensor's device memory: a pool block (a zero-byte buffer has none and a null pointer).
 class RocmBuffer final : public Buffer {
   public:
-    RocmBuffer(int device, std::size_t bytes) : device_(device), size_(bytes) {
-        check(mfr_malloc(device, bytes, &data_));
+    RocmBuffer(std::shared_ptr<BlockPool> pool, std::size_t bytes)
+        : pool_(std::move(pool)), size_(bytes) {
+        if (bytes > 0) {
+            block_ = BlockPool::size_class(bytes);
+            data_ = pool_->take(block_);
+        }
     }
-    ~RocmBuffer() override { (void)mfr_free(device_, data_); } // errors ignored, as the reference
+    ~RocmBuffer() override {
+        if (data_ != nullptr) {
+            pool_->give(block_, data_);
+        }
+    }
     RocmBuffer(const RocmBuffer&) = delete;
     RocmBuffer& operator=(const RocmBuffer&) = delete;
     std::size_t size() const override { return size_; }
     void* native() const override { return data_; }
 
   private:
-    int device_;
+    std::shared_ptr<BlockPool> pool_; // outlives every buffer taken from it
     std::size_t size_;
+    std::size_t block_ = 0;
     void* data_ = nullptr;
 };
 
@@ -506,6 +605,9 @@ class RocmBackend final : public Backend {
             count_ = count;
         }
         streams_.resize(static_cast<std::size_t>(count_));
+        for (int i = 0; i < count_; ++i) {
+            pools_.push_back(std::make_shared<BlockPool>(i));
+        }
     }
 
     DeviceType type() const override { return DeviceType::ROCm; }
@@ -519,7 +621,7 @@ class RocmBackend final : public Backend {
     }
 
     std::shared_ptr<Buffer> allocate(int index, std::size_t bytes) override {
-        return std::make_shared<RocmBuffer>(index, bytes);
+        return std::make_shared<RocmBuffer>(pools_.at(static_cast<std::size_t>(index)), bytes);
     }
 
     Stream& stream(int index) override {
@@ -566,6 +668,7 @@ class RocmBackend final : public Backend {
     int count_ = 0;
     std::mutex mutex_;
     std::vector<std::unique_ptr<RocmStream>> streams_;
+    std::vector<std::shared_ptr<BlockPool>> pools_;
 };
 
 } // namespace

@@ -140,6 +140,48 @@ void test_transfers(Device device) {
     test::require(Tensor::empty({0, 5}, DType::F32, device).to_vector<float>().empty(), "empty");
 }
 
+// A dropped tensor's device memory serves the next allocation of its size at once, while a
+// kernel that reads it may still be queued on the device's stream. Products whose inputs are
+// released before the result is read, followed by fills of new tensors of those sizes, must read
+// the inputs they were given. Quarter-integer values make every sum exact.
+void test_released_memory_reuse(Device device) {
+    const auto on = test::execution_on(device);
+    for (int round = 0; round < 24; ++round) {
+        const std::int64_t m = 64 + 8 * (round % 5), k = 96, n = 40 + round;
+        std::vector<float> av(static_cast<std::size_t>(m * k)), bv(static_cast<std::size_t>(k * n));
+        for (std::size_t i = 0; i < av.size(); ++i) {
+            av[i] = static_cast<float>(static_cast<int>((i * 7 + round) % 13) - 6) / 4.0f;
+        }
+        for (std::size_t i = 0; i < bv.size(); ++i) {
+            bv[i] = static_cast<float>(static_cast<int>((i * 5 + round) % 11) - 5) / 4.0f;
+        }
+        Tensor c;
+        {
+            const Tensor a = Tensor::from_vector(av, {m, k}, device);
+            const Tensor b = Tensor::from_vector(bv, {k, n}, device);
+            c = matmul(a, b, on);
+        } // a and b are released before the product is read back
+        const Tensor over_a = Tensor::full({m, k}, -1000.0, DType::F32, device);
+        const Tensor over_b = Tensor::full({k, n}, 1000.0, DType::F32, device);
+        std::vector<float> want(static_cast<std::size_t>(m * n));
+        for (std::int64_t i = 0; i < m; ++i) {
+            for (std::int64_t j = 0; j < n; ++j) {
+                double sum = 0.0;
+                for (std::int64_t p = 0; p < k; ++p) {
+                    sum += static_cast<double>(av[static_cast<std::size_t>(i * k + p)]) *
+                           bv[static_cast<std::size_t>(p * n + j)];
+                }
+                want[static_cast<std::size_t>(i * n + j)] = static_cast<float>(sum);
+            }
+        }
+        test::require(c.to_vector<float>() == want,
+                      "product after its inputs were released, round " + std::to_string(round));
+        test::require(over_a.to_vector<float>()[0] == -1000.0f &&
+                          over_b.to_vector<float>().back() == 1000.0f,
+                      "fills of reused memory");
+    }
+}
+
 void test_run_elsewhere() {
     // Data on the CPU, op on the GPU: inputs copied over, result written back into the CPU output.
     if (!device_available({DeviceType::ROCm, 0}) || test::options().cpu_only) {
@@ -167,6 +209,7 @@ int main(int argc, char** argv) {
         for (Device device : test::devices()) {
             std::cout << "  transfers on " << to_string(device) << '\n';
             test_transfers(device);
+            test_released_memory_reuse(device);
         }
         test_run_elsewhere();
     });
