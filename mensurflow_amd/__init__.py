@@ -66,6 +66,23 @@ class Stream:
         handle = ctypes.c_void_p()
         abi.check(lib.mfr_stream_create(device, ctypes.byref(handle)), "mfr_stream_create")
         self.handle = handle
+        self._scratch: dict = {}
+
+    def scratch(self, tag, shape, dtype=np.float32) -> "DeviceArray":
+        """A device array of `shape` for temporaries of work queued on this stream. Each tag
+        keeps one allocation between calls, replaced by a larger one when a call needs more.
+        Work on one stream runs in order, so the temporaries of an earlier call are no longer
+        read when later work on this stream writes them. The contents are whatever the last
+        user of the tag left there."""
+        dtype = np.dtype(dtype)
+        nbytes = int(np.prod(shape, dtype=np.int64)) * dtype.itemsize
+        held = self._scratch.get(tag)
+        if held is None or held.nbytes_alloc < nbytes:
+            if held is not None:
+                held.close()
+            held = DeviceArray((max(nbytes, 1),), np.uint8, self)
+            self._scratch[tag] = held
+        return DeviceArray(shape, dtype, self, _base=held, _ptr=held._ptr)
 
     def synchronize(self) -> None:
         abi.check(abi.load().mfr_stream_sync(self.handle), "mfr_stream_sync")
@@ -74,6 +91,9 @@ class Stream:
         return abi.load().mfr_stream_handle(self.handle) or 0
 
     def close(self) -> None:
+        for held in self._scratch.values():
+            held.close()
+        self._scratch.clear()
         if self.handle is not None and self.handle.value:
             abi.check(abi.load().mfr_stream_destroy(self.handle), "mfr_stream_destroy")
         self.handle = None
@@ -525,31 +545,40 @@ def attention_composed(q: DeviceArray, k: DeviceArray, v: DeviceArray,
     scalar packed to the scores' shape (as mensurflow::where packs them), the causal mask the
     same way, softmax over the keys, gemm_batched(weights, v). q [..., Lq, D], k [..., Lk, D],
     v [..., Lk, Dv] with equal batch shapes; mask a Bool (uint8) array broadcastable to
-    [..., Lq, Lk]."""
+    [..., Lq, Lk]. Every array is on q's stream; the materialised temporaries (scores, the
+    packed -inf operand and mask) are that stream's scratch arrays, reused by later calls."""
     stream = q.stream
     lq, depth = q.shape[-2:]
     lk = k.shape[-2]
     batch = q.shape[:-2]
     if scale == 0.0:
         scale = float(np.float32(1.0 / np.sqrt(depth))) if depth > 0 else 1.0
-    scores = DeviceArray.empty(batch + (lq, lk), stream)
+    scores = stream.scratch("attention.scores", batch + (lq, lk))
     gemm_batched(q, k.transpose(-2, -1), scores, alpha=scale)
     minus_inf = None
 
     def masked(keep: DeviceArray) -> DeviceArray:
         nonlocal minus_inf
         if minus_inf is None:
-            scalar = DeviceArray.empty((1,), stream)
+            scalar = stream.scratch("attention.scalar", (1,))
             fill(scalar, -np.inf)
-            minus_inf = strided_copy(scalar.expand(scores.shape))
-        full_mask = strided_copy(keep.expand(scores.shape))
+            minus_inf = strided_copy(scalar.expand(scores.shape),
+                                     out=stream.scratch("attention.minus_inf", scores.shape))
+        full_mask = strided_copy(keep.expand(scores.shape),
+                                 out=stream.scratch("attention.mask", scores.shape, np.uint8))
         return where(full_mask, scores, minus_inf, out=scores)
 
     if mask is not None:
         masked(mask)
     if causal:
-        lower = np.tril(np.ones((lq, lk), dtype=np.uint8))
-        masked(DeviceArray.from_numpy(lower, stream))
+        # The [Lq, Lk] lower triangle, kept on the stream until a call needs another shape.
+        lower = stream._scratch.get("attention.causal")
+        if lower is None or lower.shape != (lq, lk):
+            if lower is not None:
+                lower.close()
+            lower = DeviceArray.from_numpy(np.tril(np.ones((lq, lk), dtype=np.uint8)), stream)
+            stream._scratch["attention.causal"] = lower
+        masked(lower)
     weights = softmax(scores, axis=-1, out=scores)
     out = DeviceArray.empty(batch + (lq, v.shape[-1]), stream)
     gemm_batched(weights, v, out)

@@ -51,6 +51,30 @@ def test_attention_small_with_mask(stream, oracle, causal, fused):
     assert_gemm_parity(got, want, mag + 1e-6, lk, "attention small")
 
 
+def test_composed_calls_reuse_stream_scratch(oracle):
+    """The composition keeps its scores, packed mask and -inf operand as its stream's scratch
+    arrays, reused from call to call: a masked causal call, a smaller unmasked causal one, and a
+    masked non-causal one of the first shape, on one fresh stream, each match the oracle."""
+    with mf.Stream(0) as stream:
+        rng = np.random.default_rng(61)
+        for index, (lq, lk, use_mask, causal) in enumerate(
+                [(90, 120, True, True), (40, 50, False, True), (90, 120, True, False)]):
+            d = 40
+            q = normal(oracle, (2, lq, d), 0.0, 1.0, 70 + index)
+            k = normal(oracle, (2, lk, d), 0.0, 1.0, 80 + index)
+            v = normal(oracle, (2, lk, d), 0.0, 1.0, 90 + index)
+            mask = (rng.random((lq, lk)) > 0.4).astype(np.uint8) if use_mask else None
+            keep = None if mask is None else mask.copy()
+            if causal:
+                lower = np.tril(np.ones((lq, lk), np.uint8))
+                keep = lower if keep is None else keep & lower
+            got = mf.attention(dev(q, stream), dev(k, stream), dev(v, stream),
+                               mask=None if mask is None else dev(mask, stream), causal=causal,
+                               fused=False).numpy()
+            want, mag = oracle_attention(oracle, q, k, v, keep, np.float32(1.0 / np.sqrt(d)))
+            assert_gemm_parity(got, want, mag + 1e-6, lk, f"composed call {index}")
+
+
 def test_config5_attention_full(stream, oracle):
     """configs[4] at full size: B=8, H=16, S=1024, D=64, causal -- the composition and the fused
     kernel against one oracle run."""
