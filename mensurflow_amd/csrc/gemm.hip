@@ -150,12 +150,22 @@ bool thin_possible(int64_t m, int64_t n, bool ak, bool bk, bool* along_n = nullp
     return by_rows || (m <= kThinCols && bk);
 }
 
+// How the thin path will read B' (A in the transposed form), for thin_us: 2 = in pieces of
+// C columns whatever the column count (a staged copy, lines zero-padded to a multiple of 4), 1 =
+// in pieces when the column count is exactly 2, 4 or 8 (unit column stride, rows and batches
+// 16-byte aligned), 0 = one load per value. launch_thin decides from the operand itself.
+struct Plan;
+int thin_b_layout(const GemmParams& p, const Plan& plan, int64_t m, int64_t n);
+
 // Modelled time (us): every byte read or written once, at kThinBytesPerUs for one column; the
-// kernel computes the columns rounded up to C = 1, 2, 4 or 8, and each B' value is a load of its
-// own, so C > 1 costs 0.75 * C times as much; slower in proportion with fewer than 512
-// workgroups. Fit to measured times (16384^2 x 1: 168 us; 16384 x 4 x 4096: 125 us; 4096 x 8 x
-// 1024: 22 us).
-double thin_us(int64_t m, int64_t n, int64_t k, int64_t batch, bool c0, bool ak, bool bk) {
+// kernel computes the columns rounded up to C = 1, 2, 4 or 8. Read one value at a time, B' costs
+// a cache-line access per value, so C > 1 takes 0.75 * C times as long (16384^2 x 1: 168 us;
+// 16384 x 4 x 4096: 125 us; 4096 x 8 x 1024: 22 us). Read in pieces, C = 2, 4, 8 take 1.0, 1.2
+// and 2.5 times as long (16384 x 2 x 4096: 43 us; 16384 x 4 x 4096: 51 us; 65536 x 4 x 512:
+// 25 us; 16384 x 8 x 4096: 91 us; 4096 x 8 x 1024: 11 us). Slower in proportion with fewer than
+// 512 workgroups.
+double thin_us(int64_t m, int64_t n, int64_t k, int64_t batch, bool c0, bool ak, bool bk,
+               int thin_b) {
     bool along_n = true;
     thin_possible(m, n, ak, bk, &along_n);
     const double rows = static_cast<double>(along_n ? m : n);
@@ -163,9 +173,13 @@ double thin_us(int64_t m, int64_t n, int64_t k, int64_t batch, bool c0, bool ak,
     const double rounded = cols <= 1 ? 1.0 : cols <= 2 ? 2.0 : cols <= 4 ? 4.0 : 8.0;
     const double bytes = 4.0 * batch * (rows * k + k * cols + rows * cols * (c0 ? 2.0 : 1.0));
     const double blocks = batch * std::ceil(rows / kThinDotRows);
-    return bytes / kThinBytesPerUs * (rounded == 1.0 ? 1.0 : 0.75 * rounded) *
-               std::max(1.0, 512.0 / blocks) +
-           kThinLaunchUs;
+    const bool pieces = rounded > 1.0 && (thin_b == 2 || (thin_b == 1 && cols == rounded));
+    const double factor = rounded == 1.0 ? 1.0
+                          : !pieces      ? 0.75 * rounded
+                          : rounded == 2.0 ? 1.0
+                          : rounded == 4.0 ? 1.2
+                                           : 2.5;
+    return bytes / kThinBytesPerUs * factor * std::max(1.0, 512.0 / blocks) + kThinLaunchUs;
 }
 
 struct Choice {
@@ -181,7 +195,7 @@ struct Choice {
 // time. The 256x256 tile needs 16-byte loads on both operands. The thin path competes where it
 // can take the product (ak, bk: whether A and B are read along k) and no split is fixed.
 Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int cus, bool wide_loads,
-              int fixed_tile, int fixed_splits, bool c0, bool ak, bool bk) {
+              int fixed_tile, int fixed_splits, bool c0, bool ak, bool bk, int thin_b) {
     Choice best;
     best.per = k;
     const bool thin = thin_possible(m, n, ak, bk) && fixed_splits <= 1;
@@ -192,7 +206,7 @@ Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int cus, bool wide
                              "with B read along k, and no split");
         }
         best.tile = MFR_TILE_THIN;
-        best.us = thin_us(m, n, k, batch, c0, ak, bk);
+        best.us = thin_us(m, n, k, batch, c0, ak, bk, thin_b);
         return best;
     }
     if (fixed_splits > 0 && k > 0) {
@@ -249,7 +263,7 @@ Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int cus, bool wide
         }
     }
     if (fixed_tile == MFR_TILE_AUTO && thin) {
-        const double us = thin_us(m, n, k, batch, c0, ak, bk);
+        const double us = thin_us(m, n, k, batch, c0, ak, bk, thin_b);
         if (us < best.us) {
             best.tile = MFR_TILE_THIN;
             best.splits = 1;
@@ -506,6 +520,27 @@ struct Plan {
     int region_count = 1;
 };
 
+// m x n: the output rectangle the thin path would take (the product or an edge strip, whose
+// offset is a multiple of a tile and keeps the alignment).
+int thin_b_layout(const GemmParams& p, const Plan& plan, int64_t m, int64_t n) {
+    bool along_n = true;
+    if (!thin_possible(m, n, plan.ak, plan.bk, &along_n)) {
+        return 0;
+    }
+    if (along_n ? plan.stage_b : plan.stage_a) {
+        return 2;
+    }
+    const float* base = along_n ? p.b : p.a;
+    const int64_t unit = along_n ? p.b_cs : p.a_rs;
+    const int64_t line = along_n ? p.b_rs : p.a_cs;
+    const int64_t* batch_strides = along_n ? p.b_bs : p.a_bs;
+    bool aligned = unit == 1 && line % 4 == 0 && reinterpret_cast<uintptr_t>(base) % 16 == 0;
+    for (int d = 0; d < p.batch_dims; ++d) {
+        aligned = aligned && batch_strides[d] % 4 == 0;
+    }
+    return aligned ? 1 : 0;
+}
+
 // The plan's output as one region with `choice`.
 void single_region(Plan& plan, const Choice& choice) {
     plan.region_count = 1;
@@ -541,12 +576,14 @@ void consider_peeling(Plan& plan, int64_t batch, int cus, bool wide, double sing
         Region regions[4];
         int count = 0;
         const Choice main =
-            choose(main_m, main_n, p.k, batch, cus, wide, t, 1, plan.c0, plan.ak, plan.bk);
+            choose(main_m, main_n, p.k, batch, cus, wide, t, 1, plan.c0, plan.ak, plan.bk,
+                   thin_b_layout(p, plan, main_m, main_n));
         regions[count++] = Region{0, 0, main_m, main_n, main.tile, main.splits, main.per};
         double us = main.us;
         auto strip = [&](int64_t m_off, int64_t n_off, int64_t m, int64_t n) {
             const Choice c =
-                choose(m, n, p.k, batch, cus, wide, MFR_TILE_AUTO, 0, plan.c0, plan.ak, plan.bk);
+                choose(m, n, p.k, batch, cus, wide, MFR_TILE_AUTO, 0, plan.c0, plan.ak, plan.bk,
+                       thin_b_layout(p, plan, m, n));
             regions[count++] = Region{m_off, n_off, m, n, c.tile, c.splits, c.per};
             us += c.us + kLaunchUs;
         };
@@ -691,7 +728,7 @@ Plan plan_sgemm(const mfr_gemm_desc& d, int cus) {
     }
     plan.c0 = p.c0 != nullptr && p.beta != 0.0f;
     const Choice choice = choose(p.m, p.n, p.k, batch_count, cus, wide, d.tile, d.splits, plan.c0,
-                                 plan.ak, plan.bk);
+                                 plan.ak, plan.bk, thin_b_layout(p, plan, p.m, p.n));
     single_region(plan, choice);
     if (d.tile == MFR_TILE_AUTO && d.splits == 0) {
         consider_peeling(plan, batch_count, cus, wide, choice.us);
@@ -785,6 +822,33 @@ void launch_thin(const Plan& plan, const GemmParams& q, int va, int vb, hipStrea
     const unsigned grid = static_cast<unsigned>(blocks);
     // The column count rounded up to 1, 2, 4 or 8 (kThinCols).
     const int c = t.cols <= 1 ? 1 : t.cols <= 2 ? 2 : t.cols <= 4 ? 4 : kThinCols;
+    // B' pieces of 2 or 4 floats: unit column stride, rows and batches aligned to the piece, and
+    // the c columns in memory (exactly c, or a staged B' whose lines are zero-padded to a
+    // multiple of 4).
+    const bool b_padded = along_n ? plan.stage_b : plan.stage_a;
+    const int piece = c == 2 ? 2 : 4;
+    bool b_pieces = c >= 2 && t.b_cs == 1 && t.b_rs % piece == 0 &&
+                    reinterpret_cast<uintptr_t>(t.b) % (4 * piece) == 0 &&
+                    (t.cols == c || b_padded);
+    for (int d = 0; d < t.batch_dims; ++d) {
+        b_pieces = b_pieces && t.b_bs[d] % piece == 0;
+    }
+    if (b_pieces) {
+        if (width == 4) {
+            switch (c) {
+            case 2: thin_dot_kernel<4, 2, true><<<grid, kThinThreads, 0, stream>>>(t); break;
+            case 4: thin_dot_kernel<4, 4, true><<<grid, kThinThreads, 0, stream>>>(t); break;
+            default: thin_dot_kernel<4, kThinCols, true><<<grid, kThinThreads, 0, stream>>>(t);
+            }
+        } else {
+            switch (c) {
+            case 2: thin_dot_kernel<1, 2, true><<<grid, kThinThreads, 0, stream>>>(t); break;
+            case 4: thin_dot_kernel<1, 4, true><<<grid, kThinThreads, 0, stream>>>(t); break;
+            default: thin_dot_kernel<1, kThinCols, true><<<grid, kThinThreads, 0, stream>>>(t);
+            }
+        }
+        return;
+    }
     if (width == 4) {
         switch (c) {
         case 1: thin_dot_kernel<4, 1><<<grid, kThinThreads, 0, stream>>>(t); break;
@@ -980,7 +1044,8 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
             // Automatic splits without the memory: one region, one range.
             single_region(plan, choose(p.m, p.n, p.k, p.batch_count, s.compute_units,
                                        (va == 4 || plan.stage_a) && (vb == 4 || plan.stage_b),
-                                       d.tile, 1, plan.c0, plan.ak, plan.bk));
+                                       d.tile, 1, plan.c0, plan.ak, plan.bk,
+                                       thin_b_layout(p, plan, p.m, p.n)));
             if (fa + fb > 0) {
                 ws = static_cast<float*>(try_reserve(s, 4 * static_cast<size_t>(fa + fb)));
             }
@@ -998,7 +1063,7 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
             if (d.tile == MFR_TILE_AUTO) {
                 single_region(plan, choose(p.m, p.n, p.k, p.batch_count, s.compute_units,
                                            va == 4 && vb == 4, MFR_TILE_AUTO, 1, plan.c0,
-                                           plan.ak, plan.bk));
+                                           plan.ak, plan.bk, thin_b_layout(p, plan, p.m, p.n)));
             }
         }
     }
