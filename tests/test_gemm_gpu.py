@@ -543,13 +543,15 @@ def test_thin_k_zero_and_refusals(stream):
 
 def test_thin_automatic_choice(stream):
     """AUTO takes the thin path for a long product with a few columns (the MLP's 3-column edge
-    strip), and the MFMA tiles where the output fills them."""
+    strip, 4 aligned columns), and the MFMA tiles where the output fills them."""
     def plan(m, n, k, **kw):
         return mf.gemm_plan(mf.DeviceArray.empty((m, k), stream),
                             mf.DeviceArray.empty((k, n), stream),
                             mf.DeviceArray.empty((m, n), stream), **kw)
     assert plan(4093, 3, 1023)[0] == THIN
     assert plan(16384, 1, 16384)[0] == THIN
+    # 4 aligned columns: B rows read as 16-byte pieces (51 us against 101 us on 64x64 tiles).
+    assert plan(16384, 4, 4096)[0] == THIN
     assert plan(4096, 4096, 4096)[0] == mf.abi.TILE_256x256
 
 
