@@ -5,7 +5,8 @@
 // The product is C'[rows, cols] = A'[rows, k] B'[k, cols] with cols <= 8, in general strides, so
 // one kernel serves both orientations: C = A B with n <= 8 (A' = A, B' = B), and C^T = B^T A^T
 // with m <= 8 (A' = B^T, B' = A^T, C' = C^T). The work is streaming A' from HBM once (as the gemv
-// kernels stream their matrix); B' (at most 8 columns) is read through the caches by every row.
+// kernels stream their matrix); B' (at most 8 columns) is read through the caches by every row,
+// one value at a time or, where its rows allow, as 8- or 16-byte pieces of a row (VB below).
 // A' rows must run along k (unit stride along k): each wavefront takes kThinRowsPerWave rows, its
 // lanes stride through k (16-byte loads when the rows allow), and the wavefront sums its lanes at
 // the end.
