@@ -523,6 +523,27 @@ def test_thin_batched_broadcast_gelu(stream):
             assert same_bits(got[i, h], exact_product(a[i, h], bv[0, h])), (i, h)
 
 
+@pytest.mark.parametrize("n,pad", [(4, 0), (4, 2), (8, 0), (8, 4), (2, 0), (2, 1)])
+def test_thin_b_pieces_and_batch_strides(stream, n, pad):
+    """A batched product with 2, 4 or 8 columns and B's batches `pad` floats apart beyond their
+    k*n. An even (2 columns) or multiple-of-4 batch stride lets the thin path read B's rows as
+    8- or 16-byte pieces; an odd one, or 2 floats with 4 columns, makes it read one value at a
+    time. Both give the exact product's bits."""
+    batch, m, k = 3, 70, 130
+    a = quarter_matrix(batch * m, k, 261).reshape(batch, m, k)
+    bv = quarter_matrix(batch * k, n, 262).reshape(batch, k, n)
+    per = k * n + pad
+    stored = np.full((batch * per,), -5.0, np.float32)
+    for i in range(batch):
+        stored[i * per:i * per + k * n] = bv[i].reshape(-1)
+    b_d = dev(stored, stream)._view((batch, k, n), (per, n, 1), 0)
+    c = mf.DeviceArray.empty((batch, m, n), stream)
+    mf.gemm_batched(dev(a, stream), b_d, c, tile=THIN)
+    got = c.numpy()
+    for i in range(batch):
+        assert same_bits(got[i], exact_product(a[i], bv[i])), (n, pad, i)
+
+
 def test_thin_k_zero_and_refusals(stream):
     m, n = 33, 4
     c0 = quarter_matrix(m, n, 251)
