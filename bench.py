@@ -15,14 +15,18 @@ calls and 377 us after), then K steps bracketed by stream synchronisation; the p
 duration of the dominant kernel comes from HIP events recorded on the stream the kernel runs
 on. The CPU baseline (rank 0, N=1 only) times the reference's own packed
 AVX2/OpenMP GEMM (oracle/_ref, compiled from the reference sources) on a bounded sample.
+`cpp_api` repeats the workloads through the mensurflow C++ API (mensurflow_amd/_lib/
+mfr_api_bench, run as a child process): the dispatcher, the backend's adapters, per-call output
+allocation and the C ABI on top of the kernels, as host wall time per call.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-cpp-api]
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -38,6 +42,24 @@ MIN_WARMUP_MS = 50.0            # warm-up per leg, at least (see the module docs
 GEMM_N = 4096
 GEMV_N = 16384
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def cpp_api_timing():
+    """The BASELINE workloads through the mensurflow C++ API on the rocm device
+    (mensurflow_amd/host/bench/api_bench.cpp), in a child process with its own HIP context."""
+    exe = os.path.join(ROOT, "mensurflow_amd", "_lib", "mfr_api_bench")
+    if not os.path.exists(exe):
+        return {"note": "mfr_api_bench is not built"}
+    proc = subprocess.run([exe, "20"], capture_output=True, text=True, timeout=300)
+    if proc.returncode != 0:
+        return {"note": "mfr_api_bench failed: " + proc.stderr.strip()[-300:]}
+    out = json.loads(proc.stdout.strip().splitlines()[-1])
+    out["note"] = ("host wall time per call of mensurflow::gemm (4096^3, B^T, alpha 1.5, beta "
+                   "0.5), gemv (16384^2, N and T), gemm_epilogue (the MLP with bias and tanh "
+                   "gelu) and attention (config 5, causal) with Execution::GPU, each returning "
+                   "a new tensor; after 50 ms of untimed calls, runs of 20 calls ended by a "
+                   "read-back until at least 50 ms are timed")
+    return out
 
 
 def log(msg: str) -> None:
@@ -250,6 +272,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-cpp-api", action="store_true",
+                    help="skip the timing through the mensurflow C++ API")
     ap.add_argument("--only", choices=["all", "gemm", "gemv", "mlp", "copy", "attention"],
                     default="all",
                     help="run one leg (for profiling)")
@@ -364,6 +388,9 @@ def main() -> int:
                       "note": "plain device copy, read+write bytes; the practical HBM ceiling"},
         "cpu_baseline": None,
     }
+    if not args.no_cpp_api:
+        log("the same workloads through the mensurflow C++ API ...")
+        line["cpp_api"] = cpp_api_timing()
     if not args.no_cpu_baseline:
         log("cpu baseline (reference packed GEMM on host cores) ...")
         line["cpu_baseline"] = cpu_baseline()

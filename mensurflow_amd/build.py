@@ -105,9 +105,21 @@ def build_host() -> str | None:
     return out
 
 
+def build_api_bench() -> str:
+    """Link host/bench/api_bench.cpp against libmensurflow.so: bench.py's timing of the
+    BASELINE workloads through the C++ API."""
+    out = os.path.join(LIBDIR, "mfr_api_bench")
+    tmp = out + ".tmp"
+    _run(["g++", *HOST_FLAGS, "-o", tmp, os.path.join(HOST, "bench", "api_bench.cpp"),
+          f"-L{LIBDIR}", "-lmensurflow", "-lmfr_rocm", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, out)
+    return out
+
+
 def build() -> None:
     build_hip()
-    build_host()
+    if build_host() is not None:
+        build_api_bench()
 
 
 if __name__ == "__main__":
