@@ -14,7 +14,8 @@ idle run slower while the clocks ramp: the MLP leg measured 446 us per call over
 calls and 377 us after), then K steps bracketed by stream synchronisation; the per-launch
 duration of the dominant kernel comes from HIP events recorded on the stream the kernel runs
 on. The CPU baseline (rank 0, N=1 only) times the reference's own packed
-AVX2/OpenMP GEMM (oracle/_ref, compiled from the reference sources) on a bounded sample.
+AVX2/OpenMP GEMM and its double-accumulating gemv (oracle/_ref, compiled from the reference
+sources) on bounded samples.
 `cpp_api` repeats the workloads through the mensurflow C++ API (mensurflow_amd/_lib/
 mfr_api_bench, run as a child process): the dispatcher, the backend's adapters, per-call output
 allocation and the C ABI on top of the kernels, as host wall time per call.
@@ -220,12 +221,30 @@ def host_description() -> str:
     return f"{model}, {os.cpu_count()} hardware threads, {physical_cores}"
 
 
-def cpu_baseline(seconds: float = 12.0):
-    """The reference's packed AVX2/OpenMP GEMM (oracle/_ref) on the box's host cores: the
-    matmul of configs[2] (4096^3, B read transposed), repeated for about `seconds`."""
+def _time_calls(run, seconds: float, at_least: int = 3, at_most: int = 200):
+    """Median seconds per call of run() after one warm-up call, repeated for about `seconds`
+    (at least `at_least` calls), as the reference's bench::measure does for slow calls."""
+    run()  # warm-up (thread pool, page faults)
+    times = []
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < seconds or len(times) < at_least:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= at_most:
+            break
+    return float(np.median(times)), len(times)
+
+
+def cpu_baseline(gemm_seconds: float = 10.0, gemv_seconds: float = 4.0):
+    """The reference's own CPU kernels (oracle/_ref, compiled from its sources) on the box's host
+    cores, at the reference's default thread count (omp_get_max_threads(): every hardware thread,
+    or OMP_NUM_THREADS where the environment sets it):
+      * the packed AVX2/OpenMP GEMM on configs[2]'s product (4096^3, B read transposed);
+      * the double-accumulating gemv_f32 on configs[1] (16384^2, alpha 2, beta 0.5, N and T).
+    Each is repeated for a bounded time; the figure is the median call."""
     import oracle
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
     n = GEMM_N
     rng = np.random.default_rng(3)
     a = rng.uniform(-1, 1, (n, n)).astype(np.float32)
@@ -233,36 +252,49 @@ def cpu_baseline(seconds: float = 12.0):
     c = np.empty((n, n), np.float32)
     if oracle.has_reference():
         ref = oracle.Reference()
-        ref.set_threads(threads)
         kind = "reference"
+        threads = ref.max_threads()
 
-        def run():
+        def run_gemm():
             ref.matmul(a, b_stored.T, parallel=True, out=c)
     else:
-        port = oracle.Oracle()
-        port.set_threads(threads)
+        ref = oracle.Oracle()
         kind = "port"
+        threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+        ref.set_threads(threads)
 
-        def run():
-            port.matmul(a, b_stored.T)
-    run()  # warm-up (thread pool, page faults)
-    times = []
-    t_start = time.perf_counter()
-    while time.perf_counter() - t_start < seconds or len(times) < 3:
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 200:
-            break
-    median = float(np.median(times))
+        def run_gemm():
+            ref.matmul(a, b_stored.T)
+    gemm_s, gemm_calls = _time_calls(run_gemm, gemm_seconds)
+    del a, b_stored, c
+
+    gn = GEMV_N
+    big = rng.uniform(-1, 1, (gn, gn)).astype(np.float32)
+    x = rng.uniform(-1, 1, gn).astype(np.float32)
+    y0 = rng.standard_normal(gn).astype(np.float32)
+    gemv = {}
+    for key, trans in (("N", False), ("T", True)):
+        secs, calls = _time_calls(lambda: ref.gemv(big, x, 2.0, y0, 0.5, trans=trans),
+                                  gemv_seconds, at_least=2)
+        gbs = 4.0 * (gn * gn + 3 * gn) / secs / 1e9
+        gemv[key] = {"value": round(gbs, 2), "unit": "GB/s", "ms_per_call": round(secs * 1e3, 2),
+                     "calls": calls}
+    del big
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = None
     return {
-        "value": round(2.0 * n ** 3 / median / 1e12, 4),
+        "value": round(2.0 * n ** 3 / gemm_s / 1e12, 4),
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": kind,
-        "sample": (f"{len(times)} calls of the packed CPU GEMM at 4096^3 (A * B^T, fp32), median "
-                   f"{median * 1e3:.1f} ms; the alpha/beta passes (memory-bound, <1% of the "
-                   f"work) not included; host: {host_description()}, {threads} threads used"),
+        "sample": (f"{gemm_calls} calls of the packed CPU GEMM at 4096^3 (A * B^T, fp32), median "
+                   f"{gemm_s * 1e3:.1f} ms; the alpha/beta passes (memory-bound, <1% of the "
+                   f"work) not included; gemv 16384^2 N and T as in configs[1] (1 GiB of A per "
+                   f"call); host: {host_description()}, {affinity} usable by this process, "
+                   f"{threads} threads used (the reference's default, omp_get_max_threads)"),
+        "gemv": gemv,
     }
 
 
@@ -392,7 +424,7 @@ def main() -> int:
         log("the same workloads through the mensurflow C++ API ...")
         line["cpp_api"] = cpp_api_timing()
     if not args.no_cpu_baseline:
-        log("cpu baseline (reference packed GEMM on host cores) ...")
+        log("cpu baseline (reference packed GEMM and gemv on host cores) ...")
         line["cpu_baseline"] = cpu_baseline()
     stream.close()
     print(json.dumps(line), flush=True)

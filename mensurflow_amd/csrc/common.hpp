@@ -9,6 +9,7 @@
 #include "gelu_tanh.hpp"
 
 #include <cstdint>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 
@@ -58,8 +59,15 @@ template <typename Body> int guarded(Body&& body) {
 } // namespace mfr
 
 // One HIP stream on one device, plus the device workspace its kernels use for partial results
-// (gemv-T partial sums). The workspace belongs to the stream: kernels queued on one stream run
-// in order, so they can share it; two streams never share one.
+// (gemv-T partial sums, GEMM split-K sums and staged operands). The workspace belongs to the
+// stream: kernels queued on one stream run in order, so they can share it; two streams never
+// share one.
+//
+// Several host threads may call into one stream (a backend hands every thread the same stream
+// of a device). A call that uses the workspace holds `workspace_mutex` from reserve() until its
+// last launch is queued: another thread's reserve() could otherwise free the buffer between this
+// thread's reserve() and its launches. Once the launches are queued, stream order protects them
+// (reserve() waits for the stream before it frees).
 struct mfr_stream {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -67,13 +75,15 @@ struct mfr_stream {
     void* workspace = nullptr;
     size_t workspace_bytes = 0;
     int compute_units = 256; // of the stream's device, read at creation
+    std::mutex workspace_mutex;
 
     // Makes this stream's device current on the calling thread (each ABI call does, as the
     // reference's CudaStream::activate does per call).
     void activate() const { mfr::check(hipSetDevice(device), "hipSetDevice"); }
 
     // At least `bytes` of workspace. Growing it waits for the stream (the old buffer may still be
-    // in use by queued kernels) and is rare: the size only ever grows.
+    // in use by queued kernels) and is rare: the size only ever grows. The caller holds
+    // workspace_mutex.
     void* reserve(size_t bytes) {
         if (bytes <= workspace_bytes) {
             return workspace;

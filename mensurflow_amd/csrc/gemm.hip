@@ -1024,6 +1024,8 @@ Plan cached_plan(const mfr_gemm_desc& d, int cus) {
     return plan;
 }
 
+// Runs d on s. The split-K partial sums and staged operands go to the stream's workspace, laid
+// out [partial sums][staged A][staged B] (grown as needed, with fallbacks when it cannot be had).
 void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
     Plan plan = cached_plan(d, s.compute_units);
     if (plan.empty) {
@@ -1035,9 +1037,11 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
     Operand ob = operand_b(p, plan.bk);
     int64_t fa = plan.stage_a ? staged_floats_padded(oa, p) : 0;
     int64_t fb = plan.stage_b ? staged_floats_padded(ob, p) : 0;
-    // One workspace: [split-K partial sums][staged A][staged B].
     float* ws = nullptr;
+    std::unique_lock<std::mutex> hold(s.workspace_mutex, std::defer_lock);
     if (partial_floats(plan) + fa + fb > 0) {
+        // Held until every launch is queued (see mfr_stream).
+        hold.lock();
         ws = static_cast<float*>(
             try_reserve(s, 4 * static_cast<size_t>(partial_floats(plan) + fa + fb)));
         if (ws == nullptr && partial_floats(plan) > 0 && d.splits == 0) {

@@ -285,6 +285,9 @@ void launch_gemv(mfr_stream& s, bool trans, int64_t rows, int64_t cols, float al
     const int64_t chunks = rows > 0 ? (rows + per - 1) / per : 0;
     mfr::require(strips < (int64_t{1} << 31) && chunks < 65536, "gemv: matrix too large");
     double* partial = nullptr;
+    // Held until both kernels are queued: another thread's reserve() may not free `partial`
+    // in between.
+    std::lock_guard<std::mutex> hold(s.workspace_mutex);
     if (chunks > 0) {
         partial = static_cast<double*>(
             s.reserve(static_cast<size_t>(chunks) * static_cast<size_t>(cols) * sizeof(double)));

@@ -235,6 +235,15 @@ class Reference(_Lib):
         L.ref_set_threads.restype = None
         L.ref_max_threads.restype = ctypes.c_int
         L.ref_packed_supported.restype = ctypes.c_int
+        for name in ("ref_mul_f32", "ref_add_f32"):
+            getattr(L, name).argtypes = [_f32p, _f32p, _f32p, _i64]
+            getattr(L, name).restype = None
+        L.ref_scal_f32.argtypes = [ctypes.c_float, _f32p, _f32p, _i64]
+        L.ref_scal_f32.restype = None
+        L.ref_gemm_batched_f32.argtypes = [_vp, _i64p, _i64, _i64, _vp, _i64p, _i64, _i64, _vp,
+                                           _vp, _i64, _i64, _i64, _i64, ctypes.c_float,
+                                           ctypes.c_float]
+        L.ref_gemm_batched_f32.restype = None
 
     def packed_supported(self) -> bool:
         return bool(self.lib.ref_packed_supported())
@@ -261,6 +270,46 @@ class Reference(_Lib):
         self.lib.ref_matmul_packed(a.ctypes.data, a.strides[0] // isz, a.strides[1] // isz,
                                    b.ctypes.data, b.strides[0] // isz, b.strides[1] // isz,
                                    c.ctypes.data, n, m, n, k, 1 if parallel else 0)
+        return c
+
+
+    def _binary(self, name, a, b):
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        b = np.ascontiguousarray(b, dtype=np.float32)
+        out = np.empty_like(a)
+        getattr(self.lib, name)(_ptr(a), _ptr(b), _ptr(out), a.size)
+        return out
+
+    def gemm_composition(self, product, alpha, c0=None, beta=0.0):
+        """mensurflow::gemm after its matmul (src/ops/blas.cpp:246-257), with the reference's
+        own kernels: mul by alpha when alpha != 1, then add(result, scal(beta, c0)) when c0 is
+        given and beta != 0."""
+        result = np.ascontiguousarray(product, dtype=np.float32).copy()
+        if alpha != 1.0:
+            result = self._binary("ref_mul_f32", result, np.full_like(result, np.float32(alpha)))
+        if c0 is not None and beta != 0.0:
+            c0 = np.ascontiguousarray(c0, dtype=np.float32)
+            scaled = np.empty_like(c0)
+            self.lib.ref_scal_f32(beta, _ptr(c0), _ptr(scaled), c0.size)
+            result = self._binary("ref_add_f32", result, scaled)
+        return result
+
+    def gemm_batched(self, a, b, a_offsets, b_offsets, m, n, k, rsa, csa, rsb, csb, alpha=1.0,
+                     c0=None, beta=0.0):
+        """gemm_batched_f32_parallel (gemm_batched.cpp:58-70) with its finish pass: one packed
+        GEMM per matrix i of A (a.ravel() from a_offsets[i], strides rsa/csa) and B, then
+        alpha * C + beta * C0. Returns C [batch, m, n]."""
+        a = np.ascontiguousarray(a, dtype=np.float32).ravel()
+        b = np.ascontiguousarray(b, dtype=np.float32).ravel()
+        ao = np.ascontiguousarray(a_offsets, dtype=np.int64)
+        bo = np.ascontiguousarray(b_offsets, dtype=np.int64)
+        batch = ao.size
+        c = np.empty((batch, m, n), np.float32)
+        c0c = None if c0 is None else np.ascontiguousarray(c0, dtype=np.float32)
+        self.lib.ref_gemm_batched_f32(a.ctypes.data, _ptr(ao, _i64p), rsa, csa, b.ctypes.data,
+                                      _ptr(bo, _i64p), rsb, csb, c.ctypes.data,
+                                      None if c0c is None else c0c.ctypes.data, batch, m, n, k,
+                                      alpha, beta)
         return c
 
 

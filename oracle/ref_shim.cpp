@@ -7,6 +7,7 @@
 // from /root/reference/src; this file only forwards plain arguments to them.
 #include "backends/cpu/ops/blas/blas.hpp"
 #include "backends/cpu/ops/elementwise/elementwise.hpp"
+#include "backends/cpu/ops/gemm/gemm_batched.hpp"
 #include "backends/cpu/ops/gemm/gemm_packed.hpp"
 #include "backends/cpu/ops/random/philox.hpp"
 #include "backends/cpu/ops/random/random.hpp"
@@ -70,6 +71,48 @@ void ref_matvec_f32(const float* a, const float* x, float* y, std::int64_t m, st
 void ref_gemv_f32(const float* a, const float* x, float* y, std::int64_t rows, std::int64_t cols,
                   float alpha, float beta, const float* y0, int trans) {
     cpu::gemv_f32(a, x, y, rows, cols, alpha, beta, y0, trans != 0);
+}
+
+// The three kernels mensurflow::gemm's composition dispatches after the product
+// (src/ops/blas.cpp:246-257): mul by the 0-d alpha, scal of C0 by beta, add.
+void ref_mul_f32(const float* a, const float* b, float* out, std::int64_t n) {
+    cpu::mul_f32(a, b, out, n);
+}
+
+void ref_scal_f32(float alpha, const float* x, float* out, std::int64_t n) {
+    cpu::scal_f32(alpha, x, out, n);
+}
+
+void ref_add_f32(const float* a, const float* b, float* out, std::int64_t n) {
+    cpu::add_f32(a, b, out, n);
+}
+
+// gemm_strided_batched's CPU kernel (gemm_batched.cpp:58-70): packed GEMM per matrix, then the
+// finish pass alpha * C + beta * C0 (gemm_batched.cpp:12-28). C and C0 are contiguous
+// [batch, m, n]; matrix i of A / B starts at the given element offsets.
+void ref_gemm_batched_f32(const float* a, const std::int64_t* a_offsets, std::int64_t rsa,
+                          std::int64_t csa, const float* b, const std::int64_t* b_offsets,
+                          std::int64_t rsb, std::int64_t csb, float* c, const float* c0,
+                          std::int64_t batch, std::int64_t m, std::int64_t n, std::int64_t k,
+                          float alpha, float beta) {
+    cpu::BatchedGemm g;
+    g.a = a;
+    g.a_offsets = a_offsets;
+    g.rsa = rsa;
+    g.csa = csa;
+    g.b = b;
+    g.b_offsets = b_offsets;
+    g.rsb = rsb;
+    g.csb = csb;
+    g.c = c;
+    g.c0 = c0;
+    g.batch = batch;
+    g.m = m;
+    g.n = n;
+    g.k = k;
+    g.alpha = alpha;
+    g.beta = beta;
+    cpu::gemm_batched_f32_parallel(g);
 }
 
 void ref_bias_add_f32(const float* x, const float* bias, float* out, std::int64_t n,

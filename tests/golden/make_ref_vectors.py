@@ -24,6 +24,9 @@ from oracle import Reference  # noqa: E402
 
 OUT = os.path.join(HERE, "ref_vectors.npz")
 
+# (alpha, beta) pairs of the gemm composition vectors; alpha 1 and beta 0 skip their pass.
+AXPBY_CASES = [(1.5, 0.5), (1.0, 0.5), (1.5, 0.0), (-2.0, -0.75), (1.0, 0.0), (0.125, 3.0)]
+
 
 def main() -> None:
     ref = Reference()
@@ -100,6 +103,36 @@ def main() -> None:
     y = ref.normal(77, 0.0, 1.0, seed + 63, 0)
     v["where_c"], v["where_x"], v["where_y"] = cond, x.reshape(-1), y
     v["where_out"] = ref.where(cond, x.reshape(-1), y)
+
+    # mensurflow::gemm's alpha/beta chain after the product (mul, scal, add; src/ops/blas.cpp:
+    # 246-257), on values that separate one rounding from two (an fma would differ), overflow,
+    # signed zeros, subnormals, infinities and NaN.
+    prod = ref.normal(4 * 97, 0.0, 30.0, seed + 70, 0)
+    c0 = ref.normal(4 * 97, 0.0, 30.0, seed + 71, 0)
+    specials = np.array([0.0, -0.0, 1e-40, -1e-40, 3.0e38, -3.0e38, np.inf, -np.inf, np.nan,
+                         1.0, -1.0, 2.5e-38], dtype=np.float32)
+    prod[:12], c0[:12] = specials, specials[::-1]
+    prod[12:24], c0[12:24] = specials, specials
+    v["axpby_x"], v["axpby_c0"] = prod, c0
+    v["axpby_cases"] = np.array(AXPBY_CASES, dtype=np.float32)
+    for i, (alpha, beta) in enumerate(AXPBY_CASES):
+        v[f"axpby_out{i}"] = ref.gemm_composition(prod, alpha, c0, beta)
+        v[f"axpby_out{i}_noc0"] = ref.gemm_composition(prod, alpha, None, 0.0)
+
+    # gemm_strided_batched's CPU kernel with its finish pass: 3 matrices, A broadcast over the
+    # batch (every offset 0), B read transposed, alpha 1/8 without C0 (attention's scores) and
+    # alpha 1.5, beta 0.5 with C0.
+    bm, bn, bk, batch = 21, 19, 37, 3
+    ba = ref.uniform(bm * bk, -1.0, 1.0, seed + 80, 0)
+    bb = ref.uniform(batch * bn * bk, -1.0, 1.0, seed + 81, 0)  # [batch, n, k], read as B^T
+    bc0 = ref.normal(batch * bm * bn, 0.0, 1.0, seed + 82, 0).reshape(batch, bm, bn)
+    a_off = np.zeros(batch, np.int64)
+    b_off = np.arange(batch, dtype=np.int64) * bn * bk
+    v["batched_a"], v["batched_b"], v["batched_c0"] = ba, bb, bc0
+    v["batched_scores"] = ref.gemm_batched(ba, bb, a_off, b_off, bm, bn, bk, bk, 1, 1, bk,
+                                           alpha=0.125)
+    v["batched_ab"] = ref.gemm_batched(ba, bb, a_off, b_off, bm, bn, bk, bk, 1, 1, bk,
+                                       alpha=1.5, c0=bc0, beta=0.5)
 
     np.savez_compressed(OUT, **v)
     print(f"wrote {OUT} ({os.path.getsize(OUT)} bytes, {len(v)} arrays)")

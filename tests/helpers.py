@@ -72,8 +72,41 @@ def magnitude(oracle, a, b) -> np.ndarray:
     return oracle.matmul(np.abs(a), np.abs(b)).astype(np.float64)
 
 
+def same_elements(x, y) -> np.ndarray:
+    """Elementwise bit equality of two float32 arrays of one shape."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.ascontiguousarray(y, dtype=np.float32)
+    return x.view(np.uint32) == y.view(np.uint32)
+
+
 def same_bits(x, y) -> bool:
     x = np.ascontiguousarray(x)
     y = np.ascontiguousarray(y)
     return x.shape == y.shape and x.dtype == y.dtype and bool(
         np.all(x.view(np.uint8) == y.view(np.uint8)))
+
+
+def record_parity(case: str, **fields) -> None:
+    """Adds `case`'s measured parity figures to gpurun_out/parity.json (or the file named by
+    MFR_PARITY_JSON), merging with what earlier tests of the run wrote, so the figures behind the
+    pass/fail verdicts are kept, not only printed."""
+    import json
+    import os
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    path = os.environ.get("MFR_PARITY_JSON", os.path.join(root, "gpurun_out", "parity.json"))
+    os.makedirs(os.path.dirname(path), exist_ok=True)
+    data = {}
+    if os.path.exists(path):
+        try:
+            with open(path) as fh:
+                data = json.load(fh)
+        except ValueError:
+            data = {}
+    data[case] = {k: (float(v) if isinstance(v, (np.floating, float)) else
+                      int(v) if isinstance(v, (np.integer, int)) and not isinstance(v, bool) else v)
+                  for k, v in fields.items()}
+    tmp = path + ".tmp"
+    with open(tmp, "w") as fh:
+        json.dump(data, fh, indent=1, sort_keys=True)
+    os.replace(tmp, path)

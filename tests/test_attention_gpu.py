@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import mensurflow_amd as mf
-from helpers import assert_gemm_parity, normal
+from helpers import assert_gemm_parity, normal, record_parity
 
 pytestmark = pytest.mark.gpu
 
@@ -90,6 +90,7 @@ def test_config5_attention_full(stream, oracle):
         rel_mag, rel_max = assert_gemm_parity(got, want, mag + 1e-6, s, f"cfg5 fused={fused}")
         print(f"cfg5 attention fused={fused}: rel err vs magnitude {rel_mag:.3e}, "
               f"vs max|out| {rel_max:.3e}")
+        worst64 = 0.0
         # float64 reference on two heads (as tests/reference/softmax_loss.hpp:149+): rel 1e-4
         for (bi, hi) in [(0, 0), (7, 15)]:
             sc = (q[bi, hi].astype(np.float64) @ k[bi, hi].T.astype(np.float64)) * 0.125
@@ -97,7 +98,12 @@ def test_config5_attention_full(stream, oracle):
             p = np.exp(sc - sc.max(axis=1, keepdims=True))
             p /= p.sum(axis=1, keepdims=True)
             ref = p @ v[bi, hi].astype(np.float64)
-            assert np.max(np.abs(got[bi, hi] - ref) / (1.0 + np.abs(ref))) < 1e-4
+            err64 = float(np.max(np.abs(got[bi, hi] - ref) / (1.0 + np.abs(ref))))
+            assert err64 < 1e-4
+            worst64 = max(worst64, err64)
+        record_parity(f"cfg5_attention_{'fused' if fused else 'composed'}",
+                      rel_err_vs_magnitude=rel_mag, rel_err_vs_max=rel_max, bar=1e-5 * np.sqrt(s),
+                      float64_rel_err_two_heads=worst64, float64_bar=1e-4)
 
 
 @pytest.mark.parametrize("d", [16, 32, 48, 64, 80, 96, 112, 128])

@@ -12,7 +12,7 @@ import pytest
 
 import mensurflow_amd as mf
 from helpers import (assert_gemm_parity, magnitude, normal, quarter_input, quarter_matrix,
-                     same_bits, uniform)
+                     record_parity, same_bits, same_elements, tolerance, uniform)
 
 pytestmark = pytest.mark.gpu
 
@@ -630,6 +630,8 @@ def test_config1_matmul_1024_realistic(stream, oracle):
     want = oracle.matmul(a, b)
     rel_mag, rel_max = assert_gemm_parity(got, want, magnitude(oracle, a, b), n, "cfg1")
     print(f"cfg1 1024^3: rel err vs magnitude {rel_mag:.3e}, vs max|C| {rel_max:.3e}")
+    record_parity("cfg1_matmul_1024", rel_err_vs_magnitude=rel_mag, rel_err_vs_max=rel_max,
+                  bar=tolerance(n), bit_identical_share=float(np.mean(same_elements(got, want))))
 
 
 def test_config3_gemm_4096_nt_exact(stream):
@@ -660,12 +662,18 @@ def test_config3_gemm_4096_nt_realistic(stream, oracle):
     scale = 1.5 * magnitude(oracle, a, b_stored.T) + 0.5 * np.abs(c0)
     rel_mag, rel_max = assert_gemm_parity(got, want, scale, n, "cfg3")
     print(f"cfg3 4096^3 NT: rel err vs magnitude {rel_mag:.3e}, vs max|C| {rel_max:.3e}")
+    record_parity("cfg3_gemm_4096_nt", rel_err_vs_magnitude=rel_mag, rel_err_vs_max=rel_max,
+                  bar=tolerance(n), bit_identical_share=float(np.mean(same_elements(got, want))))
 
 
 def test_config4_mlp_fused_bias_gelu(stream, oracle):
     """X[4093,1023] x W[1023,4099] + bias, gelu-tanh fused in the epilogue,
-    against the reference's three-op chain gelu(bias_add(matmul(X, W), b), true). The row
-    argmax must agree exactly except on rows whose top two values are within the error bar."""
+    against the reference's three-op chain gelu(bias_add(matmul(X, W), b), true).
+
+    Row argmax: the index must be the oracle's on every row whose top two values differ by more
+    than twice the error bar, and on every other row the value the GPU's index selects must be
+    within the bar of the row's maximum (a near tie that summation order can flip). The counts
+    of decided, near-tie and differing rows are recorded."""
     m, k, n = 4093, 1023, 4099
     x = normal(oracle, (m, k), 0.0, 1.0, 7, 0)
     w = normal(oracle, (k, n), 0.0, float(np.sqrt(1.0 / 1023.0)), 8, 0)
@@ -683,9 +691,21 @@ def test_config4_mlp_fused_bias_gelu(stream, oracle):
     bar = 1e-5 * np.sqrt(k) * scale.max(axis=1)
     decided = margin > 2 * bar
     assert np.array_equal(gpu_argmax[decided], want_arg[decided])
+    differ = np.nonzero(gpu_argmax != want_arg)[0]
+    rows = np.arange(m)
+    # On a differing row the GPU's chosen entry must still be a maximum within the bar.
+    shortfall = want.max(axis=1)[differ] - want[differ, gpu_argmax[differ]]
+    assert np.all(shortfall <= bar[differ]), (differ, shortfall, bar[differ])
+    worst = float(np.max(shortfall / bar[differ])) if differ.size else 0.0
     print(f"cfg4: rel err vs magnitude {rel_mag:.3e}, vs max|C| {rel_max:.3e}; argmax equal on "
           f"{int(decided.sum())} decided rows, {int((~decided).sum())} near-tie rows, "
-          f"{int(np.sum(gpu_argmax != want_arg))} rows differ in total")
+          f"{differ.size} rows differ in total")
+    record_parity("cfg4_mlp_bias_gelu", rel_err_vs_magnitude=rel_mag, rel_err_vs_max=rel_max,
+                  bar=tolerance(k), bit_identical_share=float(np.mean(same_elements(out, want))),
+                  argmax_rows=m, argmax_decided_rows=int(decided.sum()),
+                  argmax_near_tie_rows=int((~decided).sum()), argmax_differing_rows=int(differ.size),
+                  argmax_differing_row_ids=[int(r) for r in rows[differ]],
+                  argmax_worst_shortfall_over_bar=worst)
 
 
 def test_deterministic(stream):

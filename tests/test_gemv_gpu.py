@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import mensurflow_amd as mf
-from helpers import normal, quarter_matrix, same_bits, tolerance, uniform
+from helpers import normal, quarter_matrix, record_parity, same_bits, tolerance, uniform
 
 pytestmark = pytest.mark.gpu
 
@@ -51,6 +51,9 @@ def test_config2_full_size(stream, oracle, trans):
     want = oracle.gemv(a, x, 2.0, y0, 0.5, trans=trans)
     rel, same = assert_gemv_parity(got, want, a, x, 2.0, y0, 0.5, trans, f"cfg2 trans={trans}")
     print(f"cfg2 trans={trans}: rel err {rel:.3e}, bit-identical outputs {same:.6f}")
+    record_parity(f"cfg2_gemv_16384_{'t' if trans else 'n'}", rel_err_vs_magnitude=rel,
+                  bar=tolerance(n), bit_identical_share=same,
+                  differing_outputs=int(np.sum(got.view(np.uint32) != want.view(np.uint32))))
     assert same > 0.999
 
 

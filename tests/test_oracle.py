@@ -178,6 +178,64 @@ def test_gemm_composition_rounding(oracle):
                      want.astype(np.float32))
 
 
+def test_gemm_composition_matches_reference_vectors(oracle, vectors):
+    """orc_axpby_f32 against the reference's own mul -> scal -> add chain of mensurflow::gemm
+    (src/ops/blas.cpp:246-257), bit for bit, with and without C0, on values that separate one
+    rounding from two and on overflow, signed zeros, subnormals, infinities and NaN."""
+    x, c0 = vectors["axpby_x"], vectors["axpby_c0"]
+    for i, (alpha, beta) in enumerate(vectors["axpby_cases"].tolist()):
+        assert same_bits(oracle.axpby(x, alpha, c0, beta), vectors[f"axpby_out{i}"]), (alpha, beta)
+        assert same_bits(oracle.axpby(x, alpha, None, 0.0), vectors[f"axpby_out{i}_noc0"]), alpha
+
+
+def test_batched_composition_matches_reference_vectors(oracle, vectors):
+    """The oracle's batched GEMM (packed product per matrix, then orc_axpby_f32) against the
+    reference's gemm_batched_f32_parallel with its finish pass (gemm_batched.cpp:12-28,58-70):
+    A broadcast over the batch, B read transposed, alpha alone and alpha with beta * C0."""
+    m, n, k, batch = 21, 19, 37, 3
+    a = vectors["batched_a"].reshape(m, k)
+    b = vectors["batched_b"].reshape(batch, n, k)
+    c0 = vectors["batched_c0"]
+    for i in range(batch):
+        product = oracle.matmul(a, b[i].T, kc=768)
+        assert same_bits(oracle.axpby(product, 0.125, None, 0.0), vectors["batched_scores"][i])
+        assert same_bits(oracle.axpby(product, 1.5, c0[i], 0.5), vectors["batched_ab"][i])
+
+
+def test_planted_fused_composition_is_caught(vectors):
+    """An epilogue that fused alpha*x + beta*c0 into one rounding (an fma) would not match the
+    reference's chain on these vectors."""
+    x = vectors["axpby_x"].astype(np.float64)
+    scaled_c0 = (np.float32(0.5) * vectors["axpby_c0"]).astype(np.float64)
+    with np.errstate(over="ignore", invalid="ignore"):
+        fused = (1.5 * x + scaled_c0).astype(np.float32)  # 1.5 * x is exact in float64
+    assert not same_bits(fused, vectors["axpby_out0"])
+
+
+def test_live_reference_composition(oracle, reference):
+    """Where oracle/_ref is built: more alpha/beta values and a larger batched case, live."""
+    rng = np.random.default_rng(21)
+    x = (rng.standard_normal(5000) * 100).astype(np.float32)
+    c0 = (rng.standard_normal(5000) * 100).astype(np.float32)
+    for alpha, beta in [(0.3, 0.7), (-1.25, 2.0), (1.0, -3.0), (7.0, 0.0)]:
+        assert same_bits(oracle.axpby(x, alpha, c0, beta),
+                         reference.gemm_composition(x, alpha, c0, beta)), (alpha, beta)
+    m, n, k, batch = 70, 45, 300, 4
+    a = rng.uniform(-1, 1, (batch, k, m)).astype(np.float32)  # read transposed
+    b = rng.uniform(-1, 1, (k, n)).astype(np.float32)  # broadcast over the batch
+    cz = rng.standard_normal((batch, m, n)).astype(np.float32)
+    saved = reference.get_kc()
+    try:
+        reference.set_kc(768)
+        got = reference.gemm_batched(a, b, np.arange(batch) * k * m, np.zeros(batch), m, n, k,
+                                     1, m, n, 1, alpha=0.25, c0=cz, beta=-2.0)
+    finally:
+        reference.set_kc(saved)
+    for i in range(batch):
+        want = oracle.axpby(oracle.matmul(a[i].T, b, kc=768), 0.25, cz[i], -2.0)
+        assert same_bits(got[i], want), i
+
+
 def test_softmax_special_lines(oracle):
     x = np.array([[0.0, 1.0, 2.0], [-np.inf] * 3, [1.0, np.nan, 0.0]], dtype=np.float32)
     out = oracle.softmax(x)
