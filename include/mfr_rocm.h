@@ -195,6 +195,20 @@ enum {
 
 int mfr_sgemm(mfr_stream_t stream, const mfr_gemm_desc* desc);
 
+/* mfr_sgemm without any device allocation. No counterpart in the reference: it is for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). It makes the same plan as mfr_sgemm and gives the same bits, but puts the split-K
+ * partial sums and staged operands in a fixed scratch array of MFR_SGEMM_SCRATCH_BYTES per device
+ * (a static device array, resident until the process ends) instead of the stream's workspace. A
+ * plan that needs more (the split-K sums are splits*m*n*batch floats, a staged operand its
+ * zero-padded copy) fails with MFR_E_INVALID before anything is launched; products with aligned
+ * operands and no split need none. Every call on one device shares that device's array, so calls
+ * that overlap on one device (on two streams, or from two threads) race; the array keeps the last
+ * call's contents, and nothing in it needs to start at zero. The first call on a device looks up
+ * the array's address there. */
+#define MFR_SGEMM_SCRATCH_BYTES ((size_t)64 << 20)
+int mfr_sgemm_noalloc(mfr_stream_t stream, const mfr_gemm_desc* desc);
+
 /* Edge peeling (tile and splits both AUTO): a dimension a few rows past a multiple of a big tile
  * (N = 4099 = 16 x 256 + 3) would cost that tile a whole extra wave of tiles for a sliver of work,
  * so such a remainder (at most a quarter of the tile) may run as a separate launch with its own

@@ -42,6 +42,7 @@ MAX_SPLITS = 64
 
 MAX_BATCH_DIMS = 4
 MAX_COPY_DIMS = 8
+SGEMM_SCRATCH_BYTES = 64 << 20  # MFR_SGEMM_SCRATCH_BYTES: mfr_sgemm_noalloc's fixed scratch
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -107,6 +108,7 @@ SIGNATURES = {
     "mfr_event_record": (ctypes.c_int, [_vp, _vp]),
     "mfr_event_elapsed_ms": (ctypes.c_int, [_vp, _vp, ctypes.POINTER(_f32)]),
     "mfr_sgemm": (ctypes.c_int, [_vp, ctypes.POINTER(GemmDesc)]),
+    "mfr_sgemm_noalloc": (ctypes.c_int, [_vp, ctypes.POINTER(GemmDesc)]),
     "mfr_sgemm_plan": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(GemmDesc),
                                       ctypes.POINTER(_i32), ctypes.POINTER(_i32),
                                       ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),

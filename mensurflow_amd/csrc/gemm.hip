@@ -1024,9 +1024,12 @@ Plan cached_plan(const mfr_gemm_desc& d, int cus) {
     return plan;
 }
 
-// Runs d on s. The split-K partial sums and staged operands go to the stream's workspace, laid
-// out [partial sums][staged A][staged B] (grown as needed, with fallbacks when it cannot be had).
-void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
+// Runs d on s. The split-K partial sums and staged operands go to one workspace laid out
+// [partial sums][staged A][staged B]: the stream's own (grown as needed, with fallbacks when it
+// cannot be had), or, when `scratch` is not null, that fixed buffer of `scratch_bytes`, in which
+// case a plan needing more is refused before anything is launched.
+void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d, float* scratch = nullptr,
+               size_t scratch_bytes = 0) {
     Plan plan = cached_plan(d, s.compute_units);
     if (plan.empty) {
         return;
@@ -1039,7 +1042,16 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
     int64_t fb = plan.stage_b ? staged_floats_padded(ob, p) : 0;
     float* ws = nullptr;
     std::unique_lock<std::mutex> hold(s.workspace_mutex, std::defer_lock);
-    if (partial_floats(plan) + fa + fb > 0) {
+    if (scratch != nullptr) {
+        const size_t need = 4 * static_cast<size_t>(partial_floats(plan) + fa + fb);
+        if (need > scratch_bytes) {
+            throw mfr::Error(MFR_E_INVALID,
+                             "sgemm_noalloc: this product needs " + std::to_string(need) +
+                                 " bytes of scratch (split-K sums and staged operands), more "
+                                 "than the " + std::to_string(scratch_bytes) + "-byte maximum");
+        }
+        ws = scratch;
+    } else if (partial_floats(plan) + fa + fb > 0) {
         // Held until every launch is queued (see mfr_stream).
         hold.lock();
         ws = static_cast<float*>(
@@ -1089,7 +1101,42 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d) {
 
 } // namespace
 
+// ---- the no-allocation entry point ------------------------------------------------------------
+//
+// mfr_sgemm_noalloc's workspace: one fixed array per device, held until the process ends. Host
+// code never uses its name as an address (in host code it names a host-side stand-in): each
+// device's address comes from hipGetSymbolAddress, taken once per device with that device
+// current, and only that address reaches kernels.
+static constexpr size_t kScratchBytes = MFR_SGEMM_SCRATCH_BYTES;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex scratch_mutex;
+static float* scratch_address[kMaxScratchDevices] = {};
+
+// The device address of `scratch` on s's device (current, as stream_of made it).
+static float* scratch_on(const mfr_stream& s) {
+    mfr::require(s.device >= 0 && s.device < kMaxScratchDevices,
+                 "sgemm_noalloc: device index out of range");
+    std::lock_guard<std::mutex> hold(scratch_mutex);
+    if (scratch_address[s.device] == nullptr) {
+        void* address = nullptr;
+        mfr::check(hipGetSymbolAddress(&address, HIP_SYMBOL(scratch)),
+                   "hipGetSymbolAddress(scratch)");
+        scratch_address[s.device] = static_cast<float*>(address);
+    }
+    return scratch_address[s.device];
+}
+
 extern "C" {
+
+int mfr_sgemm_noalloc(mfr_stream_t stream, const mfr_gemm_desc* desc) {
+    return mfr::guarded([&] {
+        auto& s = mfr::stream_of(stream);
+        mfr::require(desc != nullptr, "sgemm_noalloc: null descriptor");
+        run_sgemm(s, *desc, scratch_on(s), kScratchBytes);
+    });
+}
 
 int mfr_sgemm(mfr_stream_t stream, const mfr_gemm_desc* desc) {
     return mfr::guarded([&] {
