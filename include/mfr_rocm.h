@@ -267,6 +267,16 @@ int mfr_bias_act(mfr_stream_t stream, const float* x, const float* bias, float* 
 int mfr_where(mfr_stream_t stream, const uint8_t* cond, const float* x, const float* y, float* out,
               int64_t n);
 
+/* out = cond ? x : y over an ndim-dimensional output `shape` (out contiguous, row-major), each
+ * operand read through its own element strides, 0 on a broadcast dimension (ndim <= 8, strides
+ * >= 0). The form of Where for operands that broadcast: attention's -inf scalar and its [Lq, Lk]
+ * mask expanded over [B, H, Lq, Lk] are read once each instead of packed to the scores' shape,
+ * which is what the reference does (src/ops/elementwise.cpp:454-481). Same selection as
+ * mfr_where (elementwise.cpp:64-70). */
+int mfr_where_nd(mfr_stream_t stream, int32_t ndim, const int64_t* shape, const uint8_t* cond,
+                 const int64_t* cond_strides, const float* x, const int64_t* x_strides,
+                 const float* y, const int64_t* y_strides, float* out);
+
 /* Softmax of x viewed as [outer, length, inner] along the middle axis (contiguous).
  * Float maximum (a NaN poisons the line), float exp(x - max), double sum, one float scale;
  * a line whose maximum is -inf (every element masked) gives zeros.

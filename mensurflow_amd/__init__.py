@@ -25,7 +25,7 @@ from .abi import ACT_GELU_ERF, ACT_GELU_TANH, ACT_NONE, GemmDesc  # noqa: F401
 __all__ = [
     "ACT_NONE", "ACT_GELU_TANH", "ACT_GELU_ERF", "GemmDesc", "device_count", "device_info",
     "Stream", "DeviceArray", "Event", "sgemm", "gemm", "gemm_batched", "sgemv", "matvec",
-    "bias_act", "where", "elementwise", "softmax", "argmax", "strided_copy", "fill", "attention",
+    "bias_act", "where", "where_nd", "elementwise", "softmax", "argmax", "strided_copy", "fill", "attention",
     "attention_fused", "attention_composed", "gemm_plan",
 ]
 
@@ -431,6 +431,24 @@ def where(cond: DeviceArray, x: DeviceArray, y: DeviceArray,
     return out
 
 
+def where_nd(cond: DeviceArray, x: DeviceArray, y: DeviceArray,
+             out: DeviceArray | None = None) -> DeviceArray:
+    """out = cond ? x : y with each operand read through its own strides (mfr_where_nd): cond,
+    x and y are views of out's shape, expanded (stride 0) where they broadcast."""
+    shape = out.shape if out is not None else x.shape
+    for t in (cond, x, y):
+        if t.shape != shape:
+            raise ValueError(f"where_nd: operand shape {t.shape} differs from {shape}")
+    if out is None:
+        out = DeviceArray.empty(shape, x.stream)
+    nd = len(shape)
+    arr = ctypes.c_int64 * max(nd, 1)
+    abi.check(abi.load().mfr_where_nd(x.stream.handle, nd, arr(*shape), cond.ptr,
+                                      arr(*cond.strides), x.ptr, arr(*x.strides), y.ptr,
+                                      arr(*y.strides), out.ptr), "mfr_where_nd")
+    return out
+
+
 def elementwise(op: int, a: DeviceArray, b: DeviceArray | None = None, alpha=1.0,
                 out: DeviceArray | None = None) -> DeviceArray:
     """out = a + b (abi.EW_ADD), a * b (abi.EW_MUL) or alpha * a (abi.EW_SCAL, b unused) over
@@ -542,11 +560,11 @@ def attention_composed(q: DeviceArray, k: DeviceArray, v: DeviceArray,
                        scale: float = 0.0) -> DeviceArray:
     """mensurflow::attention's composition on the device (src/ops/attention.cpp:48-98): scores =
     gemm_batched(q, k^T, alpha=scale), where(mask, scores, -inf) with the mask and the -inf
-    scalar packed to the scores' shape (as mensurflow::where packs them), the causal mask the
-    same way, softmax over the keys, gemm_batched(weights, v). q [..., Lq, D], k [..., Lk, D],
-    v [..., Lk, Dv] with equal batch shapes; mask a Bool (uint8) array broadcastable to
-    [..., Lq, Lk]. Every array is on q's stream; the materialised temporaries (scores, the
-    packed -inf operand and mask) are that stream's scratch arrays, reused by later calls."""
+    scalar read through broadcast views (mfr_where_nd; mensurflow::where packs them to the
+    scores' shape), the causal mask the same way, softmax over the keys, gemm_batched(weights,
+    v). q [..., Lq, D], k [..., Lk, D], v [..., Lk, Dv] with equal batch shapes; mask a Bool
+    (uint8) array broadcastable to [..., Lq, Lk]. Every array is on q's stream; the scores are
+    that stream's scratch array, reused by later calls."""
     stream = q.stream
     lq, depth = q.shape[-2:]
     lk = k.shape[-2]
@@ -560,13 +578,10 @@ def attention_composed(q: DeviceArray, k: DeviceArray, v: DeviceArray,
     def masked(keep: DeviceArray) -> DeviceArray:
         nonlocal minus_inf
         if minus_inf is None:
-            scalar = stream.scratch("attention.scalar", (1,))
-            fill(scalar, -np.inf)
-            minus_inf = strided_copy(scalar.expand(scores.shape),
-                                     out=stream.scratch("attention.minus_inf", scores.shape))
-        full_mask = strided_copy(keep.expand(scores.shape),
-                                 out=stream.scratch("attention.mask", scores.shape, np.uint8))
-        return where(full_mask, scores, minus_inf, out=scores)
+            minus_inf = stream.scratch("attention.scalar", (1,))
+            fill(minus_inf, -np.inf)
+        return where_nd(keep.expand(scores.shape), scores, minus_inf.expand(scores.shape),
+                        out=scores)
 
     if mask is not None:
         masked(mask)

@@ -119,6 +119,8 @@ SIGNATURES = {
     "mfr_smatvec": (ctypes.c_int, [_vp, _i64, _i64, _vp, _i64, _vp, _vp]),
     "mfr_bias_act": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_int]),
     "mfr_where": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64]),
+    "mfr_where_nd": (ctypes.c_int, [_vp, _i32, ctypes.POINTER(_i64), _vp, ctypes.POINTER(_i64),
+                                    _vp, ctypes.POINTER(_i64), _vp, ctypes.POINTER(_i64), _vp]),
     "mfr_softmax": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64, _i64]),
     "mfr_argmax": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i64]),
     "mfr_elementwise": (ctypes.c_int, [_vp, ctypes.c_int, _vp, _vp, _f32, _vp, _i64]),

@@ -194,6 +194,99 @@ __global__ __launch_bounds__(kStreamThreads) void binary4_kernel(const float4* _
     }
 }
 
+// ---- where over strided operands -------------------------------------------------------------
+//
+// out (contiguous, row-major) = cond ? x : y where each operand is read through its own strides,
+// 0 on a broadcast dimension (attention's -inf scalar and [Lq, Lk] mask expanded over
+// [B, H, Lq, Lk] read 1 element and 1 MiB, not 512 and 128 MiB). The output is walked as rows of
+// its last dimension; a row's operand bases come from its index over the outer dimensions.
+struct WhereLayout {
+    int outer_dims;                     // dimensions before the last
+    int64_t shape[MFR_MAX_COPY_DIMS];   // outer extents, outermost first
+    int64_t cs[MFR_MAX_COPY_DIMS];      // outer strides of cond, x, y
+    int64_t xs[MFR_MAX_COPY_DIMS];
+    int64_t ys[MFR_MAX_COPY_DIMS];
+    int64_t rows, row_len;              // product of the outer extents; the last extent
+    int64_t c_inner, x_inner, y_inner;  // strides along the last dimension
+};
+
+__device__ inline void where_row_bases(const WhereLayout& l, int64_t row, int64_t* c, int64_t* x,
+                                       int64_t* y) {
+    int64_t oc = 0, ox = 0, oy = 0;
+    for (int d = l.outer_dims - 1; d >= 0; --d) {
+        const int64_t i = row % l.shape[d];
+        row /= l.shape[d];
+        oc += i * l.cs[d];
+        ox += i * l.xs[d];
+        oy += i * l.ys[d];
+    }
+    *c = oc;
+    *x = ox;
+    *y = oy;
+}
+
+// Rows whose length is a multiple of 4, out 16-byte aligned; each operand's inner stride is 0
+// (one value per row) or 1 with 16-byte (x, y) / 4-byte (cond) aligned row starts, checked on the
+// host. Workgroups take rows in turn, threads the row's quads.
+template <bool STREAM>
+__global__ __launch_bounds__(256) void where_rows4_kernel(const uint8_t* __restrict__ cond,
+                                                          const float* __restrict__ x,
+                                                          const float* __restrict__ y,
+                                                          float* __restrict__ out, WhereLayout l) {
+    const int64_t quads = l.row_len / 4;
+    for (int64_t row = blockIdx.x; row < l.rows; row += gridDim.x) {
+        int64_t oc, ox, oy;
+        where_row_bases(l, row, &oc, &ox, &oy);
+        float4* o = reinterpret_cast<float4*>(out + row * l.row_len);
+        for (int64_t q = threadIdx.x; q < quads; q += 256) {
+            uint32_t c;
+            if (l.c_inner == 0) {
+                c = cond[oc] != 0 ? 0x01010101u : 0u;
+            } else {
+                c = *reinterpret_cast<const uint32_t*>(cond + oc + 4 * q);
+            }
+            float4 xv, yv;
+            if (l.x_inner == 0) {
+                const float v = x[ox];
+                xv = make_float4(v, v, v, v);
+            } else {
+                xv = mfr::dev::load_streaming(x + ox + 4 * q);
+            }
+            if (l.y_inner == 0) {
+                const float v = y[oy];
+                yv = make_float4(v, v, v, v);
+            } else {
+                yv = mfr::dev::load_streaming(y + oy + 4 * q);
+            }
+            float4 v;
+            v.x = (c & 0xffu) != 0 ? xv.x : yv.x;
+            v.y = (c & 0xff00u) != 0 ? xv.y : yv.y;
+            v.z = (c & 0xff0000u) != 0 ? xv.z : yv.z;
+            v.w = (c & 0xff000000u) != 0 ? xv.w : yv.w;
+            if constexpr (STREAM) {
+                mfr::dev::store_streaming(reinterpret_cast<float*>(o + q), v);
+            } else {
+                o[q] = v;
+            }
+        }
+    }
+}
+
+// Any strides: one element per thread and step.
+__global__ __launch_bounds__(256) void where_rows_kernel(const uint8_t* __restrict__ cond,
+                                                         const float* __restrict__ x,
+                                                         const float* __restrict__ y,
+                                                         float* __restrict__ out, WhereLayout l) {
+    for (int64_t row = blockIdx.x; row < l.rows; row += gridDim.x) {
+        int64_t oc, ox, oy;
+        where_row_bases(l, row, &oc, &ox, &oy);
+        float* o = out + row * l.row_len;
+        for (int64_t j = threadIdx.x; j < l.row_len; j += 256) {
+            o[j] = cond[oc + j * l.c_inner] != 0 ? x[ox + j * l.x_inner] : y[oy + j * l.y_inner];
+        }
+    }
+}
+
 // The reference's line maximum: a NaN anywhere makes it NaN (the scan stops at the first NaN),
 // otherwise the largest value (-inf for an empty or all -inf line).
 __device__ inline float line_max(float m, int has_nan) { return has_nan ? NAN : m; }
@@ -498,6 +591,94 @@ int mfr_where(mfr_stream_t stream, const uint8_t* cond, const float* x, const fl
             where_kernel<<<mfr::grid_blocks(rest, 256, 16384), 256, 0, s.stream>>>(
                 cond + done, x + done, y + done, out + done, rest);
             mfr::check_launch("where_kernel");
+        }
+    });
+}
+
+int mfr_where_nd(mfr_stream_t stream, int32_t ndim, const int64_t* shape, const uint8_t* cond,
+                 const int64_t* cond_strides, const float* x, const int64_t* x_strides,
+                 const float* y, const int64_t* y_strides, float* out) {
+    return mfr::guarded([&] {
+        auto& s = mfr::stream_of(stream);
+        mfr::require(ndim >= 0 && ndim <= MFR_MAX_COPY_DIMS, "where_nd: too many dimensions");
+        mfr::require(ndim == 0 || (shape != nullptr && cond_strides != nullptr &&
+                                   x_strides != nullptr && y_strides != nullptr),
+                     "where_nd: null shape or strides");
+        // Dimensions of extent 1 are dropped (never stepped along); a 0-d call is one element.
+        WhereLayout l{};
+        int64_t ext[MFR_MAX_COPY_DIMS], cs[MFR_MAX_COPY_DIMS], xs[MFR_MAX_COPY_DIMS],
+            ys[MFR_MAX_COPY_DIMS];
+        int dims = 0;
+        int64_t total = 1;
+        for (int d = 0; d < ndim; ++d) {
+            mfr::require(shape[d] >= 0, "where_nd: negative dimension");
+            mfr::require(cond_strides[d] >= 0 && x_strides[d] >= 0 && y_strides[d] >= 0,
+                         "where_nd: negative stride");
+            total *= shape[d];
+            if (shape[d] != 1) {
+                ext[dims] = shape[d];
+                cs[dims] = cond_strides[d];
+                xs[dims] = x_strides[d];
+                ys[dims] = y_strides[d];
+                ++dims;
+            }
+        }
+        if (total == 0) {
+            return;
+        }
+        mfr::require(cond != nullptr && x != nullptr && y != nullptr && out != nullptr,
+                     "where_nd: null pointer");
+        if (dims == 0) {
+            ext[0] = 1;
+            cs[0] = xs[0] = ys[0] = 0;
+            dims = 1;
+        }
+        l.outer_dims = dims - 1;
+        l.rows = 1;
+        for (int d = 0; d + 1 < dims; ++d) {
+            l.shape[d] = ext[d];
+            l.cs[d] = cs[d];
+            l.xs[d] = xs[d];
+            l.ys[d] = ys[d];
+            l.rows *= ext[d];
+        }
+        l.row_len = ext[dims - 1];
+        l.c_inner = cs[dims - 1];
+        l.x_inner = xs[dims - 1];
+        l.y_inner = ys[dims - 1];
+        // Quads need: unit or zero inner strides, rows of a multiple of 4, and aligned row starts
+        // (every outer stride a multiple of the vector's elements, aligned bases).
+        auto rows_aligned = [&](const int64_t* strides, int64_t inner, int64_t elems,
+                                const void* base, uintptr_t bytes) {
+            if (inner == 0) {
+                return true;
+            }
+            if (inner != 1 || !aligned_to(base, bytes)) {
+                return false;
+            }
+            for (int d = 0; d < l.outer_dims; ++d) {
+                if (strides[d] % elems != 0) {
+                    return false;
+                }
+            }
+            return true;
+        };
+        const bool quads = l.row_len % 4 == 0 && aligned_to(out, 16) &&
+                           rows_aligned(l.cs, l.c_inner, 4, cond, 4) &&
+                           rows_aligned(l.xs, l.x_inner, 4, x, 16) &&
+                           rows_aligned(l.ys, l.y_inner, 4, y, 16);
+        const unsigned blocks = static_cast<unsigned>(l.rows < 65536 ? l.rows : 65536);
+        if (quads) {
+            const bool stream_out = 4.0 * static_cast<double>(total) > mfr::kLastLevelCacheBytes;
+            if (stream_out) {
+                where_rows4_kernel<true><<<blocks, 256, 0, s.stream>>>(cond, x, y, out, l);
+            } else {
+                where_rows4_kernel<false><<<blocks, 256, 0, s.stream>>>(cond, x, y, out, l);
+            }
+            mfr::check_launch("where_rows4_kernel");
+        } else {
+            where_rows_kernel<<<blocks, 256, 0, s.stream>>>(cond, x, y, out, l);
+            mfr::check_launch("where_rows_kernel");
         }
     });
 }

@@ -1,6 +1,6 @@
-// Tensor: a typed, shaped, strided view over shared device memory -- the reference's public
-// Tensor (include/mensurflow/tensor.hpp:25-162) for the BLAS hot path. Copying a Tensor shares
-// memory. Autograd (requires_grad/backward) is not part of this backend's scope.
+// Tensor: an element type, a shape and strides over memory shared with other views. The public
+// calls are mensurflow's (include/mensurflow/tensor.hpp:25-162) minus autograd, which is not on
+// this backend's path. Copying a Tensor copies the view, not the memory.
 #pragma once
 
 #include "mensurflow/device.hpp"
@@ -22,9 +22,9 @@ struct TensorAccess;
 
 class Tensor {
   public:
-    Tensor() = default; // undefined: everything but defined() throws
+    Tensor() = default; // undefined; any use but defined() throws logic_error
 
-    // Uninitialized memory on `device` (CPU by default); runtime_error if it is unavailable.
+    // New memory on `device` (the CPU unless given); runtime_error when it is not available.
     static Tensor empty(Shape shape, DType dtype = DType::F32, Device device = {});
     static Tensor constant(Shape shape, double value, DType dtype = DType::F32, Device device = {});
     static Tensor zeros(Shape shape, DType dtype = DType::F32, Device device = {});
@@ -35,7 +35,7 @@ class Tensor {
     static Tensor ones_like(const Tensor& other);
     static Tensor full_like(const Tensor& other, double value);
 
-    // numel(shape) * dtype_size(dtype) bytes from contiguous host memory.
+    // A new tensor holding numel(shape) elements read from contiguous host memory at `data`.
     static Tensor from_host(const void* data, Shape shape, DType dtype, Device device = {});
 
     template <typename T>
@@ -48,29 +48,28 @@ class Tensor {
         return from_host(data.data(), std::move(shape), dtype_of<T>, device);
     }
 
-    // Views: same storage, new shape/strides/offset, O(dim).
+    // Views over the same memory.
     Tensor transpose(int d0, int d1) const;
     Tensor permute(const std::vector<int>& order) const;
     Tensor slice(int d, std::int64_t start, std::int64_t end, std::int64_t step = 1) const;
     Tensor expand(const Shape& shape) const;
     Tensor unsqueeze(int d) const;
-    Tensor view(Shape shape) const; // needs a contiguous tensor; one dimension may be -1
+    Tensor view(Shape shape) const; // of a contiguous tensor; at most one extent may be -1
 
     bool shares_storage(const Tensor& other) const;
 
-    // The same data on `device` as a contiguous tensor (copied through host memory), or *this
-    // when already there.
+    // A contiguous copy on `device`, or *this when the tensor already lives there.
     Tensor to(Device device) const;
 
-    // *this if contiguous, else a packed copy on the same device. On a device whose backend
-    // registers a strided-copy kernel (ROCm) the packing stays on the device; otherwise it is
-    // staged through host memory, as the reference does (src/core/tensor.cpp:208-230).
+    // *this when contiguous, else a packed copy on the same device. A device whose backend has a
+    // strided-copy kernel (ROCm) packs there; others pack through host memory, as mensurflow does
+    // (src/core/tensor.cpp:208-230).
     Tensor contiguous() const;
 
-    // Overwrites this tensor's elements with `source` (same shape, dtype and device).
+    // Overwrites this view's elements with `source`'s (same shape, dtype and device).
     void copy_from(const Tensor& source);
 
-    // numel() elements in row-major order; blocks until the data is ready.
+    // The elements in row-major order into `dst`; waits for queued device work.
     void copy_to_host(void* dst) const;
 
     template <typename T> T item() const {
@@ -94,11 +93,11 @@ class Tensor {
     bool defined() const { return storage_ != nullptr; }
     const Shape& shape() const;
     const Strides& strides() const;
-    std::int64_t offset() const; // elements from the start of the storage
+    std::int64_t offset() const; // in elements, from the start of the memory
     DType dtype() const;
     Device device() const;
     int dim() const;
-    std::int64_t size(int d) const;
+    std::int64_t size(int d) const; // d may count from the end (-1 = last)
     std::int64_t numel() const;
     std::size_t itemsize() const;
     std::size_t nbytes() const;
@@ -111,7 +110,7 @@ class Tensor {
            Strides strides, DType dtype);
 
     void require_defined() const;
-    Tensor make_view(std::int64_t offset, Shape shape, Strides strides) const;
+    Tensor reshaped(std::int64_t offset, Shape shape, Strides strides) const;
 
     std::shared_ptr<detail::Storage> storage_;
     std::int64_t offset_ = 0;

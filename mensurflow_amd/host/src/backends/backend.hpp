@@ -1,7 +1,7 @@
-// The interface every backend implements (the reference's src/backends/backend.hpp:16-68): one
-// allocation (Buffer), an ordered queue with host transfers (Stream), and the backend itself.
-// Nothing above the dispatcher includes a vendor header; the ROCm backend reaches HIP only
-// through the C ABI of include/mfr_rocm.h.
+// What a backend provides to mensurflow's core (the classes of src/backends/backend.hpp): memory
+// (Buffer), an in-order queue with host transfers (Stream), and the device family itself
+// (Backend). The ROCm backend implements them on top of include/mfr_rocm.h, so no vendor header
+// is visible above this line.
 #pragma once
 
 #include "mensurflow/device.hpp"
@@ -9,6 +9,7 @@
 #include <cstddef>
 #include <memory>
 #include <string>
+#include <vector>
 
 namespace mensurflow::detail {
 
@@ -18,39 +19,48 @@ class Buffer {
   public:
     virtual ~Buffer() = default;
     virtual std::size_t size() const = 0;
-    // The backend's handle (a device address for CPU and ROCm); null for a zero-byte buffer.
+    // The backend's handle for the memory (a device address on CPU and ROCm); null when size() is
+    // 0. Only the owning backend's kernels interpret it.
     virtual void* native() const = 0;
-    // Host-addressable memory, or nullptr for device-only memory.
+    // Memory the host can address directly, else nullptr.
     virtual void* host_ptr() const { return nullptr; }
 };
 
 class Stream {
   public:
     virtual ~Stream() = default;
-    // Complete on return: src may be reused. d2h also waits for earlier work on the stream.
+    // Transfers that are finished on return (the source may be reused, the destination read).
+    // copy_d2h first waits for what is already queued.
     virtual void copy_h2d(Buffer& dst, std::size_t offset, const void* src, std::size_t bytes) = 0;
     virtual void copy_d2h(void* dst, const Buffer& src, std::size_t offset, std::size_t bytes) = 0;
+    // Returns once everything queued has finished.
     virtual void synchronize() = 0;
-    // A copy between two buffers of this stream's device, ordered with its other work. Added for
-    // device-resident Tensor::copy_from; the default stages the bytes through host memory.
+    // Bytes from one buffer of this stream's device to another, in queue order. An addition of
+    // this backend's integration (device-side Tensor::copy_from); a backend without a native copy
+    // gets this host round trip.
     virtual void copy_d2d(Buffer& dst, std::size_t dst_offset, const Buffer& src,
-                          std::size_t src_offset, std::size_t bytes);
+                          std::size_t src_offset, std::size_t bytes) {
+        std::vector<std::byte> bounce(bytes);
+        copy_d2h(bounce.data(), src, src_offset, bytes);
+        copy_h2d(dst, dst_offset, bounce.data(), bytes);
+    }
 };
 
 struct DeviceInfo {
     std::string name;
-    std::size_t memory_bytes = 0;
+    std::size_t memory_bytes = 0; // 0 when the runtime does not say
 };
 
 class Backend {
   public:
     virtual ~Backend() = default;
     virtual DeviceType type() const = 0;
-    // 0 when the backend is built in but finds no hardware; must not throw.
+    // Devices of this type that can be used; 0 (never an exception) when the hardware or its
+    // runtime is missing, so the registry can drop the backend.
     virtual int device_count() const = 0;
     virtual DeviceInfo info(int index) const = 0;
     virtual std::shared_ptr<Buffer> allocate(int index, std::size_t bytes) = 0;
-    // The stream kernels for this device run on (one per device).
+    // The queue every kernel of device `index` runs on.
     virtual Stream& stream(int index) = 0;
     virtual void register_kernels(Dispatcher& dispatcher) = 0;
 };

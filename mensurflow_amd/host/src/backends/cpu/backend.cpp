@@ -1,11 +1,12 @@
-// The CPU device: host memory and inline "streams" (the reference's CpuBuffer/CpuStream,
-// src/backends/cpu/backend.cpp:43-83). This backend registers no compute kernels: in a
-// mensurflow build the reference's own CPU kernels sit here; this repository is the ROCm
-// backend, and its tests plug the CPU oracle in at this point.
+// The CPU device of this build: host memory and a queue that runs everything at once. It holds no
+// compute kernels. In a mensurflow tree the CPU backend is mensurflow's own, with its kernels;
+// this repository ships the ROCm backend, and its C++ tests install the CPU oracle's kernels here
+// (tests/cpp/oracle_cpu.cpp).
 #include "backends/backend.hpp"
 #include "core/dispatcher.hpp"
 #include "core/registry.hpp"
 
+#include <cstdlib>
 #include <cstring>
 #include <new>
 
@@ -13,64 +14,71 @@ namespace mensurflow::detail {
 
 namespace {
 
-constexpr std::size_t kAlignment = 64;
+// Host allocations start on a cache line, which also suits the widest vector loads.
+constexpr std::size_t kLine = 64;
 
-class CpuBuffer final : public Buffer {
-  public:
-    explicit CpuBuffer(std::size_t bytes) : size_(bytes) {
-        if (bytes > 0) {
-            data_ = ::operator new(bytes, std::align_val_t{kAlignment});
-        }
-    }
-    ~CpuBuffer() override {
-        if (data_ != nullptr) {
-            ::operator delete(data_, std::align_val_t{kAlignment});
-        }
-    }
-    CpuBuffer(const CpuBuffer&) = delete;
-    CpuBuffer& operator=(const CpuBuffer&) = delete;
-    std::size_t size() const override { return size_; }
-    void* native() const override { return data_; }
-    void* host_ptr() const override { return data_; }
-
-  private:
-    std::size_t size_;
-    void* data_ = nullptr;
+struct FreeWithFree {
+    void operator()(std::byte* p) const { std::free(p); }
 };
 
-class CpuStream final : public Stream {
+class HostBuffer final : public Buffer {
+  public:
+    explicit HostBuffer(std::size_t bytes) : bytes_(bytes) {
+        if (bytes == 0) {
+            return; // a zero-byte buffer has no address
+        }
+        const std::size_t rounded = (bytes + kLine - 1) / kLine * kLine;
+        memory_.reset(static_cast<std::byte*>(std::aligned_alloc(kLine, rounded)));
+        if (!memory_) {
+            throw std::bad_alloc();
+        }
+    }
+    std::size_t size() const override { return bytes_; }
+    void* native() const override { return memory_.get(); }
+    void* host_ptr() const override { return memory_.get(); }
+
+  private:
+    std::size_t bytes_;
+    std::unique_ptr<std::byte, FreeWithFree> memory_;
+};
+
+std::byte* at(const Buffer& buffer, std::size_t offset) {
+    return static_cast<std::byte*>(buffer.native()) + offset;
+}
+
+// Host work finishes before the call returns, so there is never anything to wait for.
+class InlineQueue final : public Stream {
   public:
     void copy_h2d(Buffer& dst, std::size_t offset, const void* src, std::size_t bytes) override {
-        std::memcpy(static_cast<std::byte*>(dst.native()) + offset, src, bytes);
+        std::memcpy(at(dst, offset), src, bytes);
     }
     void copy_d2h(void* dst, const Buffer& src, std::size_t offset, std::size_t bytes) override {
-        std::memcpy(dst, static_cast<const std::byte*>(src.native()) + offset, bytes);
+        std::memcpy(dst, at(src, offset), bytes);
     }
     void copy_d2d(Buffer& dst, std::size_t dst_offset, const Buffer& src, std::size_t src_offset,
                   std::size_t bytes) override {
-        std::memmove(static_cast<std::byte*>(dst.native()) + dst_offset,
-                     static_cast<const std::byte*>(src.native()) + src_offset, bytes);
+        std::memmove(at(dst, dst_offset), at(src, src_offset), bytes); // ranges may overlap
     }
     void synchronize() override {}
 };
 
-class CpuBackend final : public Backend {
+class HostBackend final : public Backend {
   public:
     DeviceType type() const override { return DeviceType::CPU; }
     int device_count() const override { return 1; }
-    DeviceInfo info(int) const override { return {"cpu", 0}; }
+    DeviceInfo info(int) const override { return DeviceInfo{"cpu", 0}; }
     std::shared_ptr<Buffer> allocate(int, std::size_t bytes) override {
-        return std::make_shared<CpuBuffer>(bytes);
+        return std::make_shared<HostBuffer>(bytes);
     }
-    Stream& stream(int) override { return stream_; }
+    Stream& stream(int) override { return queue_; }
     void register_kernels(Dispatcher&) override {}
 
   private:
-    CpuStream stream_;
+    InlineQueue queue_;
 };
 
 } // namespace
 
-void register_cpu_backend(Registry& registry) { registry.add(std::make_unique<CpuBackend>()); }
+void register_cpu_backend(Registry& registry) { registry.add(std::make_unique<HostBackend>()); }
 
 } // namespace mensurflow::detail

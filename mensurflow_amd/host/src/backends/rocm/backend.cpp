@@ -188,6 +188,13 @@ mfr_stream_t handle(Stream& stream) { return static_cast<RocmStream&>(stream).ha
 
 template <typename T> T* ptr(const Tensor& t) { return TensorAccess::data<T>(t); }
 
+// The address of a tensor's first element whatever its dtype (TensorAccess::data<T> counts the
+// offset in sizeof(T) steps, so a byte pointer needs the element size here).
+std::byte* first_byte(const Tensor& t) {
+    return static_cast<std::byte*>(TensorAccess::buffer(t).native()) +
+           static_cast<std::size_t>(t.offset()) * t.itemsize();
+}
+
 // ---- GEMM family -------------------------------------------------------------------------------
 
 // A matrix operand the GEMM kernel can read: a unit stride in one of its two dimensions (or an
@@ -548,11 +555,27 @@ void gelu_kernel(const OpArgs& args, Stream& stream) {
                        out.numel(), args.approximate ? MFR_ACT_GELU_TANH : MFR_ACT_GELU_ERF));
 }
 
-// Inputs: x, y, condition (values first: the dispatch key is their dtype), all out's shape.
+// Inputs: x, y, condition (values first: the dispatch key is their dtype), each a view of out's
+// shape, expanded (stride 0) where it broadcasts; mfr_where_nd reads them through their strides.
 void where_kernel(const OpArgs& args, Stream& stream) {
     const Tensor& out = args.outputs[0];
-    check(mfr_where(handle(stream), ptr<std::uint8_t>(args.inputs[2]), ptr<float>(args.inputs[0]),
-                    ptr<float>(args.inputs[1]), ptr<float>(out), out.numel()));
+    const Tensor& x = args.inputs[0];
+    const Tensor& y = args.inputs[1];
+    const Tensor& cond = args.inputs[2];
+    if (x.is_contiguous() && y.is_contiguous() && cond.is_contiguous()) {
+        check(mfr_where(handle(stream), ptr<std::uint8_t>(cond), ptr<float>(x), ptr<float>(y),
+                        ptr<float>(out), out.numel()));
+        return;
+    }
+    if (out.dim() > MFR_MAX_COPY_DIMS) {
+        const Tensor px = x.contiguous(), py = y.contiguous(), pc = cond.contiguous();
+        check(mfr_where(handle(stream), ptr<std::uint8_t>(pc), ptr<float>(px), ptr<float>(py),
+                        ptr<float>(out), out.numel()));
+        return;
+    }
+    check(mfr_where_nd(handle(stream), out.dim(), out.shape().data(), ptr<std::uint8_t>(cond),
+                       cond.strides().data(), ptr<float>(x), x.strides().data(), ptr<float>(y),
+                       y.strides().data(), ptr<float>(out)));
 }
 
 void softmax_kernel(const OpArgs& args, Stream& stream) {
@@ -592,7 +615,7 @@ void strided_copy_kernel(const OpArgs& args, Stream& stream) {
         throw NotImplemented("strided_copy: more than " + std::to_string(MFR_MAX_COPY_DIMS) +
                              " dimensions on rocm");
     }
-    check(mfr_strided_copy(handle(stream), ptr<std::byte>(x), ptr<std::byte>(args.outputs[0]),
+    check(mfr_strided_copy(handle(stream), first_byte(x), first_byte(args.outputs[0]),
                            static_cast<std::int32_t>(x.itemsize()), x.dim(), x.shape().data(),
                            x.strides().data()));
 }

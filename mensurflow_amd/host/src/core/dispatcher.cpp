@@ -1,153 +1,209 @@
-// The op table and dispatch (semantics of the reference's src/core/dispatcher.cpp:228-353).
+// The op table and dispatch (the contract of mensurflow's src/core/dispatcher.cpp:228-353). The
+// kernels sit in a dense table indexed by (op, device type, dtype); a call's device comes from
+// execution_device(), or from the active tuning scope (core/tuning.hpp), and a call whose data
+// lives on another device is moved there and back by a Relocation.
 #include "core/dispatcher.hpp"
 
 #include "core/registry.hpp"
+#include "core/tuning.hpp"
 
 #include <stdexcept>
+#include <string>
 
 namespace mensurflow::detail {
 
-const char* op_name(OpId op) {
-    switch (op) {
-    case OpId::Scal: return "scal";
-    case OpId::Copy: return "copy";
-    case OpId::Add: return "add";
-    case OpId::Mul: return "mul";
-    case OpId::Matvec: return "matvec";
-    case OpId::Gemv: return "gemv";
-    case OpId::Matmul: return "matmul";
-    case OpId::Gelu: return "gelu";
-    case OpId::Where: return "where";
-    case OpId::BiasAdd: return "bias_add";
-    case OpId::Argmax: return "argmax";
-    case OpId::GemmBatched: return "gemm_strided_batched";
-    case OpId::Uniform: return "uniform";
-    case OpId::Normal: return "normal";
-    case OpId::Softmax: return "softmax";
-    case OpId::Gemm: return "gemm";
-    case OpId::StridedCopy: return "strided_copy";
-    case OpId::Attention: return "attention";
+namespace {
+
+constexpr const char* kOpNames[] = {
+    "scal",    "copy",     "add",         "mul",     "matvec",  "gemv",
+    "matmul",  "gelu",     "where",       "bias_add", "argmax", "gemm_strided_batched",
+    "uniform", "normal",   "softmax",     "gemm",    "strided_copy", "attention",
+};
+constexpr std::size_t kOpCount = sizeof(kOpNames) / sizeof(kOpNames[0]);
+static_assert(kOpCount == static_cast<std::size_t>(OpId::Attention) + 1, "a name for every op");
+
+constexpr std::size_t kDeviceTypeCount = static_cast<std::size_t>(DeviceType::ROCm) + 1;
+constexpr std::size_t kDTypeCount = static_cast<std::size_t>(DType::Bool) + 1;
+
+// The table slot of `key`, or kOpCount * ... (out of range) for values outside the enums.
+std::size_t slot_of(KernelKey key) {
+    const auto op = static_cast<std::size_t>(key.op);
+    const auto device = static_cast<std::size_t>(key.device);
+    const auto dtype = static_cast<std::size_t>(key.dtype);
+    if (op >= kOpCount || device >= kDeviceTypeCount || dtype >= kDTypeCount) {
+        throw std::invalid_argument("invalid kernel key");
     }
-    throw std::invalid_argument("invalid OpId");
+    return (op * kDeviceTypeCount + device) * kDTypeCount + dtype;
 }
+
+std::string describe(KernelKey key) {
+    return std::string(op_name(key.op)) + " on " + device_type_name(key.device) + " for " +
+           dtype_name(key.dtype);
+}
+
+// The tensor a call is keyed and placed by: its first input, or for a factory (no inputs) its
+// first output.
+const Tensor& anchor_of(OpId op, const OpArgs& args) {
+    const bool factory = op == OpId::Uniform || op == OpId::Normal;
+    if (!args.inputs.empty()) {
+        return args.inputs.front();
+    }
+    if (factory && !args.outputs.empty()) {
+        return args.outputs.front();
+    }
+    throw std::invalid_argument(std::string(op_name(op)) + ": no input tensors");
+}
+
+void require_single_device(OpId op, const OpArgs& args, Device home) {
+    auto check = [&](const Tensor& t) {
+        if (t.device() != home) {
+            throw std::invalid_argument(std::string(op_name(op)) + ": tensors are on " +
+                                        to_string(home) + " and " + to_string(t.device()) +
+                                        "; move one with Tensor::to()");
+        }
+    };
+    for (const Tensor& t : args.inputs) {
+        check(t);
+    }
+    for (const Tensor& t : args.outputs) {
+        check(t);
+    }
+}
+
+// A call run away from its data: the inputs copied to the target, the outputs computed into
+// temporaries there, then copied into the caller's tensors.
+class Relocation {
+  public:
+    Relocation(const OpArgs& original, Device target) : original_(original), moved_(original) {
+        for (Tensor& input : moved_.inputs) {
+            input = input.to(target);
+        }
+        for (Tensor& output : moved_.outputs) {
+            output = Tensor::empty(output.shape(), output.dtype(), target);
+        }
+    }
+    const OpArgs& args() const { return moved_; }
+    void write_back(Device home) const {
+        for (std::size_t i = 0; i < moved_.outputs.size(); ++i) {
+            Tensor destination = original_.outputs[i]; // shares the caller's storage
+            destination.copy_from(moved_.outputs[i].to(home));
+        }
+    }
+
+  private:
+    const OpArgs& original_;
+    OpArgs moved_;
+};
+
+void run_where(OpId op, const OpArgs& args, Device target, Device home) {
+    Registry& registry = Registry::instance();
+    Backend& backend = registry.get(target);
+    const KernelFn kernel =
+        registry.dispatcher().lookup({op, target.type, anchor_of(op, args).dtype()});
+    Stream& stream = backend.stream(target.index);
+    if (target == home) {
+        kernel(args, stream);
+        return;
+    }
+    const Relocation relocation(args, target);
+    kernel(relocation.args(), stream);
+    relocation.write_back(home);
+}
+
+} // namespace
+
+const char* op_name(OpId op) {
+    const auto index = static_cast<std::size_t>(op);
+    if (index >= kOpCount) {
+        throw std::invalid_argument("invalid OpId");
+    }
+    return kOpNames[index];
+}
+
+Dispatcher::Dispatcher() : table_(kOpCount * kDeviceTypeCount * kDTypeCount, nullptr) {}
 
 void Dispatcher::register_kernel(KernelKey key, KernelFn kernel) {
     if (kernel == nullptr) {
         throw std::invalid_argument("register_kernel: null kernel");
     }
-    if (!kernels_.emplace(key, kernel).second) {
-        throw std::logic_error(std::string("kernel registered twice: ") + op_name(key.op) + " on " +
-                               device_type_name(key.device) + " for " + dtype_name(key.dtype));
+    KernelFn& slot = table_[slot_of(key)];
+    if (slot != nullptr) {
+        throw std::logic_error("kernel registered twice: " + describe(key));
     }
+    slot = kernel;
 }
 
-KernelFn Dispatcher::find(KernelKey key) const {
-    const auto it = kernels_.find(key);
-    return it == kernels_.end() ? nullptr : it->second;
-}
+KernelFn Dispatcher::find(KernelKey key) const { return table_[slot_of(key)]; }
 
 KernelFn Dispatcher::lookup(KernelKey key) const {
-    if (KernelFn kernel = find(key)) {
-        return kernel;
+    const KernelFn kernel = find(key);
+    if (kernel == nullptr) {
+        throw NotImplemented(std::string(op_name(key.op)) + " is not implemented on " +
+                             device_type_name(key.device) + " for " + dtype_name(key.dtype));
     }
-    throw NotImplemented(std::string(op_name(key.op)) + " is not implemented on " +
-                         device_type_name(key.device) + " for " + dtype_name(key.dtype));
+    return kernel;
 }
 
 void Dispatcher::register_tunable(KernelKey key, TunableKernel tunable) {
-    if (tunable.key == nullptr || tunable.defaults == nullptr || tunable.space == nullptr ||
-        tunable.allowed == nullptr) {
+    const bool complete = tunable.key && tunable.defaults && tunable.space && tunable.allowed;
+    if (!complete) {
         throw std::invalid_argument("register_tunable: " + tunable.name + " is missing a function");
     }
     if (tunable.params.size() > static_cast<std::size_t>(TuningConfig::capacity)) {
         throw std::invalid_argument("register_tunable: " + tunable.name + " has more than " +
                                     std::to_string(TuningConfig::capacity) + " parameters");
     }
-    const std::string name = tunable.name;
-    if (!tunables_.emplace(key, std::move(tunable)).second) {
-        throw std::logic_error("tunable kernel registered twice: " + name);
+    if (tunables_.count(key) != 0) {
+        throw std::logic_error("tunable kernel registered twice: " + tunable.name);
     }
+    tunables_.emplace(key, std::move(tunable));
 }
 
 const TunableKernel* Dispatcher::tunable(KernelKey key) const {
-    const auto it = tunables_.find(key);
-    return it == tunables_.end() ? nullptr : &it->second;
+    const auto found = tunables_.find(key);
+    return found != tunables_.end() ? &found->second : nullptr;
 }
 
 Device execution_device(Execution execution, Device data_device) {
-    switch (execution) {
-    case Execution::Auto:
-    case Execution::CPU:
-        return {DeviceType::CPU, 0};
-    case Execution::GPU:
-        if (data_device.type != DeviceType::CPU) {
-            return data_device;
+    if (execution == Execution::Auto || execution == Execution::CPU) {
+        return Device{DeviceType::CPU, 0};
+    }
+    if (execution != Execution::GPU) {
+        throw std::invalid_argument("invalid Execution value");
+    }
+    if (data_device.type != DeviceType::CPU) {
+        return data_device; // data already on a GPU stays there
+    }
+    constexpr DeviceType kGpuOrder[] = {DeviceType::CUDA, DeviceType::Metal, DeviceType::ROCm};
+    for (const DeviceType type : kGpuOrder) {
+        if (Registry::instance().find(type) != nullptr) {
+            return Device{type, 0};
         }
-        for (DeviceType type : {DeviceType::CUDA, DeviceType::Metal, DeviceType::ROCm}) {
-            if (Registry::instance().find(type) != nullptr) {
-                return {type, 0};
-            }
-        }
-        throw std::runtime_error("Execution::GPU requested, but no GPU is available");
     }
-    throw std::invalid_argument("invalid Execution value");
+    throw std::runtime_error("Execution::GPU requested, but no GPU is available");
 }
-
-namespace {
-
-// Runs the kernel on `target`. When the data lives elsewhere, the inputs are copied over, the
-// kernel fills fresh outputs there, and those are copied back into the caller's outputs.
-void run_on(OpId op, const OpArgs& args, Device target, Device data_device) {
-    const Tensor& source = args.inputs.empty() ? args.outputs[0] : args.inputs[0];
-    Registry& registry = Registry::instance();
-    Backend& backend = registry.get(target);
-    const KernelFn kernel = registry.dispatcher().lookup({op, target.type, source.dtype()});
-    if (target == data_device) {
-        kernel(args, backend.stream(target.index));
-        return;
-    }
-    OpArgs moved = args;
-    for (Tensor& input : moved.inputs) {
-        input = input.to(target);
-    }
-    for (Tensor& output : moved.outputs) {
-        output = Tensor::empty(output.shape(), output.dtype(), target);
-    }
-    kernel(moved, backend.stream(target.index));
-    for (std::size_t i = 0; i < args.outputs.size(); ++i) {
-        Tensor destination = args.outputs[i]; // shares the caller's storage
-        destination.copy_from(moved.outputs[i].to(data_device));
-    }
-}
-
-} // namespace
 
 void dispatch(OpId op, const OpArgs& args, Execution execution) {
-    const bool factory = op == OpId::Uniform || op == OpId::Normal;
-    if (args.inputs.empty() && (!factory || args.outputs.empty())) {
-        throw std::invalid_argument(std::string(op_name(op)) + ": no input tensors");
+    const Device home = anchor_of(op, args).device();
+    require_single_device(op, args, home);
+    if (!tuning_active()) {
+        run_where(op, args, execution_device(execution, home), home);
+        return;
     }
-    const Tensor& source = args.inputs.empty() ? args.outputs[0] : args.inputs[0];
-    const Device data_device = source.device();
-    for (const auto* group : {&args.inputs, &args.outputs}) {
-        for (const Tensor& t : *group) {
-            if (t.device() != data_device) {
-                throw std::invalid_argument(std::string(op_name(op)) + ": tensors are on " +
-                                            to_string(data_device) + " and " +
-                                            to_string(t.device()) + "; move one with Tensor::to()");
-            }
-        }
-    }
-    run_on(op, args, execution_device(execution, data_device), data_device);
+    // A tuning scope may pick the device of an Auto call and the kernel's settings.
+    OpArgs tuned = args;
+    const Device target = apply_tuning(op, execution, home, tuned);
+    run_where(op, tuned, target, home);
 }
 
 bool has_kernel_for(OpId op, Execution execution, Device data_device) {
+    Device target;
     try {
-        const Device target = execution_device(execution, data_device);
-        return Registry::instance().dispatcher().find({op, target.type, DType::F32}) != nullptr;
+        target = execution_device(execution, data_device);
     } catch (const std::exception&) {
         return false;
     }
+    return Registry::instance().dispatcher().find({op, target.type, DType::F32}) != nullptr;
 }
 
 } // namespace mensurflow::detail

@@ -1,23 +1,44 @@
-// Backend discovery, the default-device policy, and Storage (the reference's
-// src/core/{registry,device_selection,storage}.cpp).
+// Backend discovery and the device-choice policy built on it (behaviour of mensurflow's
+// src/core/registry.cpp and src/core/device_selection.cpp, plus the ROCm backend).
 #include "core/registry.hpp"
 
-#include "core/storage.hpp"
-
+#include <algorithm>
 #include <cstdlib>
-#include <cstring>
 #include <exception>
 #include <stdexcept>
-#include <vector>
+#include <string>
 
 namespace mensurflow::detail {
 
+namespace {
+
+std::size_t slot_of(DeviceType type) { return static_cast<std::size_t>(type); }
+
+struct BackendHook {
+    void (*install)(Registry&);
+    bool optional; // a failure leaves the backend out instead of failing the process
+};
+
+// The CPU must come up. A GPU backend whose driver, runtime or device is missing throws or reports
+// zero devices; either way the library keeps running on the CPU.
+constexpr BackendHook kHooks[] = {
+    {register_cpu_backend, false},
+    {register_rocm_backend, true},
+};
+
+} // namespace
+
 Registry::Registry() {
-    register_cpu_backend(*this); // required: a failure here propagates
-    // A GPU backend whose runtime or device is missing is skipped, not fatal.
-    try {
-        register_rocm_backend(*this);
-    } catch (const std::exception&) {
+    for (const BackendHook& hook : kHooks) {
+        if (!hook.optional) {
+            hook.install(*this);
+            continue;
+        }
+        try {
+            hook.install(*this);
+        } catch (const std::exception&) {
+            // left out: find() reports it absent
+        }
     }
 }
 
@@ -27,74 +48,42 @@ Registry& Registry::instance() {
 }
 
 void Registry::add(std::unique_ptr<Backend> backend) {
-    if (backend->device_count() <= 0) {
+    if (backend->device_count() < 1) {
         return;
     }
+    const DeviceType type = backend->type();
+    std::unique_ptr<Backend>& slot = by_type_.at(slot_of(type));
+    if (slot != nullptr) {
+        throw std::logic_error(std::string("backend registered twice: ") + device_type_name(type));
+    }
     backend->register_kernels(dispatcher_);
-    backends_.push_back(std::move(backend));
+    slot = std::move(backend);
+    arrival_.push_back(type);
 }
 
 Backend* Registry::find(DeviceType type) const {
-    for (const auto& backend : backends_) {
-        if (backend->type() == type) {
-            return backend.get();
-        }
-    }
-    return nullptr;
+    const std::size_t slot = slot_of(type);
+    return slot < by_type_.size() ? by_type_[slot].get() : nullptr;
 }
 
 Backend& Registry::get(Device device) const {
-    Backend* backend = find(device.type);
-    if (backend == nullptr || device.index < 0 || device.index >= backend->device_count()) {
-        throw std::runtime_error("device " + to_string(device) + " is not available");
+    if (Backend* backend = find(device.type)) {
+        if (device.index >= 0 && device.index < backend->device_count()) {
+            return *backend;
+        }
     }
-    return *backend;
+    throw std::runtime_error("device " + to_string(device) + " is not available");
 }
 
 std::vector<Device> Registry::devices() const {
     std::vector<Device> out;
-    for (const auto& backend : backends_) {
-        for (int i = 0; i < backend->device_count(); ++i) {
-            out.push_back({backend->type(), i});
+    for (const DeviceType type : arrival_) {
+        const int count = find(type)->device_count();
+        for (int index = 0; index < count; ++index) {
+            out.push_back(Device{type, index});
         }
     }
     return out;
-}
-
-void Stream::copy_d2d(Buffer& dst, std::size_t dst_offset, const Buffer& src,
-                      std::size_t src_offset, std::size_t bytes) {
-    std::vector<std::byte> staged(bytes);
-    copy_d2h(staged.data(), src, src_offset, bytes);
-    copy_h2d(dst, dst_offset, staged.data(), bytes);
-}
-
-Storage::Storage(Device device, std::size_t nbytes)
-    : device(device), nbytes(nbytes), backend_(&Registry::instance().get(device)) {
-    buffer = backend_->allocate(device.index, nbytes);
-}
-
-std::byte* Storage::host_data() const { return static_cast<std::byte*>(buffer->host_ptr()); }
-
-Stream& Storage::stream() const { return backend_->stream(device.index); }
-
-void Storage::copy_from_host(std::size_t offset, const void* src, std::size_t bytes) {
-    if (bytes == 0) {
-        return;
-    }
-    if (offset > nbytes || bytes > nbytes - offset) {
-        throw std::out_of_range("Storage::copy_from_host: range exceeds the allocation");
-    }
-    stream().copy_h2d(*buffer, offset, src, bytes);
-}
-
-void Storage::copy_to_host(void* dst, std::size_t offset, std::size_t bytes) const {
-    if (bytes == 0) {
-        return;
-    }
-    if (offset > nbytes || bytes > nbytes - offset) {
-        throw std::out_of_range("Storage::copy_to_host: range exceeds the allocation");
-    }
-    stream().copy_d2h(dst, *buffer, offset, bytes);
 }
 
 } // namespace mensurflow::detail
@@ -104,29 +93,27 @@ namespace mensurflow {
 std::vector<Device> list_devices() { return detail::Registry::instance().devices(); }
 
 bool device_available(Device device) {
-    for (Device d : list_devices()) {
-        if (d == device) {
-            return true;
-        }
-    }
-    return false;
+    const std::vector<Device> usable = list_devices();
+    return std::find(usable.begin(), usable.end(), device) != usable.end();
 }
 
 Device default_device() {
-    if (const char* env = std::getenv("MENSURFLOW_DEVICE")) {
-        const Device wanted = parse_device(env);
-        if (!device_available(wanted)) {
-            throw std::runtime_error("MENSURFLOW_DEVICE=" + std::string(env) + " is not available");
+    if (const char* forced = std::getenv("MENSURFLOW_DEVICE")) {
+        const Device wanted = parse_device(forced);
+        if (device_available(wanted)) {
+            return wanted;
         }
-        return wanted;
+        throw std::runtime_error("MENSURFLOW_DEVICE=" + std::string(forced) + " is not available");
     }
-    for (DeviceType type :
-         {DeviceType::CUDA, DeviceType::Metal, DeviceType::ROCm, DeviceType::Vulkan}) {
-        if (device_available({type, 0})) {
-            return {type, 0};
+    // Accelerators before the CPU; ROCm sits with the vendor backends, before Vulkan.
+    constexpr DeviceType kPreference[] = {DeviceType::CUDA, DeviceType::Metal, DeviceType::ROCm,
+                                          DeviceType::Vulkan};
+    for (const DeviceType type : kPreference) {
+        if (device_available(Device{type, 0})) {
+            return Device{type, 0};
         }
     }
-    return {DeviceType::CPU, 0};
+    return Device{DeviceType::CPU, 0};
 }
 
 } // namespace mensurflow

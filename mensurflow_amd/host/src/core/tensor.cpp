@@ -1,6 +1,8 @@
-// Tensor creation, views and transfers (behaviour of the reference's src/core/tensor.cpp,
-// without autograd). Device-resident strided views are packed on the device when the backend
-// registers OpId::StridedCopy for the dtype; otherwise they are staged through host memory.
+// Tensor creation, views and transfers. The behaviour (checks, messages, results) is mensurflow's
+// src/core/tensor.cpp without autograd. The moves between memory and views are built on one
+// walker: every strided view is visited as runs of consecutive elements, which packing (host
+// gather), unpacking (host scatter) and the exact byte span a view reaches all share. Device
+// views are packed on the device when its backend registers OpId::StridedCopy for the dtype.
 #include "mensurflow/tensor.hpp"
 
 #include "core/dispatcher.hpp"
@@ -9,6 +11,7 @@
 #include "core/tensor_access.hpp"
 
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <cstring>
 #include <limits>
@@ -17,101 +20,137 @@ namespace mensurflow {
 
 namespace {
 
-void validate_fill_value(double value, DType dtype) {
-    if (!std::isfinite(value)) {
-        if (dtype != DType::F32) {
-            throw std::invalid_argument("full: non-finite values require f32 dtype");
-        }
-        return;
+// ---- fill values ---------------------------------------------------------------------------------
+
+// The bit pattern of `value` as one element of `dtype`, after the checks of mensurflow's Tensor::
+// full (a value the dtype cannot hold exactly is refused).
+struct Element {
+    std::array<std::byte, 8> bytes{};
+    std::size_t width = 0;
+};
+
+template <typename T> Element element_of(T value) {
+    Element e;
+    e.width = sizeof(T);
+    std::memcpy(e.bytes.data(), &value, sizeof(T));
+    return e;
+}
+
+bool whole_within(double value, double low, double high) {
+    return std::trunc(value) == value && value >= low && value <= high;
+}
+
+Element fill_element(double value, DType dtype) {
+    if (!std::isfinite(value) && dtype != DType::F32) {
+        throw std::invalid_argument("full: non-finite values require f32 dtype");
     }
-    auto whole_in = [&](double lo, double hi) {
-        return std::trunc(value) == value && value >= lo && value <= hi;
-    };
     switch (dtype) {
     case DType::F32:
-        if (std::fabs(value) > std::numeric_limits<float>::max()) {
+        if (std::isfinite(value) && std::fabs(value) > std::numeric_limits<float>::max()) {
             throw std::invalid_argument("full: value does not fit f32");
         }
-        return;
+        return element_of(static_cast<float>(value));
     case DType::I32:
-        if (!whole_in(std::numeric_limits<std::int32_t>::min(),
-                      std::numeric_limits<std::int32_t>::max())) {
+        if (!whole_within(value, std::numeric_limits<std::int32_t>::min(),
+                          std::numeric_limits<std::int32_t>::max())) {
             throw std::invalid_argument("full: value does not fit i32");
         }
-        return;
+        return element_of(static_cast<std::int32_t>(value));
     case DType::I64:
-        if (!whole_in(static_cast<double>(std::numeric_limits<std::int64_t>::min()),
-                      static_cast<double>(std::numeric_limits<std::int64_t>::max()))) {
+        if (!whole_within(value, static_cast<double>(std::numeric_limits<std::int64_t>::min()),
+                          static_cast<double>(std::numeric_limits<std::int64_t>::max()))) {
             throw std::invalid_argument("full: value does not fit i64");
         }
-        return;
+        return element_of(static_cast<std::int64_t>(value));
     case DType::U8:
-        if (!whole_in(0, 255)) {
+        if (!whole_within(value, 0.0, 255.0)) {
             throw std::invalid_argument("full: value does not fit u8");
         }
-        return;
+        return element_of(static_cast<std::uint8_t>(value));
     case DType::Bool:
-        return;
+        return element_of(static_cast<std::uint8_t>(value != 0.0 ? 1 : 0));
     case DType::F16:
     case DType::BF16:
-        throw std::invalid_argument("full: f16 and bf16 construction is not supported");
+        throw std::invalid_argument("full: f16 and bf16 construction is not supported yet");
     }
     throw std::invalid_argument("full: invalid dtype");
 }
 
-void write_fill(std::byte* data, std::size_t count, DType dtype, double value) {
-    switch (dtype) {
-    case DType::F32:
-        std::fill_n(reinterpret_cast<float*>(data), count, static_cast<float>(value));
+// `count` copies of `element`, back to back.
+std::vector<std::byte> repeated(const Element& element, std::size_t count) {
+    std::vector<std::byte> out(count * element.width);
+    for (std::size_t at = 0; at < out.size(); at += element.width) {
+        std::memcpy(out.data() + at, element.bytes.data(), element.width);
+    }
+    return out;
+}
+
+// ---- strided views ---------------------------------------------------------------------------------
+
+// Calls visit(first, length) for the elements of a (shape, strides) view in row-major order, as
+// runs of `length` consecutive elements starting `first` elements from the view's origin. The
+// innermost dimension forms one run when its stride is 1, else runs of one element.
+template <typename Visit>
+void walk(const Shape& shape, const Strides& strides, std::size_t d, std::int64_t base,
+          Visit& visit) {
+    const std::int64_t extent = shape[d];
+    if (d + 1 == shape.size()) {
+        if (strides[d] == 1) {
+            visit(base, extent);
+        } else {
+            for (std::int64_t i = 0; i < extent; ++i) {
+                visit(base + i * strides[d], std::int64_t{1});
+            }
+        }
         return;
-    case DType::I32:
-        std::fill_n(reinterpret_cast<std::int32_t*>(data), count, static_cast<std::int32_t>(value));
-        return;
-    case DType::I64:
-        std::fill_n(reinterpret_cast<std::int64_t*>(data), count, static_cast<std::int64_t>(value));
-        return;
-    case DType::U8:
-        std::fill_n(data, count, static_cast<std::byte>(static_cast<std::uint8_t>(value)));
-        return;
-    case DType::Bool:
-        std::fill_n(data, count, value == 0 ? std::byte{0} : std::byte{1});
-        return;
-    default:
-        throw std::invalid_argument("full: unsupported dtype");
+    }
+    for (std::int64_t i = 0; i < extent; ++i) {
+        walk(shape, strides, d + 1, base + i * strides[d], visit);
     }
 }
 
-// Row-major gather of a strided view from host-addressable memory: an odometer over the
-// indices, copying the last dimension as one run when its stride is 1.
-void gather(const std::byte* base, std::byte* out, const Shape& shape, const Strides& strides,
+template <typename Visit> void for_each_run(const Shape& shape, const Strides& strides, Visit visit) {
+    if (numel(shape) == 0) {
+        return;
+    }
+    if (shape.empty()) {
+        visit(std::int64_t{0}, std::int64_t{1}); // a 0-d view is one element
+        return;
+    }
+    walk(shape, strides, 0, 0, visit);
+}
+
+// Packs the view whose origin is `origin` into contiguous `packed`.
+void gather(const std::byte* origin, std::byte* packed, const Shape& shape, const Strides& strides,
             std::size_t item) {
-    const int nd = static_cast<int>(shape.size());
-    const std::int64_t count = numel(shape);
-    if (count == 0) {
-        return;
+    for_each_run(shape, strides, [&](std::int64_t first, std::int64_t length) {
+        const std::size_t bytes = static_cast<std::size_t>(length) * item;
+        std::memcpy(packed, origin + static_cast<std::ptrdiff_t>(first) * static_cast<std::ptrdiff_t>(item), bytes);
+        packed += bytes;
+    });
+}
+
+// The inverse: contiguous `packed` into the view whose origin is `origin`.
+void scatter(const std::byte* packed, std::byte* origin, const Shape& shape, const Strides& strides,
+             std::size_t item) {
+    for_each_run(shape, strides, [&](std::int64_t first, std::int64_t length) {
+        const std::size_t bytes = static_cast<std::size_t>(length) * item;
+        std::memcpy(origin + static_cast<std::ptrdiff_t>(first) * static_cast<std::ptrdiff_t>(item), packed, bytes);
+        packed += bytes;
+    });
+}
+
+// Elements from a view's origin to one past the furthest element it reaches (views made by this
+// class never have negative strides).
+std::int64_t reach(const Shape& shape, const Strides& strides) {
+    if (numel(shape) == 0) {
+        return 0;
     }
-    if (nd == 0) {
-        std::memcpy(out, base, item);
-        return;
+    std::int64_t last = 0;
+    for (std::size_t d = 0; d < shape.size(); ++d) {
+        last += (shape[d] - 1) * strides[d];
     }
-    const bool unit_rows = strides[nd - 1] == 1;
-    const std::int64_t run = unit_rows ? shape[nd - 1] : 1;
-    const int outer = unit_rows ? nd - 1 : nd;
-    std::vector<std::int64_t> index(static_cast<std::size_t>(nd), 0);
-    std::int64_t pos = 0;
-    for (std::int64_t done = 0; done < count; done += run) {
-        std::memcpy(out, base + pos * static_cast<std::int64_t>(item),
-                    static_cast<std::size_t>(run) * item);
-        out += static_cast<std::size_t>(run) * item;
-        for (int d = outer - 1; d >= 0; --d) {
-            if (++index[d] < shape[d]) {
-                pos += strides[d];
-                break;
-            }
-            pos -= (shape[d] - 1) * strides[d];
-            index[d] = 0;
-        }
-    }
+    return last + 1;
 }
 
 bool packs_on_device(Device device, DType dtype) {
@@ -122,6 +161,8 @@ bool packs_on_device(Device device, DType dtype) {
 
 } // namespace
 
+// ---- construction ---------------------------------------------------------------------------------
+
 Tensor::Tensor(std::shared_ptr<detail::Storage> storage, std::int64_t offset, Shape shape,
                Strides strides, DType dtype)
     : storage_(std::move(storage)), offset_(offset), shape_(std::move(shape)),
@@ -129,18 +170,16 @@ Tensor::Tensor(std::shared_ptr<detail::Storage> storage, std::int64_t offset, Sh
 
 Tensor Tensor::empty(Shape shape, DType dtype, Device device) {
     validate_shape(shape);
-    const auto bytes = static_cast<std::size_t>(mensurflow::numel(shape)) * dtype_size(dtype);
-    auto storage = std::make_shared<detail::Storage>(device, bytes);
+    const std::size_t bytes = static_cast<std::size_t>(mensurflow::numel(shape)) * dtype_size(dtype);
     Strides strides = contiguous_strides(shape);
-    return Tensor(std::move(storage), 0, std::move(shape), std::move(strides), dtype);
+    return Tensor(std::make_shared<detail::Storage>(device, bytes), 0, std::move(shape),
+                  std::move(strides), dtype);
 }
 
 Tensor Tensor::full(Shape shape, double value, DType dtype, Device device) {
     validate_shape(shape);
-    validate_fill_value(value, dtype);
-    const auto count = static_cast<std::size_t>(mensurflow::numel(shape));
-    std::vector<std::byte> host(count * dtype_size(dtype));
-    write_fill(host.data(), count, dtype, value);
+    const Element element = fill_element(value, dtype);
+    const auto host = repeated(element, static_cast<std::size_t>(mensurflow::numel(shape)));
     return from_host(host.data(), std::move(shape), dtype, device);
 }
 
@@ -150,8 +189,8 @@ Tensor Tensor::constant(Shape shape, double value, DType dtype, Device device) {
 
 Tensor Tensor::zeros(Shape shape, DType dtype, Device device) {
     validate_shape(shape);
-    std::vector<std::byte> host(static_cast<std::size_t>(mensurflow::numel(shape)) *
-                                dtype_size(dtype));
+    const std::vector<std::byte> host(static_cast<std::size_t>(mensurflow::numel(shape)) *
+                                      dtype_size(dtype));
     return from_host(host.data(), std::move(shape), dtype, device);
 }
 
@@ -163,13 +202,11 @@ Tensor Tensor::eye(std::int64_t n, DType dtype, Device device) {
     if (n < 0) {
         throw std::invalid_argument("eye: dimension must be non-negative");
     }
-    validate_fill_value(1.0, dtype);
-    const auto count = static_cast<std::size_t>(n) * static_cast<std::size_t>(n);
-    std::vector<std::byte> host(count * dtype_size(dtype));
-    write_fill(host.data(), count, dtype, 0.0);
+    const Element one = fill_element(1.0, dtype);
+    std::vector<std::byte> host(static_cast<std::size_t>(n * n) * one.width);
     for (std::int64_t i = 0; i < n; ++i) {
-        write_fill(host.data() + static_cast<std::size_t>(i * n + i) * dtype_size(dtype), 1, dtype,
-                   1.0);
+        std::memcpy(host.data() + static_cast<std::size_t>(i * (n + 1)) * one.width,
+                    one.bytes.data(), one.width);
     }
     return from_host(host.data(), {n, n}, dtype, device);
 }
@@ -188,25 +225,28 @@ Tensor Tensor::full_like(const Tensor& other, double value) {
 
 Tensor Tensor::from_host(const void* data, Shape shape, DType dtype, Device device) {
     Tensor out = empty(std::move(shape), dtype, device);
-    if (out.nbytes() > 0) {
-        if (data == nullptr) {
-            throw std::invalid_argument("from_host: data is null");
-        }
-        out.storage_->copy_from_host(0, data, out.nbytes());
+    if (out.nbytes() == 0) {
+        return out;
     }
+    if (data == nullptr) {
+        throw std::invalid_argument("from_host: data is null");
+    }
+    out.storage_->copy_from_host(0, data, out.nbytes());
     return out;
 }
 
+// ---- transfers ----------------------------------------------------------------------------------------
+
 Tensor Tensor::to(Device target) const {
     require_defined();
-    if (target == device()) {
+    if (device() == target) {
         return *this;
     }
     Tensor out = empty(shape_, dtype_, target);
     if (out.nbytes() > 0) {
-        std::vector<std::byte> host(out.nbytes());
-        copy_to_host(host.data());
-        out.storage_->copy_from_host(0, host.data(), host.size());
+        std::vector<std::byte> bounce(out.nbytes());
+        copy_to_host(bounce.data());
+        out.storage_->copy_from_host(0, bounce.data(), bounce.size());
     }
     return out;
 }
@@ -217,19 +257,42 @@ Tensor Tensor::contiguous() const {
         return *this;
     }
     Tensor out = empty(shape_, dtype_, device());
-    if (const std::byte* host = storage_->host_data()) {
-        gather(host + static_cast<std::size_t>(offset_) * itemsize(),
-               static_cast<std::byte*>(out.storage_->host_data()), shape_, strides_, itemsize());
-        return out;
-    }
-    if (packs_on_device(device(), dtype_)) {
+    if (std::byte* host = storage_->host_data()) {
+        gather(host + static_cast<std::size_t>(offset_) * itemsize(), out.storage_->host_data(),
+               shape_, strides_, itemsize());
+    } else if (packs_on_device(device(), dtype_)) {
         detail::dispatch(detail::OpId::StridedCopy, {{*this}, {out}}, Execution::GPU);
-        return out;
+    } else {
+        std::vector<std::byte> packed(out.nbytes());
+        copy_to_host(packed.data());
+        out.storage_->copy_from_host(0, packed.data(), packed.size());
     }
-    std::vector<std::byte> staged(out.nbytes());
-    copy_to_host(staged.data());
-    out.storage_->copy_from_host(0, staged.data(), staged.size());
     return out;
+}
+
+void Tensor::copy_to_host(void* dst) const {
+    require_defined();
+    if (nbytes() == 0) {
+        return;
+    }
+    if (dst == nullptr) {
+        throw std::invalid_argument("copy_to_host: dst is null");
+    }
+    const std::size_t item = itemsize();
+    const std::size_t origin = static_cast<std::size_t>(offset_) * item;
+    auto* out = static_cast<std::byte*>(dst);
+    if (is_contiguous()) {
+        storage_->copy_to_host(out, origin, nbytes());
+    } else if (const std::byte* host = storage_->host_data()) {
+        gather(host + origin, out, shape_, strides_, item);
+    } else if (packs_on_device(device(), dtype_)) {
+        contiguous().copy_to_host(out);
+    } else {
+        // Only the bytes the view reaches come over, then they are packed on the host.
+        std::vector<std::byte> span(static_cast<std::size_t>(reach(shape_, strides_)) * item);
+        storage_->copy_to_host(span.data(), origin, span.size());
+        gather(span.data(), out, shape_, strides_, item);
+    }
 }
 
 void Tensor::copy_from(const Tensor& source) {
@@ -244,163 +307,129 @@ void Tensor::copy_from(const Tensor& source) {
     }
     const Tensor packed = source.contiguous();
     const std::size_t item = itemsize();
+    const std::size_t origin = static_cast<std::size_t>(offset_) * item;
+    const std::size_t packed_origin = static_cast<std::size_t>(packed.offset_) * item;
+    std::byte* host = storage_->host_data();
     if (is_contiguous()) {
-        if (storage_->host_data() != nullptr) {
-            std::memmove(storage_->host_data() + static_cast<std::size_t>(offset_) * item,
-                         packed.storage_->host_data() +
-                             static_cast<std::size_t>(packed.offset_) * item,
-                         nbytes());
+        if (host != nullptr) {
+            std::memmove(host + origin, packed.storage_->host_data() + packed_origin, nbytes());
         } else {
-            storage_->stream().copy_d2d(*storage_->buffer,
-                                        static_cast<std::size_t>(offset_) * item,
-                                        *packed.storage_->buffer,
-                                        static_cast<std::size_t>(packed.offset_) * item, nbytes());
+            storage_->stream().copy_d2d(*storage_->buffer, origin, *packed.storage_->buffer,
+                                        packed_origin, nbytes());
         }
         return;
     }
-    // A strided destination: write element by element through host memory.
+    // A strided destination: its elements are unpacked into place. Device memory goes through
+    // host memory: the span the view reaches is read, updated and written back.
     std::vector<std::byte> values(packed.nbytes());
     packed.copy_to_host(values.data());
-    if (std::byte* host = storage_->host_data()) {
-        const Shape& shape = shape_;
-        std::vector<std::int64_t> index(shape.size(), 0);
-        for (std::int64_t i = 0; i < numel(); ++i) {
-            std::int64_t pos = offset_;
-            std::int64_t rest = i;
-            for (std::size_t d = shape.size(); d-- > 0;) {
-                pos += (rest % shape[d]) * strides_[d];
-                rest /= shape[d];
-            }
-            std::memcpy(host + pos * static_cast<std::int64_t>(item),
-                        values.data() + i * static_cast<std::int64_t>(item), item);
-        }
+    if (host != nullptr) {
+        scatter(values.data(), host + origin, shape_, strides_, item);
         return;
     }
-    throw std::invalid_argument("copy_from: a strided destination must be host memory");
+    std::vector<std::byte> span(static_cast<std::size_t>(reach(shape_, strides_)) * item);
+    storage_->copy_to_host(span.data(), origin, span.size());
+    scatter(values.data(), span.data(), shape_, strides_, item);
+    storage_->copy_from_host(origin, span.data(), span.size());
 }
 
-void Tensor::copy_to_host(void* dst) const {
-    require_defined();
-    if (nbytes() == 0) {
-        return;
-    }
-    if (dst == nullptr) {
-        throw std::invalid_argument("copy_to_host: dst is null");
-    }
-    const std::size_t item = itemsize();
-    const std::size_t byte_offset = static_cast<std::size_t>(offset_) * item;
-    if (is_contiguous()) {
-        storage_->copy_to_host(dst, byte_offset, nbytes());
-        return;
-    }
-    if (const std::byte* host = storage_->host_data()) {
-        gather(host + byte_offset, static_cast<std::byte*>(dst), shape_, strides_, item);
-        return;
-    }
-    if (packs_on_device(device(), dtype_)) {
-        contiguous().copy_to_host(dst);
-        return;
-    }
-    // Stage the allocation from the view's offset onward, then gather on the host.
-    std::vector<std::byte> staged(storage_->nbytes - byte_offset);
-    storage_->copy_to_host(staged.data(), byte_offset, staged.size());
-    gather(staged.data(), static_cast<std::byte*>(dst), shape_, strides_, item);
-}
+// ---- views ----------------------------------------------------------------------------------------------
 
-Tensor Tensor::make_view(std::int64_t offset, Shape shape, Strides strides) const {
+Tensor Tensor::reshaped(std::int64_t offset, Shape shape, Strides strides) const {
     return Tensor(storage_, offset, std::move(shape), std::move(strides), dtype_);
 }
 
 Tensor Tensor::transpose(int d0, int d1) const {
-    const int a = normalize_dim(d0, dim());
-    const int b = normalize_dim(d1, dim());
+    const auto a = static_cast<std::size_t>(normalize_dim(d0, dim()));
+    const auto b = static_cast<std::size_t>(normalize_dim(d1, dim()));
     Shape shape = shape_;
     Strides strides = strides_;
     std::swap(shape[a], shape[b]);
     std::swap(strides[a], strides[b]);
-    return make_view(offset_, std::move(shape), std::move(strides));
+    return reshaped(offset_, std::move(shape), std::move(strides));
 }
 
 Tensor Tensor::permute(const std::vector<int>& order) const {
-    if (order.size() != static_cast<std::size_t>(dim())) {
-        throw std::invalid_argument("permute: expected " + std::to_string(dim()) +
+    const int rank = dim();
+    if (order.size() != static_cast<std::size_t>(rank)) {
+        throw std::invalid_argument("permute: expected " + std::to_string(rank) +
                                     " dimensions, got " + std::to_string(order.size()));
     }
-    std::vector<bool> used(order.size(), false);
-    Shape shape;
-    Strides strides;
-    for (int value : order) {
-        int axis = 0;
-        try {
-            axis = normalize_dim(value, dim());
-        } catch (const std::out_of_range&) {
-            throw std::invalid_argument("permute: dimension " + std::to_string(value) +
-                                        " is out of range");
+    Shape shape(order.size());
+    Strides strides(order.size());
+    std::vector<char> taken(order.size(), 0);
+    for (std::size_t slot = 0; slot < order.size(); ++slot) {
+        const int wanted = order[slot];
+        const int source = wanted < 0 ? wanted + rank : wanted;
+        if (source < 0 || source >= rank) {
+            throw std::invalid_argument("permute: dimension " + std::to_string(wanted) +
+                                        " is out of range for a " + std::to_string(rank) +
+                                        "-d tensor");
         }
-        if (used[static_cast<std::size_t>(axis)]) {
-            throw std::invalid_argument("permute: dimension " + std::to_string(value) +
+        if (taken[static_cast<std::size_t>(source)]++ != 0) {
+            throw std::invalid_argument("permute: dimension " + std::to_string(wanted) +
                                         " appears more than once");
         }
-        used[static_cast<std::size_t>(axis)] = true;
-        shape.push_back(shape_[static_cast<std::size_t>(axis)]);
-        strides.push_back(strides_[static_cast<std::size_t>(axis)]);
+        shape[slot] = shape_[static_cast<std::size_t>(source)];
+        strides[slot] = strides_[static_cast<std::size_t>(source)];
     }
-    return make_view(offset_, std::move(shape), std::move(strides));
+    return reshaped(offset_, std::move(shape), std::move(strides));
 }
 
 Tensor Tensor::slice(int d, std::int64_t start, std::int64_t end, std::int64_t step) const {
-    const int axis = normalize_dim(d, dim());
+    const auto axis = static_cast<std::size_t>(normalize_dim(d, dim()));
     if (step < 1) {
         throw std::invalid_argument("slice: step must be >= 1");
     }
+    // Python's rules: a negative bound counts from the end, then both are clamped to [0, n].
     const std::int64_t n = shape_[axis];
-    auto clamp = [n](std::int64_t i) { return std::clamp(i < 0 ? i + n : i, std::int64_t{0}, n); };
-    start = clamp(start);
-    end = std::max(clamp(end), start);
+    const auto bound = [n](std::int64_t i) { return std::min(std::max(i < 0 ? i + n : i, std::int64_t{0}), n); };
+    const std::int64_t first = bound(start);
+    const std::int64_t stop = std::max(bound(end), first);
     Shape shape = shape_;
     Strides strides = strides_;
-    shape[axis] = (end - start + step - 1) / step;
-    strides[axis] *= step;
-    return make_view(offset_ + start * strides_[axis], std::move(shape), std::move(strides));
+    shape[axis] = (stop - first + step - 1) / step;
+    strides[axis] = strides_[axis] * step;
+    return reshaped(offset_ + first * strides_[axis], std::move(shape), std::move(strides));
 }
 
 Tensor Tensor::expand(const Shape& shape) const {
     validate_shape(shape);
-    Strides strides = broadcast_strides(this->shape(), strides_, shape);
-    return make_view(offset_, shape, std::move(strides));
+    return reshaped(offset_, shape, broadcast_strides(this->shape(), strides_, shape));
 }
 
 Tensor Tensor::unsqueeze(int d) const {
-    const int axis = normalize_dim(d, dim() + 1);
+    // The new extent-1 dimension may also follow the last one: dim() + 1 positions.
+    const int at = normalize_dim(d, dim() + 1);
     Shape shape = shape_;
     Strides strides = strides_;
-    const std::int64_t stride = axis < dim() ? shape_[axis] * strides_[axis] : 1;
-    shape.insert(shape.begin() + axis, 1);
-    strides.insert(strides.begin() + axis, stride);
-    return make_view(offset_, std::move(shape), std::move(strides));
+    // Never stepped along; give it the stride a packed tensor would have there.
+    const std::int64_t stride = at < dim() ? shape_[static_cast<std::size_t>(at)] *
+                                                 strides_[static_cast<std::size_t>(at)]
+                                           : 1;
+    shape.insert(shape.begin() + at, 1);
+    strides.insert(strides.begin() + at, stride);
+    return reshaped(offset_, std::move(shape), std::move(strides));
 }
 
 Tensor Tensor::view(Shape shape) const {
     if (!is_contiguous()) {
         throw std::invalid_argument("view: tensor is not contiguous");
     }
-    auto inferred = shape.end();
-    std::int64_t known = 1;
-    for (auto it = shape.begin(); it != shape.end(); ++it) {
-        if (*it == -1) {
-            if (inferred != shape.end()) {
-                throw std::invalid_argument("view: only one dimension can be -1");
-            }
-            inferred = it;
-        } else {
-            known *= *it;
-        }
+    const auto holes = std::count(shape.begin(), shape.end(), std::int64_t{-1});
+    if (holes > 1) {
+        throw std::invalid_argument("view: only one dimension can be -1");
     }
-    if (inferred != shape.end()) {
-        if (known == 0 || numel() % known != 0) {
-            throw std::invalid_argument("view: cannot infer -1 in " + to_string(shape));
+    if (holes == 1) {
+        std::int64_t known = 1;
+        for (const std::int64_t extent : shape) {
+            known *= extent == -1 ? 1 : extent;
         }
-        *inferred = numel() / known;
+        if (known == 0 || numel() % known != 0) {
+            throw std::invalid_argument("view: cannot infer -1 in " + to_string(shape) + " for " +
+                                        std::to_string(numel()) + " elements");
+        }
+        *std::find(shape.begin(), shape.end(), std::int64_t{-1}) = numel() / known;
     }
     validate_shape(shape);
     if (mensurflow::numel(shape) != numel()) {
@@ -408,15 +437,17 @@ Tensor Tensor::view(Shape shape) const {
                                     std::to_string(numel()) + " elements");
     }
     Strides strides = contiguous_strides(shape);
-    return make_view(offset_, std::move(shape), std::move(strides));
+    return reshaped(offset_, std::move(shape), std::move(strides));
 }
+
+// ---- metadata -------------------------------------------------------------------------------------------
 
 bool Tensor::shares_storage(const Tensor& other) const {
     return defined() && storage_ == other.storage_;
 }
 
 void Tensor::require_defined() const {
-    if (!defined()) {
+    if (storage_ == nullptr) {
         throw std::logic_error("operation on an undefined Tensor");
     }
 }

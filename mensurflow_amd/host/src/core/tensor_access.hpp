@@ -1,4 +1,7 @@
-// Kernel-side access to a Tensor's buffer (the reference's src/core/tensor_access.hpp).
+// Backend-side access to a Tensor's memory, outside Tensor's public surface (the helper
+// mensurflow's core gives kernels, src/core/tensor_access.hpp). `data<T>` is the element address
+// for backends whose Buffer::native() is a plain address; T is the element type, so the offset
+// is counted in sizeof(T) steps.
 #pragma once
 
 #include "core/storage.hpp"
@@ -10,10 +13,10 @@ struct TensorAccess {
     static Buffer& buffer(const Tensor& t) { return *t.storage_->buffer; }
     static Storage& storage(const Tensor& t) { return *t.storage_; }
 
-    // Address of the tensor's first element, for backends whose native() is an address.
     template <typename T> static T* data(const Tensor& t) {
-        auto* base = static_cast<std::byte*>(buffer(t).native());
-        return reinterpret_cast<T*>(base + static_cast<std::size_t>(t.offset()) * t.itemsize());
+        std::byte* const first = static_cast<std::byte*>(buffer(t).native()) +
+                                 static_cast<std::size_t>(t.offset()) * sizeof(T);
+        return reinterpret_cast<T*>(first);
     }
 };
 

@@ -1,0 +1,349 @@
+// Algorithm and Tuner: record an algorithm's calls, measure each one's device choice and kernel
+// settings, store the winners (public side: include/mensurflow/tuning.hpp).
+#include "mensurflow/tuning.hpp"
+
+#include "core/registry.hpp"
+#include "core/tuning.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <functional>
+#include <iostream>
+#include <limits>
+#include <sstream>
+#include <stdexcept>
+
+namespace mensurflow {
+
+namespace {
+
+using detail::KernelFn;
+using detail::OpArgs;
+using detail::RecordedCall;
+using detail::Registry;
+using detail::TunableKernel;
+using detail::TuningConfig;
+using detail::TuningEntry;
+
+using Clock = std::chrono::steady_clock;
+
+// The call's arguments with its inputs on `device` and fresh outputs there, so measuring never
+// writes the algorithm's own tensors.
+OpArgs staged_on(const OpArgs& args, Device device) {
+    OpArgs copy = args;
+    for (Tensor& input : copy.inputs) {
+        input = input.device() == device ? input : input.to(device);
+    }
+    for (Tensor& output : copy.outputs) {
+        output = Tensor::empty(output.shape(), output.dtype(), device);
+    }
+    return copy;
+}
+
+std::vector<std::vector<float>> host_outputs(const OpArgs& args) {
+    std::vector<std::vector<float>> values;
+    for (const Tensor& out : args.outputs) {
+        values.push_back(out.dtype() == DType::F32 ? out.to_vector<float>() : std::vector<float>{});
+    }
+    return values;
+}
+
+// Each output element within 1e-3 of the default output's largest magnitude (tiles sum in
+// different orders), NaN where the default has NaN.
+bool agrees(const std::vector<std::vector<float>>& want,
+            const std::vector<std::vector<float>>& got) {
+    if (want.size() != got.size()) {
+        return false;
+    }
+    for (std::size_t o = 0; o < want.size(); ++o) {
+        if (want[o].size() != got[o].size()) {
+            return false;
+        }
+        double largest = 0.0;
+        for (const float v : want[o]) {
+            largest = std::max(largest, std::fabs(static_cast<double>(v)));
+        }
+        const double slack = 1e-3 * largest + 1e-6;
+        for (std::size_t i = 0; i < want[o].size(); ++i) {
+            const double w = want[o][i], g = got[o][i];
+            const bool both_nan = std::isnan(w) && std::isnan(g);
+            if (!both_nan && !(std::fabs(g - w) <= slack)) {
+                return false;
+            }
+        }
+    }
+    return true;
+}
+
+// Median milliseconds of `run`, which waits for its own work. Each sample repeats the call until
+// it lasts about a millisecond.
+double median_ms(const std::function<void()>& run, const TuneOptions& options) {
+    run(); // warm-up
+    const auto probe = Clock::now();
+    run();
+    const double once = std::max(std::chrono::duration<double>(Clock::now() - probe).count(), 1e-7);
+    const int repeats = std::max(1, static_cast<int>(1e-3 / once));
+    std::vector<double> samples;
+    const auto start = Clock::now();
+    while (static_cast<int>(samples.size()) < options.min_samples ||
+           std::chrono::duration<double>(Clock::now() - start).count() < options.min_time_s) {
+        const auto t0 = Clock::now();
+        for (int i = 0; i < repeats; ++i) {
+            run();
+        }
+        samples.push_back(std::chrono::duration<double>(Clock::now() - t0).count() / repeats);
+        if (samples.size() >= 500) {
+            break;
+        }
+    }
+    std::nth_element(samples.begin(), samples.begin() + static_cast<std::ptrdiff_t>(samples.size() / 2),
+                     samples.end());
+    return samples[samples.size() / 2] * 1e3;
+}
+
+// Every point of `region` (the product of its axes, the last axis fastest) that the kernel allows
+// for this call.
+std::vector<TuningConfig> points_of(const TunableKernel& tunable, const detail::SearchRegion& region,
+                                    const OpArgs& args) {
+    std::vector<TuningConfig> points;
+    for (const detail::SearchAxis& axis : region.axes) {
+        if (axis.values.empty()) {
+            return points;
+        }
+    }
+    std::vector<std::size_t> at(region.axes.size(), 0);
+    for (;;) {
+        TuningConfig point = region.start;
+        for (std::size_t a = 0; a < region.axes.size(); ++a) {
+            point.values[static_cast<std::size_t>(region.axes[a].param)] = region.axes[a].values[at[a]];
+        }
+        if (tunable.allowed(args, point)) {
+            points.push_back(point);
+        }
+        std::size_t a = region.axes.size();
+        while (a > 0) {
+            --a;
+            if (++at[a] < region.axes[a].values.size()) {
+                break;
+            }
+            at[a] = 0;
+            if (a == 0) {
+                return points;
+            }
+        }
+        if (region.axes.empty()) {
+            return points;
+        }
+    }
+}
+
+} // namespace
+
+Algorithm::Algorithm(Function function) : function_(std::move(function)) {
+    if (!function_) {
+        throw std::invalid_argument("Algorithm: empty function");
+    }
+}
+
+std::vector<Tensor> Algorithm::run(const std::vector<Tensor>& inputs) const {
+    return function_(inputs);
+}
+
+std::vector<Tensor> Algorithm::run(const std::vector<Tensor>& inputs, const Tuner& tuner) const {
+    const detail::TuningScope scope({tuner.cache_.get(), nullptr});
+    return function_(inputs);
+}
+
+Tuner::Tuner(std::string path)
+    : path_(std::move(path)), cache_(std::make_shared<detail::TuningCache>()) {
+    cache_->load(path_);
+}
+
+void Tuner::save() const { cache_->save(path_); }
+
+std::size_t Tuner::size() const {
+    const std::string& here = detail::machine_name();
+    return static_cast<std::size_t>(std::count_if(
+        cache_->entries().begin(), cache_->entries().end(),
+        [&](const TuningEntry& e) { return e.machine == here; }));
+}
+
+std::string Tuner::describe() const {
+    detail::TuningCache here;
+    for (const TuningEntry& e : cache_->entries()) {
+        if (e.machine == detail::machine_name()) {
+            here.store(e);
+        }
+    }
+    std::ostringstream text;
+    here.write(text);
+    return text.str();
+}
+
+TuneReport Tuner::tune(const Algorithm& algorithm, const std::vector<Tensor>& inputs,
+                       const TuneOptions& options) {
+    Registry& registry = Registry::instance();
+    const std::string& machine = detail::machine_name();
+    TuneReport report;
+
+    // 1. The calls the algorithm makes, seen with nothing applied.
+    std::vector<RecordedCall> calls;
+    {
+        const detail::TuningScope scope({nullptr, &calls});
+        algorithm.run(inputs);
+    }
+
+    const auto store = [&](TunedCall result, const std::string& op, const std::string& device,
+                           int version) {
+        TuningEntry entry;
+        entry.machine = machine;
+        entry.op = op;
+        entry.device = device;
+        entry.version = version;
+        entry.key = result.key;
+        entry.config = result.best_settings;
+        entry.best_ms = result.best_ms;
+        entry.default_ms = result.default_ms;
+        entry.mode = "tested";
+        cache_->store(entry);
+        if (options.verbose) {
+            std::cout << "  " << result.op << " on " << result.device << " " << result.key << ": "
+                      << to_string(result.best_settings) << " " << result.best_ms
+                      << " ms (default " << result.default_ms << " ms)\n";
+        }
+        report.calls.push_back(std::move(result));
+    };
+    const auto stored = [&](TunedCall& result, const std::string& op, const std::string& device,
+                            int version) {
+        const TuningEntry* held = cache_->find(machine, op, device, version, result.key);
+        if (held == nullptr || options.retune) {
+            return false;
+        }
+        result.reused = true;
+        result.best_settings = held->config;
+        result.best_ms = held->best_ms;
+        result.default_ms = held->default_ms;
+        report.calls.push_back(result);
+        return true;
+    };
+
+    for (const RecordedCall& call : calls) {
+        const detail::OpId op = call.op;
+        const DType dtype = (call.args.inputs.empty() ? call.args.outputs.at(0)
+                                                      : call.args.inputs[0]).dtype();
+        Device target = call.device;
+
+        // 2. The device of an Auto call: the CPU (the default) against every GPU with a kernel,
+        //    each timed with its copies in and out.
+        if (call.execution == Execution::Auto && !call.args.inputs.empty()) {
+            TunedCall result;
+            result.op = detail::op_name(op);
+            result.device = detail::kAutoDevice;
+            result.key = detail::placement_key(call.args, call.data_device);
+            result.default_settings = {{"gpu", 0}};
+            if (!stored(result, result.op, detail::kAutoDevice, 1)) {
+                double best = std::numeric_limits<double>::infinity();
+                for (const Device device : registry.devices()) {
+                    if (device.index != 0 ||
+                        registry.dispatcher().find({op, device.type, dtype}) == nullptr) {
+                        continue;
+                    }
+                    const KernelFn kernel = registry.dispatcher().find({op, device.type, dtype});
+                    detail::Stream& stream = registry.get(device).stream(device.index);
+                    const double ms = median_ms(
+                        [&] {
+                            OpArgs moved = staged_on(call.args, device);
+                            kernel(moved, stream);
+                            for (Tensor& out : moved.outputs) {
+                                out = out.to(call.data_device);
+                            }
+                            if (!moved.outputs.empty()) {
+                                (void)host_outputs(moved);
+                            }
+                        },
+                        options);
+                    ++result.space_size;
+                    if (device.type == DeviceType::CPU) {
+                        result.default_ms = ms;
+                    }
+                    if (ms < best) {
+                        best = ms;
+                        result.best_ms = ms;
+                        result.best_settings = {{"gpu", device.type == DeviceType::CPU ? 0 : 1}};
+                        target = device;
+                    }
+                }
+                if (result.space_size > 0) {
+                    store(result, result.op, detail::kAutoDevice, 1);
+                }
+            } else {
+                for (const auto& [name, value] : result.best_settings) {
+                    if (name == "gpu") {
+                        target = detail::execution_device(value != 0 ? Execution::GPU
+                                                                     : Execution::CPU,
+                                                          call.data_device);
+                    }
+                }
+            }
+        }
+
+        // 3. The settings of the kernel on the device the call runs on.
+        const TunableKernel* tunable = registry.dispatcher().tunable({op, target.type, dtype});
+        if (tunable == nullptr) {
+            continue;
+        }
+        const OpArgs base = staged_on(call.args, target);
+        TunedCall result;
+        result.op = tunable->name;
+        result.device = to_string(target);
+        result.key = detail::call_key(*tunable, base, target);
+        result.default_settings = detail::from_config(*tunable, tunable->defaults());
+        if (stored(result, tunable->name, device_type_name(target.type), tunable->version)) {
+            continue;
+        }
+        const KernelFn kernel = registry.dispatcher().lookup({op, target.type, dtype});
+        detail::Stream& stream = registry.get(target).stream(target.index);
+        const auto timed = [&](const TuningConfig& config, std::vector<std::vector<float>>* out) {
+            OpArgs args = staged_on(base, target);
+            args.tuning = config;
+            kernel(args, stream);
+            if (out != nullptr) {
+                *out = host_outputs(args);
+            }
+            return median_ms(
+                [&] {
+                    kernel(args, stream);
+                    stream.synchronize();
+                },
+                options);
+        };
+        std::vector<std::vector<float>> reference;
+        result.default_ms = timed(tunable->defaults(), &reference);
+        result.best_ms = result.default_ms;
+        result.best_settings = result.default_settings;
+        for (const detail::SearchRegion& region : tunable->space(base)) {
+            for (const TuningConfig& point : points_of(*tunable, region, base)) {
+                std::vector<std::vector<float>> outputs;
+                double ms = std::numeric_limits<double>::infinity();
+                try {
+                    ms = timed(point, &outputs);
+                } catch (const std::exception&) {
+                    continue; // a point the kernel refuses at run time
+                }
+                ++result.space_size;
+                if (ms < result.best_ms && agrees(reference, outputs)) {
+                    result.best_ms = ms;
+                    result.best_settings = detail::from_config(*tunable, point);
+                }
+            }
+        }
+        store(result, tunable->name, device_type_name(target.type), tunable->version);
+    }
+    if (options.save) {
+        save();
+    }
+    return report;
+}
+
+} // namespace mensurflow

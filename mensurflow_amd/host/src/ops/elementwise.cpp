@@ -1,111 +1,101 @@
-// Elementwise ops of the hot path: validation, broadcasting by packing, dispatch (the
-// reference's src/ops/elementwise.cpp:18,158,251,307,454 for unary_op, binary_op, bias_add,
-// gelu and where).
+// Elementwise ops of the hot path: add and mul (used by gemm's unfused composition), bias_add,
+// gelu and where. Checks, messages and broadcasting rules are mensurflow's
+// (src/ops/elementwise.cpp:18,140-201,251-309,454-481). Operands that broadcast, or are not
+// packed, become packed tensors of the output's shape before the kernel sees them, except where a
+// device's where kernel reads broadcast views itself (ROCm), which saves materializing them.
 #include "mensurflow/ops/elementwise.hpp"
 
 #include "core/dispatcher.hpp"
+#include "ops/checks.hpp"
 
-#include <stdexcept>
 #include <string>
 
 namespace mensurflow {
 
 namespace {
 
-void require_compatible(const Tensor& a, const Tensor& b, const std::string& op) {
-    if (!a.defined() || !b.defined()) {
-        throw std::invalid_argument(op + ": undefined tensor");
-    }
-    if (a.dtype() != b.dtype()) {
-        throw std::invalid_argument(op + ": dtypes differ (" + dtype_name(a.dtype()) + " and " +
-                                    dtype_name(b.dtype()) + ")");
-    }
-    if (a.device() != b.device()) {
-        throw std::invalid_argument(op + ": tensors are on " + to_string(a.device()) + " and " +
-                                    to_string(b.device()) + "; move one with Tensor::to()");
-    }
-}
+using detail::OpArgs;
+using detail::OpCheck;
+using detail::OpId;
 
-// An input smaller than the output, or not packed, becomes a contiguous tensor of `shape`.
-Tensor packed(const Tensor& t, const Shape& shape) {
+// `t` as a packed tensor of `shape` (itself when it already is one).
+Tensor packed_as(const Tensor& t, const Shape& shape) {
     return t.shape() == shape && t.is_contiguous() ? t : t.expand(shape).contiguous();
 }
 
-Tensor binary_op(detail::OpId op, const Tensor& a, const Tensor& b, Execution execution) {
-    const std::string name = detail::op_name(op);
-    require_compatible(a, b, name);
-    Shape shape;
-    try {
-        shape = broadcast_shapes(a.shape(), b.shape());
-    } catch (const std::invalid_argument& e) {
-        throw std::invalid_argument(name + ": " + e.what());
-    }
+Tensor pairwise(OpId op, const Tensor& a, const Tensor& b, Execution execution) {
+    const OpCheck check(detail::op_name(op));
+    check.compatible(a, b);
+    const Shape shape = detail::broadcast_for(check, a.shape(), b.shape());
     Tensor out = Tensor::empty(shape, a.dtype(), a.device());
-    if (numel(shape) == 0) {
-        return out;
+    if (out.numel() > 0) {
+        detail::dispatch(op, {{packed_as(a, shape), packed_as(b, shape)}, {out}}, execution);
     }
-    detail::dispatch(op, {{packed(a, shape), packed(b, shape)}, {out}}, execution);
     return out;
 }
+
+// Devices whose where kernel reads its operands through strides (stride 0 for a broadcast
+// dimension), so broadcast operands need no packed copy.
+bool where_reads_views(Device device) { return device.type == DeviceType::ROCm; }
 
 } // namespace
 
 Tensor add(const Tensor& a, const Tensor& b, Execution execution) {
-    return binary_op(detail::OpId::Add, a, b, execution);
+    return pairwise(OpId::Add, a, b, execution);
 }
 
 Tensor mul(const Tensor& a, const Tensor& b, Execution execution) {
-    return binary_op(detail::OpId::Mul, a, b, execution);
+    return pairwise(OpId::Mul, a, b, execution);
 }
 
 Tensor bias_add(const Tensor& x, const Tensor& bias, Execution execution) {
-    require_compatible(x, bias, "bias_add");
+    const OpCheck check("bias_add");
+    check.compatible(x, bias);
     if (x.dim() != 2 || bias.dim() != 1) {
-        throw std::invalid_argument("bias_add: expected [batch, features] and [features], got " +
-                                    to_string(x.shape()) + " and " + to_string(bias.shape()));
+        check.fail("expected [batch, features] and [features], got " + to_string(x.shape()) +
+                   " and " + to_string(bias.shape()));
     }
     if (x.size(1) != bias.size(0)) {
-        throw std::invalid_argument("bias_add: bias length must match the matrix's feature count");
+        check.fail("bias length must match the matrix's feature count");
     }
     Tensor out = Tensor::empty(x.shape(), x.dtype(), x.device());
-    detail::dispatch(detail::OpId::BiasAdd, {{x.contiguous(), bias.contiguous()}, {out}},
-                     execution);
+    detail::dispatch(OpId::BiasAdd, {{x.contiguous(), bias.contiguous()}, {out}}, execution);
     return out;
 }
 
 Tensor gelu(const Tensor& x, bool approximate, Execution execution) {
     if (!x.defined()) {
-        throw std::invalid_argument("gelu: undefined tensor");
+        OpCheck("gelu").fail("undefined tensor");
     }
     Tensor out = Tensor::empty(x.shape(), x.dtype(), x.device());
-    detail::OpArgs args{{x.contiguous()}, {out}};
+    OpArgs args{{x.contiguous()}, {out}};
     args.approximate = approximate;
-    detail::dispatch(detail::OpId::Gelu, args, execution);
+    detail::dispatch(OpId::Gelu, args, execution);
     return out;
 }
 
 Tensor where(const Tensor& condition, const Tensor& x, const Tensor& y, Execution execution) {
-    require_compatible(x, y, "where");
+    const OpCheck check("where");
+    check.compatible(x, y);
     if (!condition.defined()) {
-        throw std::invalid_argument("where: undefined condition tensor");
+        check.fail("undefined condition tensor");
     }
     if (condition.dtype() != DType::Bool) {
-        throw std::invalid_argument("where: condition must have Bool dtype");
+        check.fail("condition must have Bool dtype");
     }
     if (condition.device() != x.device()) {
-        throw std::invalid_argument("where: condition and values must be on the same device");
+        check.fail("condition and values must be on the same device");
     }
-    Shape shape;
-    try {
-        shape = broadcast_shapes(broadcast_shapes(x.shape(), y.shape()), condition.shape());
-    } catch (const std::invalid_argument& e) {
-        throw std::invalid_argument(std::string("where: ") + e.what());
-    }
+    const Shape shape = detail::broadcast_for(
+        check, detail::broadcast_for(check, x.shape(), y.shape()), condition.shape());
     Tensor out = Tensor::empty(shape, x.dtype(), x.device());
-    // Values first, so the dispatch key is the values' dtype.
-    detail::dispatch(detail::OpId::Where,
-                     {{packed(x, shape), packed(y, shape), packed(condition, shape)}, {out}},
-                     execution);
+    const bool as_views =
+        where_reads_views(x.device()) && detail::has_kernel_for(OpId::Where, execution, x.device());
+    const auto operand = [&](const Tensor& t) {
+        return as_views ? t.expand(shape) : packed_as(t, shape);
+    };
+    // The values come first: the kernel is keyed by their dtype, not the condition's.
+    detail::dispatch(OpId::Where, {{operand(x), operand(y), operand(condition)}, {out}}, execution);
     return out;
 }
 

@@ -6,11 +6,18 @@
 // rocm device there is nothing registered to check.
 #include "core/dispatcher.hpp"
 #include "core/registry.hpp"
+#include "core/tuning.hpp"
+#include "mensurflow/mensurflow.hpp"
+#include "mensurflow/tuning.hpp"
 #include "oracle_cpu.hpp"
 #include "test_util.hpp"
 
 #include "mfr_rocm.h"
 
+#include <cstdio>
+#include <cstdlib>
+#include <fstream>
+#include <sstream>
 #include <string>
 #include <vector>
 
@@ -213,11 +220,179 @@ void test_start_is_the_automatic_choice(Device device) {
     test::require(t.space(empty).empty(), "an empty product has no space");
 }
 
+// ---- tuned placement: the results file and dispatch()'s hook ------------------------------------
+
+std::string results_path(const char* name) {
+    if (const char* dir = std::getenv("MFR_TUNING_DIR")) {
+        return std::string(dir) + "/" + name;
+    }
+    return std::string("/tmp/") + name;
+}
+
+void test_results_file_round_trip() {
+    TuningCache cache;
+    TuningEntry kernel{"Some CPU | gfx950", "matmul", "rocm", 2, "m=300 n=200 k=500",
+                       {{"tile", 5}, {"stage", 1}, {"splits", 2}}, 0.0123, 0.0456, "tested"};
+    TuningEntry place{"Some CPU | gfx950", "matmul", "auto", 1, "data=cpu f32 300x500 500x200",
+                      {{"gpu", 1}}, 0.5, 12.25, "tested"};
+    cache.store(kernel);
+    cache.store(place);
+    const std::string path = results_path("mfr_tuning_round_trip.txt");
+    cache.save(path);
+    TuningCache back;
+    back.load(path);
+    test::require(back.entries().size() == 2, "two results read back");
+    const TuningEntry* k = back.find(kernel.machine, "matmul", "rocm", 2, kernel.key);
+    test::require(k != nullptr && k->config == kernel.config && k->mode == "tested" &&
+                      std::abs(k->best_ms - 0.0123) < 1e-9,
+                  "the kernel line reads back");
+    test::require(back.find(kernel.machine, "matmul", "rocm", 1, kernel.key) == nullptr,
+                  "another version does not match");
+    test::require(back.find(place.machine, "matmul", "auto", 1, place.key) != nullptr,
+                  "the device-choice line reads back");
+    // The reference's own line shape, written by hand (extra spaces are allowed in the key).
+    {
+        std::ofstream out(path);
+        out << "# mensurflow tuning results\n\nmachine A | B\n"
+            << "matmul  metal v1  m=64   n=256 k=784 -> kernel=1 bm=32 | 0.0410 ms (default "
+               "0.0470 ms) tested\n";
+    }
+    back.load(path);
+    test::require(back.entries().size() == 1 && back.entries()[0].key == "m=64 n=256 k=784" &&
+                      back.entries()[0].device == "metal",
+                  "a hand-written line is read");
+    {
+        std::ofstream out(path);
+        out << "machine A\nmatmul rocm v2 m=1 -> tile=5 | 1 ms (default 2 ms) tested\n"
+            << "matmul rocm v2 m=2 -> tile=x | 1 ms (default 2 ms) tested\n";
+    }
+    bool threw = false;
+    try {
+        back.load(path);
+    } catch (const std::runtime_error& e) {
+        threw = std::string(e.what()).find(":3: ") != std::string::npos;
+    }
+    test::require(threw, "a malformed line is reported with its number");
+    std::remove(path.c_str());
+}
+
+// An Auto matmul under a scope holding `cache`; returns the recorded calls and the result.
+std::vector<RecordedCall> run_recorded(const TuningCache& cache, const Tensor& a, const Tensor& b,
+                                       std::vector<float>* result) {
+    std::vector<RecordedCall> calls;
+    {
+        const TuningScope scope({&cache, &calls});
+        const Tensor c = matmul(a, b); // Execution::Auto
+        *result = c.to_vector<float>();
+    }
+    return calls;
+}
+
+void test_auto_placement_on_cpu() {
+    // A stored gpu=0 keeps an Auto call on the CPU, and no entry leaves it there too.
+    const std::int64_t m = 20, n = 12, k = 33;
+    const auto av = test::quarter_input(m * k, 71);
+    const auto bv = test::quarter_input(k * n, 72);
+    const Tensor a = Tensor::from_vector(av, {m, k});
+    const Tensor b = Tensor::from_vector(bv, {k, n});
+    OpArgs args{{a, b}, {}};
+    TuningCache cache;
+    cache.store({machine_name(), "matmul", kAutoDevice, 1, placement_key(args, a.device()),
+                 {{"gpu", 0}}, 1.0, 1.0, "tested"});
+    test::require(placement_key(args, a.device()) == "data=cpu f32 20x33 33x12",
+                  "placement key as the reference writes it");
+    std::vector<float> c;
+    const auto calls = run_recorded(cache, a, b, &c);
+    test::require(calls.size() == 1 && calls[0].op == OpId::Matmul &&
+                      calls[0].execution == Execution::Auto &&
+                      calls[0].device == Device{DeviceType::CPU, 0},
+                  "gpu=0: the call runs on the CPU");
+    test::require(test::same_bits(c, exact_gemm(av, bv, m, n, k, 1.0, nullptr, 0.0, nullptr)),
+                  "the CPU result is exact");
+}
+
+void test_tuner_places_auto_on_rocm(Device device) {
+    // configs[0]-like product on CPU data, called with Execution::Auto. The tuner times the CPU
+    // against rocm:0 (copies included) and every allowed point of the rocm matmul's space, and
+    // stores both; running under those results places the call on rocm:0 with the stored tile.
+    const std::int64_t m = 512, n = 384, k = 1024;
+    const auto av = test::quarter_input(m * k, 81);
+    const auto bv = test::quarter_input(k * n, 82);
+    const Tensor a = Tensor::from_vector(av, {m, k});
+    const Tensor b = Tensor::from_vector(bv, {k, n});
+    const auto want = exact_gemm(av, bv, m, n, k, 1.0, nullptr, 0.0, nullptr);
+    const std::string path = results_path("mfr_tuning_results.txt");
+    std::remove(path.c_str());
+    Algorithm step([](const std::vector<Tensor>& in) {
+        return std::vector<Tensor>{matmul(in[0], in[1])};
+    });
+    TuneOptions options;
+    options.min_time_s = 0.005;
+    Tuner tuner(path);
+    const TuneReport report = tuner.tune(step, {a, b}, options);
+    std::cout << tuner.describe();
+    test::require(report.calls.size() == 2, "a device choice and a kernel result");
+
+    TuningCache cache;
+    cache.load(path);
+    OpArgs args{{a, b}, {}};
+    const TuningEntry* place = cache.find(machine_name(), "matmul", kAutoDevice, 1,
+                                          placement_key(args, a.device()));
+    test::require(place != nullptr && place->config == TuningValues{{"gpu", 1}},
+                  "the GPU wins this product and is stored");
+    const TunableKernel& tunable =
+        *Registry::instance().dispatcher().tunable({OpId::Matmul, DeviceType::ROCm, DType::F32});
+    OpArgs on_gpu{{a.to(device), b.to(device)}, {Tensor::empty({m, n}, DType::F32, device)}};
+    const std::string key = call_key(tunable, on_gpu, device);
+    test::require(key == "m=512 n=384 k=1024", "kernel key as the reference writes it");
+    const TuningEntry* kernel = cache.find(machine_name(), "matmul", "rocm", tunable.version, key);
+    test::require(kernel != nullptr && kernel->config.size() == 3, "the tile is stored");
+
+    std::vector<float> c;
+    const auto calls = run_recorded(cache, a, b, &c);
+    test::require(calls.size() == 1 && calls[0].device == device, "the Auto call ran on rocm:0");
+    test::require(test::same_bits(c, want), "bit-exact on quarter-integer inputs");
+    // The hook, as dispatch() called it for that call (the record is taken before the settings
+    // are applied): it picks rocm:0 and sets the stored tile.
+    {
+        OpArgs seen = calls[0].args;
+        const TuningScope scope({&cache, nullptr});
+        const Device target = apply_tuning(OpId::Matmul, Execution::Auto, a.device(), seen);
+        test::require(target == device && seen.tuning == to_config(tunable, kernel->config) &&
+                          seen.tuning.values[0] == kernel->config[0].second,
+                      "the hook applies the stored settings");
+    }
+    // The settings reach the kernel: a stored thin tile, which this product cannot take, makes
+    // the same call fail in the kernel.
+    {
+        TuningCache refused = cache;
+        TuningEntry thin = *kernel;
+        thin.config = {{"tile", MFR_TILE_THIN}, {"stage", MFR_STAGE_NEVER}, {"splits", 1}};
+        refused.store(thin);
+        bool kernel_refused = false;
+        try {
+            std::vector<float> unused;
+            run_recorded(refused, a, b, &unused);
+        } catch (const NotImplemented&) {
+            kernel_refused = true;
+        }
+        test::require(kernel_refused, "a stored thin tile reaches mfr_sgemm, which refuses it");
+    }
+    // The public path: Algorithm::run with the tuner gives the same bits.
+    const std::vector<Tensor> out = step.run({a, b}, tuner);
+    test::require(out.size() == 1 && test::same_bits(out[0].to_vector<float>(), want),
+                  "Algorithm::run(inputs, tuner)");
+    std::cout << "  tuned: " << to_string(kernel->config) << " (" << kernel->best_ms
+              << " ms, default " << kernel->default_ms << " ms)\n";
+}
+
 } // namespace
 
 int main(int argc, char** argv) {
     return test::run("tuning_test", argc, argv, [] {
         test::register_oracle_cpu_kernels();
+        test_results_file_round_trip();
+        test_auto_placement_on_cpu();
         bool rocm = false;
         for (Device device : test::devices()) {
             if (device.type != DeviceType::ROCm) {
@@ -230,6 +405,7 @@ int main(int argc, char** argv) {
             test_gemm_fused(device);
             test_batched(device);
             test_start_is_the_automatic_choice(device);
+            test_tuner_places_auto_on_rocm(device);
         }
         if (!rocm) {
             std::cout << "  no rocm device: the backend registers no tunables to check\n";

@@ -233,3 +233,53 @@ def test_fill(stream):
     ints = mf.DeviceArray.empty((77,), stream, np.int64)
     mf.fill(ints, -5)
     assert np.all(ints.numpy() == -5)
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_where_nd_broadcast_views(stream, oracle, case):
+    """mfr_where_nd reads each operand through its strides (0 where it broadcasts): seeded shapes
+    with broadcast, sliced and transposed operands, rows that do and do not take 16-byte
+    accesses, against the oracle's where on the packed operands, bit for bit."""
+    rng = np.random.default_rng(900 + case)
+    nd = int(rng.integers(1, 5))
+    shape = tuple(int(rng.integers(1, 9)) for _ in range(nd - 1)) + (int(rng.choice([1, 3, 4, 8, 64, 130, 1024])),)
+    print(f"where_nd case {case}: shape {shape}", flush=True)
+
+    def operand(dtype, seed):
+        kind = case % 3 if seed != 2 else (case // 3) % 3
+        if kind == 0:  # full, packed
+            host = rng.standard_normal(shape).astype(dtype) if dtype == np.float32 else \
+                (rng.random(shape) > 0.5).astype(np.uint8)
+            return host, dev(host, stream)
+        if kind == 1:  # broadcast: extent 1 in random dimensions, then expanded
+            small = tuple(1 if rng.random() < 0.5 else s for s in shape)
+            host = rng.standard_normal(small).astype(dtype) if dtype == np.float32 else \
+                (rng.random(small) > 0.5).astype(np.uint8)
+            return np.broadcast_to(host, shape), dev(host, stream).expand(shape)
+        # a slice of a wider array (row stride past the row length)
+        wide = shape[:-1] + (shape[-1] + 3,)
+        host = rng.standard_normal(wide).astype(dtype) if dtype == np.float32 else \
+            (rng.random(wide) > 0.5).astype(np.uint8)
+        return host[..., 1:1 + shape[-1]], dev(host, stream).slice(len(shape) - 1, 1, 1 + shape[-1])
+
+    x_host, x = operand(np.float32, 0)
+    y_host, y = operand(np.float32, 1)
+    c_host, c = operand(np.uint8, 2)
+    out = mf.where_nd(c, x, y, out=mf.DeviceArray.empty(shape, stream))
+    want = oracle.where(np.ascontiguousarray(c_host), np.ascontiguousarray(x_host),
+                        np.ascontiguousarray(y_host))
+    assert same_bits(out.numpy(), want.reshape(shape))
+
+
+def test_where_nd_attention_mask_shape(stream):
+    """The composed attention's call: scores [2, 3, 64, 96], a -inf scalar and a [64, 96] mask
+    expanded over the batch."""
+    rng = np.random.default_rng(7)
+    scores = rng.standard_normal((2, 3, 64, 96)).astype(np.float32)
+    keep = np.tril(np.ones((64, 96), np.uint8))
+    s_d = dev(scores, stream)
+    minus_inf = dev(np.array([-np.inf], np.float32), stream)
+    out = mf.where_nd(dev(keep, stream).expand(scores.shape), s_d, minus_inf.expand(scores.shape),
+                      out=s_d)
+    want = np.where(np.broadcast_to(keep, scores.shape) != 0, scores, np.float32(-np.inf))
+    assert same_bits(out.numpy(), want.astype(np.float32))
