@@ -29,6 +29,11 @@
 //     (X[4093,1023] row-major) is copied first into the stream's workspace with its lines padded
 //     to a multiple of 4 by zeros (stage_kernel); vector loads that reach past the end of a line
 //     then read zeros of its own line, and the zeros add nothing to any sum.
+//   - Direct-to-LDS slices (sgemm_direct_kernel, the 256x256 tile with a 4-byte operand): each
+//     lane's buffer load writes its element into the LDS image itself, so 4-byte operands take
+//     no registers and need no staging copy; elements outside the matrix get an offset past the
+//     buffer's record limit and load as zeros. AUTO takes this over staging when its main launch
+//     is that tile.
 //   - The epilogue applies the activation chosen once per workgroup, with copies for interior
 //     tiles and for C0, so each copy is straight-line code (gemm_kernel.hpp, write_tile).
 //   - Split-K cuts a long depth into ranges run as workgroups of their own, reduced in order by
@@ -192,12 +197,19 @@ struct Choice {
 // The automatic tile and split count (either may be fixed by the caller: tile != AUTO, splits !=
 // 0). A short depth (K <= 128) is latency-bound per tile, so it takes the high-occupancy 128x64 /
 // 64x128 tiles (the one padding the output less). Otherwise the pair with the least modelled
-// time. The 256x256 tile needs 16-byte loads on both operands. The thin path competes where it
+// time. The thin path competes where it
 // can take the product (ak, bk: whether A and B are read along k) and no split is fixed.
-Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int cus, bool wide_loads,
-              int fixed_tile, int fixed_splits, bool c0, bool ak, bool bk, int thin_b) {
+// big_ok: whether the 256x256 tile can read the operands (big_tile_ok).
+Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int cus,
+              int fixed_tile, int fixed_splits, bool c0, bool ak, bool bk, int thin_b,
+              bool big_ok) {
     Choice best;
     best.per = k;
+    if (fixed_tile == MFR_TILE_256x256 && !big_ok) {
+        throw mfr::Error(MFR_E_UNSUPPORTED,
+                         "sgemm: the 256x256 tile reads an operand with 4-byte loads here, and "
+                         "its strides put a slice more than 2^30 bytes across");
+    }
     const bool thin = thin_possible(m, n, ak, bk) && fixed_splits <= 1;
     if (fixed_tile == MFR_TILE_THIN) {
         if (!thin) {
@@ -225,7 +237,7 @@ Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int cus, bool wide
         double best_us = 1e300;
         for (int t = 1; t < MFR_TILE_THIN; ++t) {
             if ((fixed_tile != MFR_TILE_AUTO && t != fixed_tile) ||
-                (fixed_tile == MFR_TILE_AUTO && t == MFR_TILE_256x256 && !wide_loads)) {
+                (t == MFR_TILE_256x256 && !big_ok)) {
                 continue;
             }
             if (fixed_splits > 0) {
@@ -343,8 +355,16 @@ template <bool AK, bool BK>
 void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned blocks, bool one_per_cu,
                    hipStream_t stream) {
     switch (tile) {
-    case MFR_TILE_256x256: // 16-byte loads only (checked by the caller)
-        sgemm_kernel<256, 256, 32, 4, 4, AK, BK, 4, 4><<<blocks, 1024, 0, stream>>>(p);
+    case MFR_TILE_256x256:
+        if (va == 4 && vb == 4) {
+            sgemm_kernel<256, 256, 32, 4, 4, AK, BK, 4, 4><<<blocks, 1024, 0, stream>>>(p);
+        } else if (va == 4) {
+            sgemm_direct_kernel<256, 256, 32, 4, 4, AK, BK, 4, 1><<<blocks, 1024, 0, stream>>>(p);
+        } else if (vb == 4) {
+            sgemm_direct_kernel<256, 256, 32, 4, 4, AK, BK, 1, 4><<<blocks, 1024, 0, stream>>>(p);
+        } else {
+            sgemm_direct_kernel<256, 256, 32, 4, 4, AK, BK, 1, 1><<<blocks, 1024, 0, stream>>>(p);
+        }
         break;
     case MFR_TILE_128x64:
         launch_vec<128, 64, 16, 2, 2, AK, BK>(p, va, vb, blocks, stream);
@@ -557,13 +577,12 @@ void single_region(Plan& plan, const Choice& choice) {
 constexpr double kLaunchUs = 5.0;
 constexpr double kPeelMargin = 0.95;
 
-void consider_peeling(Plan& plan, int64_t batch, int cus, bool wide, double single_us) {
+bool big_tile_ok(const Plan& plan);
+
+void consider_peeling(Plan& plan, int64_t batch, int cus, double single_us) {
     const GemmParams& p = plan.p;
     double best_us = single_us * kPeelMargin;
     for (int t = 1; t < MFR_TILE_THIN; ++t) {
-        if (t == MFR_TILE_256x256 && !wide) {
-            continue;
-        }
         const int64_t bm = kTiles[t].bm, bn = kTiles[t].bn;
         const int64_t rem_m = p.m % bm, rem_n = p.n % bn;
         const bool peel_m = p.m > bm && rem_m > 0 && rem_m * 4 <= bm;
@@ -576,14 +595,14 @@ void consider_peeling(Plan& plan, int64_t batch, int cus, bool wide, double sing
         Region regions[4];
         int count = 0;
         const Choice main =
-            choose(main_m, main_n, p.k, batch, cus, wide, t, 1, plan.c0, plan.ak, plan.bk,
-                   thin_b_layout(p, plan, main_m, main_n));
+            choose(main_m, main_n, p.k, batch, cus, t, 1, plan.c0, plan.ak, plan.bk,
+                   thin_b_layout(p, plan, main_m, main_n), big_tile_ok(plan));
         regions[count++] = Region{0, 0, main_m, main_n, main.tile, main.splits, main.per};
         double us = main.us;
         auto strip = [&](int64_t m_off, int64_t n_off, int64_t m, int64_t n) {
             const Choice c =
-                choose(m, n, p.k, batch, cus, wide, MFR_TILE_AUTO, 0, plan.c0, plan.ak, plan.bk,
-                       thin_b_layout(p, plan, m, n));
+                choose(m, n, p.k, batch, cus, MFR_TILE_AUTO, 0, plan.c0, plan.ak, plan.bk,
+                       thin_b_layout(p, plan, m, n), big_tile_ok(plan));
             regions[count++] = Region{m_off, n_off, m, n, c.tile, c.splits, c.per};
             us += c.us + kLaunchUs;
         };
@@ -618,6 +637,26 @@ Operand operand_b(GemmParams& p, bool bk) {
 
 int64_t staged_floats_padded(const Operand& o, const GemmParams& p) {
     return (staged_floats(o, p) + 63) / 64 * 64; // 256-byte aligned parts of the workspace
+}
+
+// Whether the 256x256 tile can read the plan's operands (as they will be after staging): always
+// when both take 16-byte loads (its register-staged form); otherwise it copies both slices
+// straight into LDS with buffer loads, whose byte offsets within a slice must stay below 2^30:
+// 255 lines of a K-major operand, or 31 depth lines of the other, plus a line's own extent.
+bool big_tile_ok(const Plan& plan) {
+    const int va = plan.stage_a ? 4 : plan.va;
+    const int vb = plan.stage_b ? 4 : plan.vb;
+    if (va == 4 && vb == 4) {
+        return true;
+    }
+    GemmParams p = plan.p;
+    const auto fits = [](const Operand& o, bool kmaj, bool staged) {
+        const int64_t line = staged ? round4(o.inner) : *o.line_stride;
+        const int64_t last = kmaj ? 255 * line + 32 : 31 * line + 256;
+        return line >= 0 && last < (int64_t{1} << 28);
+    };
+    return fits(operand_a(p, plan.ak), plan.ak, plan.stage_a) &&
+           fits(operand_b(p, plan.bk), plan.bk, plan.stage_b);
 }
 
 // Validates d (the checks and error codes of mfr_sgemm) and makes the plan for a device with
@@ -706,7 +745,7 @@ Plan plan_sgemm(const mfr_gemm_desc& d, int cus) {
     }
 
     // Staging (see the design notes at the top): ALWAYS, or AUTO when the product is large next
-    // to the copy, or when the caller fixed the 256x256 tile (which needs 16-byte loads).
+    // to the copy.
     if ((plan.va == 1 || plan.vb == 1) && d.stage != MFR_STAGE_NEVER) {
         const Operand oa = operand_a(p, plan.ak);
         const Operand ob = operand_b(p, plan.bk);
@@ -716,22 +755,34 @@ Plan plan_sgemm(const mfr_gemm_desc& d, int cus) {
         const double staged_bytes = 4.0 * static_cast<double>(fa + fb);
         const bool worth = flops >= 1073741824.0 && staged_bytes * 64.0 <= flops &&
                            staged_bytes <= 4294967296.0;
-        if (d.stage == MFR_STAGE_ALWAYS || worth || d.tile == MFR_TILE_256x256) {
+        if (d.stage == MFR_STAGE_ALWAYS || worth) {
             plan.stage_a = plan.va == 1;
             plan.stage_b = plan.vb == 1;
         }
     }
-    const bool wide = (plan.va == 4 || plan.stage_a) && (plan.vb == 4 || plan.stage_b);
-    if (d.tile == MFR_TILE_256x256 && !wide) {
-        throw mfr::Error(MFR_E_UNSUPPORTED,
-                         "sgemm: the 256x256 tile needs 16-byte loads (staging is off)");
-    }
     plan.c0 = p.c0 != nullptr && p.beta != 0.0f;
-    const Choice choice = choose(p.m, p.n, p.k, batch_count, cus, wide, d.tile, d.splits, plan.c0,
-                                 plan.ak, plan.bk, thin_b_layout(p, plan, p.m, p.n));
-    single_region(plan, choice);
-    if (d.tile == MFR_TILE_AUTO && d.splits == 0) {
-        consider_peeling(plan, batch_count, cus, wide, choice.us);
+    const auto tile_plan = [&](Plan& q) {
+        const Choice choice = choose(p.m, p.n, p.k, batch_count, cus, d.tile, d.splits, q.c0,
+                                     q.ak, q.bk, thin_b_layout(q.p, q, p.m, p.n), big_tile_ok(q));
+        single_region(q, choice);
+        if (d.tile == MFR_TILE_AUTO && d.splits == 0) {
+            consider_peeling(q, batch_count, cus, choice.us);
+        }
+    };
+    tile_plan(plan);
+    // AUTO staging whose main launch is the 256x256 tile: that tile copies the operands straight
+    // into LDS instead (MLP configs[3]: 330 against 334 us, and neither the copies' launches nor
+    // their workspace), when its main launch is still that tile without the copies.
+    if (d.stage == MFR_STAGE_AUTO && (plan.stage_a || plan.stage_b) &&
+        plan.regions[0].tile == MFR_TILE_256x256) {
+        Plan direct = plan;
+        direct.stage_a = direct.stage_b = false;
+        if (big_tile_ok(direct)) {
+            tile_plan(direct);
+            if (direct.regions[0].tile == MFR_TILE_256x256) {
+                plan = direct;
+            }
+        }
     }
     for (int i = 0; i < plan.region_count; ++i) {
         const Region& r = plan.regions[i];
@@ -1058,10 +1109,9 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d, float* scratch = nullptr,
             try_reserve(s, 4 * static_cast<size_t>(partial_floats(plan) + fa + fb)));
         if (ws == nullptr && partial_floats(plan) > 0 && d.splits == 0) {
             // Automatic splits without the memory: one region, one range.
-            single_region(plan, choose(p.m, p.n, p.k, p.batch_count, s.compute_units,
-                                       (va == 4 || plan.stage_a) && (vb == 4 || plan.stage_b),
-                                       d.tile, 1, plan.c0, plan.ak, plan.bk,
-                                       thin_b_layout(p, plan, p.m, p.n)));
+            single_region(plan, choose(p.m, p.n, p.k, p.batch_count, s.compute_units, d.tile, 1,
+                                       plan.c0, plan.ak, plan.bk,
+                                       thin_b_layout(p, plan, p.m, p.n), big_tile_ok(plan)));
             if (fa + fb > 0) {
                 ws = static_cast<float*>(try_reserve(s, 4 * static_cast<size_t>(fa + fb)));
             }
@@ -1070,16 +1120,17 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d, float* scratch = nullptr,
             if (partial_floats(plan) > 0) {
                 throw mfr::Error(MFR_E_RUNTIME, "sgemm: no workspace for split-K partial sums");
             }
-            if (d.stage == MFR_STAGE_ALWAYS || d.tile == MFR_TILE_256x256) {
+            if (d.stage == MFR_STAGE_ALWAYS) {
                 throw mfr::Error(MFR_E_RUNTIME, "sgemm: no workspace for operand staging");
             }
-            // AUTO without the memory: read in place, and choose the tile for 4-byte loads.
+            // AUTO without the memory: read in place (4-byte loads; the 256x256 tile copies them
+            // straight into LDS).
             plan.stage_a = plan.stage_b = false;
             fa = fb = 0;
             if (d.tile == MFR_TILE_AUTO) {
                 single_region(plan, choose(p.m, p.n, p.k, p.batch_count, s.compute_units,
-                                           va == 4 && vb == 4, MFR_TILE_AUTO, 1, plan.c0,
-                                           plan.ak, plan.bk, thin_b_layout(p, plan, p.m, p.n)));
+                                           MFR_TILE_AUTO, 1, plan.c0, plan.ak, plan.bk,
+                                           thin_b_layout(p, plan, p.m, p.n), big_tile_ok(plan)));
             }
         }
     }

@@ -121,9 +121,12 @@ template <int ROWS, int KT, bool KMAJ, int V, int THREADS> struct SliceLoader {
             out[2] = v.z;
             out[3] = v.w;
         } else {
+            // One per-lane address; the depth offsets are constants the LDS reads carry as
+            // immediates (per-depth addresses would each take a register across the depth loop).
+            const float* column = lds + 4 * half * kPitch + row;
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                out[s] = lds[(8 * g + 4 * half + s) * kPitch + row];
+                out[s] = column[(8 * g + s) * kPitch];
             }
         }
     }
@@ -230,6 +233,126 @@ __device__ __forceinline__ void epilogue(const floatx16 (&acc)[FM][FN], float* c
     }
 }
 
+// Which output tile a workgroup computes: the XCD-aware remap of the hardware workgroup index,
+// grouped row-major order within the batch, the depth split outermost; and the operand offsets
+// of its batch entry.
+struct TileWork {
+    int64_t split, batch_linear, m0, n0;
+    int64_t off_a, off_b, off_c, off_c0;
+    int rows_a, rows_b; // rows of A (M) and of B (N) inside the matrix, capped at the tile
+    int64_t k_begin, kk; // depth range [k_begin, k_begin + kk)
+};
+
+template <int BM, int BN> __device__ __forceinline__ TileWork tile_work(const GemmParams& p) {
+    TileWork w;
+    const int64_t tiles_per_batch = static_cast<int64_t>(p.tiles_m) * p.tiles_n;
+    const int64_t tiles_per_split = tiles_per_batch * p.batch_count;
+    const int64_t total = tiles_per_split * p.splits;
+    const int64_t hw = blockIdx.x;
+    const int64_t per_xcd = total / 8;
+    const int64_t logical_all = hw < per_xcd * 8 ? (hw % 8) * per_xcd + hw / 8 : hw;
+    w.split = logical_all / tiles_per_split;
+    const int64_t logical = logical_all - w.split * tiles_per_split;
+    w.batch_linear = logical / tiles_per_batch;
+    int64_t batch_index = w.batch_linear;
+    const int64_t t = logical % tiles_per_batch;
+    const int64_t group_tiles = static_cast<int64_t>(p.group_m) * p.tiles_n;
+    const int64_t group = t / group_tiles;
+    const int64_t first_m = group * p.group_m;
+    const int64_t rows_in_group =
+        p.tiles_m - first_m < p.group_m ? p.tiles_m - first_m : p.group_m;
+    const int64_t in_group = t % group_tiles;
+    const int64_t tile_m = first_m + in_group % rows_in_group;
+    const int64_t tile_n = in_group / rows_in_group;
+    w.off_a = w.off_b = w.off_c = w.off_c0 = 0;
+    for (int d = p.batch_dims - 1; d >= 0; --d) {
+        const int64_t idx = batch_index % p.batch[d];
+        batch_index /= p.batch[d];
+        w.off_a += idx * p.a_bs[d];
+        w.off_b += idx * p.b_bs[d];
+        w.off_c += idx * p.c_bs[d];
+        w.off_c0 += idx * p.c0_bs[d];
+    }
+    w.m0 = tile_m * BM;
+    w.n0 = tile_n * BN;
+    w.rows_a = p.m - w.m0 < BM ? static_cast<int>(p.m - w.m0) : BM;
+    w.rows_b = p.n - w.n0 < BN ? static_cast<int>(p.n - w.n0) : BN;
+    w.k_begin = w.split * p.k_per_split;
+    w.kk = p.k - w.k_begin < p.k_per_split ? p.k - w.k_begin : p.k_per_split;
+    return w;
+}
+
+// One depth slice of MFMAs from the LDS tiles sa, sb: the wavefront's FM x FN 32x32 blocks over
+// the 8-deep groups it takes (wave_k, wave_k + WAVES_K, ...).
+template <typename LoadA, typename LoadB, int KT, int FM, int FN, int WM, int WN, int WAVES_K>
+__device__ __forceinline__ void slice_mfma(floatx16 (&acc)[FM][FN], const float* sa,
+                                           const float* sb, int wave_m, int wave_n, int wave_k,
+                                           int half, int r32) {
+#pragma unroll
+    for (int gi = 0; gi < KT / 8 / WAVES_K; ++gi) {
+        const int g = gi * WAVES_K + wave_k;
+        float fa[FM][4];
+        float fb[FN][4];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            LoadA::fragment(sa, wave_m * WM + i * 32 + r32, g, half, fa[i]);
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            LoadB::fragment(sb, wave_n * WN + j * 32 + r32, g, half, fb[j]);
+        }
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][st], fb[j][st],
+                                                                      acc[i][j], 0, 0, 0);
+                }
+            }
+        }
+    }
+}
+
+// The end of a tile: split-K partial sums, or the epilogue with the activation chosen once.
+template <int BM, int BN, int WM, int WN, int FM, int FN>
+__device__ __forceinline__ void finish_tile(const floatx16 (&acc)[FM][FN], const GemmParams& p,
+                                            const TileWork& w, int wave_m, int wave_n, int half,
+                                            int r32) {
+    // Accumulator e of block (i, j) is C(row, col) with row = 32i + 8(e/4) + 4*half + e%4,
+    // col = 32j + lane%32 (v_mfma_f32_32x32x2_f32 layout).
+    const int64_t row0 = w.m0 + wave_m * WM + 4 * half;
+    const int64_t col0 = w.n0 + wave_n * WN + r32;
+    const bool interior = w.m0 + BM <= p.m && w.n0 + BN <= p.n;
+    if (p.partial != nullptr) {
+        // Split-K: raw sums only, to partial[split][batch] (dense m x n).
+        float* part = p.partial + (w.split * p.batch_count + w.batch_linear) * p.m * p.n;
+        if (interior) {
+            write_tile<FM, FN, MFR_ACT_NONE, true, true, kC0None>(acc, part, p.n, nullptr, 0, p,
+                                                                  row0, col0);
+        } else {
+            write_tile<FM, FN, MFR_ACT_NONE, false, true, kC0None>(acc, part, p.n, nullptr, 0, p,
+                                                                   row0, col0);
+        }
+        return;
+    }
+    float* c_base = p.c + w.off_c;
+    const float* c0_base = p.c0 != nullptr && p.beta != 0.0f ? p.c0 + w.off_c0 : nullptr;
+    // One activation per branch (uniform), so each epilogue is straight-line code: unrolled
+    // over every accumulator, the three would not fit the instruction cache together.
+    if (p.act == MFR_ACT_NONE) {
+        epilogue<FM, FN, MFR_ACT_NONE>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
+                                       interior);
+    } else if (p.act == MFR_ACT_GELU_TANH) {
+        epilogue<FM, FN, MFR_ACT_GELU_TANH>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
+                                            interior);
+    } else {
+        epilogue<FM, FN, MFR_ACT_GELU_ERF>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
+                                           interior);
+    }
+}
+
 // WAVES_K > 1: WAVES_K sets of WAVES_M x WAVES_N wavefronts share each depth slice, set w taking
 // its 8-deep groups w, w + WAVES_K, ...; the sets' accumulators are then added through LDS, in
 // set order, and set 0 runs the epilogue. It gives a small grid (a workgroup per CU) several
@@ -251,47 +374,9 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * WAVES_K * 64) void sgemm_kernel
     auto lds_a = [&](int which) { return smem + which * LoadA::kFloats; };
     auto lds_b = [&](int which) { return smem + 2 * LoadA::kFloats + which * LoadB::kFloats; };
 
-    // ---- which tile: XCD-aware remap, then grouped row-major order within the batch; the
-    //      depth split is the outermost index ----
-    const int64_t tiles_per_batch = static_cast<int64_t>(p.tiles_m) * p.tiles_n;
-    const int64_t tiles_per_split = tiles_per_batch * p.batch_count;
-    const int64_t total = tiles_per_split * p.splits;
-    const int64_t hw = blockIdx.x;
-    const int64_t per_xcd = total / 8;
-    const int64_t logical_all = hw < per_xcd * 8 ? (hw % 8) * per_xcd + hw / 8 : hw;
-    const int64_t split = logical_all / tiles_per_split;
-    const int64_t logical = logical_all - split * tiles_per_split;
-    const int64_t batch_linear = logical / tiles_per_batch;
-    int64_t batch_index = batch_linear;
-    const int64_t t = logical % tiles_per_batch;
-    const int64_t group_tiles = static_cast<int64_t>(p.group_m) * p.tiles_n;
-    const int64_t group = t / group_tiles;
-    const int64_t first_m = group * p.group_m;
-    const int64_t rows_in_group =
-        p.tiles_m - first_m < p.group_m ? p.tiles_m - first_m : p.group_m;
-    const int64_t in_group = t % group_tiles;
-    const int64_t tile_m = first_m + in_group % rows_in_group;
-    const int64_t tile_n = in_group / rows_in_group;
-
-    int64_t off_a = 0, off_b = 0, off_c = 0, off_c0 = 0;
-    for (int d = p.batch_dims - 1; d >= 0; --d) {
-        const int64_t idx = batch_index % p.batch[d];
-        batch_index /= p.batch[d];
-        off_a += idx * p.a_bs[d];
-        off_b += idx * p.b_bs[d];
-        off_c += idx * p.c_bs[d];
-        off_c0 += idx * p.c0_bs[d];
-    }
-    const int64_t m0 = tile_m * BM;
-    const int64_t n0 = tile_n * BN;
-    const int rows_a = p.m - m0 < BM ? static_cast<int>(p.m - m0) : BM;
-    const int rows_b = p.n - n0 < BN ? static_cast<int>(p.n - n0) : BN;
-
-    // This workgroup's depth range [k_begin, k_begin + kk).
-    const int64_t k_begin = split * p.k_per_split;
-    const int64_t kk = p.k - k_begin < p.k_per_split ? p.k - k_begin : p.k_per_split;
-    const float* a_base = p.a + off_a + m0 * p.a_rs + k_begin * p.a_cs;
-    const float* b_base = p.b + off_b + n0 * p.b_cs + k_begin * p.b_rs;
+    const TileWork w = tile_work<BM, BN>(p);
+    const float* a_base = p.a + w.off_a + w.m0 * p.a_rs + w.k_begin * p.a_cs;
+    const float* b_base = p.b + w.off_b + w.n0 * p.b_cs + w.k_begin * p.b_rs;
     // Per slice the bases advance by KT depths.
     const int64_t a_step = KT * p.a_cs;
     const int64_t b_step = KT * p.b_rs;
@@ -320,13 +405,14 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * WAVES_K * 64) void sgemm_kernel
         }
     }
 
+    const int64_t kk = w.kk;
     const int64_t slices = kk > 0 ? (kk + KT - 1) / KT : 0;
     LoadA la;
     LoadB lb;
     if (slices > 0) {
         const int k_left = kk < KT ? static_cast<int>(kk) : KT;
-        la.load(a_base, p.a_rs, p.a_cs, rows_a, k_left);
-        lb.load(b_base, p.b_cs, p.b_rs, rows_b, k_left);
+        la.load(a_base, p.a_rs, p.a_cs, w.rows_a, k_left);
+        lb.load(b_base, p.b_cs, p.b_rs, w.rows_b, k_left);
         la.store(lds_a(0));
         lb.store(lds_b(0));
         __syncthreads();
@@ -337,36 +423,11 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * WAVES_K * 64) void sgemm_kernel
         if (more) {
             const int64_t k_next = (s + 1) * KT;
             const int k_left = kk - k_next < KT ? static_cast<int>(kk - k_next) : KT;
-            la.load(a_base + (s + 1) * a_step, p.a_rs, p.a_cs, rows_a, k_left);
-            lb.load(b_base + (s + 1) * b_step, p.b_cs, p.b_rs, rows_b, k_left);
+            la.load(a_base + (s + 1) * a_step, p.a_rs, p.a_cs, w.rows_a, k_left);
+            lb.load(b_base + (s + 1) * b_step, p.b_cs, p.b_rs, w.rows_b, k_left);
         }
-        const float* sa = lds_a(cur);
-        const float* sb = lds_b(cur);
-#pragma unroll
-        for (int gi = 0; gi < KT / 8 / WAVES_K; ++gi) {
-            const int g = gi * WAVES_K + wave_k;
-            float fa[FM][4];
-            float fb[FN][4];
-#pragma unroll
-            for (int i = 0; i < FM; ++i) {
-                LoadA::fragment(sa, wave_m * WM + i * 32 + r32, g, half, fa[i]);
-            }
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                LoadB::fragment(sb, wave_n * WN + j * 32 + r32, g, half, fb[j]);
-            }
-#pragma unroll
-            for (int st = 0; st < 4; ++st) {
-#pragma unroll
-                for (int i = 0; i < FM; ++i) {
-#pragma unroll
-                    for (int j = 0; j < FN; ++j) {
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][st], fb[j][st],
-                                                                          acc[i][j], 0, 0, 0);
-                    }
-                }
-            }
-        }
+        slice_mfma<LoadA, LoadB, KT, FM, FN, WM, WN, WAVES_K>(acc, lds_a(cur), lds_b(cur), wave_m,
+                                                                wave_n, wave_k, half, r32);
         if (more) {
             la.store(lds_a(cur ^ 1));
             lb.store(lds_b(cur ^ 1));
@@ -399,8 +460,8 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * WAVES_K * 64) void sgemm_kernel
             return;
         }
 #pragma unroll
-        for (int w = 1; w < WAVES_K; ++w) {
-            const float* theirs = smem + ((w - 1) * WAVES_M * WAVES_N + wave_mn) * kPerWave;
+        for (int ws = 1; ws < WAVES_K; ++ws) {
+            const float* theirs = smem + ((ws - 1) * WAVES_M * WAVES_N + wave_mn) * kPerWave;
 #pragma unroll
             for (int i = 0; i < FM; ++i) {
 #pragma unroll
@@ -413,38 +474,181 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * WAVES_K * 64) void sgemm_kernel
             }
         }
     }
+    finish_tile<BM, BN, WM, WN, FM, FN>(acc, p, w, wave_m, wave_n, half, r32);
+}
 
-    // ---- epilogue: accumulator e of block (i, j) is C(row, col) with
-    //      row = 32i + 8(e/4) + 4*half + e%4, col = 32j + lane%32 (v_mfma_f32_32x32x2_f32 layout)
-    const int64_t row0 = m0 + wave_m * WM + 4 * half;
-    const int64_t col0 = n0 + wave_n * WN + r32;
-    const bool interior = m0 + BM <= p.m && n0 + BN <= p.n;
-    if (p.partial != nullptr) {
-        // Split-K: raw sums only, to partial[split][batch] (dense m x n).
-        float* part = p.partial + (split * p.batch_count + batch_linear) * p.m * p.n;
-        if (interior) {
-            write_tile<FM, FN, MFR_ACT_NONE, true, true, kC0None>(acc, part, p.n, nullptr, 0, p,
-                                                                  row0, col0);
-        } else {
-            write_tile<FM, FN, MFR_ACT_NONE, false, true, kC0None>(acc, part, p.n, nullptr, 0, p,
-                                                                   row0, col0);
+// ---- the direct-to-LDS form ---------------------------------------------------------------------
+
+// Global -> LDS copy of one operand slice by buffer loads that write LDS (buffer_load ... lds):
+// lane L of a wave-instruction lands its V floats at the instruction's LDS base + L * V floats, so
+// each instruction fills 64 * V consecutive floats of the slice's LDS image (the layout of
+// SliceLoader, so the fragments read it unchanged) and its lanes gather them from wherever they
+// live. No register holds the slice, so 4-byte loads (operands that 16-byte loads cannot read)
+// cost no registers and need no staging copy. The instructions are split over the waves in
+// contiguous blocks.
+//
+// Addressing: a buffer resource per slice at the slice's first element, and a 32-bit byte offset
+// per lane. A lane whose element is outside the matrix (or is a pad float of the layout) gets an
+// offset at the resource's record limit, which the buffer unit answers with zeros without reading
+// memory. Every in-range byte of a slice must lie below 2^30 bytes from its first element: the
+// host checks the strides (direct_slices_fit) before it picks this loader.
+constexpr uint32_t kDirectLimit = 0x80000000u;
+// Word 3 of a gfx9-family buffer resource: 32-bit float data, no swizzle, raw (stride 0)
+// addressing.
+constexpr int kBufferWord3 = 0x00020000;
+
+template <int ROWS, int KT, bool KMAJ, int V, int THREADS> struct DirectSliceLoader {
+    static constexpr int kPitch = KMAJ ? KT + 4 : ROWS + 8;
+    static constexpr int kFloats = KMAJ ? ROWS * (KT + 4) : KT * (ROWS + 8);
+    // K-major: the whole image, pads included; otherwise ROWS / (64 V) instructions per depth.
+    static constexpr int kPerLine = KMAJ ? 1 : ROWS / (64 * V);
+    static constexpr int kInstr = KMAJ ? kFloats / (64 * V) : KT * kPerLine;
+    static constexpr int kWaves = THREADS / 64;
+    static constexpr int kPerWave = (kInstr + kWaves - 1) / kWaves;
+    static_assert(!KMAJ || kFloats % (64 * V) == 0, "the image is a whole number of instructions");
+    static_assert(KMAJ || ROWS % (64 * V) == 0, "a depth line is a whole number of instructions");
+    static_assert(kPitch % V == 0, "a chunk of V floats never crosses a line of the image");
+
+    // base: element (row 0, depth 0) of the slice; rows_left / k_left: rows and depths inside
+    // (a multiple of V along the unit-stride dimension).
+    __device__ __forceinline__ static void issue(float* lds, const float* base, int64_t row_stride,
+                                                 int64_t k_stride, int rows_left, int k_left) {
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(base), 0, static_cast<int>(kDirectLimit - 1), kBufferWord3);
+        const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / 64));
+        const int lane = static_cast<int>(__lane_id());
+        const uint32_t row_bytes = static_cast<uint32_t>(row_stride) * 4u;
+        const uint32_t k_bytes = static_cast<uint32_t>(k_stride) * 4u;
+        const int depth_end = k_left < KT ? k_left : KT; // depths of the slice inside the matrix
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            const int instr = wave * kPerWave + j;
+            if (kInstr % kWaves != 0 && instr >= kInstr) {
+                break; // uniform: this wave's block ended
+            }
+            uint32_t offset;
+            float* dst;
+            if constexpr (KMAJ) {
+                // line = row, at = depth (at >= KT: a pad).
+                const int f = (instr * 64 + lane) * V;
+                const int row = f / kPitch;
+                const int at = f - row * kPitch;
+                const bool inside = row < rows_left && at < depth_end;
+                offset = inside ? static_cast<uint32_t>(row) * row_bytes +
+                                      static_cast<uint32_t>(at) * 4u
+                                : kDirectLimit;
+                dst = lds + instr * 64 * V;
+            } else {
+                // line = depth (uniform per instruction), at = row.
+                const int line = instr / kPerLine;
+                const int row = (instr % kPerLine) * 64 * V + lane * V;
+                const bool inside = line < depth_end && row < rows_left;
+                offset = inside ? static_cast<uint32_t>(line) * k_bytes +
+                                      static_cast<uint32_t>(row) * 4u
+                                : kDirectLimit;
+                dst = lds + line * kPitch + (instr % kPerLine) * 64 * V;
+            }
+            if constexpr (V == 4) {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 16, static_cast<int>(offset), 0,
+                                                         0, 0);
+            } else {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 4, static_cast<int>(offset), 0,
+                                                         0, 0);
+            }
         }
-        return;
     }
-    float* c_base = p.c + off_c;
-    const float* c0_base = p.c0 != nullptr && p.beta != 0.0f ? p.c0 + off_c0 : nullptr;
-    // One activation per branch (uniform), so each epilogue is straight-line code: unrolled
-    // over every accumulator, the three would not fit the instruction cache together.
-    if (p.act == MFR_ACT_NONE) {
-        epilogue<FM, FN, MFR_ACT_NONE>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
-                                       interior);
-    } else if (p.act == MFR_ACT_GELU_TANH) {
-        epilogue<FM, FN, MFR_ACT_GELU_TANH>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
-                                            interior);
-    } else {
-        epilogue<FM, FN, MFR_ACT_GELU_ERF>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
-                                           interior);
+};
+
+// The 256x256 tile (16 wavefronts of 64x64) with direct-to-LDS slices. The depth loop is
+// unrolled by two so each half knows at compile time which buffer it reads and which it fills;
+// the copy of slice s + 1 is issued before slice s's MFMAs and waited for (vmcnt 0) before the
+// barrier that ends the slice. Same arithmetic as sgemm_kernel, so the same bits.
+template <int BM, int BN, int KT, int WAVES_M, int WAVES_N, bool AK, bool BK, int VA, int VB>
+__global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_direct_kernel(GemmParams p) {
+    constexpr int THREADS = WAVES_M * WAVES_N * 64;
+    constexpr int WM = BM / WAVES_M;
+    constexpr int WN = BN / WAVES_N;
+    constexpr int FM = WM / 32;
+    constexpr int FN = WN / 32;
+    static_assert(KT % 8 == 0 && WM % 32 == 0 && WN % 32 == 0, "tile shape");
+    using LoadA = DirectSliceLoader<BM, KT, AK, VA, THREADS>;
+    using LoadB = DirectSliceLoader<BN, KT, BK, VB, THREADS>;
+    using FragA = SliceLoader<BM, KT, AK, VA, THREADS>;
+    using FragB = SliceLoader<BN, KT, BK, VB, THREADS>;
+    static_assert(LoadA::kFloats == FragA::kFloats && LoadB::kFloats == FragB::kFloats,
+                  "one LDS image");
+    // One LDS object per buffer: the compiler tells LDS objects apart, so it sees that the copy
+    // into one buffer does not write the one the MFMAs read (within one object it would wait for
+    // the copy to land before the first LDS read of every slice).
+    __shared__ __align__(16) float tile_a0[LoadA::kFloats];
+    __shared__ __align__(16) float tile_a1[LoadA::kFloats];
+    __shared__ __align__(16) float tile_b0[LoadB::kFloats];
+    __shared__ __align__(16) float tile_b1[LoadB::kFloats];
+
+    const TileWork w = tile_work<BM, BN>(p);
+    const float* a_base = p.a + w.off_a + w.m0 * p.a_rs + w.k_begin * p.a_cs;
+    const float* b_base = p.b + w.off_b + w.n0 * p.b_cs + w.k_begin * p.b_rs;
+    const int64_t a_step = KT * p.a_cs;
+    const int64_t b_step = KT * p.b_rs;
+
+    const int lane = threadIdx.x % 64;
+    const int wave = threadIdx.x / 64;
+    const int wave_m = wave / WAVES_N;
+    const int wave_n = wave % WAVES_N;
+    const int half = lane / 32;
+    const int r32 = lane % 32;
+
+    floatx16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                acc[i][j][e] = 0.0f;
+            }
+        }
     }
+
+    // Slices are taken in pairs, buffer 0 then buffer 1, with no exit between the two halves (an
+    // exit there splits the accumulators' live ranges and they spill). An odd count gets one
+    // more slice past the end, all of whose elements are outside the matrix: the buffer unit
+    // loads zeros, and adding zero products leaves every sum as it was.
+    const int64_t kk = w.kk;
+    const int64_t slices = kk > 0 ? (kk + KT - 1) / KT : 0;
+    const auto k_left_of = [&](int64_t s) {
+        const int64_t left = kk - s * KT;
+        return left <= 0 ? 0 : left < KT ? static_cast<int>(left) : KT;
+    };
+    if (slices > 0) {
+        LoadA::issue(tile_a0, a_base, p.a_rs, p.a_cs, w.rows_a, k_left_of(0));
+        LoadB::issue(tile_b0, b_base, p.b_cs, p.b_rs, w.rows_b, k_left_of(0));
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+    for (int64_t s = 0; s < slices; s += 2) {
+        // Slice s from buffer 0; slice s + 1 (zeros past the end) into buffer 1.
+        LoadA::issue(tile_a1, a_base + (s + 1) * a_step, p.a_rs, p.a_cs, w.rows_a,
+                     k_left_of(s + 1));
+        LoadB::issue(tile_b1, b_base + (s + 1) * b_step, p.b_cs, p.b_rs, w.rows_b,
+                     k_left_of(s + 1));
+        slice_mfma<FragA, FragB, KT, FM, FN, WM, WN, 1>(acc, tile_a0, tile_b0, wave_m, wave_n, 0,
+                                                         half, r32);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        // Slice s + 1 from buffer 1; slice s + 2 into buffer 0.
+        if (s + 2 < slices) {
+            LoadA::issue(tile_a0, a_base + (s + 2) * a_step, p.a_rs, p.a_cs, w.rows_a,
+                         k_left_of(s + 2));
+            LoadB::issue(tile_b0, b_base + (s + 2) * b_step, p.b_cs, p.b_rs, w.rows_b,
+                         k_left_of(s + 2));
+        }
+        slice_mfma<FragA, FragB, KT, FM, FN, WM, WN, 1>(acc, tile_a1, tile_b1, wave_m, wave_n, 0,
+                                                         half, r32);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+    finish_tile<BM, BN, WM, WN, FM, FN>(acc, p, w, wave_m, wave_n, half, r32);
 }
 
 } // namespace mfr::gemm

@@ -69,10 +69,11 @@ std::int64_t ranges_run(std::int64_t k, std::int64_t splits) {
 }
 
 // Runs every point of `op`'s space that `allowed` accepts and checks the output each time.
-// Points refused are exactly the 256x256 tile with staging off when `narrow` (an operand that
-// 16-byte loads cannot read) and split counts the depth k is too short for.
-void sweep(Device device, OpId op, OpArgs args, const std::vector<float>& want, bool narrow,
-           std::int64_t k, const std::string& what) {
+// Points refused are exactly the thin path (no product here is thin) and split counts the depth
+// k is too short for; with staging off, the 256x256 tile reads an operand 16-byte loads cannot
+// read (the matmul and batched cases) in place.
+void sweep(Device device, OpId op, OpArgs args, const std::vector<float>& want, std::int64_t k,
+           const std::string& what) {
     Registry& registry = Registry::instance();
     const TunableKernel& tunable = *registry.dispatcher().tunable({op, DeviceType::ROCm, DType::F32});
     const KernelFn kernel = registry.dispatcher().lookup({op, DeviceType::ROCm, DType::F32});
@@ -92,9 +93,7 @@ void sweep(Device device, OpId op, OpArgs args, const std::vector<float>& want, 
                 const TuningConfig config = point(tile, stage, splits);
                 const bool allowed = tunable.allowed(args, config);
                 // None of these products is thin enough (m, n > 8) for the thin path.
-                const bool expected =
-                    !(narrow && tile == MFR_TILE_256x256 && stage == MFR_STAGE_NEVER) &&
-                    tile != MFR_TILE_THIN && ranges_run(k, splits) == splits;
+                const bool expected = tile != MFR_TILE_THIN && ranges_run(k, splits) == splits;
                 const std::string name = "tile " + std::to_string(tile) + " stage " +
                                          std::to_string(stage) + " splits " +
                                          std::to_string(splits);
@@ -110,8 +109,7 @@ void sweep(Device device, OpId op, OpArgs args, const std::vector<float>& want, 
             }
         }
     }
-    test::require(counts >= 2 && ran == (narrow ? 9 : 10) * counts,
-                  what + ": every allowed point ran");
+    test::require(counts >= 2 && ran == 10 * counts, what + ": every allowed point ran");
     // Not a point: AUTO is only the default, and unknown values are refused.
     test::require(!tunable.allowed(args, point(MFR_TILE_AUTO, MFR_STAGE_NEVER, 1)) &&
                       !tunable.allowed(args, point(MFR_TILE_64x64, 7, 1)) &&
@@ -146,7 +144,7 @@ void test_matmul(Device device) {
         *Registry::instance().dispatcher().tunable({OpId::Matmul, DeviceType::ROCm, DType::F32});
     test::require(t.key(args) == std::vector<std::int64_t>{m, n, k}, "matmul key");
     const auto want = exact_gemm(av, bv, m, n, k, 1.0, nullptr, 0.0, nullptr);
-    sweep(device, OpId::Matmul, args, want, true, k, "matmul 300x261x1023");
+    sweep(device, OpId::Matmul, args, want, k, "matmul 300x261x1023");
 }
 
 void test_gemm_fused(Device device) {
@@ -171,7 +169,7 @@ void test_gemm_fused(Device device) {
     args.beta = 0.5f;
     args.has_bias = true;
     const auto want = exact_gemm(av, bv, m, n, k, 1.5, &cv, 0.5, &biasv);
-    sweep(device, OpId::Gemm, args, want, false, k, "gemm 257x200x96 NT");
+    sweep(device, OpId::Gemm, args, want, k, "gemm 257x200x96 NT");
 }
 
 void test_batched(Device device) {
@@ -199,7 +197,7 @@ void test_batched(Device device) {
             want.insert(want.end(), c.begin(), c.end());
         }
     }
-    sweep(device, OpId::GemmBatched, args, want, true, k, "batched 2x3x70x45x63");
+    sweep(device, OpId::GemmBatched, args, want, k, "batched 2x3x70x45x63");
 }
 
 void test_start_is_the_automatic_choice(Device device) {

@@ -117,19 +117,14 @@ def test_exact_alpha_beta_in_place(stream, trans_a, trans_b):
 TILES = list(range(1, mf.abi.TILE_THIN))  # the MFMA tiles
 
 
-def wide_loads_possible(a_stored, b_stored):
-    """Whether both stored (row-major) operands qualify for 16-byte loads: the unit-stride extent
-    and the row stride are the row length, which must be a multiple of 4."""
-    return all(x.shape[1] % 4 == 0 for x in (a_stored, b_stored))
-
-
 @pytest.mark.parametrize("tile", TILES)
 @pytest.mark.parametrize("m,n,k", [(300, 260, 1000), (257, 129, 257), (1, 300, 64),
                                    (513, 7, 96), (64, 64, 2000), (129, 65, 36), (2100, 2100, 64)])
 def test_exact_every_tile(stream, tile, m, n, k):
     """Every workgroup tile on edge shapes and all four layouts: bits equal the exact product.
     2100^2 has more tiles than CUs for the 128x128 tile, so both of its launch forms (8
-    wavefronts at one workgroup per CU, 4 beyond) are covered."""
+    wavefronts at one workgroup per CU, 4 beyond) are covered. With staging off, the 256x256
+    tile reads operands that 16-byte loads cannot take with 4-byte direct-to-LDS loads."""
     a = quarter_matrix(m, k, 71)
     b = quarter_matrix(k, n, 72)
     c0 = quarter_matrix(m, n, 73)
@@ -141,18 +136,9 @@ def test_exact_every_tile(stream, tile, m, n, k):
             a_st = np.ascontiguousarray(a.T) if trans_a else a
             b_st = np.ascontiguousarray(b.T) if trans_b else b
             c, buf = guarded_output(stream, (m, n))
-            run = lambda: mf.gemm(dev(a_st, stream), dev(b_st, stream), alpha=1.5,  # noqa: E731
-                                  c0=dev(c0, stream), beta=0.5, trans_a=trans_a,
-                                  trans_b=trans_b, bias=dev(bias, stream), out=c, tile=tile,
-                                  stage=mf.abi.STAGE_NEVER)
-            if tile == mf.abi.TILE_256x256 and not wide_loads_possible(a_st, b_st):
-                # Degenerate extents (m or n of 1) may still qualify; otherwise it is refused.
-                try:
-                    run()
-                except NotImplementedError:
-                    continue
-            else:
-                run()
+            mf.gemm(dev(a_st, stream), dev(b_st, stream), alpha=1.5, c0=dev(c0, stream), beta=0.5,
+                    trans_a=trans_a, trans_b=trans_b, bias=dev(bias, stream), out=c, tile=tile,
+                    stage=mf.abi.STAGE_NEVER)
             assert same_bits(c.numpy(), want), (tile, trans_a, trans_b)
             check_guards(buf)
 
@@ -216,12 +202,13 @@ def test_exact_staged_batched_broadcast(stream):
 
 def test_stage_modes_agree_bitwise(stream, oracle):
     """Staging changes only where operands are read from: with the same tile, realistic inputs
-    give the same bits staged and unstaged (the zero padding adds +0 to each sum)."""
+    give the same bits staged and unstaged (the zero padding adds +0 to each sum). For the
+    256x256 tile that compares the register-staged 16-byte kernel with the direct-to-LDS one."""
     m, n, k = 1021, 515, 1023
     x = oracle.normal(m * k, 0.0, 1.0, 11, 0).reshape(m, k)
     w = oracle.normal(k * n, 0.0, 1.0 / np.sqrt(k), 12, 0).reshape(k, n)
     x_d, w_d = dev(x, stream), dev(w, stream)
-    for tile in TILES[1:]:
+    for tile in TILES:
         plain = mf.gemm(x_d, w_d, tile=tile, stage=mf.abi.STAGE_NEVER).numpy()
         staged = mf.gemm(x_d, w_d, tile=tile, stage=mf.abi.STAGE_ALWAYS).numpy()
         assert np.array_equal(plain.view(np.uint32), staged.view(np.uint32)), tile
@@ -230,9 +217,10 @@ def test_stage_modes_agree_bitwise(stream, oracle):
 
 
 def test_plan_on_baseline_shapes(stream):
-    """mfr_sgemm_plan reports what AUTO runs: the 256x256 tile in place for configs[2], staged
-    operands for configs[3], a short-depth tile for the attention scores; a fixed 256x256 tile
-    with staging off is refused on operands 16-byte loads cannot read, and staged otherwise."""
+    """mfr_sgemm_plan reports what AUTO runs: the 256x256 tile in place for configs[2] and for
+    configs[3] (whose rows 16-byte loads cannot take: that tile copies them straight into LDS),
+    staged operands for configs[3] when staging is asked for, a short-depth tile for the
+    attention scores."""
     abi = mf.abi
     big = mf.DeviceArray.empty((4096, 4096), stream)
     assert mf.gemm_plan(big, big.T, big) == (abi.TILE_256x256, abi.STAGE_NEVER, 1, 1)
@@ -240,16 +228,15 @@ def test_plan_on_baseline_shapes(stream):
     w = mf.DeviceArray.empty((1023, 4099), stream)
     out = mf.DeviceArray.empty((4093, 4099), stream)
     tile, stage, splits, regions = mf.gemm_plan(x, w, out)
-    assert splits == 1
-    assert stage == abi.STAGE_ALWAYS and tile != abi.TILE_AUTO
-    assert mf.gemm_plan(x, w, out, stage=abi.STAGE_NEVER)[1] == abi.STAGE_NEVER
+    assert (tile, stage, splits) == (abi.TILE_256x256, abi.STAGE_NEVER, 1)
+    assert mf.gemm_plan(x, w, out, stage=abi.STAGE_ALWAYS)[1] == abi.STAGE_ALWAYS
     q = mf.DeviceArray.empty((128, 1024, 64), stream)
     scores = mf.DeviceArray.empty((128, 1024, 1024), stream)
     assert mf.gemm_plan(q, q.transpose(-2, -1), scores)[0] in (abi.TILE_128x64, abi.TILE_64x128)
-    with pytest.raises(NotImplementedError):
-        mf.gemm_plan(x, w, out, tile=abi.TILE_256x256, stage=abi.STAGE_NEVER)
+    assert mf.gemm_plan(x, w, out, tile=abi.TILE_256x256, stage=abi.STAGE_NEVER)[:2] == (
+        abi.TILE_256x256, abi.STAGE_NEVER)
     assert mf.gemm_plan(x, w, out, tile=abi.TILE_256x256)[:2] == (abi.TILE_256x256,
-                                                                  abi.STAGE_ALWAYS)
+                                                                  abi.STAGE_NEVER)
     empty = mf.DeviceArray.empty((0, 4099), stream)
     assert mf.gemm_plan(mf.DeviceArray.empty((0, 1023), stream), w, empty)[0] == abi.TILE_AUTO
     # The fixed 256x256 tile on odd operands runs staged, bit-exact.

@@ -8,8 +8,8 @@ pre-activation values are exact: the output must equal the exact result in every
 gelu is bit-exact against the oracle for every float input; the erf form, which uses the device
 library's erfc, is held to 2 ulp). The output sits in a poisoned buffer with guard bands and, in
 some cases, poisoned padding columns, which must survive. A point the ABI refuses
-(NotImplementedError: the 256x256 tile without 16-byte loads, the thin path where it does not
-apply or with a split) must leave the output untouched."""
+(NotImplementedError: the thin path where it does not apply or with a split) must leave the output
+untouched."""
 import numpy as np
 import pytest
 
@@ -123,7 +123,7 @@ def test_random_gemm_exact(stream, oracle, index):
                         tile=tile, stage=stage, splits=splits)
     except NotImplementedError:
         assert same_bits(buf.numpy(), image), what + ": refused, but the output changed"
-        assert tile in (A.TILE_256x256, A.TILE_THIN), what + ": refused"
+        assert tile == A.TILE_THIN, what + ": refused"
         return
 
     got_image = buf.numpy()

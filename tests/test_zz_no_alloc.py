@@ -42,13 +42,14 @@ def _both(stream, a, b, c0=None, bias=None, *, alpha=1.0, beta=0.0, act=abi.ACT_
 
 
 def test_noalloc_matches_sgemm_on_two_calls(stream, oracle):
-    # Call 1: configs[3]'s MLP layer. X [4093, 1023] and W [1023, 4099] are staged (their rows are
-    # not 16-byte multiples): 2 x ~16.8 MB of the scratch array.
+    # Call 1: configs[3]'s MLP layer with staging asked for. X [4093, 1023] and W [1023, 4099]
+    # are copied (their rows are not 16-byte multiples): 2 x ~16.8 MB of the scratch array.
     x = normal(oracle, (4093, 1023), 0.0, 1.0, 41)
     w = normal(oracle, (1023, 4099), 0.0, float(1.0 / np.sqrt(1023.0)), 42)
     bias = uniform(oracle, (4099,), -0.1, 0.1, 43)
     dx, dw, db = _dev(x, stream), _dev(w, stream), _dev(bias, stream)
-    want, got, plan = _both(stream, dx, dw, bias=db, act=abi.ACT_GELU_TANH)
+    want, got, plan = _both(stream, dx, dw, bias=db, act=abi.ACT_GELU_TANH,
+                            stage=abi.STAGE_ALWAYS)
     assert plan[1] == abi.STAGE_ALWAYS, plan
     assert same_bits(got, want), "call 1 (staged MLP layer) differs from mfr_sgemm"
 
