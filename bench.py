@@ -412,11 +412,11 @@ def main() -> int:
                                           / 1e9, 1),
             "note": "fused: one kernel, online softmax, FLOP = 4*B*H*D*S(S+1)/2 (causal pairs); "
                     "composed: the reference's 2 batched GEMMs (4*B*H*S^2*D FLOP, dense), where "
-                    "with packed mask and -inf operands, softmax over materialized scores; its "
-                    "ms_per_call is host wall time per call, with the 512 MiB scores, 512 MiB "
-                    "-inf operand and 128 MiB mask it materializes kept as the stream's scratch "
-                    "arrays between calls and its 32 MiB output allocated per call (its kernels "
-                    "alone take about 1.05 ms)"},
+                    "(the [S, S] causal mask and a -inf scalar read through broadcast views, the "
+                    "scores masked in place: only the removed keys' -inf is written), softmax "
+                    "over the materialized scores; its ms_per_call is host wall time per call, "
+                    "with the 512 MiB scores kept as the stream's scratch array between calls and "
+                    "the 32 MiB output allocated per call"},
         "copy_1gib": {"gbs": round(result["copy"]["bytes"] / (result["copy"]["event_ms"] * 1e-3)
                                    / 1e9, 1),
                       "note": "plain device copy, read+write bytes; the practical HBM ceiling"},

@@ -11,6 +11,7 @@
 #include "mensurflow/ops/elementwise.hpp"
 #include "mensurflow/ops/softmax.hpp"
 #include "ops/checks.hpp"
+#include "ops/where_into.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -80,11 +81,14 @@ Tensor fused_call(const Tensor& q, const Tensor& k, const Tensor& v, const Tenso
     return args.outputs.front();
 }
 
-// -inf wherever `keep` is false, so softmax gives those keys no weight.
-Tensor drop_where_not(const Tensor& keep, const Tensor& scores, Execution execution) {
+// -inf wherever `keep` is false, so softmax gives those keys no weight: where(keep, scores, -inf)
+// written into the scores themselves. They are this call's own temporary, so the values are
+// where()'s without a second scores-sized buffer, and a device whose where kernel reads views
+// (ROCm) writes only the removed keys.
+void drop_where_not(const Tensor& keep, const Tensor& scores, Execution execution) {
     const Tensor minus_infinity =
         Tensor::full({}, -std::numeric_limits<double>::infinity(), DType::F32, scores.device());
-    return where(keep, scores, minus_infinity, execution);
+    detail::where_into(keep, scores, minus_infinity, scores, execution);
 }
 
 // The [lq, lk] Bool lower triangle: query i keeps keys 0..i.
@@ -146,12 +150,12 @@ Tensor attention(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor
         }
     }
     // The composition: the scaled scores come from the GEMM's alpha.
-    Tensor scores = gemm_strided_batched(q, k, scale, nullptr, 0.0f, false, true, execution);
+    const Tensor scores = gemm_strided_batched(q, k, scale, nullptr, 0.0f, false, true, execution);
     if (mask != nullptr) {
-        scores = drop_where_not(*mask, scores, execution);
+        drop_where_not(*mask, scores, execution);
     }
     if (causal) {
-        scores = drop_where_not(causal_keep(lq, lk, q.device()), scores, execution);
+        drop_where_not(causal_keep(lq, lk, q.device()), scores, execution);
     }
     const Tensor weights = softmax(scores, -1, execution);
     return gemm_strided_batched(weights, v, 1.0f, nullptr, 0.0f, false, false, execution);

@@ -7,6 +7,7 @@
 
 #include "core/dispatcher.hpp"
 #include "ops/checks.hpp"
+#include "ops/where_into.hpp"
 
 #include <string>
 
@@ -74,7 +75,10 @@ Tensor gelu(const Tensor& x, bool approximate, Execution execution) {
     return out;
 }
 
-Tensor where(const Tensor& condition, const Tensor& x, const Tensor& y, Execution execution) {
+namespace {
+
+// where()'s checks; the shape its operands broadcast to.
+Shape where_shape(const Tensor& condition, const Tensor& x, const Tensor& y) {
     const OpCheck check("where");
     check.compatible(x, y);
     if (!condition.defined()) {
@@ -86,16 +90,37 @@ Tensor where(const Tensor& condition, const Tensor& x, const Tensor& y, Executio
     if (condition.device() != x.device()) {
         check.fail("condition and values must be on the same device");
     }
-    const Shape shape = detail::broadcast_for(
-        check, detail::broadcast_for(check, x.shape(), y.shape()), condition.shape());
-    Tensor out = Tensor::empty(shape, x.dtype(), x.device());
+    return detail::broadcast_for(check, detail::broadcast_for(check, x.shape(), y.shape()),
+                                 condition.shape());
+}
+
+} // namespace
+
+namespace detail {
+
+void where_into(const Tensor& condition, const Tensor& x, const Tensor& y, const Tensor& out,
+                Execution execution) {
+    const Shape shape = where_shape(condition, x, y);
+    if (!out.defined() || out.shape() != shape || out.dtype() != x.dtype() ||
+        out.device() != x.device() || !out.is_contiguous()) {
+        OpCheck("where").fail("output must be a packed " + std::string(dtype_name(x.dtype())) +
+                              " tensor of shape " + to_string(shape) + " on the inputs' device");
+    }
     const bool as_views =
-        where_reads_views(x.device()) && detail::has_kernel_for(OpId::Where, execution, x.device());
+        where_reads_views(x.device()) && has_kernel_for(OpId::Where, execution, x.device());
     const auto operand = [&](const Tensor& t) {
         return as_views ? t.expand(shape) : packed_as(t, shape);
     };
     // The values come first: the kernel is keyed by their dtype, not the condition's.
-    detail::dispatch(OpId::Where, {{operand(x), operand(y), operand(condition)}, {out}}, execution);
+    dispatch(OpId::Where, {{operand(x), operand(y), operand(condition)}, {out}}, execution);
+}
+
+} // namespace detail
+
+Tensor where(const Tensor& condition, const Tensor& x, const Tensor& y, Execution execution) {
+    const Shape shape = where_shape(condition, x, y);
+    Tensor out = Tensor::empty(shape, x.dtype(), x.device());
+    detail::where_into(condition, x, y, out, execution);
     return out;
 }
 

@@ -283,3 +283,40 @@ def test_where_nd_attention_mask_shape(stream):
                       out=s_d)
     want = np.where(np.broadcast_to(keep, scores.shape) != 0, scores, np.float32(-np.inf))
     assert same_bits(out.numpy(), want.astype(np.float32))
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_where_nd_in_place(stream, oracle, case):
+    """where_nd with out being x or y itself (the same packed array): only the elements that take
+    the other operand are written, so the result must equal the oracle's where on the operands as
+    they were. Masks dense or broadcast (a lower triangle over the last two dimensions), the other
+    operand a broadcast scalar or a full array; rows of a multiple of 4 (the quad kernel) and not
+    (the generic one)."""
+    shapes = [(2, 3, 64, 96), (5, 130), (4, 1024), (3, 7, 8), (2, 2, 6, 3), (1, 4), (16, 256),
+              (3, 5, 12)]
+    shape = shapes[case]
+    rng = np.random.default_rng(950 + case)
+    alias_x = case % 2 == 0
+    print(f"where_nd in place case {case}: shape {shape}, out is {'x' if alias_x else 'y'}",
+          flush=True)
+    base = rng.standard_normal(shape).astype(np.float32)
+    if case % 3 == 0 and len(shape) >= 2:
+        keep = np.tril(np.ones(shape[-2:], np.uint8))
+        c_host, c = np.broadcast_to(keep, shape), dev(keep, stream).expand(shape)
+    else:
+        c_host = (rng.random(shape) > 0.5).astype(np.uint8)
+        c = dev(c_host, stream)
+    if case % 4 < 2:
+        scalar = np.array([-np.inf], np.float32)
+        o_host, other = np.broadcast_to(scalar, shape), dev(scalar, stream).expand(shape)
+    else:
+        o_host = rng.standard_normal(shape).astype(np.float32)
+        other = dev(o_host, stream)
+    out = dev(base, stream)
+    if alias_x:
+        got = mf.where_nd(c, out, other, out=out)
+        want = oracle.where(np.ascontiguousarray(c_host), base, np.ascontiguousarray(o_host))
+    else:
+        got = mf.where_nd(c, other, out, out=out)
+        want = oracle.where(np.ascontiguousarray(c_host), np.ascontiguousarray(o_host), base)
+    assert same_bits(got.numpy(), want.reshape(shape))
