@@ -392,6 +392,7 @@ __global__ __launch_bounds__(WAVES * 64, MIN_WAVES) void attention_kernel(AttnPa
 }
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // Wavefronts per workgroup of attention16_kernel: 16 (256 queries, one workgroup per CU, 4 per
 // SIMD). 8 (two workgroups per CU) measured 165.2 against 162.9 us at configs[4].
@@ -491,42 +492,78 @@ __global__ __launch_bounds__(WAVES * 64) void attention16_kernel(AttnParams p) {
     auto needed = [&](int64_t blk) { return wave_live && (!p.causal || blk * BK <= wq0 + 15); };
 
     // Tile loads: piece u of K is (key u / (D/4), depths 4(u % (D/4))..+3); piece u of V is
-    // (key u % BK, depths 4(u / BK)..+3). Keys at or past `keys` read as zeros.
+    // (key u % BK, depths 4(u / BK)..+3). They are buffer loads: the block's first key row is
+    // the resource's base and its record count ends after the block's last key, so pieces of
+    // keys past the end read as zeros with no per-lane test, and a lane's byte offset within a
+    // tile is one register fixed for the whole key loop (the host keeps BK rows under 2^30
+    // bytes). Loads through a per-block address register made the compiler wait for them
+    // before the next LDS reads.
     float4 kr[kLoads], vr[kLoads];
-    auto load_tiles = [&](int64_t blk) {
+    uint32_t k_off[kLoads], v_off[kLoads];
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+        const int u = static_cast<int>(threadIdx.x) + i * THREADS;
+        const int kkey = u / (D / 4), kq = u % (D / 4);
+        const int vkey = u % BK, vq = u / BK;
+        k_off[i] = u < kQuads ? static_cast<uint32_t>((kkey * p.k_rs + 4 * kq) * 4) : 0x80000000u;
+        v_off[i] = u < kQuads ? static_cast<uint32_t>((vkey * p.v_rs + 4 * vq) * 4) : 0x80000000u;
+    }
+    auto tile_load = [](const float* rows, int64_t row_stride, int keys, uint32_t offset) {
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(rows), 0, static_cast<int>(keys * row_stride * 4), 0x00020000);
+        const u32x4 raw = __builtin_amdgcn_raw_buffer_load_b128(rsrc, static_cast<int>(offset),
+                                                                0, 0);
+        return make_float4(__uint_as_float(raw.x), __uint_as_float(raw.y),
+                           __uint_as_float(raw.z), __uint_as_float(raw.w));
+    };
+    auto load_k = [&](int64_t blk) {
         const int keys = keys_in(blk);
         const float* kb = k_base + blk * BK * p.k_rs;
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) {
+            kr[i] = tile_load(kb, p.k_rs, keys, k_off[i]);
+        }
+    };
+    auto load_v = [&](int64_t blk) {
+        const int keys = keys_in(blk);
         const float* vb = v_base + blk * BK * p.v_rs;
 #pragma unroll
         for (int i = 0; i < kLoads; ++i) {
-            const int u = static_cast<int>(threadIdx.x) + i * THREADS;
-            const int kkey = u / (D / 4), kq = u % (D / 4);
-            const int vkey = u % BK, vq = u / BK;
-            const bool in = u < kQuads;
-            kr[i] = in && kkey < keys
-                        ? *reinterpret_cast<const float4*>(kb + kkey * p.k_rs + 4 * kq)
-                        : make_float4(0.f, 0.f, 0.f, 0.f);
-            vr[i] = in && vkey < keys
-                        ? *reinterpret_cast<const float4*>(vb + vkey * p.v_rs + 4 * vq)
-                        : make_float4(0.f, 0.f, 0.f, 0.f);
+            vr[i] = tile_load(vb, p.v_rs, keys, v_off[i]);
         }
     };
-    auto store_tiles = [&](int which) {
+    auto store_k = [&](int which) {
         float* sk = lds_k(which);
-        float* sv = lds_v(which);
 #pragma unroll
         for (int i = 0; i < kLoads; ++i) {
             const int u = static_cast<int>(threadIdx.x) + i * THREADS;
             if (u < kQuads) {
                 const int kkey = u / (D / 4), kq = u % (D / 4);
-                const int vkey = u % BK, vq = u / BK;
                 *reinterpret_cast<float4*>(sk + kkey * KP + 4 * kq) = kr[i];
+            }
+        }
+    };
+    auto store_v = [&](int which) {
+        float* sv = lds_v(which);
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) {
+            const int u = static_cast<int>(threadIdx.x) + i * THREADS;
+            if (u < kQuads) {
+                const int vkey = u % BK, vq = u / BK;
                 sv[(4 * vq + 0) * VP + vkey] = vr[i].x;
                 sv[(4 * vq + 1) * VP + vkey] = vr[i].y;
                 sv[(4 * vq + 2) * VP + vkey] = vr[i].z;
                 sv[(4 * vq + 3) * VP + vkey] = vr[i].w;
             }
         }
+    };
+    auto load_tiles = [&](int64_t blk) {
+        load_k(blk);
+        load_v(blk);
+    };
+    auto store_tiles = [&](int which) {
+        store_k(which);
+        store_v(which);
     };
 
     auto scores = [&](const float* sk, floatx4(&sacc)[KB]) {
@@ -560,13 +597,17 @@ __global__ __launch_bounds__(WAVES * 64) void attention16_kernel(AttnParams p) {
     auto softmax = [&](int64_t k0, floatx4(&sacc)[KB]) {
         const bool edge = k0 + BK > p.lk || (p.causal && k0 + BK - 1 > wq0);
         if (MASKED || edge) {
+            // In 32-bit lane arithmetic (the 64-bit forms cost registers the key loop lacks):
+            // the wavefront's first query's diagonal offset, clamped to [-32, BK] while uniform,
+            // then this lane's query added (col < 16 keeps both clamps' outcomes).
             const int64_t keys_left = p.lk - k0;
-            const int64_t diag = query - k0;
+            const int64_t first_diag = wq0 - k0;
+            const int base = static_cast<int>(first_diag < -32 ? -32
+                                              : first_diag > BK ? BK
+                                                                : first_diag);
+            const int diag = base + col;
             const int lim_k = static_cast<int>(keys_left < BK ? keys_left : BK) - 4 * g;
-            const int lim_q = static_cast<int>(!p.causal || diag >= BK ? BK
-                                               : diag < -1 ? -1
-                                                           : diag) -
-                              4 * g;
+            const int lim_q = (!p.causal || diag >= BK ? BK : diag < -1 ? -1 : diag) - 4 * g;
 #pragma unroll
             for (int j = 0; j < KB; ++j) {
 #pragma unroll
@@ -813,7 +854,8 @@ void run_attention(mfr_stream& s, const mfr_attention_desc& d) {
     // last diagonal key blocks keep every SIMD busy (configs[4]: 163.6 against 170.0 us).
     // Non-causal it measured 291 against 288 us, at d = 32 96.9 against 93.5 us (causal) and
     // 169.6 against 159.8 us, and its masked form spills; those keep the 32-query kernel.
-    const bool use16 = d.d == 64 && d.causal != 0 && d.mask == nullptr && waves == waves_for(64);
+    const bool use16 = d.d == 64 && d.causal != 0 && d.mask == nullptr && waves == waves_for(64) &&
+                       d.k_rs < (int64_t{1} << 22) && d.v_rs < (int64_t{1} << 22);
     const int64_t block_q = use16 ? 16 * kWaves16 : 32 * waves; // queries per workgroup
     const int64_t q_blocks = (d.lq + block_q - 1) / block_q;
     const int64_t blocks = q_blocks * batch_count;
