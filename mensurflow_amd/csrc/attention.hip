@@ -445,19 +445,23 @@ __global__ __launch_bounds__(WAVES * 64) void attention16_kernel(AttnParams p) {
     const int64_t query = wq0 + col;
     const bool wave_live = wq0 < p.lq;
 
+    // q is held pre-multiplied by scale * log2(e), so the scores come out of the MFMAs already
+    // scaled and in base-2 units: the softmax's weights are then exp2(s - m) with no multiply
+    // per score.
     float qf[DB][4];
     {
         const float* qrow = p.q + off_q + query * p.q_rs + 4 * g;
+        const float to_log2 = p.scale * kLog2e;
 #pragma unroll
         for (int a = 0; a < DB; ++a) {
             float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
             if (query < p.lq) {
                 v = *reinterpret_cast<const float4*>(qrow + 16 * a);
             }
-            qf[a][0] = v.x;
-            qf[a][1] = v.y;
-            qf[a][2] = v.z;
-            qf[a][3] = v.w;
+            qf[a][0] = v.x * to_log2;
+            qf[a][1] = v.y * to_log2;
+            qf[a][2] = v.z * to_log2;
+            qf[a][3] = v.w * to_log2;
         }
     }
     const uint8_t* mask_row = nullptr;
@@ -619,15 +623,7 @@ __global__ __launch_bounds__(WAVES * 64) void attention16_kernel(AttnParams p) {
                             keep = mask_row[(k0 + rel + 4 * g) * p.mask_cs] != 0;
                         }
                     }
-                    sacc[j][r] = keep ? p.scale * sacc[j][r] : -INFINITY;
-                }
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < KB; ++j) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    sacc[j][r] = p.scale * sacc[j][r];
+                    sacc[j][r] = keep ? sacc[j][r] : -INFINITY;
                 }
             }
         }
@@ -643,21 +639,25 @@ __global__ __launch_bounds__(WAVES * 64) void attention16_kernel(AttnParams p) {
         block_max = fmaxf(block_max, __shfl_xor(block_max, 32, 64));
         const float m_new = fmaxf(m_run, block_max);
         const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float rescale = weight(m_run, m_use);
-        m_run = m_new;
-        l_run *= rescale;
+        // The rescale is 1 for every lane whose maximum stayed (most blocks past the first few):
+        // skipped when that holds for the whole wavefront.
+        if (__ballot(m_new != m_run) != 0) {
+            const float rescale = __builtin_amdgcn_exp2f(m_run - m_use);
+            l_run *= rescale;
 #pragma unroll
-        for (int c = 0; c < DB; ++c) {
+            for (int c = 0; c < DB; ++c) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                oacc[c][r] *= rescale;
+                for (int r = 0; r < 4; ++r) {
+                    oacc[c][r] *= rescale;
+                }
             }
         }
+        m_run = m_new;
 #pragma unroll
         for (int j = 0; j < KB; ++j) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float w = weight(sacc[j][r], m_use);
+                const float w = __builtin_amdgcn_exp2f(sacc[j][r] - m_use);
                 sacc[j][r] = w;
                 l_run += w;
             }
