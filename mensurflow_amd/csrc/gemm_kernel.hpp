@@ -497,7 +497,11 @@ constexpr uint32_t kDirectLimit = 0x80000000u;
 // addressing.
 constexpr int kBufferWord3 = 0x00020000;
 
-template <int ROWS, int KT, bool KMAJ, int V, int THREADS> struct DirectSliceLoader {
+// HOIST: keep the K-major offsets in registers across the depth loop (one per instruction of a
+// wave); otherwise they are worked out at every issue (the choice for two 4-byte K-major
+// operands, whose 18 offsets together spilled).
+template <int ROWS, int KT, bool KMAJ, int V, int THREADS, bool HOIST = true>
+struct DirectSliceLoader {
     static constexpr int kPitch = KMAJ ? KT + 4 : ROWS + 8;
     static constexpr int kFloats = KMAJ ? ROWS * (KT + 4) : KT * (ROWS + 8);
     // K-major: the whole image, pads included; otherwise ROWS / (64 V) instructions per depth.
@@ -509,22 +513,88 @@ template <int ROWS, int KT, bool KMAJ, int V, int THREADS> struct DirectSliceLoa
     static_assert(KMAJ || ROWS % (64 * V) == 0, "a depth line is a whole number of instructions");
     static_assert(kPitch % V == 0, "a chunk of V floats never crosses a line of the image");
 
+    // This lane's byte offsets, fixed for the whole depth loop. K-major: one per instruction of
+    // this wave (element (row, depth) of the image position it fills; a pad takes depth KT - V of
+    // its row, in range whenever the slice is). Otherwise: the lane's offset along a depth line
+    // (the line and the instruction's place in it come as the scalar offset).
+    uint32_t off[KMAJ && HOIST ? kPerWave : 1];
+    uint32_t row_bytes, k_bytes;
+
+    // The K-major offset of this lane in instruction j of this wave.
+    __device__ __forceinline__ uint32_t kmaj_offset(int j) const {
+        const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / 64));
+        const int f = ((wave * kPerWave + j) * 64 + static_cast<int>(__lane_id())) * V;
+        const int row = f / kPitch;
+        const int at = f - row * kPitch;
+        const int d = at < KT ? at : KT - V;
+        return static_cast<uint32_t>(row) * row_bytes + static_cast<uint32_t>(d) * 4u;
+    }
+
+    __device__ __forceinline__ DirectSliceLoader(int64_t row_stride, int64_t k_stride) {
+        row_bytes = static_cast<uint32_t>(row_stride) * 4u;
+        k_bytes = static_cast<uint32_t>(k_stride) * 4u;
+        if constexpr (KMAJ && HOIST) {
+#pragma unroll
+            for (int j = 0; j < kPerWave; ++j) {
+                off[j] = kmaj_offset(j);
+            }
+        } else if constexpr (!KMAJ) {
+            off[0] = static_cast<uint32_t>(static_cast<int>(__lane_id()) * V) * 4u;
+        } else {
+            off[0] = 0u;
+        }
+    }
+
+    // One wave-instruction: lane L's V floats from byte voffset + soffset of the resource land at
+    // dst + L * V floats. (No immediate offset: the hardware adds it to the LDS address too.)
+    __device__ __forceinline__ static void load(__amdgpu_buffer_rsrc_t rsrc, float* dst,
+                                                uint32_t voffset, uint32_t soffset) {
+        if constexpr (V == 4) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 16, static_cast<int>(voffset),
+                                                     static_cast<int>(soffset), 0, 0);
+        } else {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 4, static_cast<int>(voffset),
+                                                     static_cast<int>(soffset), 0, 0);
+        }
+    }
+
     // base: element (row 0, depth 0) of the slice; rows_left / k_left: rows and depths inside
-    // (a multiple of V along the unit-stride dimension).
-    __device__ __forceinline__ static void issue(float* lds, const float* base, int64_t row_stride,
-                                                 int64_t k_stride, int rows_left, int k_left) {
+    // (a multiple of V along the unit-stride dimension). A whole slice uses the fixed offsets;
+    // an edge slice works out each lane's element and sends the ones outside to the limit.
+    __device__ __forceinline__ void issue(float* lds, const float* base, int rows_left,
+                                          int k_left) const {
         const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<float*>(base), 0, static_cast<int>(kDirectLimit - 1), kBufferWord3);
         const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / 64));
+        if (rows_left >= ROWS && k_left >= KT) {
+#pragma unroll
+            for (int j = 0; j < kPerWave; ++j) {
+                const int instr = wave * kPerWave + j;
+                if (kInstr % kWaves != 0 && instr >= kInstr) {
+                    break; // uniform: this wave's block ended
+                }
+                if constexpr (KMAJ) {
+                    load(rsrc, lds + instr * 64 * V, HOIST ? off[HOIST ? j : 0] : kmaj_offset(j),
+                         0u);
+                } else {
+                    // The line and the instruction's place in it come as the scalar offset (the
+                    // immediate offset would move the LDS destination as well).
+                    const int line = instr / kPerLine;
+                    const int q = instr % kPerLine;
+                    load(rsrc, lds + line * kPitch + q * 64 * V, off[0],
+                         static_cast<uint32_t>(line) * k_bytes +
+                             static_cast<uint32_t>(q * 64 * V * 4));
+                }
+            }
+            return;
+        }
         const int lane = static_cast<int>(__lane_id());
-        const uint32_t row_bytes = static_cast<uint32_t>(row_stride) * 4u;
-        const uint32_t k_bytes = static_cast<uint32_t>(k_stride) * 4u;
         const int depth_end = k_left < KT ? k_left : KT; // depths of the slice inside the matrix
 #pragma unroll
         for (int j = 0; j < kPerWave; ++j) {
             const int instr = wave * kPerWave + j;
             if (kInstr % kWaves != 0 && instr >= kInstr) {
-                break; // uniform: this wave's block ended
+                break;
             }
             uint32_t offset;
             float* dst;
@@ -548,13 +618,7 @@ template <int ROWS, int KT, bool KMAJ, int V, int THREADS> struct DirectSliceLoa
                                 : kDirectLimit;
                 dst = lds + line * kPitch + (instr % kPerLine) * 64 * V;
             }
-            if constexpr (V == 4) {
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 16, static_cast<int>(offset), 0,
-                                                         0, 0);
-            } else {
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst, 4, static_cast<int>(offset), 0,
-                                                         0, 0);
-            }
+            load(rsrc, dst, offset, 0u);
         }
     }
 };
@@ -571,8 +635,10 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_direct_kernel(Ge
     constexpr int FM = WM / 32;
     constexpr int FN = WN / 32;
     static_assert(KT % 8 == 0 && WM % 32 == 0 && WN % 32 == 0, "tile shape");
-    using LoadA = DirectSliceLoader<BM, KT, AK, VA, THREADS>;
-    using LoadB = DirectSliceLoader<BN, KT, BK, VB, THREADS>;
+    // Two 4-byte K-major operands: 18 hoisted offsets do not fit beside the accumulators.
+    constexpr bool kHoist = !(AK && BK && VA == 1 && VB == 1);
+    using LoadA = DirectSliceLoader<BM, KT, AK, VA, THREADS, kHoist>;
+    using LoadB = DirectSliceLoader<BN, KT, BK, VB, THREADS, kHoist>;
     using FragA = SliceLoader<BM, KT, AK, VA, THREADS>;
     using FragB = SliceLoader<BN, KT, BK, VB, THREADS>;
     static_assert(LoadA::kFloats == FragA::kFloats && LoadB::kFloats == FragB::kFloats,
@@ -620,28 +686,26 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_direct_kernel(Ge
         const int64_t left = kk - s * KT;
         return left <= 0 ? 0 : left < KT ? static_cast<int>(left) : KT;
     };
+    const LoadA load_a(p.a_rs, p.a_cs);
+    const LoadB load_b(p.b_cs, p.b_rs);
     if (slices > 0) {
-        LoadA::issue(tile_a0, a_base, p.a_rs, p.a_cs, w.rows_a, k_left_of(0));
-        LoadB::issue(tile_b0, b_base, p.b_cs, p.b_rs, w.rows_b, k_left_of(0));
+        load_a.issue(tile_a0, a_base, w.rows_a, k_left_of(0));
+        load_b.issue(tile_b0, b_base, w.rows_b, k_left_of(0));
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
     }
     for (int64_t s = 0; s < slices; s += 2) {
         // Slice s from buffer 0; slice s + 1 (zeros past the end) into buffer 1.
-        LoadA::issue(tile_a1, a_base + (s + 1) * a_step, p.a_rs, p.a_cs, w.rows_a,
-                     k_left_of(s + 1));
-        LoadB::issue(tile_b1, b_base + (s + 1) * b_step, p.b_cs, p.b_rs, w.rows_b,
-                     k_left_of(s + 1));
+        load_a.issue(tile_a1, a_base + (s + 1) * a_step, w.rows_a, k_left_of(s + 1));
+        load_b.issue(tile_b1, b_base + (s + 1) * b_step, w.rows_b, k_left_of(s + 1));
         slice_mfma<FragA, FragB, KT, FM, FN, WM, WN, 1>(acc, tile_a0, tile_b0, wave_m, wave_n, 0,
                                                          half, r32);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         // Slice s + 1 from buffer 1; slice s + 2 into buffer 0.
         if (s + 2 < slices) {
-            LoadA::issue(tile_a0, a_base + (s + 2) * a_step, p.a_rs, p.a_cs, w.rows_a,
-                         k_left_of(s + 2));
-            LoadB::issue(tile_b0, b_base + (s + 2) * b_step, p.b_cs, p.b_rs, w.rows_b,
-                         k_left_of(s + 2));
+            load_a.issue(tile_a0, a_base + (s + 2) * a_step, w.rows_a, k_left_of(s + 2));
+            load_b.issue(tile_b0, b_base + (s + 2) * b_step, w.rows_b, k_left_of(s + 2));
         }
         slice_mfma<FragA, FragB, KT, FM, FN, WM, WN, 1>(acc, tile_a1, tile_b1, wave_m, wave_n, 0,
                                                          half, r32);
