@@ -32,8 +32,10 @@
 //   - Direct-to-LDS slices (sgemm_direct_kernel, the 256x256 tile with a 4-byte operand): each
 //     lane's buffer load writes its element into the LDS image itself, so 4-byte operands take
 //     no registers and need no staging copy; elements outside the matrix get an offset past the
-//     buffer's record limit and load as zeros. AUTO takes this over staging when its main launch
-//     is that tile.
+//     buffer's record limit and load as zeros. Its 16-byte form also replaces the register copy
+//     on aligned operands. AUTO still stages a large product's 4-byte operands: the 16-byte
+//     form on the copies is faster than the 4-byte form in place (the MLP: 316 against 327 us,
+//     copies included).
 //   - The epilogue applies the activation chosen once per workgroup, with copies for interior
 //     tiles and for C0, so each copy is straight-line code (gemm_kernel.hpp, write_tile).
 //   - Split-K cuts a long depth into ranges run as workgroups of their own, reduced in order by
@@ -764,28 +766,12 @@ Plan plan_sgemm(const mfr_gemm_desc& d, int cus) {
         }
     }
     plan.c0 = p.c0 != nullptr && p.beta != 0.0f;
-    const auto tile_plan = [&](Plan& q) {
-        const Choice choice = choose(p.m, p.n, p.k, batch_count, cus, d.tile, d.splits, q.c0,
-                                     q.ak, q.bk, thin_b_layout(q.p, q, p.m, p.n), big_tile_ok(q));
-        single_region(q, choice);
-        if (d.tile == MFR_TILE_AUTO && d.splits == 0) {
-            consider_peeling(q, batch_count, cus, choice.us);
-        }
-    };
-    tile_plan(plan);
-    // AUTO staging whose main launch is the 256x256 tile: that tile copies the operands straight
-    // into LDS instead (MLP configs[3]: 330 against 334 us, and neither the copies' launches nor
-    // their workspace), when its main launch is still that tile without the copies.
-    if (d.stage == MFR_STAGE_AUTO && (plan.stage_a || plan.stage_b) &&
-        plan.regions[0].tile == MFR_TILE_256x256) {
-        Plan direct = plan;
-        direct.stage_a = direct.stage_b = false;
-        if (big_tile_ok(direct)) {
-            tile_plan(direct);
-            if (direct.regions[0].tile == MFR_TILE_256x256) {
-                plan = direct;
-            }
-        }
+    const Choice choice = choose(p.m, p.n, p.k, batch_count, cus, d.tile, d.splits, plan.c0,
+                                 plan.ak, plan.bk, thin_b_layout(p, plan, p.m, p.n),
+                                 big_tile_ok(plan));
+    single_region(plan, choice);
+    if (d.tile == MFR_TILE_AUTO && d.splits == 0) {
+        consider_peeling(plan, batch_count, cus, choice.us);
     }
     for (int i = 0; i < plan.region_count; ++i) {
         const Region& r = plan.regions[i];

@@ -217,10 +217,10 @@ def test_stage_modes_agree_bitwise(stream, oracle):
 
 
 def test_plan_on_baseline_shapes(stream):
-    """mfr_sgemm_plan reports what AUTO runs: the 256x256 tile in place for configs[2] and for
-    configs[3] (whose rows 16-byte loads cannot take: that tile copies them straight into LDS),
-    staged operands for configs[3] when staging is asked for, a short-depth tile for the
-    attention scores."""
+    """mfr_sgemm_plan reports what AUTO runs: the 256x256 tile in place for configs[2], staged
+    operands for configs[3] (whose rows 16-byte loads cannot take), the 256x256 tile reading them
+    in place (straight into LDS) when staging is off, a short-depth tile for the attention
+    scores."""
     abi = mf.abi
     big = mf.DeviceArray.empty((4096, 4096), stream)
     assert mf.gemm_plan(big, big.T, big) == (abi.TILE_256x256, abi.STAGE_NEVER, 1, 1)
@@ -228,15 +228,16 @@ def test_plan_on_baseline_shapes(stream):
     w = mf.DeviceArray.empty((1023, 4099), stream)
     out = mf.DeviceArray.empty((4093, 4099), stream)
     tile, stage, splits, regions = mf.gemm_plan(x, w, out)
-    assert (tile, stage, splits) == (abi.TILE_256x256, abi.STAGE_NEVER, 1)
-    assert mf.gemm_plan(x, w, out, stage=abi.STAGE_ALWAYS)[1] == abi.STAGE_ALWAYS
+    assert (tile, stage, splits) == (abi.TILE_256x256, abi.STAGE_ALWAYS, 1)
+    assert mf.gemm_plan(x, w, out, stage=abi.STAGE_NEVER)[:2] == (abi.TILE_256x256,
+                                                                  abi.STAGE_NEVER)
     q = mf.DeviceArray.empty((128, 1024, 64), stream)
     scores = mf.DeviceArray.empty((128, 1024, 1024), stream)
     assert mf.gemm_plan(q, q.transpose(-2, -1), scores)[0] in (abi.TILE_128x64, abi.TILE_64x128)
     assert mf.gemm_plan(x, w, out, tile=abi.TILE_256x256, stage=abi.STAGE_NEVER)[:2] == (
         abi.TILE_256x256, abi.STAGE_NEVER)
     assert mf.gemm_plan(x, w, out, tile=abi.TILE_256x256)[:2] == (abi.TILE_256x256,
-                                                                  abi.STAGE_NEVER)
+                                                                  abi.STAGE_ALWAYS)
     empty = mf.DeviceArray.empty((0, 4099), stream)
     assert mf.gemm_plan(mf.DeviceArray.empty((0, 1023), stream), w, empty)[0] == abi.TILE_AUTO
     # The fixed 256x256 tile on odd operands runs staged, bit-exact.
