@@ -392,9 +392,9 @@ def main() -> int:
         "gemv": gemv,
         "mlp_fused": {"tflops": round(mlp["flops"] / (mlp["event_ms"] * 1e-3) / 1e12, 3),
                       "note": "bias + gelu-tanh in the epilogue; includes staging the odd-strided "
-                              "X and W into aligned copies (faster than reading them in place "
-                              "with 4-byte loads); the 3-column remainder of N = 4099 is a "
-                              "launch of its own",
+                              "X into an aligned copy (W is read in place: the 256x256 tile's "
+                              "buffer loads write its slices straight into LDS); the 3-column "
+                              "remainder of N = 4099 is a launch of its own",
                       "ms_per_call": round(mlp["event_ms"], 4),
                       "traffic": load_traffic("sgemm_mlp"),
                       "frac": round(mlp["flops"] / (mlp["event_ms"] * 1e-3) / 1e12

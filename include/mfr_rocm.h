@@ -155,9 +155,10 @@ typedef struct mfr_gemm_desc {
  * unit-stride extent and its other strides to be multiples of 4 and its base 16-byte aligned
  * (X[4093,1023] row-major is not). Such an operand can first be copied, zero-padded to that
  * shape, into the stream's workspace (one extra pass over it). AUTO stages when the product is
- * large (>= 2^30 flops) and the copy is small next to it (<= 1 byte per 64 flops); the result is
- * the same either way. Without staging, the 256x256 tile reads such an operand in place, with
- * 4-byte buffer loads that write LDS directly. */
+ * large (>= 2^30 flops) and the copy is small next to it (<= 1 byte per 64 flops), except that
+ * under the 256x256 tile it stages only operands with a unit stride along the depth and reads the
+ * others in place; the result is the same either way. Without staging, the 256x256 tile reads
+ * such operands in place, with 4-byte buffer loads that write LDS directly. */
 enum { MFR_STAGE_AUTO = 0, MFR_STAGE_NEVER = 1, MFR_STAGE_ALWAYS = 2 };
 
 /* Workgroup tile of mfr_sgemm (rows x cols x depth slice). AUTO picks one from the shape (with

@@ -33,9 +33,8 @@
 //     lane's buffer load writes its element into the LDS image itself, so 4-byte operands take
 //     no registers and need no staging copy; elements outside the matrix get an offset past the
 //     buffer's record limit and load as zeros. Its 16-byte form also replaces the register copy
-//     on aligned operands. AUTO still stages a large product's 4-byte operands: the 16-byte
-//     form on the copies is faster than the 4-byte form in place (the MLP: 316 against 327 us,
-//     copies included).
+//     on aligned operands. Under it AUTO stages only K-major 4-byte operands (whose in-place
+//     runs of 32 floats touch twice the cache lines) and reads M/N-major ones in place.
 //   - The epilogue applies the activation chosen once per workgroup, with copies for interior
 //     tiles and for C0, so each copy is straight-line code (gemm_kernel.hpp, write_tile).
 //   - Split-K cuts a long depth into ranges run as workgroups of their own, reduced in order by
@@ -766,12 +765,31 @@ Plan plan_sgemm(const mfr_gemm_desc& d, int cus) {
         }
     }
     plan.c0 = p.c0 != nullptr && p.beta != 0.0f;
-    const Choice choice = choose(p.m, p.n, p.k, batch_count, cus, d.tile, d.splits, plan.c0,
-                                 plan.ak, plan.bk, thin_b_layout(p, plan, p.m, p.n),
-                                 big_tile_ok(plan));
-    single_region(plan, choice);
-    if (d.tile == MFR_TILE_AUTO && d.splits == 0) {
-        consider_peeling(plan, batch_count, cus, choice.us);
+    const auto tile_plan = [&](Plan& q) {
+        const Choice choice = choose(p.m, p.n, p.k, batch_count, cus, d.tile, d.splits, q.c0,
+                                     q.ak, q.bk, thin_b_layout(q.p, q, p.m, p.n), big_tile_ok(q));
+        single_region(q, choice);
+        if (d.tile == MFR_TILE_AUTO && d.splits == 0) {
+            consider_peeling(q, batch_count, cus, choice.us);
+        }
+    };
+    tile_plan(plan);
+    // AUTO staging under the 256x256 tile: an operand whose unit stride runs along its rows (M
+    // or N) is read in place instead. Its direct-to-LDS slices are whole runs of 256 floats,
+    // about one cache line more per run than the aligned copy, where a K-major operand's runs of
+    // 32 floats would touch twice the lines. configs[3]: X staged and W in place 323 us, both
+    // staged 331 us, both in place 333 us.
+    if (d.stage == MFR_STAGE_AUTO && plan.regions[0].tile == MFR_TILE_256x256 &&
+        ((plan.stage_a && !plan.ak) || (plan.stage_b && !plan.bk))) {
+        Plan partial = plan;
+        partial.stage_a = plan.stage_a && plan.ak;
+        partial.stage_b = plan.stage_b && plan.bk;
+        if (big_tile_ok(partial)) {
+            tile_plan(partial);
+            if (partial.regions[0].tile == MFR_TILE_256x256) {
+                plan = partial;
+            }
+        }
     }
     for (int i = 0; i < plan.region_count; ++i) {
         const Region& r = plan.regions[i];
