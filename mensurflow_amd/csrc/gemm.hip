@@ -905,6 +905,7 @@ void launch_thin(const Plan& plan, const GemmParams& q, int va, int vb, hipStrea
             default: thin_dot_kernel<1, kThinCols, true><<<grid, kThinThreads, 0, stream>>>(t);
             }
         }
+        mfr::check_launch("thin_dot_kernel");
         return;
     }
     if (width == 4) {
