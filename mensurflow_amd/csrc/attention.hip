@@ -394,9 +394,12 @@ __global__ __launch_bounds__(WAVES * 64, MIN_WAVES) void attention_kernel(AttnPa
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-// Wavefronts per workgroup of attention16_kernel: 16 (256 queries, one workgroup per CU, 4 per
-// SIMD). 8 (two workgroups per CU) measured 165.2 against 162.9 us at configs[4].
-constexpr int kWaves16 = 16;
+// Wavefronts per workgroup of attention16_kernel: 8 (128 queries, two workgroups per CU, 4
+// wavefronts per SIMD), so one workgroup's prologue, diagonal blocks and output store overlap the
+// other's key loop: configs[4] 173.9 against 176.2 us with 16 (256 queries, one per CU) on one box.
+// (Before the K/V buffer loads took the kernel from 120 to 100 registers, 16 measured faster:
+// 162.9 against 165.2 us.)
+constexpr int kWaves16 = 8;
 
 // The same op with 16 queries per wavefront on v_mfma_f32_16x16x4_f32 (4x4 accumulators per
 // lane per 16x16 block): a wavefront holds 16 scores, 16 output values and D/4 query values per
@@ -413,7 +416,7 @@ constexpr int kWaves16 = 16;
 //     one key and stores them down a column; adjacent lanes take adjacent keys, so the stores
 //     hit distinct banks). Both are double-buffered with one barrier per key block.
 template <int D, int BK, bool MASKED, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) void attention16_kernel(AttnParams p) {
+__global__ __launch_bounds__(WAVES * 64, 4) void attention16_kernel(AttnParams p) {
     constexpr int THREADS = WAVES * 64;
     constexpr int BLOCK_Q = WAVES * 16;
     constexpr int KB = BK / 16;  // 16-key blocks per key block
