@@ -208,8 +208,8 @@ Choice choose(int64_t m, int64_t n, int64_t k, int64_t batch, int cus,
     best.per = k;
     if (fixed_tile == MFR_TILE_256x256 && !big_ok) {
         throw mfr::Error(MFR_E_UNSUPPORTED,
-                         "sgemm: the 256x256 tile reads an operand with 4-byte loads here, and "
-                         "its strides put a slice more than 2^30 bytes across");
+                         "sgemm: the 256x256 tile reads its slices with 32-bit offsets, and an "
+                         "operand's strides put a slice more than 2^30 bytes across");
     }
     const bool thin = thin_possible(m, n, ak, bk) && fixed_splits <= 1;
     if (fixed_tile == MFR_TILE_THIN) {
@@ -643,16 +643,11 @@ int64_t staged_floats_padded(const Operand& o, const GemmParams& p) {
     return (staged_floats(o, p) + 63) / 64 * 64; // 256-byte aligned parts of the workspace
 }
 
-// Whether the 256x256 tile can read the plan's operands (as they will be after staging): always
-// when both take 16-byte loads (its register-staged form); otherwise it copies both slices
-// straight into LDS with buffer loads, whose byte offsets within a slice must stay below 2^30:
-// 255 lines of a K-major operand, or 31 depth lines of the other, plus a line's own extent.
+// Whether the 256x256 tile can read the plan's operands (as they will be after staging): it
+// copies both slices straight into LDS with buffer loads, whose byte offsets within a slice must
+// stay below 2^30: 255 lines of a K-major operand, or 31 depth lines of the other, plus a line's
+// own extent.
 bool big_tile_ok(const Plan& plan) {
-    const int va = plan.stage_a ? 4 : plan.va;
-    const int vb = plan.stage_b ? 4 : plan.vb;
-    if (va == 4 && vb == 4) {
-        return true;
-    }
     GemmParams p = plan.p;
     const auto fits = [](const Operand& o, bool kmaj, bool staged) {
         const int64_t line = staged ? round4(o.inner) : *o.line_stride;

@@ -550,6 +550,28 @@ def test_thin_k_zero_and_refusals(stream):
                 dev(np.ones((64, 3), np.float32), stream), tile=THIN, splits=2)
 
 
+def test_big_tile_slice_offset_limit(stream):
+    """The 256x256 tile addresses each depth slice with 32-bit offsets below 2^30 bytes. An
+    operand whose rows lie 2^22 floats apart (a slice of 256 such rows spans 4 GiB) makes a fixed
+    256x256 tile refused, for 4-byte and 16-byte loads alike; AUTO takes another tile, and the
+    bits are exact (quarter-integer inputs)."""
+    far = 1 << 22
+    for k in (5, 8):  # 4-byte loads (odd k), 16-byte loads
+        m, n = 3, 40
+        a = quarter_matrix(m, k, 271)
+        b = quarter_matrix(k, n, 272)
+        host = np.zeros((m, far), np.float32)
+        host[:, :k] = a
+        a_view = dev(host, stream).slice(1, 0, k)  # [m, k], rows 2^22 floats apart
+        b_d = dev(b, stream)
+        with pytest.raises(NotImplementedError):
+            mf.gemm(a_view, b_d, tile=mf.abi.TILE_256x256, stage=mf.abi.STAGE_NEVER)
+        assert mf.gemm_plan(a_view, b_d, mf.DeviceArray.empty((m, n), stream),
+                            stage=mf.abi.STAGE_NEVER)[0] != mf.abi.TILE_256x256
+        got = mf.gemm(a_view, b_d, stage=mf.abi.STAGE_NEVER).numpy()
+        assert same_bits(got, exact_product(a, b).astype(np.float32)), k
+
+
 def test_thin_automatic_choice(stream):
     """AUTO takes the thin path for a long product with a few columns (the MLP's 3-column edge
     strip, 4 aligned columns), and the MFMA tiles where the output fills them."""
