@@ -480,6 +480,8 @@ int64_t staged_floats(const Operand& o, const GemmParams& p) {
     return count;
 }
 
+void repoint_staged(Operand& o, float* dst, const GemmParams& p);
+
 // Copies `o` into dst (staged_floats(o, p) floats, 16-byte aligned) and points the GEMM at it.
 void stage_operand(Operand& o, float* dst, const GemmParams& p, hipStream_t stream) {
     const int64_t pitch = round4(o.inner);
@@ -498,7 +500,13 @@ void stage_operand(Operand& o, float* dst, const GemmParams& p, hipStream_t stre
     stage_kernel<<<static_cast<unsigned>(rows), 256, 0, stream>>>(o.base, dst, o.lines, o.inner,
                                                                   *o.line_stride, pitch, sb);
     mfr::check_launch("stage_kernel");
-    // New strides: lines `pitch` apart, matrices contiguous in the order of StageBatch.
+    repoint_staged(o, dst, p);
+}
+
+// Points the GEMM at o's staged copy in dst: lines round4(inner) apart, matrices contiguous in
+// the order of StageBatch.
+void repoint_staged(Operand& o, float* dst, const GemmParams& p) {
+    const int64_t pitch = round4(o.inner);
     int64_t next = o.lines * pitch;
     for (int d = p.batch_dims - 1; d >= 0; --d) {
         if (o.batch_stride[d] != 0) {
@@ -810,8 +818,11 @@ int64_t partial_floats(const Plan& plan) {
 }
 
 // The thin path on the product q describes (thin_possible holds): C = A B by rows of A when
-// n <= 8 and A is read along k, else C^T = B^T A^T by rows of B^T.
-void launch_thin(const Plan& plan, const GemmParams& q, int va, int vb, hipStream_t stream) {
+// n <= 8 and A is read along k, else C^T = B^T A^T by rows of B^T. With stage != nullptr (rows of
+// A read 4 bytes at a time, one matrix, k * columns within kStripLdsFloats), the same launch also
+// writes A's zero-padded copy, lines stage_rs floats apart (strip_stage_kernel).
+void launch_thin(const Plan& plan, const GemmParams& q, int va, int vb, hipStream_t stream,
+                 float* stage = nullptr, int64_t stage_rs = 0) {
     ThinParams t{};
     bool along_n = true;
     thin_possible(q.m, q.n, plan.ak, plan.bk, &along_n);
@@ -870,6 +881,10 @@ void launch_thin(const Plan& plan, const GemmParams& q, int va, int vb, hipStrea
     t.alpha = q.alpha;
     t.beta = q.beta;
     t.blocks_per_batch = (t.rows + kThinDotRows - 1) / kThinDotRows;
+    t.stage = stage;
+    t.stage_rs = stage_rs;
+    mfr::require(stage == nullptr || (along_n && width == 1 && q.batch_count == 1),
+                 "sgemm: the strip stages A only from 4-byte rows of one matrix");
     const int64_t blocks = t.blocks_per_batch * q.batch_count;
     mfr::require(blocks < (int64_t{1} << 31), "sgemm: problem too large for one launch");
     const unsigned grid = static_cast<unsigned>(blocks);
@@ -885,6 +900,20 @@ void launch_thin(const Plan& plan, const GemmParams& q, int va, int vb, hipStrea
                     (t.cols == c || b_padded);
     for (int d = 0; d < t.batch_dims; ++d) {
         b_pieces = b_pieces && t.b_bs[d] % piece == 0;
+    }
+    if (stage != nullptr) {
+        mfr::require(t.k * c <= kStripLdsFloats, "sgemm: the strip's B' does not fit in LDS");
+        const unsigned strip_grid = static_cast<unsigned>((t.rows + kStripWaves - 1) / kStripWaves);
+        const size_t lds = sizeof(float) * static_cast<size_t>(t.k * c);
+        switch (c) {
+        case 1: strip_stage_kernel<1><<<strip_grid, 64 * kStripWaves, lds, stream>>>(t); break;
+        case 2: strip_stage_kernel<2><<<strip_grid, 64 * kStripWaves, lds, stream>>>(t); break;
+        case 4: strip_stage_kernel<4><<<strip_grid, 64 * kStripWaves, lds, stream>>>(t); break;
+        default:
+            strip_stage_kernel<kThinCols><<<strip_grid, 64 * kStripWaves, lds, stream>>>(t);
+        }
+        mfr::check_launch("strip_stage_kernel");
+        return;
     }
     if (b_pieces) {
         if (width == 4) {
@@ -944,7 +973,8 @@ bool streamed_output(const GemmParams& q) {
 
 // Launches the kernel (and the reduce, when split) for region r of the product p describes.
 void launch_region(const Plan& plan, const GemmParams& p, const Region& r, int va, int vb,
-                   float* partial, int cus, hipStream_t stream) {
+                   float* partial, int cus, hipStream_t stream, float* stage = nullptr,
+                   int64_t stage_rs = 0) {
     using mfr::require;
     GemmParams q = p;
     q.m = r.m;
@@ -955,7 +985,7 @@ void launch_region(const Plan& plan, const GemmParams& p, const Region& r, int v
     q.c0 = p.c0 != nullptr ? p.c0 + r.m_off * p.c0_rs + r.n_off : nullptr;
     q.bias = p.bias != nullptr ? p.bias + r.n_off : nullptr;
     if (r.tile == MFR_TILE_THIN) {
-        launch_thin(plan, q, va, vb, stream);
+        launch_thin(plan, q, va, vb, stream, stage, stage_rs);
         return;
     }
     const int tile = r.tile;
@@ -1138,18 +1168,44 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d, float* scratch = nullptr,
         }
     }
     float* partial = partial_floats(plan) > 0 ? ws : nullptr;
-    if (plan.stage_a) {
-        stage_operand(oa, ws + partial_floats(plan), p, s.stream);
-        p.a = oa.base;
-        va = 4;
-    }
     if (plan.stage_b) {
         stage_operand(ob, ws + partial_floats(plan) + fa, p, s.stream);
         p.b = ob.base;
         vb = 4;
     }
+    // A staged K-major A (rows of k floats) beside a peeled strip of at most 8 columns over all of
+    // its rows (the MLP's 4093 x 3): the strip's launch reads A's rows once and writes the copy
+    // too, instead of a copy launch and then the strip reading the copy.
+    int fused = -1;
+    if (plan.stage_a && plan.ak && va == 1 && p.batch_count == 1) {
+        for (int i = 1; i < plan.region_count; ++i) {
+            const Region& r = plan.regions[i];
+            bool along_n = false;
+            if (r.tile == MFR_TILE_THIN && r.m_off == 0 && r.m == p.m &&
+                thin_possible(r.m, r.n, plan.ak, plan.bk, &along_n) && along_n &&
+                p.k * (r.n <= 1 ? 1 : r.n <= 2 ? 2 : r.n <= 4 ? 4 : kThinCols) <=
+                    kStripLdsFloats) {
+                fused = i;
+                break;
+            }
+        }
+    }
+    if (fused >= 0) {
+        float* dst = ws + partial_floats(plan);
+        launch_region(plan, p, plan.regions[fused], va, vb, partial, s.compute_units, s.stream,
+                      dst, round4(oa.inner));
+        repoint_staged(oa, dst, p);
+        p.a = oa.base;
+        va = 4;
+    } else if (plan.stage_a) {
+        stage_operand(oa, ws + partial_floats(plan), p, s.stream);
+        p.a = oa.base;
+        va = 4;
+    }
     for (int i = 0; i < plan.region_count; ++i) {
-        launch_region(plan, p, plan.regions[i], va, vb, partial, s.compute_units, s.stream);
+        if (i != fused) {
+            launch_region(plan, p, plan.regions[i], va, vb, partial, s.compute_units, s.stream);
+        }
     }
 }
 

@@ -135,8 +135,9 @@ template <int ROWS, int KT, bool KMAJ, int V, int THREADS> struct SliceLoader {
 // Writes a wavefront's accumulators: block (i, j), element e is C(row0 + 32i + 8(e/4) + e%4,
 // col0 + 32j), as
 //   C = act(fl(fl(fl(alpha * acc) + fl(beta * C0)) + bias))      (RAW: C = acc),
-// the C0 term only when c0 is non-null and the bias only when p.bias is non-null, so the roundings
-// are the reference's. alpha * acc is exact for alpha == 1. INTERIOR: every row and column is
+// the C0 term only when c0 is non-null, so the roundings are the reference's. Without a bias, -0
+// is added (x + -0 is x for every x, -0 included), which spares a test per element. alpha * acc
+// is exact for alpha == 1. INTERIOR: every row and column is
 // inside C (no checks). C0 == kC0Batched: c0 is non-null and a row-block's C0 values are all
 // loaded before any is used, so the loads overlap; kC0None: no C0; kC0Checked: c0 checked per
 // element (one copy of the code for both cases). STREAM: non-temporal stores.
@@ -144,7 +145,23 @@ enum { kC0None = 0, kC0Batched = 1, kC0Checked = 2 };
 template <int FM, int FN, int ACT, bool INTERIOR, bool RAW, int C0, bool STREAM = false>
 __device__ __forceinline__ void write_tile(const floatx16 (&acc)[FM][FN], float* c, int64_t c_rs,
                                            const float* c0, int64_t c0_rs, const GemmParams& p,
-                                           int64_t row0, int64_t col0) {
+                                           int64_t row0, int64_t col0,
+                                           const double* exp_table = nullptr) {
+    // Kernel parameters read once: per element, the compiler would reload them after each store.
+    const float alpha = p.alpha;
+    const float beta = p.beta;
+    const float* const bias_base = RAW ? nullptr : p.bias;
+    // The bias of each column block, loaded before any store and waited for at once (the empty
+    // asm reads it): a first use inside a predicated element would leave the load pending on the
+    // paths that skip it, and every later element would wait for the memory counter, which also
+    // counts the stores issued since.
+    float bias_of[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int64_t col = col0 + 32 * j;
+        bias_of[j] = bias_base != nullptr && (INTERIOR || col < p.n) ? bias_base[col] : -0.0f;
+        asm volatile("" ::"v"(bias_of[j]));
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
         const int64_t row_i = row0 + 32 * i;
@@ -168,36 +185,60 @@ __device__ __forceinline__ void write_tile(const floatx16 (&acc)[FM][FN], float*
             if (!INTERIOR && col >= p.n) {
                 continue;
             }
-            const float bias = !RAW && p.bias != nullptr ? p.bias[col] : 0.0f;
+            const float bias = bias_of[j];
+            // Elements outside C (rows past m) are computed all the same and only the loads and
+            // stores are predicated, so no branch separates them. The tanh gelu takes them two
+            // at a time (gelu_tanh_n): each wavefront then has two independent double-precision
+            // chains to interleave.
+            constexpr int kGroup = ACT == MFR_ACT_GELU_TANH ? 2 : 1;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int dr = 8 * (e / 4) + e % 4;
-                if (!INTERIOR && row_i + dr >= p.m) {
-                    continue;
-                }
-                float v = acc[i][j][e];
-                if constexpr (!RAW) {
-                    v = p.alpha * v;
-                    if constexpr (C0 == kC0Batched) {
-                        const float scaled = p.beta * c0v[j][e];
-                        v = v + scaled;
-                    } else if constexpr (C0 == kC0Checked) {
-                        if (c0 != nullptr) {
-                            const float scaled = p.beta * c0[(row_i + dr) * c0_rs + col];
-                            v = v + scaled;
+            for (int e0 = 0; e0 < 16; e0 += kGroup) {
+                float v[kGroup];
+                bool row_ok[kGroup];
+#pragma unroll
+                for (int g = 0; g < kGroup; ++g) {
+                    const int e = e0 + g;
+                    const int dr = 8 * (e / 4) + e % 4;
+                    row_ok[g] = INTERIOR || row_i + dr < p.m;
+                    float x = acc[i][j][e];
+                    if constexpr (!RAW) {
+                        x = alpha * x;
+                        if constexpr (C0 == kC0Batched) {
+                            const float scaled = beta * c0v[j][e];
+                            x = x + scaled;
+                        } else if constexpr (C0 == kC0Checked) {
+                            if (c0 != nullptr) {
+                                const float c0_value =
+                                    row_ok[g] ? c0[(row_i + dr) * c0_rs + col] : 0.0f;
+                                const float scaled = beta * c0_value;
+                                x = x + scaled;
+                            }
                         }
+                        x = x + bias; // -0 without a bias: x + -0 is x
                     }
-                    if (p.bias != nullptr) {
-                        v = v + bias;
-                    }
-                    if constexpr (ACT != MFR_ACT_NONE) {
-                        v = mfr::dev::gelu(v, ACT);
+                    v[g] = x;
+                }
+                float out[kGroup];
+                if constexpr (ACT == MFR_ACT_GELU_TANH) {
+                    gelu_math::gelu_tanh_n<kGroup>(v, out, exp_table);
+                } else {
+#pragma unroll
+                    for (int g = 0; g < kGroup; ++g) {
+                        out[g] = ACT == MFR_ACT_NONE ? v[g] : mfr::dev::gelu(v[g], ACT);
                     }
                 }
-                if constexpr (STREAM) {
-                    __builtin_nontemporal_store(v, &c_i[dr * c_rs + 32 * j]);
-                } else {
-                    c_i[dr * c_rs + 32 * j] = v;
+#pragma unroll
+                for (int g = 0; g < kGroup; ++g) {
+                    const int e = e0 + g;
+                    const int dr = 8 * (e / 4) + e % 4;
+                    if (!row_ok[g]) {
+                        continue;
+                    }
+                    if constexpr (STREAM) {
+                        __builtin_nontemporal_store(out[g], &c_i[dr * c_rs + 32 * j]);
+                    } else {
+                        c_i[dr * c_rs + 32 * j] = out[g];
+                    }
                 }
             }
         }
@@ -205,12 +246,27 @@ __device__ __forceinline__ void write_tile(const floatx16 (&acc)[FM][FN], float*
 }
 
 // The epilogue for activation ACT. Without one it is dispatched on C0 and on whether the tile is
-// interior; a gelu epilogue is one copy (its transcendental work outweighs the checks).
+// interior. The tanh gelu has two copies without C0 (the MLP's case), interior and edge: with C0
+// tested and loaded between the elements, each element waits for the memory counter, which also
+// counts the stores before it, and the double-precision chains run one after another. Every
+// other gelu epilogue is one checked copy.
 template <int FM, int FN, int ACT>
 __device__ __forceinline__ void epilogue(const floatx16 (&acc)[FM][FN], float* c, int64_t c_rs,
                                          const float* c0, int64_t c0_rs, const GemmParams& p,
-                                         int64_t row0, int64_t col0, bool interior) {
-    if constexpr (ACT != MFR_ACT_NONE) {
+                                         int64_t row0, int64_t col0, bool interior,
+                                         const double* exp_table) {
+    if constexpr (ACT == MFR_ACT_GELU_TANH) {
+        if (interior && c0 == nullptr) {
+            write_tile<FM, FN, ACT, true, false, kC0None>(acc, c, c_rs, c0, c0_rs, p, row0, col0,
+                                                          exp_table);
+        } else if (c0 == nullptr) {
+            write_tile<FM, FN, ACT, false, false, kC0None>(acc, c, c_rs, c0, c0_rs, p, row0, col0,
+                                                           exp_table);
+        } else {
+            write_tile<FM, FN, ACT, false, false, kC0Checked>(acc, c, c_rs, c0, c0_rs, p, row0,
+                                                              col0, exp_table);
+        }
+    } else if constexpr (ACT != MFR_ACT_NONE) {
         write_tile<FM, FN, ACT, false, false, kC0Checked>(acc, c, c_rs, c0, c0_rs, p, row0, col0);
     } else if (c0 != nullptr) {
         if (interior) {
@@ -319,7 +375,7 @@ __device__ __forceinline__ void slice_mfma(floatx16 (&acc)[FM][FN], const float*
 template <int BM, int BN, int WM, int WN, int FM, int FN>
 __device__ __forceinline__ void finish_tile(const floatx16 (&acc)[FM][FN], const GemmParams& p,
                                             const TileWork& w, int wave_m, int wave_n, int half,
-                                            int r32) {
+                                            int r32, const double* exp_table) {
     // Accumulator e of block (i, j) is C(row, col) with row = 32i + 8(e/4) + 4*half + e%4,
     // col = 32j + lane%32 (v_mfma_f32_32x32x2_f32 layout).
     const int64_t row0 = w.m0 + wave_m * WM + 4 * half;
@@ -343,13 +399,13 @@ __device__ __forceinline__ void finish_tile(const floatx16 (&acc)[FM][FN], const
     // over every accumulator, the three would not fit the instruction cache together.
     if (p.act == MFR_ACT_NONE) {
         epilogue<FM, FN, MFR_ACT_NONE>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
-                                       interior);
+                                       interior, exp_table);
     } else if (p.act == MFR_ACT_GELU_TANH) {
         epilogue<FM, FN, MFR_ACT_GELU_TANH>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
-                                            interior);
+                                            interior, exp_table);
     } else {
         epilogue<FM, FN, MFR_ACT_GELU_ERF>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
-                                           interior);
+                                           interior, exp_table);
     }
 }
 
@@ -474,7 +530,8 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * WAVES_K * 64) void sgemm_kernel
             }
         }
     }
-    finish_tile<BM, BN, WM, WN, FM, FN>(acc, p, w, wave_m, wave_n, half, r32);
+    finish_tile<BM, BN, WM, WN, FM, FN>(acc, p, w, wave_m, wave_n, half, r32,
+                                        gelu_math::kExp2Table);
 }
 
 // ---- the direct-to-LDS form ---------------------------------------------------------------------
@@ -650,6 +707,13 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_direct_kernel(Ge
     __shared__ __align__(16) float tile_a1[LoadA::kFloats];
     __shared__ __align__(16) float tile_b0[LoadB::kFloats];
     __shared__ __align__(16) float tile_b1[LoadB::kFloats];
+    // The tanh gelu's exp table, copied into LDS: the epilogue's per-lane reads of it then wait
+    // on the LDS counter alone. From global memory, each value's wait for its table load would
+    // also wait for the output stores issued before it (one counter covers both).
+    __shared__ double gelu_table[64];
+    if (p.act == MFR_ACT_GELU_TANH && threadIdx.x < 64) {
+        gelu_table[threadIdx.x] = gelu_math::kExp2Table[threadIdx.x];
+    }
 
     const TileWork w = tile_work<BM, BN>(p);
     const float* a_base = p.a + w.off_a + w.m0 * p.a_rs + w.k_begin * p.a_cs;
@@ -712,7 +776,10 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_direct_kernel(Ge
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
     }
-    finish_tile<BM, BN, WM, WN, FM, FN>(acc, p, w, wave_m, wave_n, half, r32);
+    if (slices == 0) {
+        __syncthreads(); // the gelu table's copy (no slice barrier has made it visible)
+    }
+    finish_tile<BM, BN, WM, WN, FM, FN>(acc, p, w, wave_m, wave_n, half, r32, gelu_table);
 }
 
 } // namespace mfr::gemm

@@ -25,6 +25,14 @@ constexpr int kThinThreads = 64 * kThinWaves;
 constexpr int kThinDotRows = kThinRowsPerWave * kThinWaves; // rows per workgroup
 constexpr int kThinUnroll = 2;
 
+// Steps of 64 * VA depths a wavefront loads before it adds any. 4-byte loads take 4 times the
+// steps for the same depths, so as many loads are in flight per round trip to memory. The count
+// is part of the arithmetic: each lane adds its depths in increasing order, and the steps past k
+// add 0 * 0, which turns a sum of -0 into +0, so strip_stage_kernel takes the same count.
+constexpr int thin_unroll(int va, int c) {
+    return va == 4 ? kThinUnroll : c == kThinCols ? 2 * kThinUnroll : 4 * kThinUnroll;
+}
+
 struct ThinParams {
     const float* a;
     const float* b;
@@ -43,6 +51,10 @@ struct ThinParams {
     int32_t act;
     int64_t blocks_per_batch;
     float alpha, beta;
+    // strip_stage_kernel only: A' row r is also copied to stage + r * stage_rs, zero-padded from
+    // k to stage_rs (one matrix, no batch).
+    float* stage;
+    int64_t stage_rs;
 };
 
 // Offsets of batch matrix `index` (linear order) into A', B', C' and C0'.
@@ -109,14 +121,15 @@ __global__ __launch_bounds__(kThinThreads) void thin_dot_kernel(ThinParams p) {
         valid[r] = row0 + r < p.rows;
         a_row[r] = t.a + (valid[r] ? row0 + r : 0) * p.a_rs;
     }
-    constexpr int kStep = 64 * VA * kThinUnroll; // depths per group
-    // kThinUnroll steps of 64 * VA depths: every load of a group is issued before any is used;
-    // steps past k load nothing and add nothing.
+    // kUnroll steps of 64 * VA depths: every load of a group is issued before any is used;
+    // steps past k load zeros and add 0 * 0.
+    constexpr int kUnroll = thin_unroll(VA, C);
+    constexpr int kStep = 64 * VA * kUnroll; // depths per group
     for (int64_t base = static_cast<int64_t>(lane) * VA; base < p.k; base += kStep) {
-        float a[kThinUnroll][kThinRowsPerWave][VA];
-        float b[kThinUnroll][VA][C];
+        float a[kUnroll][kThinRowsPerWave][VA];
+        float b[kUnroll][VA][C];
 #pragma unroll
-        for (int u = 0; u < kThinUnroll; ++u) {
+        for (int u = 0; u < kUnroll; ++u) {
             const int64_t kk = base + u * 64 * VA;
             const bool in_k = kk < p.k;
 #pragma unroll
@@ -164,7 +177,7 @@ __global__ __launch_bounds__(kThinThreads) void thin_dot_kernel(ThinParams p) {
             }
         }
 #pragma unroll
-        for (int u = 0; u < kThinUnroll; ++u) {
+        for (int u = 0; u < kUnroll; ++u) {
 #pragma unroll
             for (int v = 0; v < VA; ++v) {
 #pragma unroll
@@ -197,6 +210,113 @@ __global__ __launch_bounds__(kThinThreads) void thin_dot_kernel(ThinParams p) {
     const int j = lane % C;
     if (r < kThinRowsPerWave && row0 + r < p.rows && j < cols) {
         thin_store(p, t, row0 + r, j, mine);
+    }
+}
+
+// A peeled strip of at most 8 columns over every row of a K-major A whose rows 16-byte loads
+// cannot take, and the staging of that A for the MFMA tiles, in one launch: each wavefront takes
+// one row of A' = A, copies it to p.stage (zero-padded from k to stage_rs) as it reads it, and sums
+// its products with B', which the workgroup keeps in LDS (k x C floats, filled once). The sums are
+// thin_dot_kernel<1, C>'s bit for bit: lane l adds depths l, l + 64, ... in increasing order in
+// groups of thin_unroll(1, C) steps, then the wavefront's butterfly. One matrix, no batch.
+constexpr int kStripWaves = 16;
+constexpr int64_t kStripLdsFloats = 16384; // k * C at most (64 KiB of LDS)
+
+template <int C>
+__global__ __launch_bounds__(64 * kStripWaves) void strip_stage_kernel(ThinParams p) {
+    static_assert(C == 1 || C == 2 || C == 4 || C == kThinCols, "C is 1, 2, 4 or 8");
+    extern __shared__ float b_lds[]; // B'(d, j) at b_lds[d * C + j], zero past p.cols
+    constexpr int kUnroll = thin_unroll(1, C);
+    constexpr int64_t kStep = 64 * kUnroll;
+    const int lane = threadIdx.x % 64;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kStripWaves + threadIdx.x / 64;
+    const bool active = row < p.rows;
+    const float* a_row = p.a + (active ? row : 0) * p.a_rs;
+    // A group of depths of this lane's row (zeros past k); the next group is always in flight
+    // while the current one is copied and added, and the first while B' fills LDS.
+    const auto load_group = [&](int64_t base, float (&a)[kUnroll]) {
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int64_t kk = base + 64 * u;
+            a[u] = active && kk < p.k ? a_row[kk] : 0.0f;
+        }
+    };
+    float a[kUnroll];
+    load_group(lane, a);
+    const int cols = static_cast<int>(p.cols);
+    for (int64_t i = threadIdx.x; i < p.k * C; i += blockDim.x) {
+        const int64_t d = i / C;
+        const int j = static_cast<int>(i % C);
+        b_lds[i] = j < cols ? p.b[d * p.b_rs + j * p.b_cs] : 0.0f;
+    }
+    __syncthreads();
+    if (!active) {
+        return;
+    }
+    float* copy = p.stage + row * p.stage_rs;
+    float acc[C] = {};
+    for (int64_t base = lane; base < p.k; base += kStep) {
+        float next[kUnroll];
+        load_group(base + kStep, next);
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int64_t kk = base + 64 * u;
+            if (kk < p.k) {
+                copy[kk] = a[u];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int64_t kk = base + 64 * u;
+            float b[C];
+            if (kk < p.k) {
+                if constexpr (C >= 4) {
+#pragma unroll
+                    for (int h = 0; h < C / 4; ++h) {
+                        const float4 w = *reinterpret_cast<const float4*>(b_lds + kk * C + 4 * h);
+                        b[4 * h + 0] = w.x;
+                        b[4 * h + 1] = w.y;
+                        b[4 * h + 2] = w.z;
+                        b[4 * h + 3] = w.w;
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < C; ++j) {
+                        b[j] = b_lds[kk * C + j];
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < C; ++j) {
+                    b[j] = 0.0f;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < C; ++j) {
+                acc[j] = __builtin_fmaf(a[u], b[j], acc[j]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            a[u] = next[u];
+        }
+    }
+    if (p.k + lane < p.stage_rs) {
+        copy[p.k + lane] = 0.0f; // the padding (fewer than 4 floats)
+    }
+    float mine = 0.0f;
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+        float v = acc[j];
+#pragma unroll
+        for (int offset = 32; offset > 0; offset >>= 1) {
+            v += __shfl_xor(v, offset, 64);
+        }
+        mine = lane == j ? v : mine;
+    }
+    if (lane < cols) {
+        const ThinBatch t{p.a, p.b, p.c, p.c0};
+        thin_store(p, t, row, lane, mine);
     }
 }
 

@@ -216,6 +216,44 @@ def test_stage_modes_agree_bitwise(stream, oracle):
     assert_gemm_parity(got, oracle.gemm(x, w), magnitude(oracle, x, w), k, "staged 256x256")
 
 
+TILE_BN = {1: 256, 2: 128, 3: 64, 4: 128, 5: 64}  # output columns per tile, by abi.TILE_* id
+
+
+@pytest.mark.parametrize("m, n, k, b_kmajor", [
+    (4093, 4099, 1023, False),  # configs[3]: 4093 x 4096 on the 256x256 tile, a 3-column strip
+    (2045, 2053, 1023, False),  # a 5-column strip (the 8-column kernel)
+    (2045, 2049, 1021, True),   # B read along k through a transposed view, staged as well
+])
+def test_strip_stages_a_in_one_launch(stream, oracle, m, n, k, b_kmajor):
+    """AUTO stages a K-major A whose rows 16-byte loads cannot take; when a peeled strip of at
+    most 8 columns covers all of A's rows, the strip's launch writes that copy as it reads A.
+
+    The strip's columns must be the thin path's bits on A read in place (tile THIN, staging off),
+    and the main rectangle's the same tile's bits with A copied by the staging kernel, so the
+    copy (with its zero padding) is the staging kernel's. Both parts within the parity bar."""
+    x = normal(oracle, (m, k), 0.0, 1.0, 21, 0)
+    w = normal(oracle, (k, n), 0.0, float(1.0 / np.sqrt(k)), 22, 0)
+    bias = uniform(oracle, (n,), -0.1, 0.1, 23, 0)
+    x_d, b_d = dev(x, stream), dev(bias, stream)
+    w_d = dev(np.ascontiguousarray(w.T), stream).T if b_kmajor else dev(w, stream)
+    out_d = mf.DeviceArray.empty((m, n), stream)
+    tile, stage, splits, regions = mf.gemm_plan(x_d, w_d, out_d)
+    assert stage == mf.abi.STAGE_ALWAYS and splits == 1 and regions == 2, (tile, stage, regions)
+    main_n = n - n % TILE_BN[tile]
+    assert 0 < n - main_n <= 8
+    got = mf.gemm(x_d, w_d, bias=b_d, act=mf.ACT_GELU_TANH, out=out_d).numpy()
+    strip = mf.gemm(x_d, w_d.slice(1, main_n, n), bias=b_d.slice(0, main_n, n),
+                    act=mf.ACT_GELU_TANH, tile=mf.abi.TILE_THIN, stage=mf.abi.STAGE_NEVER).numpy()
+    main = mf.gemm(x_d, w_d.slice(1, 0, main_n), bias=b_d.slice(0, 0, main_n),
+                   act=mf.ACT_GELU_TANH, tile=tile, stage=mf.abi.STAGE_ALWAYS).numpy()
+    assert same_bits(got[:, main_n:], strip)
+    assert same_bits(got[:, :main_n], main)
+    if m * n * k < 2**33:
+        want = oracle.gelu(oracle.bias_add(oracle.matmul(x, w), bias), approximate=True)
+        scale = 1.13 * (magnitude(oracle, x, w) + np.abs(bias))
+        assert_gemm_parity(got, want, scale, k, f"strip staging {m}x{n}x{k}")
+
+
 def test_plan_on_baseline_shapes(stream):
     """mfr_sgemm_plan reports what AUTO runs: the 256x256 tile in place for configs[2], staged
     operands for configs[3] (whose rows 16-byte loads cannot take), the 256x256 tile reading them
