@@ -10,6 +10,11 @@ namespace mfr::gemm {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
+// Word 3 of a raw buffer resource on gfx9 (32-bit dword format, no swizzle): the buffer unit
+// checks each access against the resource's size in bytes, returning zeros for loads past it and
+// dropping stores past it.
+constexpr int kBufferWord3 = 0x00020000;
+
 struct GemmParams {
     const float* a;
     const float* b;
@@ -142,11 +147,19 @@ template <int ROWS, int KT, bool KMAJ, int V, int THREADS> struct SliceLoader {
 // loaded before any is used, so the loads overlap; kC0None: no C0; kC0Checked: c0 checked per
 // element (one copy of the code for both cases). STREAM: non-temporal stores.
 enum { kC0None = 0, kC0Batched = 1, kC0Checked = 2 };
-template <int FM, int FN, int ACT, bool INTERIOR, bool RAW, int C0, bool STREAM = false>
+// ROWS_PAST_M: a tile whose columns are all inside C and whose rows may run past m; every element
+// is computed and stored through a buffer resource of m rows, which drops the stores to rows past
+// m (no per-element test; the caller checks that (m + 256) * c_rs * 4 fits 32 bits).
+template <int FM, int FN, int ACT, bool INTERIOR, bool RAW, int C0, bool STREAM = false,
+          bool ROWS_PAST_M = false>
 __device__ __forceinline__ void write_tile(const floatx16 (&acc)[FM][FN], float* c, int64_t c_rs,
                                            const float* c0, int64_t c0_rs, const GemmParams& p,
                                            int64_t row0, int64_t col0,
                                            const double* exp_table = nullptr) {
+    static_assert(!ROWS_PAST_M || (!INTERIOR && C0 == kC0None && !STREAM), "row-edge copy");
+    // Byte offsets into C within the resource (32 bits by the caller's check).
+    const __amdgpu_buffer_rsrc_t c_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        c, 0, ROWS_PAST_M ? static_cast<int>(4 * p.m * c_rs) : 0, kBufferWord3);
     // Kernel parameters read once: per element, the compiler would reload them after each store.
     const float alpha = p.alpha;
     const float beta = p.beta;
@@ -182,7 +195,7 @@ __device__ __forceinline__ void write_tile(const floatx16 (&acc)[FM][FN], float*
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const int64_t col = col0 + 32 * j;
-            if (!INTERIOR && col >= p.n) {
+            if (!INTERIOR && !ROWS_PAST_M && col >= p.n) {
                 continue;
             }
             const float bias = bias_of[j];
@@ -199,7 +212,7 @@ __device__ __forceinline__ void write_tile(const floatx16 (&acc)[FM][FN], float*
                 for (int g = 0; g < kGroup; ++g) {
                     const int e = e0 + g;
                     const int dr = 8 * (e / 4) + e % 4;
-                    row_ok[g] = INTERIOR || row_i + dr < p.m;
+                    row_ok[g] = INTERIOR || ROWS_PAST_M || row_i + dr < p.m;
                     float x = acc[i][j][e];
                     if constexpr (!RAW) {
                         x = alpha * x;
@@ -231,6 +244,13 @@ __device__ __forceinline__ void write_tile(const floatx16 (&acc)[FM][FN], float*
                 for (int g = 0; g < kGroup; ++g) {
                     const int e = e0 + g;
                     const int dr = 8 * (e / 4) + e % 4;
+                    if constexpr (ROWS_PAST_M) {
+                        const uint32_t offset =
+                            static_cast<uint32_t>(4 * ((row_i + dr) * c_rs + col0 + 32 * j));
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out[g]),
+                                                              c_rsrc, offset, 0, 0);
+                        continue;
+                    }
                     if (!row_ok[g]) {
                         continue;
                     }
@@ -254,11 +274,14 @@ template <int FM, int FN, int ACT>
 __device__ __forceinline__ void epilogue(const floatx16 (&acc)[FM][FN], float* c, int64_t c_rs,
                                          const float* c0, int64_t c0_rs, const GemmParams& p,
                                          int64_t row0, int64_t col0, bool interior,
-                                         const double* exp_table) {
+                                         bool rows_only_edge, const double* exp_table) {
     if constexpr (ACT == MFR_ACT_GELU_TANH) {
         if (interior && c0 == nullptr) {
             write_tile<FM, FN, ACT, true, false, kC0None>(acc, c, c_rs, c0, c0_rs, p, row0, col0,
                                                           exp_table);
+        } else if (rows_only_edge && c0 == nullptr) {
+            write_tile<FM, FN, ACT, false, false, kC0None, false, true>(acc, c, c_rs, c0, c0_rs, p,
+                                                                        row0, col0, exp_table);
         } else if (c0 == nullptr) {
             write_tile<FM, FN, ACT, false, false, kC0None>(acc, c, c_rs, c0, c0_rs, p, row0, col0,
                                                            exp_table);
@@ -381,6 +404,9 @@ __device__ __forceinline__ void finish_tile(const floatx16 (&acc)[FM][FN], const
     const int64_t row0 = w.m0 + wave_m * WM + 4 * half;
     const int64_t col0 = w.n0 + wave_n * WN + r32;
     const bool interior = w.m0 + BM <= p.m && w.n0 + BN <= p.n;
+    // Rows past m only, and C's byte offsets (rows past m included) within 32 bits.
+    const bool rows_only_edge = !interior && w.n0 + BN <= p.n &&
+                                (p.m + BM) * p.c_rs * 4 < (int64_t{1} << 32);
     if (p.partial != nullptr) {
         // Split-K: raw sums only, to partial[split][batch] (dense m x n).
         float* part = p.partial + (w.split * p.batch_count + w.batch_linear) * p.m * p.n;
@@ -399,13 +425,13 @@ __device__ __forceinline__ void finish_tile(const floatx16 (&acc)[FM][FN], const
     // over every accumulator, the three would not fit the instruction cache together.
     if (p.act == MFR_ACT_NONE) {
         epilogue<FM, FN, MFR_ACT_NONE>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
-                                       interior, exp_table);
+                                       interior, rows_only_edge, exp_table);
     } else if (p.act == MFR_ACT_GELU_TANH) {
         epilogue<FM, FN, MFR_ACT_GELU_TANH>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
-                                            interior, exp_table);
+                                            interior, rows_only_edge, exp_table);
     } else {
         epilogue<FM, FN, MFR_ACT_GELU_ERF>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
-                                           interior, exp_table);
+                                           interior, rows_only_edge, exp_table);
     }
 }
 
@@ -550,9 +576,6 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * WAVES_K * 64) void sgemm_kernel
 // memory. Every in-range byte of a slice must lie below 2^30 bytes from its first element: the
 // host checks the strides (direct_slices_fit) before it picks this loader.
 constexpr uint32_t kDirectLimit = 0x80000000u;
-// Word 3 of a gfx9-family buffer resource: 32-bit float data, no swizzle, raw (stride 0)
-// addressing.
-constexpr int kBufferWord3 = 0x00020000;
 
 // HOIST: keep the K-major offsets in registers across the depth loop (one per instruction of a
 // wave); otherwise they are worked out at every issue (the choice for two 4-byte K-major

@@ -405,6 +405,23 @@ def test_epilogue_gelu_bits_equal_oracle(stream, oracle, tile):
         assert same_bits(got, oracle.gelu(pre, approximate=True)), alpha
 
 
+@pytest.mark.parametrize("tile", TILES)
+def test_gelu_row_edge_tiles_drop_rows_past_m(stream, oracle, tile):
+    """Tiles whose columns are all inside C but whose rows run past m compute every row and
+    store through a buffer resource of m rows, which drops the stores past m: C is an exact
+    output inside a poisoned buffer (the rows past m would land in the guard after it), and the
+    values are the oracle's bits."""
+    m, n, k = 300, 256, 96
+    av, bv = quarter_matrix(m, k, 221), quarter_matrix(k, n, 222)
+    biasv = quarter_matrix(1, n, 223)[0]
+    out, buf = guarded_output(stream, (m, n), guard=64 * 1024)
+    mf.gemm(dev(av, stream), dev(bv, stream), bias=dev(biasv, stream), act=mf.ACT_GELU_TANH,
+            tile=tile, out=out)
+    check_guards(buf, guard=64 * 1024)
+    pre = (exact_product(av, bv) + biasv).astype(np.float32)
+    assert same_bits(out.numpy(), oracle.gelu(pre, approximate=True))
+
+
 def test_split_k_automatic_choice(stream):
     """AUTO splits a product with few output tiles and a long depth, and leaves products that
     fill the device (4096^3, the MLP) or have a short depth unsplit."""
