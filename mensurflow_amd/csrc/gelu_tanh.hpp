@@ -48,89 +48,53 @@ MFR_GELU_TABLE double kExp2Table[64] = {
     0x1.ea4afa2a490dap+0, 0x1.efa1bee615a27p+0, 0x1.f50765b6e4540p+0, 0x1.fa7c1819e90d8p+0,
 };
 
-// gelu_tanh_n evaluates N values in lockstep: each step below runs over the N values before the
-// next begins, so a kernel that passes N = 2 gives every wavefront two independent
-// double-precision chains to interleave (one chain alone waits on each operation's latency).
-// gelu_tanh is N = 1. Per value:
-//
-// 2u = 2 sqrt(2/pi) v (1 + 0.044715 v^2): the factor 2 is folded into the constant, which is exact
-// (a product by 2 only moves the exponent), so this is the reference's 2u to the bit.
-//
-// exp(t), t = -|2u| <= 0, by Tang's table-driven method (ACM TOMS 15(2), 1989): with
+// exp(t) for t <= 0 in double by Tang's table-driven method (ACM TOMS 15(2), 1989): with
 // k = rint(t * 64/ln2) = 64m + j, t = k ln2/64 + r, |r| <= ln2/128, and
 // exp(t) = 2^m * 2^(j/64) * (1 + p(r)), p the degree-5 Taylor polynomial of e^r - 1 (its
 // truncation is below 3.5e-17, a third of an ulp). ln2/64 is split into a 36-bit head, so
 // k * head is exact for |k| < 2^17, and a tail. t below -800 is taken as -800 (exp gives 0 for
 // both); a NaN t also gives 0 (only a NaN input makes t NaN, and its result is NaN anyway).
 // `table` is kExp2Table or a copy of it (a kernel may keep one in LDS).
-//
-// s = num / (1 + z), num = z for 2u < 0 and 1 otherwise, 1 + z in [1, 2]: the reciprocal, one
-// Newton step and one correction of the quotient with its remainder.
-//
-// No branch: the formula runs for every input. For +inf it gives +inf, as the reference does;
-// for -inf it gives NaN (-inf * 0), and the reference's -0 is selected at the end.
-template <int N>
-MFR_GELU_FN void gelu_tanh_n(const float (&value)[N], float (&out)[N], const double* table) {
-    constexpr double kTwiceSqrt2OverPi = 2.0 * 0.79788456080286535588;
+MFR_GELU_FN double exp_nonpositive(double t, const double* table) {
     constexpr double kInvStep = 0x1.71547652b82fep+6;  // 64 / ln2
     constexpr double kStepHead = 0x1.62e42fefa0000p-7; // ln2/64, 36 bits
     constexpr double kStepTail = 0x1.cf79abc9e3b3ap-46; // ln2/64 - head
-    double v[N], twice[N], kd[N], r[N], q[N], z[N], d[N], num[N], rcp[N], quot[N];
-    int k[N];
-    for (int i = 0; i < N; ++i) {
-        v[i] = static_cast<double>(value[i]);
-        twice[i] = kTwiceSqrt2OverPi * v[i] * (1.0 + 0.044715 * v[i] * v[i]);
-    }
-    for (int i = 0; i < N; ++i) {
-        const double t = fmax(-fabs(twice[i]), -800.0);
-        kd[i] = rint(t * kInvStep);
-        k[i] = static_cast<int>(kd[i]);
-        r[i] = fma(-kd[i], kStepHead, t);
-    }
-    for (int i = 0; i < N; ++i) {
-        r[i] = fma(-kd[i], kStepTail, r[i]);
-    }
-    for (int i = 0; i < N; ++i) {
-        q[i] = fma(r[i], 1.0 / 120.0, 1.0 / 24.0);
-    }
-    for (int i = 0; i < N; ++i) {
-        q[i] = fma(r[i], q[i], 1.0 / 6.0);
-    }
-    for (int i = 0; i < N; ++i) {
-        q[i] = fma(r[i], q[i], 0.5);
-    }
-    for (int i = 0; i < N; ++i) {
-        const double pm1 = fma(r[i] * r[i], q[i], r[i]); // e^r - 1
-        const double two_j = table[k[i] & 63];
-        z[i] = ldexp(fma(two_j, pm1, two_j), k[i] >> 6);
-    }
-    for (int i = 0; i < N; ++i) {
-        d[i] = 1.0 + z[i];
-        num[i] = twice[i] < 0.0 ? z[i] : 1.0;
-        rcp[i] = MFR_GELU_RCP(d[i]);
-    }
-    for (int i = 0; i < N; ++i) {
-        const double e = fma(-d[i], rcp[i], 1.0);
-        rcp[i] = fma(rcp[i], e, rcp[i]);
-    }
-    for (int i = 0; i < N; ++i) {
-        quot[i] = num[i] * rcp[i];
-    }
-    for (int i = 0; i < N; ++i) {
-        const double rem = fma(-d[i], quot[i], num[i]);
-        quot[i] = fma(rem, rcp[i], quot[i]);
-    }
-    for (int i = 0; i < N; ++i) {
-        const float result = static_cast<float>(v[i] * quot[i]);
-        out[i] = value[i] == -__builtin_inff() ? -0.0f : result;
-    }
+    t = fmax(t, -800.0);
+    const double kd = rint(t * kInvStep);
+    const int k = static_cast<int>(kd);
+    double r = fma(-kd, kStepHead, t);
+    r = fma(-kd, kStepTail, r);
+    double q = fma(r, 1.0 / 120.0, 1.0 / 24.0);
+    q = fma(r, q, 1.0 / 6.0);
+    q = fma(r, q, 0.5);
+    const double pm1 = fma(r * r, q, r); // e^r - 1
+    const double two_j = table[k & 63];
+    return ldexp(fma(two_j, pm1, two_j), k >> 6);
 }
 
+// num / d for d in [1, 2]: the reciprocal, one Newton step and one correction of the quotient
+// with its remainder.
+MFR_GELU_FN double divide_by_1_to_2(double num, double d) {
+    double q = MFR_GELU_RCP(d);
+    const double e = fma(-d, q, 1.0);
+    q = fma(q, e, q);
+    const double s = num * q;
+    const double rem = fma(-d, s, num);
+    return fma(rem, q, s);
+}
+
+// 2u = 2 sqrt(2/pi) v (1 + 0.044715 v^2) takes the factor 2 into the constant, which is exact (a
+// product by 2 only moves the exponent), so it is the reference's 2u to the bit. No branch: the
+// formula runs for every input (a kernel's unrolled epilogue then has no branch between values).
+// For +inf it gives +inf, as the reference does; for -inf it gives NaN (-inf * 0), and the
+// reference's -0 is selected at the end.
 MFR_GELU_FN float gelu_tanh(float value, const double* table) {
-    const float in[1] = {value};
-    float out[1];
-    gelu_tanh_n<1>(in, out, table);
-    return out[0];
+    const double v = static_cast<double>(value);
+    const double twice = (2.0 * 0.79788456080286535588) * v * (1.0 + 0.044715 * v * v);
+    const double z = exp_nonpositive(-fabs(twice), table);
+    const double s = divide_by_1_to_2(twice < 0.0 ? z : 1.0, 1.0 + z);
+    const float result = static_cast<float>(v * s);
+    return value == -__builtin_inff() ? -0.0f : result;
 }
 
 MFR_GELU_FN float gelu_tanh(float value) { return gelu_tanh(value, kExp2Table); }

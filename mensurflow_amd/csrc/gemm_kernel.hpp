@@ -200,64 +200,41 @@ __device__ __forceinline__ void write_tile(const floatx16 (&acc)[FM][FN], float*
             }
             const float bias = bias_of[j];
             // Elements outside C (rows past m) are computed all the same and only the loads and
-            // stores are predicated, so no branch separates them. The tanh gelu takes them two
-            // at a time (gelu_tanh_n): each wavefront then has two independent double-precision
-            // chains to interleave.
-            constexpr int kGroup = ACT == MFR_ACT_GELU_TANH ? 2 : 1;
+            // stores are predicated, so no branch separates them.
 #pragma unroll
-            for (int e0 = 0; e0 < 16; e0 += kGroup) {
-                float v[kGroup];
-                bool row_ok[kGroup];
-#pragma unroll
-                for (int g = 0; g < kGroup; ++g) {
-                    const int e = e0 + g;
-                    const int dr = 8 * (e / 4) + e % 4;
-                    row_ok[g] = INTERIOR || ROWS_PAST_M || row_i + dr < p.m;
-                    float x = acc[i][j][e];
-                    if constexpr (!RAW) {
-                        x = alpha * x;
-                        if constexpr (C0 == kC0Batched) {
-                            const float scaled = beta * c0v[j][e];
-                            x = x + scaled;
-                        } else if constexpr (C0 == kC0Checked) {
-                            if (c0 != nullptr) {
-                                const float c0_value =
-                                    row_ok[g] ? c0[(row_i + dr) * c0_rs + col] : 0.0f;
-                                const float scaled = beta * c0_value;
-                                x = x + scaled;
-                            }
+            for (int e = 0; e < 16; ++e) {
+                const int dr = 8 * (e / 4) + e % 4;
+                const bool row_ok = INTERIOR || ROWS_PAST_M || row_i + dr < p.m;
+                float v = acc[i][j][e];
+                if constexpr (!RAW) {
+                    v = alpha * v;
+                    if constexpr (C0 == kC0Batched) {
+                        const float scaled = beta * c0v[j][e];
+                        v = v + scaled;
+                    } else if constexpr (C0 == kC0Checked) {
+                        if (c0 != nullptr) {
+                            const float c0_value = row_ok ? c0[(row_i + dr) * c0_rs + col] : 0.0f;
+                            const float scaled = beta * c0_value;
+                            v = v + scaled;
                         }
-                        x = x + bias; // -0 without a bias: x + -0 is x
                     }
-                    v[g] = x;
-                }
-                float out[kGroup];
-                if constexpr (ACT == MFR_ACT_GELU_TANH) {
-                    gelu_math::gelu_tanh_n<kGroup>(v, out, exp_table);
-                } else {
-#pragma unroll
-                    for (int g = 0; g < kGroup; ++g) {
-                        out[g] = ACT == MFR_ACT_NONE ? v[g] : mfr::dev::gelu(v[g], ACT);
+                    v = v + bias; // -0 without a bias: x + -0 is x
+                    if constexpr (ACT == MFR_ACT_GELU_TANH) {
+                        v = gelu_math::gelu_tanh(v, exp_table);
+                    } else if constexpr (ACT != MFR_ACT_NONE) {
+                        v = mfr::dev::gelu(v, ACT);
                     }
                 }
-#pragma unroll
-                for (int g = 0; g < kGroup; ++g) {
-                    const int e = e0 + g;
-                    const int dr = 8 * (e / 4) + e % 4;
-                    if constexpr (ROWS_PAST_M) {
-                        const uint32_t offset =
-                            static_cast<uint32_t>(4 * ((row_i + dr) * c_rs + col0 + 32 * j));
-                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out[g]),
-                                                              c_rsrc, offset, 0, 0);
-                        continue;
-                    }
-                    if (!row_ok[g]) {
-                        continue;
-                    }
+                if constexpr (ROWS_PAST_M) {
+                    const uint32_t offset =
+                        static_cast<uint32_t>(4 * ((row_i + dr) * c_rs + col0 + 32 * j));
+                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), c_rsrc,
+                                                          offset, 0, 0);
+                } else if (row_ok) {
                     if constexpr (STREAM) {
-                        __builtin_nontemporal_store(out[g], &c_i[dr * c_rs + 32 * j]);
+                        __builtin_nontemporal_store(v, &c_i[dr * c_rs + 32 * j]);
                     } else {
-                        c_i[dr * c_rs + 32 * j] = out[g];
+                        c_i[dr * c_rs + 32 * j] = v;
                     }
                 }
             }
@@ -266,10 +243,10 @@ __device__ __forceinline__ void write_tile(const floatx16 (&acc)[FM][FN], float*
 }
 
 // The epilogue for activation ACT. Without one it is dispatched on C0 and on whether the tile is
-// interior. The tanh gelu has two copies without C0 (the MLP's case), interior and edge: with C0
-// tested and loaded between the elements, each element waits for the memory counter, which also
-// counts the stores before it, and the double-precision chains run one after another. Every
-// other gelu epilogue is one checked copy.
+// interior. The tanh gelu has three copies without C0 (the MLP's case): interior tiles, tiles
+// whose rows alone run past m (stores through a buffer resource that drops those rows), and other
+// edges. With C0 tested and loaded between the elements, each element would wait for the memory
+// counter, which also counts the stores before it. Every other gelu epilogue is one checked copy.
 template <int FM, int FN, int ACT>
 __device__ __forceinline__ void epilogue(const floatx16 (&acc)[FM][FN], float* c, int64_t c_rs,
                                          const float* c0, int64_t c0_rs, const GemmParams& p,

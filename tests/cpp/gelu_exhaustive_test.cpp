@@ -56,19 +56,11 @@ int main(int argc, char** argv) {
             orc_gelu_f32(x.data(), want.data(), n, 1);
             for (int64_t i = 0; i < n; ++i) {
                 const float got = mfr::gelu_math::gelu_tanh(x[static_cast<size_t>(i)]);
-                // The two-value form the GEMM epilogue runs, on this input and its neighbour.
-                const float pair_in[2] = {x[static_cast<size_t>(i)],
-                                          x[static_cast<size_t>(i + 1 < n ? i + 1 : 0)]};
-                float pair_out[2];
-                mfr::gelu_math::gelu_tanh_n<2>(pair_in, pair_out,
-                                               mfr::gelu_math::kExp2Table);
                 const float ref = want[static_cast<size_t>(i)];
-                uint32_t gb, rb, pb;
+                uint32_t gb, rb;
                 std::memcpy(&gb, &got, 4);
                 std::memcpy(&rb, &ref, 4);
-                std::memcpy(&pb, &pair_out[0], 4);
-                const bool same = (gb == rb && pb == rb) ||
-                                  (std::isnan(got) && std::isnan(ref) && std::isnan(pair_out[0]));
+                const bool same = gb == rb || (std::isnan(got) && std::isnan(ref));
                 if (!same) {
                     ++mismatches;
 #pragma omp critical

@@ -40,7 +40,6 @@ def test_host_layer_rocm(name):
 def test_device_gelu_arithmetic_every_61st_float():
     """The device's tanh gelu (csrc/gelu_tanh.hpp, the same operations compiled for the CPU)
     gives the oracle's bits on every 61st float bit pattern (70 M inputs) for three stand-ins of
-    the reciprocal instruction, one value at a time and two in lockstep (the GEMM epilogue's
-    form). `gelu_exhaustive_test --stride 1` covers all 2^32 (about 4 minutes on 8 threads; it
-    passes as well)."""
+    the reciprocal instruction. `gelu_exhaustive_test --stride 1` covers all 2^32 (about 90 s on
+    8 threads; it passes as well)."""
     run("gelu_exhaustive_test", "--stride", "61")
