@@ -223,6 +223,8 @@ TILE_BN = {1: 256, 2: 128, 3: 64, 4: 128, 5: 64}  # output columns per tile, by 
     (4093, 4099, 1023, False),  # configs[3]: 4093 x 4096 on the 256x256 tile, a 3-column strip
     (2045, 2053, 1023, False),  # a 5-column strip (the 8-column kernel)
     (2045, 2049, 1021, True),   # B read along k through a transposed view, staged as well
+    (2045, 2049, 1023, False),  # one column (the 1-column kernel)
+    (2045, 2050, 999, False),   # two columns, an odd depth (the copy's line padded by one zero)
 ])
 def test_strip_stages_a_in_one_launch(stream, oracle, m, n, k, b_kmajor):
     """AUTO stages a K-major A whose rows 16-byte loads cannot take; when a peeled strip of at
