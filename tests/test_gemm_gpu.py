@@ -733,6 +733,22 @@ def test_config3_gemm_4096_nt_realistic(stream, oracle):
                   bar=tolerance(n), bit_identical_share=float(np.mean(same_elements(got, want))))
 
 
+def test_config4_fused_epilogue_equals_unfused_chain(stream, oracle):
+    """BASELINE configs[3] at full size: the fused bias + gelu-tanh epilogue (exp table in LDS,
+    interior and row-edge copies, the strip's launch with the copy of X) gives the bits of the
+    unfused chain on the same device: the product without an epilogue, then mfr_bias_act's
+    gelu (its own kernel, table read from global memory). Both sides run the same plan, so the
+    pre-activation values are the same floats."""
+    m, k, n = 4093, 1023, 4099
+    x = normal(oracle, (m, k), 0.0, 1.0, 7, 0)
+    w = normal(oracle, (k, n), 0.0, float(np.sqrt(1.0 / 1023.0)), 8, 0)
+    bias = uniform(oracle, (n,), -0.1, 0.1, 9, 0)
+    x_d, w_d, b_d = dev(x, stream), dev(w, stream), dev(bias, stream)
+    fused = mf.gemm(x_d, w_d, bias=b_d, act=mf.ACT_GELU_TANH).numpy()
+    chain = mf.bias_act(mf.gemm(x_d, w_d), b_d, mf.ACT_GELU_TANH).numpy()
+    assert same_bits(fused, chain)
+
+
 def test_config4_mlp_fused_bias_gelu(stream, oracle):
     """X[4093,1023] x W[1023,4099] + bias, gelu-tanh fused in the epilogue,
     against the reference's three-op chain gelu(bias_add(matmul(X, W), b), true).
