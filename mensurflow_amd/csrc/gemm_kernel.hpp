@@ -158,8 +158,10 @@ __device__ __forceinline__ void write_tile(const floatx16 (&acc)[FM][FN], float*
                                            const double* exp_table = nullptr) {
     static_assert(!ROWS_PAST_M || (!INTERIOR && C0 == kC0None && !STREAM), "row-edge copy");
     // Byte offsets into C within the resource (32 bits by the caller's check).
+    // The record count is a 32-bit unsigned field; the caller keeps 4 (m + 256) c_rs below 2^32.
     const __amdgpu_buffer_rsrc_t c_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        c, 0, ROWS_PAST_M ? static_cast<int>(4 * p.m * c_rs) : 0, kBufferWord3);
+        c, 0, ROWS_PAST_M ? static_cast<int>(static_cast<uint32_t>(4 * p.m * c_rs)) : 0,
+        kBufferWord3);
     // Kernel parameters read once: per element, the compiler would reload them after each store.
     const float alpha = p.alpha;
     const float beta = p.beta;
