@@ -28,7 +28,9 @@
 //     start 16-byte aligned and hold a multiple of 4 floats. An operand that is not laid out so
 //     (X[4093,1023] row-major) is copied first into the stream's workspace with its lines padded
 //     to a multiple of 4 by zeros (stage_kernel); vector loads that reach past the end of a line
-//     then read zeros of its own line, and the zeros add nothing to any sum.
+//     then read zeros of its own line, and the zeros add nothing to any sum. When a peeled strip
+//     of at most 8 columns covers every row of such an A, the strip's launch writes the copy as
+//     it reads A (strip_stage_kernel in thin_kernel.hpp), one launch instead of two.
 //   - Direct-to-LDS slices (sgemm_direct_kernel, the 256x256 tile with a 4-byte operand): each
 //     lane's buffer load writes its element into the LDS image itself, so 4-byte operands take
 //     no registers and need no staging copy; elements outside the matrix get an offset past the
@@ -36,7 +38,8 @@
 //     on aligned operands. Under it AUTO stages only K-major 4-byte operands (whose in-place
 //     runs of 32 floats touch twice the cache lines) and reads M/N-major ones in place.
 //   - The epilogue applies the activation chosen once per workgroup, with copies for interior
-//     tiles and for C0, so each copy is straight-line code (gemm_kernel.hpp, write_tile).
+//     tiles and for C0, so each copy is straight-line code (gemm_kernel.hpp, write_tile); the
+//     tanh gelu's copies read its exp table from LDS and have no branch between elements.
 //   - Split-K cuts a long depth into ranges run as workgroups of their own, reduced in order by
 //     split_reduce_kernel; edge peeling runs a thin remainder of the output as launches of its
 //     own; the thin path (thin_kernel.hpp) takes products with at most 8 output columns or rows.
