@@ -203,11 +203,12 @@ __global__ __launch_bounds__(kStreamThreads) void binary4_kernel(const float4* _
 //
 // Launch: workgroup (i, j) takes rows R * i .. R * i + R - 1 and, in each, the column chunks
 // j, j + gridDim.y, ... of 256 threads. The R rows' loads are all issued before any is used, and
-// the row index is divided into its outer coordinates once per workgroup, then stepped as an
-// odometer (a 64-bit division per dimension per row made the attention mask's where bound by
-// integer arithmetic, not memory). R: 8 for the in-place kernel (attention's mask over 512 MiB
-// of scores: 188 us with one row per workgroup, 117 with 4, 102 with 8), 4 for the others (the
-// same where out of place: 244, 234 and 274 us with 1, 4 and 8).
+// the row index is divided into its outer coordinates once per workgroup (in 32 bits where the
+// row count allows), then stepped (a 64-bit division per dimension per row made the attention
+// mask's where bound by integer arithmetic, not memory; once per workgroup in 64 bits it still
+// cost attention's mask 103 against 78 us). R: 8 for the in-place kernel (attention's mask over
+// 512 MiB of scores: 130, 97, 78 and 80 us with 2, 4, 8 and 16 rows per workgroup), 4 for the
+// others (the same where out of place: 239, 247, 228 and 251 us with 1, 2, 4 and 8).
 struct WhereLayout {
     int outer_dims;                     // dimensions before the last
     int64_t shape[MFR_MAX_COPY_DIMS];   // outer extents, outermost first
@@ -227,19 +228,52 @@ template <int R> struct WhereRows {
     int64_t c[R], x[R], y[R];
 
     __device__ WhereRows(const WhereLayout& l, int64_t first) {
+        // Outer coordinates of `first`, innermost first: in 32 bits when every row index fits
+        // (a 64-bit division is a long instruction sequence, run by every workgroup of R rows
+        // once per dimension), else in 64.
         int64_t idx[MFR_MAX_COPY_DIMS];
-        int64_t oc = 0, ox = 0, oy = 0, row = first;
+        int64_t oc = 0, ox = 0, oy = 0;
+        // The innermost outer dimension's index, extent and strides.
+        int64_t i0 = 0, n0 = 1, c0 = 0, x0 = 0, y0 = 0;
+        const bool narrow = l.rows <= int64_t{0xffffffff};
+        uint32_t row32 = static_cast<uint32_t>(first);
+        int64_t row = first;
 #pragma unroll
         for (int d = MFR_MAX_COPY_DIMS - 1; d >= 0; --d) {
             idx[d] = 0;
             if (d < l.outer_dims) {
-                const int64_t i = row % l.shape[d];
-                row /= l.shape[d];
+                int64_t i;
+                if (narrow) {
+                    const uint32_t n = static_cast<uint32_t>(l.shape[d]);
+                    i = row32 % n;
+                    row32 /= n;
+                } else {
+                    i = row % l.shape[d];
+                    row /= l.shape[d];
+                }
                 idx[d] = i;
                 oc += i * l.cs[d];
                 ox += i * l.xs[d];
                 oy += i * l.ys[d];
+                if (d == l.outer_dims - 1) {
+                    i0 = i;
+                    n0 = l.shape[d];
+                    c0 = l.cs[d];
+                    x0 = l.xs[d];
+                    y0 = l.ys[d];
+                }
             }
+        }
+        if (i0 + R <= n0) {
+            // The R rows stay within the innermost outer dimension: each row is the one before
+            // plus that dimension's strides (attention's rows: 8 of every 1024 queries).
+#pragma unroll
+            for (int u = 0; u < R; ++u) {
+                c[u] = oc + u * c0;
+                x[u] = ox + u * x0;
+                y[u] = oy + u * y0;
+            }
+            return;
         }
 #pragma unroll
         for (int u = 0; u < R; ++u) {
