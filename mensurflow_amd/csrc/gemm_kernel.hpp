@@ -303,29 +303,42 @@ struct TileWork {
 
 template <int BM, int BN> __device__ __forceinline__ TileWork tile_work(const GemmParams& p) {
     TileWork w;
-    const int64_t tiles_per_batch = static_cast<int64_t>(p.tiles_m) * p.tiles_n;
-    const int64_t tiles_per_split = tiles_per_batch * p.batch_count;
-    const int64_t total = tiles_per_split * p.splits;
-    const int64_t hw = blockIdx.x;
-    const int64_t per_xcd = total / 8;
-    const int64_t logical_all = hw < per_xcd * 8 ? (hw % 8) * per_xcd + hw / 8 : hw;
-    w.split = logical_all / tiles_per_split;
-    const int64_t logical = logical_all - w.split * tiles_per_split;
-    w.batch_linear = logical / tiles_per_batch;
-    int64_t batch_index = w.batch_linear;
-    const int64_t t = logical % tiles_per_batch;
-    const int64_t group_tiles = static_cast<int64_t>(p.group_m) * p.tiles_n;
-    const int64_t group = t / group_tiles;
-    const int64_t first_m = group * p.group_m;
-    const int64_t rows_in_group =
-        p.tiles_m - first_m < p.group_m ? p.tiles_m - first_m : p.group_m;
-    const int64_t in_group = t % group_tiles;
+    // Every index here is below the launch's workgroup count, which the host keeps under 2^31,
+    // so the decomposition runs in 32-bit unsigned arithmetic: a 64-bit division is a long
+    // scalar instruction sequence, and every wavefront of every workgroup runs these (about a
+    // thousand instructions before a small tile's first load in 64 bits).
+    const uint32_t tiles_m = static_cast<uint32_t>(p.tiles_m);
+    const uint32_t tiles_n = static_cast<uint32_t>(p.tiles_n);
+    const uint32_t tiles_per_batch = tiles_m * tiles_n;
+    const uint32_t tiles_per_split = tiles_per_batch * static_cast<uint32_t>(p.batch_count);
+    const uint32_t total = tiles_per_split * static_cast<uint32_t>(p.splits);
+    const uint32_t hw = blockIdx.x;
+    const uint32_t per_xcd = total / 8;
+    const uint32_t logical_all = hw < per_xcd * 8 ? (hw % 8) * per_xcd + hw / 8 : hw;
+    const uint32_t split = logical_all / tiles_per_split;
+    const uint32_t logical = logical_all - split * tiles_per_split;
+    const uint32_t batch_linear = logical / tiles_per_batch;
+    const uint32_t t = logical - batch_linear * tiles_per_batch;
+    // Groups of group_m tile-rows; a group taller than the matrix is the matrix (the same order,
+    // and group_tiles stays within the batch's tile count).
+    const uint32_t gm = static_cast<uint32_t>(p.group_m) < tiles_m
+                            ? static_cast<uint32_t>(p.group_m)
+                            : tiles_m;
+    const uint32_t group_tiles = gm * tiles_n;
+    const uint32_t group = t / group_tiles;
+    const uint32_t first_m = group * gm;
+    const uint32_t rows_in_group = tiles_m - first_m < gm ? tiles_m - first_m : gm;
+    const uint32_t in_group = t - group * group_tiles;
     const int64_t tile_m = first_m + in_group % rows_in_group;
     const int64_t tile_n = in_group / rows_in_group;
+    w.split = split;
+    w.batch_linear = batch_linear;
+    uint32_t batch_index = batch_linear;
     w.off_a = w.off_b = w.off_c = w.off_c0 = 0;
     for (int d = p.batch_dims - 1; d >= 0; --d) {
-        const int64_t idx = batch_index % p.batch[d];
-        batch_index /= p.batch[d];
+        const uint32_t extent = static_cast<uint32_t>(p.batch[d]);
+        const int64_t idx = batch_index % extent;
+        batch_index /= extent;
         w.off_a += idx * p.a_bs[d];
         w.off_b += idx * p.b_bs[d];
         w.off_c += idx * p.c_bs[d];
