@@ -86,16 +86,22 @@ struct BlockWork {
     int64_t off_q, off_k, off_v, off_o, off_m;
 };
 
+// The indices are below the workgroup count (under 2^31), so the decomposition runs in 32-bit
+// unsigned arithmetic: a 64-bit division is a long scalar instruction sequence that every
+// wavefront of the workgroup runs before its first load.
 __device__ inline BlockWork block_work(const AttnParams& p) {
-    const int64_t bid = blockIdx.x;
-    const int64_t level = bid / p.batch_count;
-    const int64_t longer = (p.q_blocks + 1) / 2;
+    const uint32_t bid = blockIdx.x;
+    const uint32_t batch_count = static_cast<uint32_t>(p.batch_count);
+    const uint32_t q_blocks = static_cast<uint32_t>(p.q_blocks);
+    const uint32_t level = bid / batch_count;
+    const uint32_t longer = (q_blocks + 1) / 2;
     BlockWork w{};
-    w.qb = !p.paired || level < longer ? p.q_blocks - 1 - level : level - longer;
-    int64_t bi = bid % p.batch_count;
+    w.qb = !p.paired || level < longer ? q_blocks - 1 - level : level - longer;
+    uint32_t bi = bid - level * batch_count;
     for (int d = p.batch_dims - 1; d >= 0; --d) {
-        const int64_t idx = bi % p.batch[d];
-        bi /= p.batch[d];
+        const uint32_t extent = static_cast<uint32_t>(p.batch[d]);
+        const int64_t idx = bi % extent;
+        bi /= extent;
         w.off_q += idx * p.q_bs[d];
         w.off_k += idx * p.k_bs[d];
         w.off_v += idx * p.v_bs[d];
