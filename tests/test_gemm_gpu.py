@@ -256,6 +256,35 @@ def test_strip_stages_a_in_one_launch(stream, oracle, m, n, k, b_kmajor):
         assert_gemm_parity(got, want, scale, k, f"strip staging {m}x{n}x{k}")
 
 
+def test_strip_staging_with_alpha_beta_c0(stream, oracle):
+    """The strip's launch that copies A also runs the full epilogue: alpha, beta * C0 and the
+    bias (no activation), bit for bit the thin path's on A read in place, and the main rectangle
+    the staged tile's; both within the parity bar."""
+    m, n, k = 2045, 2051, 1023
+    alpha, beta = 1.5, 0.5
+    x = normal(oracle, (m, k), 0.0, 1.0, 31, 0)
+    w = normal(oracle, (k, n), 0.0, float(1.0 / np.sqrt(k)), 32, 0)
+    c0 = normal(oracle, (m, n), 0.0, 1.0, 33, 0)
+    bias = uniform(oracle, (n,), -0.1, 0.1, 34, 0)
+    x_d, w_d, c0_d, b_d = dev(x, stream), dev(w, stream), dev(c0, stream), dev(bias, stream)
+    out_d = mf.DeviceArray.empty((m, n), stream)
+    tile, stage, splits, regions = mf.gemm_plan(x_d, w_d, out_d, c0=c0_d, beta=beta)
+    assert stage == mf.abi.STAGE_ALWAYS and splits == 1 and regions == 2, (tile, stage, regions)
+    main_n = n - n % TILE_BN[tile]
+    got = mf.gemm(x_d, w_d, alpha=alpha, beta=beta, c0=c0_d, bias=b_d, out=out_d).numpy()
+    strip = mf.gemm(x_d, w_d.slice(1, main_n, n), alpha=alpha, beta=beta,
+                    c0=c0_d.slice(1, main_n, n), bias=b_d.slice(0, main_n, n),
+                    tile=mf.abi.TILE_THIN, stage=mf.abi.STAGE_NEVER).numpy()
+    main = mf.gemm(x_d, w_d.slice(1, 0, main_n), alpha=alpha, beta=beta,
+                   c0=c0_d.slice(1, 0, main_n), bias=b_d.slice(0, 0, main_n), tile=tile,
+                   stage=mf.abi.STAGE_ALWAYS).numpy()
+    assert same_bits(got[:, main_n:], strip)
+    assert same_bits(got[:, :main_n], main)
+    want = oracle.bias_add(oracle.gemm(x, w, alpha=alpha, c0=c0, beta=beta), bias)
+    scale = alpha * magnitude(oracle, x, w) + beta * np.abs(c0) + np.abs(bias)
+    assert_gemm_parity(got, want, scale, k, "strip staging, alpha beta C0")
+
+
 def test_plan_on_baseline_shapes(stream):
     """mfr_sgemm_plan reports what AUTO runs: the 256x256 tile in place for configs[2], staged
     operands for configs[3] (whose rows 16-byte loads cannot take), the 256x256 tile reading them
