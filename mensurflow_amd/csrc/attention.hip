@@ -111,6 +111,44 @@ __device__ inline BlockWork block_work(const AttnParams& p) {
     return w;
 }
 
+// max / sum of the values in lanes l and l ^ 16 (rows16) or l and l ^ 32 (halves), in every lane.
+// gfx950's v_permlane16_swap / v_permlane32_swap exchange 16-lane rows (32-lane halves) of two
+// registers in the vector ALU; given x twice, one result holds the even rows' values in every
+// lane and the other the odd rows', so one max or add of the two combines each pair. This
+// replaces an LDS-crossbar permute and its wait on the softmax's critical path. Both operands
+// are symmetric, so every lane gets the same bits that lane l ^ 16 (l ^ 32) gets.
+template <bool HALVES>
+__device__ inline void swap_pair(float x, float& a, float& b) {
+    const unsigned u = __float_as_uint(x);
+    const auto r = HALVES ? __builtin_amdgcn_permlane32_swap(u, u, false, false)
+                          : __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    // The two elements are read into scalars first: a bit cast of an element of the returned
+    // vector reads element 0 whatever index it names.
+    const unsigned lo = r[0], hi = r[1];
+    a = __uint_as_float(lo);
+    b = __uint_as_float(hi);
+}
+__device__ inline float max_rows16(float x) {
+    float a, b;
+    swap_pair<false>(x, a, b);
+    return fmaxf(a, b);
+}
+__device__ inline float max_halves(float x) {
+    float a, b;
+    swap_pair<true>(x, a, b);
+    return fmaxf(a, b);
+}
+__device__ inline float sum_rows16(float x) {
+    float a, b;
+    swap_pair<false>(x, a, b);
+    return a + b;
+}
+__device__ inline float sum_halves(float x) {
+    float a, b;
+    swap_pair<true>(x, a, b);
+    return a + b;
+}
+
 // exp(x - m) through the hardware's 2^x (v_exp_f32, 1 ulp; results below 2^-126 may flush to
 // zero, which is below the rounding of any row sum, whose largest term is exp(0) = 1). m is
 // never -inf here (the caller substitutes 0), so x = -inf gives exp2(-inf) = 0 without a NaN.
@@ -286,7 +324,7 @@ __global__ __launch_bounds__(WAVES * 64, MIN_WAVES) void attention_kernel(AttnPa
                 block_max = fmaxf(block_max, sacc[sb][e]);
             }
         }
-        block_max = fmaxf(block_max, __shfl_xor(block_max, 32, 64));
+        block_max = max_halves(block_max);
         const float m_new = fmaxf(m_run, block_max);
         const float m_use = m_new == -INFINITY ? 0.0f : m_new;
         const float rescale = weight(m_run, m_use); // exactly 1 where the maximum stayed
@@ -367,7 +405,7 @@ __global__ __launch_bounds__(WAVES * 64, MIN_WAVES) void attention_kernel(AttnPa
     }
 
     // ---- normalise, stage [32 queries][D] per wavefront in LDS, store 16-byte rows ----
-    const float l_total = l_run + __shfl_xor(l_run, 32, 64);
+    const float l_total = sum_halves(l_run);
     // A row whose every key was removed has l_total == 0 and gives zeros; a NaN score makes
     // l_total NaN and so the whole row.
     const float inv = l_total == 0.0f ? 0.0f : 1.0f / l_total;
@@ -644,8 +682,7 @@ __global__ __launch_bounds__(WAVES * 64, 4) void attention16_kernel(AttnParams p
                 block_max = fmaxf(block_max, sacc[j][r]);
             }
         }
-        block_max = fmaxf(block_max, __shfl_xor(block_max, 16, 64));
-        block_max = fmaxf(block_max, __shfl_xor(block_max, 32, 64));
+        block_max = max_halves(max_rows16(block_max));
         const float m_new = fmaxf(m_run, block_max);
         const float m_use = m_new == -INFINITY ? 0.0f : m_new;
         // The rescale is 1 for every lane whose maximum stayed (most blocks past the first few):
@@ -716,8 +753,7 @@ __global__ __launch_bounds__(WAVES * 64, 4) void attention16_kernel(AttnParams p
     }
 
     // ---- normalise, stage [16 queries][D] per wavefront in LDS, store 16-byte rows ----
-    float l_total = l_run + __shfl_xor(l_run, 16, 64);
-    l_total += __shfl_xor(l_total, 32, 64);
+    const float l_total = sum_halves(sum_rows16(l_run));
     const float inv = l_total == 0.0f ? 0.0f : 1.0f / l_total;
     float* stage = smem + wave * 16 * kStagePitch;
     __syncthreads();
