@@ -111,23 +111,10 @@ __device__ inline BlockWork block_work(const AttnParams& p) {
     return w;
 }
 
-// max / sum of the values in lanes l and l ^ 16 (rows16) or l and l ^ 32 (halves), in every lane.
-// gfx950's v_permlane16_swap / v_permlane32_swap exchange 16-lane rows (32-lane halves) of two
-// registers in the vector ALU; given x twice, one result holds the even rows' values in every
-// lane and the other the odd rows', so one max or add of the two combines each pair. This
-// replaces an LDS-crossbar permute and its wait on the softmax's critical path. Both operands
-// are symmetric, so every lane gets the same bits that lane l ^ 16 (l ^ 32) gets.
-template <bool HALVES>
-__device__ inline void swap_pair(float x, float& a, float& b) {
-    const unsigned u = __float_as_uint(x);
-    const auto r = HALVES ? __builtin_amdgcn_permlane32_swap(u, u, false, false)
-                          : __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    // The two elements are read into scalars first: a bit cast of an element of the returned
-    // vector reads element 0 whatever index it names.
-    const unsigned lo = r[0], hi = r[1];
-    a = __uint_as_float(lo);
-    b = __uint_as_float(hi);
-}
+// max / sum of the values in lanes l and l ^ 16 (rows16) or l and l ^ 32 (halves), in every lane,
+// through the vector ALU's lane swaps (mfr::dev::swap_pair), not an LDS-crossbar permute and its
+// wait on the softmax's critical path; every lane of a pair gets the same bits.
+using mfr::dev::swap_pair;
 __device__ inline float max_rows16(float x) {
     float a, b;
     swap_pair<false>(x, a, b);

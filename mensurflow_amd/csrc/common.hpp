@@ -174,6 +174,61 @@ __device__ inline float wave_max(float v) {
     return v;
 }
 
+// Lane exchanges in the vector ALU (no LDS-crossbar permute and no wait on the LDS counter).
+// swap_pair<true>(x, a, b): gfx950's v_permlane32_swap given x twice, so a holds lanes 0-31's
+// values and b lanes 32-63's, each in both halves: lane l finds its own value and lane l ^ 32's
+// in (a, b), in that order for l < 32 and swapped for l >= 32. swap_pair<false> does the same
+// for 16-lane rows (v_permlane16_swap: a the even rows', b the odd rows'), partners l and l ^ 16.
+// A max or a sum of a and b therefore gives every lane of a pair the same bits.
+template <bool HALVES>
+__device__ inline void swap_pair(float x, float& a, float& b) {
+    const unsigned u = __float_as_uint(x);
+    const auto r = HALVES ? __builtin_amdgcn_permlane32_swap(u, u, false, false)
+                          : __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    // The elements are read into scalars first: a bit cast of an element of the returned vector
+    // reads element 0 whatever index it names.
+    const unsigned lo = r[0], hi = r[1];
+    a = __uint_as_float(lo);
+    b = __uint_as_float(hi);
+}
+
+// Lane l ^ m's value for m = 1, 2, 4, 8, through DPP: quad permutations for 1 and 2, a row
+// rotation by 8 for 8, and for 4 a row shift left by 4 in the lanes with bit 2 clear (DPP banks
+// 0 and 2) merged with a shift right by 4 in the others (banks 1 and 3).
+template <int M>
+__device__ inline float xor_lane(float x) {
+    const int u = __float_as_int(x);
+    int r;
+    if constexpr (M == 1) {
+        r = __builtin_amdgcn_update_dpp(u, u, 0xB1, 0xF, 0xF, false); // quad_perm [1,0,3,2]
+    } else if constexpr (M == 2) {
+        r = __builtin_amdgcn_update_dpp(u, u, 0x4E, 0xF, 0xF, false); // quad_perm [2,3,0,1]
+    } else if constexpr (M == 4) {
+        const int up = __builtin_amdgcn_update_dpp(u, u, 0x104, 0xF, 0x5, false); // row_shl:4
+        r = __builtin_amdgcn_update_dpp(up, u, 0x114, 0xF, 0xA, false);          // row_shr:4
+    } else {
+        static_assert(M == 8, "xor_lane takes 1, 2, 4 or 8");
+        r = __builtin_amdgcn_update_dpp(u, u, 0x128, 0xF, 0xF, false); // row_ror:8
+    }
+    return __int_as_float(r);
+}
+
+// The sum over the 64 lanes by the xor butterfly (partners l ^ 32, 16, 8, 4, 2, 1 in turn), the
+// total in every lane; each step adds a lane's value and its partner's, so the bits are those
+// of v += __shfl_xor(v, m) over the same steps.
+__device__ inline float butterfly_sum(float v) {
+    float a, b;
+    swap_pair<true>(v, a, b);
+    v = a + b;
+    swap_pair<false>(v, a, b);
+    v = a + b;
+    v += xor_lane<8>(v);
+    v += xor_lane<4>(v);
+    v += xor_lane<2>(v);
+    v += xor_lane<1>(v);
+    return v;
+}
+
 __device__ inline int wave_or(int v) {
 #pragma unroll
     for (int offset = 32; offset > 0; offset >>= 1) {

@@ -198,11 +198,7 @@ __global__ __launch_bounds__(kThinThreads) void thin_dot_kernel(ThinParams p) {
     for (int r = 0; r < kThinRowsPerWave; ++r) {
 #pragma unroll
         for (int j = 0; j < C; ++j) {
-            float v = acc[r][j];
-#pragma unroll
-            for (int offset = 32; offset > 0; offset >>= 1) {
-                v += __shfl_xor(v, offset, 64);
-            }
+            const float v = mfr::dev::butterfly_sum(acc[r][j]);
             mine = lane == r * C + j ? v : mine;
         }
     }
@@ -307,11 +303,7 @@ __global__ __launch_bounds__(64 * kStripWaves) void strip_stage_kernel(ThinParam
     float mine = 0.0f;
 #pragma unroll
     for (int j = 0; j < C; ++j) {
-        float v = acc[j];
-#pragma unroll
-        for (int offset = 32; offset > 0; offset >>= 1) {
-            v += __shfl_xor(v, offset, 64);
-        }
+        const float v = mfr::dev::butterfly_sum(acc[j]);
         mine = lane == j ? v : mine;
     }
     if (lane < cols) {
