@@ -443,27 +443,37 @@ constexpr int kWaves16 = 8;
 //   - O^T += V^T P^T over key steps (j, r): lane l's B value is its own score register
 //     sacc[j][r] (query l%16, key 16j + 4(l/16) + r), and its A value V(key, 16c + l%16), read
 //     from a transposed V tile [d][BK+4] as one 16-byte read per 4 steps.
-//   - K tiles are [keys][D+4]; V tiles are written transposed (each thread loads 4 adjacent d of
-//     one key and stores them down a column; adjacent lanes take adjacent keys, so the stores
-//     hit distinct banks). Both are double-buffered with one barrier per key block.
+//   - K tiles come by direct-to-LDS buffer loads into [keys][D], their 16-byte pieces swizzled
+//     (piece c of key r at c ^ (r & 15)) in place of padding; V tiles are written transposed
+//     (each thread loads 4 adjacent d of one key and stores them down a column; adjacent lanes
+//     take adjacent keys, so the stores hit distinct banks). Both are double-buffered with one
+//     barrier per key block, the key loop unrolled by two so each half names its K buffers.
+//     (V^T by 4-byte direct loads, each a 64-key gather, measured 182 against 174 us.)
 template <int D, int BK, bool MASKED, int WAVES>
 __global__ __launch_bounds__(WAVES * 64, 4) void attention16_kernel(AttnParams p) {
     constexpr int THREADS = WAVES * 64;
     constexpr int BLOCK_Q = WAVES * 16;
     constexpr int KB = BK / 16;  // 16-key blocks per key block
     constexpr int DB = D / 16;   // 16-wide output column blocks; 16-deep groups of q . k
-    constexpr int KP = D + 4;    // K tile pitch
     constexpr int VP = BK + 4;   // V^T tile pitch
-    constexpr int kKFloats = BK * KP;
     constexpr int kVFloats = D * VP;
-    constexpr int kTileFloats = 2 * (kKFloats + kVFloats);
     constexpr int kStagePitch = D + 4;
     constexpr int kStageFloats = BLOCK_Q * kStagePitch;
-    constexpr int kQuads = BK * (D / 4);                              // 16-byte pieces per tile
+    constexpr int kQuads = BK * (D / 4);                              // 16-byte pieces per V tile
     constexpr int kLoads = (kQuads + THREADS - 1) / THREADS;          // per thread per tile
-    __shared__ float smem[kTileFloats > kStageFloats ? kTileFloats : kStageFloats];
-    auto lds_k = [&](int which) { return smem + which * kKFloats; };
-    auto lds_v = [&](int which) { return smem + 2 * kKFloats + which * kVFloats; };
+    static_assert(D == 64 && BK == 64, "the swizzled K tile takes 64 keys of 16 pieces");
+    constexpr int kKFloats = BK * D;
+    constexpr int kKInstr = kKFloats / 256; // 1 KiB wave-instructions per K tile
+    constexpr int kKPerWave = kKInstr / WAVES;
+    static_assert(kKInstr % WAVES == 0, "K tile instructions per wavefront");
+    constexpr int kVTiles = 2 * kVFloats > kStageFloats ? 2 * kVFloats : kStageFloats;
+    // One LDS object per K buffer: the compiler then sees that the direct-to-LDS copy into one
+    // does not write the one the score MFMAs read, and does not wait for the copy to land before
+    // those reads. The output stage reuses the V tiles.
+    __shared__ __align__(16) float k_tile0[kKFloats];
+    __shared__ __align__(16) float k_tile1[kKFloats];
+    __shared__ __align__(16) float v_tiles[kVTiles];
+    auto lds_v = [&](int which) { return v_tiles + which * kVFloats; };
 
     const BlockWork work = block_work(p);
     const int64_t qb = work.qb;
@@ -529,21 +539,18 @@ __global__ __launch_bounds__(WAVES * 64, 4) void attention16_kernel(AttnParams p
     };
     auto needed = [&](int64_t blk) { return wave_live && (!p.causal || blk * BK <= wq0 + 15); };
 
-    // Tile loads: piece u of K is (key u / (D/4), depths 4(u % (D/4))..+3); piece u of V is
-    // (key u % BK, depths 4(u / BK)..+3). They are buffer loads: the block's first key row is
-    // the resource's base and its record count ends after the block's last key, so pieces of
-    // keys past the end read as zeros with no per-lane test, and a lane's byte offset within a
-    // tile is one register fixed for the whole key loop (the host keeps BK rows under 2^30
-    // bytes). Loads through a per-block address register made the compiler wait for them
-    // before the next LDS reads.
-    float4 kr[kLoads], vr[kLoads];
-    uint32_t k_off[kLoads], v_off[kLoads];
+    // Tile loads: piece u of V is (key u % BK, depths 4(u / BK)..+3). K and V come by buffer
+    // loads: the block's first key row is the resource's base and its record count ends after
+    // the block's last key, so pieces of keys past the end read as zeros with no per-lane test,
+    // and a lane's byte offset within a tile is a register fixed for the whole key loop (the
+    // host keeps BK rows under 2^30 bytes). Loads through a per-block address register made the
+    // compiler wait for them before the next LDS reads.
+    float4 vr[kLoads];
+    uint32_t v_off[kLoads];
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
         const int u = static_cast<int>(threadIdx.x) + i * THREADS;
-        const int kkey = u / (D / 4), kq = u % (D / 4);
         const int vkey = u % BK, vq = u / BK;
-        k_off[i] = u < kQuads ? static_cast<uint32_t>((kkey * p.k_rs + 4 * kq) * 4) : 0x80000000u;
         v_off[i] = u < kQuads ? static_cast<uint32_t>((vkey * p.v_rs + 4 * vq) * 4) : 0x80000000u;
     }
     auto tile_load = [](const float* rows, int64_t row_stride, int keys, uint32_t offset) {
@@ -554,31 +561,12 @@ __global__ __launch_bounds__(WAVES * 64, 4) void attention16_kernel(AttnParams p
         return make_float4(__uint_as_float(raw.x), __uint_as_float(raw.y),
                            __uint_as_float(raw.z), __uint_as_float(raw.w));
     };
-    auto load_k = [&](int64_t blk) {
-        const int keys = keys_in(blk);
-        const float* kb = k_base + blk * BK * p.k_rs;
-#pragma unroll
-        for (int i = 0; i < kLoads; ++i) {
-            kr[i] = tile_load(kb, p.k_rs, keys, k_off[i]);
-        }
-    };
     auto load_v = [&](int64_t blk) {
         const int keys = keys_in(blk);
         const float* vb = v_base + blk * BK * p.v_rs;
 #pragma unroll
         for (int i = 0; i < kLoads; ++i) {
             vr[i] = tile_load(vb, p.v_rs, keys, v_off[i]);
-        }
-    };
-    auto store_k = [&](int which) {
-        float* sk = lds_k(which);
-#pragma unroll
-        for (int i = 0; i < kLoads; ++i) {
-            const int u = static_cast<int>(threadIdx.x) + i * THREADS;
-            if (u < kQuads) {
-                const int kkey = u / (D / 4), kq = u % (D / 4);
-                *reinterpret_cast<float4*>(sk + kkey * KP + 4 * kq) = kr[i];
-            }
         }
     };
     auto store_v = [&](int which) {
@@ -595,13 +583,28 @@ __global__ __launch_bounds__(WAVES * 64, 4) void attention16_kernel(AttnParams p
             }
         }
     };
-    auto load_tiles = [&](int64_t blk) {
-        load_k(blk);
-        load_v(blk);
-    };
-    auto store_tiles = [&](int which) {
-        store_k(which);
-        store_v(which);
+    // K by direct-to-LDS buffer loads into [keys][D] with no padding: instruction i of a tile
+    // (keys 4i..4i+3) writes lane L's 16 bytes at L * 16, key 4i + L/16, physical piece L % 16,
+    // which holds logical piece (L % 16) ^ (key & 15). A lane reading key 16j + col, piece c,
+    // finds it at piece c ^ col, so 16 lanes with 16 keys read 16 different pieces. (Loaded into
+    // registers and stored to a padded tile, config 5 measured 1-2 % slower.)
+    uint32_t kd_off[kKPerWave];
+#pragma unroll
+    for (int j = 0; j < kKPerWave; ++j) {
+        const int key = 4 * (wave * kKPerWave + j) + lane / 16;
+        const int piece = (lane % 16) ^ (key & 15);
+        kd_off[j] = static_cast<uint32_t>((key * p.k_rs + 4 * piece) * 4);
+    }
+    auto direct_k = [&](int64_t blk, float* dst) {
+        const int keys = keys_in(blk);
+        const float* kb = k_base + blk * BK * p.k_rs;
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(kb), 0, static_cast<int>(keys * p.k_rs * 4), 0x00020000);
+#pragma unroll
+        for (int j = 0; j < kKPerWave; ++j) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, dst + (wave * kKPerWave + j) * 256, 16,
+                                                     static_cast<int>(kd_off[j]), 0, 0, 0);
+        }
     };
 
     auto scores = [&](const float* sk, floatx4(&sacc)[KB]) {
@@ -617,7 +620,8 @@ __global__ __launch_bounds__(WAVES * 64, 4) void attention16_kernel(AttnParams p
             float4 kf[KB];
 #pragma unroll
             for (int j = 0; j < KB; ++j) {
-                kf[j] = *reinterpret_cast<const float4*>(sk + (16 * j + col) * KP + 16 * a + 4 * g);
+                kf[j] = *reinterpret_cast<const float4*>(sk + (16 * j + col) * D +
+                                                         4 * ((4 * a + g) ^ col));
             }
 #pragma unroll
             for (int b = 0; b < 4; ++b) {
@@ -716,33 +720,44 @@ __global__ __launch_bounds__(WAVES * 64, 4) void attention16_kernel(AttnParams p
         }
     };
 
-    if (blocks > 0) {
-        load_tiles(0);
-        store_tiles(0);
-        __syncthreads();
-    }
-    for (int64_t kb = 0; kb < blocks; ++kb) {
-        const int cur = static_cast<int>(kb & 1);
+    // One key block: the next block's K copy (direct to LDS) and V loads are issued first, the
+    // V tile stored after this block's products, and the copy waited for before the barrier.
+    auto step = [&](int64_t kb, float* k_cur, float* k_next, int cur) {
         const bool more = kb + 1 < blocks;
         if (more) {
-            load_tiles(kb + 1);
+            direct_k(kb + 1, k_next);
+            load_v(kb + 1);
         }
         if (needed(kb)) {
             floatx4 sacc[KB];
-            scores(lds_k(cur), sacc);
+            scores(k_cur, sacc);
             softmax(kb * BK, sacc);
             accumulate(lds_v(cur), sacc);
         }
         if (more) {
-            store_tiles(cur ^ 1);
+            store_v(cur ^ 1);
         }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+    };
+    if (blocks > 0) {
+        direct_k(0, k_tile0);
+        load_v(0);
+        store_v(0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+    for (int64_t kb = 0; kb < blocks; kb += 2) {
+        step(kb, k_tile0, k_tile1, 0);
+        if (kb + 1 < blocks) {
+            step(kb + 1, k_tile1, k_tile0, 1);
+        }
     }
 
     // ---- normalise, stage [16 queries][D] per wavefront in LDS, store 16-byte rows ----
     const float l_total = sum_halves(sum_rows16(l_run));
     const float inv = l_total == 0.0f ? 0.0f : 1.0f / l_total;
-    float* stage = smem + wave * 16 * kStagePitch;
+    float* stage = v_tiles + wave * 16 * kStagePitch;
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < DB; ++c) {
