@@ -76,30 +76,39 @@ bool agrees(const std::vector<std::vector<float>>& want,
     return true;
 }
 
-// Median milliseconds of `run`, which waits for its own work. Each sample repeats the call until
-// it lasts about a millisecond.
+// Median milliseconds per call of `run`, which waits for its own work. Calls are timed in
+// batches. The batch doubles from one call until it lasts at least a millisecond, so that short
+// calls stay above the clock's resolution, and that calibrating batch is the first sample. More
+// batches follow until there are options.min_samples of them and options.min_time_s has passed,
+// 500 at most.
 double median_ms(const std::function<void()>& run, const TuneOptions& options) {
-    run(); // warm-up
-    const auto probe = Clock::now();
-    run();
-    const double once = std::max(std::chrono::duration<double>(Clock::now() - probe).count(), 1e-7);
-    const int repeats = std::max(1, static_cast<int>(1e-3 / once));
-    std::vector<double> samples;
-    const auto start = Clock::now();
-    while (static_cast<int>(samples.size()) < options.min_samples ||
-           std::chrono::duration<double>(Clock::now() - start).count() < options.min_time_s) {
+    const auto batch_seconds = [&run](int calls) {
         const auto t0 = Clock::now();
-        for (int i = 0; i < repeats; ++i) {
+        for (int i = 0; i < calls; ++i) {
             run();
         }
-        samples.push_back(std::chrono::duration<double>(Clock::now() - t0).count() / repeats);
-        if (samples.size() >= 500) {
-            break;
-        }
+        return std::chrono::duration<double>(Clock::now() - t0).count();
+    };
+    run(); // the first call carries one-time costs (plans, caches)
+    int batch = 1;
+    double seconds = batch_seconds(batch);
+    while (seconds < 1e-3 && batch < (1 << 20)) {
+        batch *= 2;
+        seconds = batch_seconds(batch);
     }
-    std::nth_element(samples.begin(), samples.begin() + static_cast<std::ptrdiff_t>(samples.size() / 2),
-                     samples.end());
-    return samples[samples.size() / 2] * 1e3;
+    std::vector<double> per_call{seconds / batch};
+    const auto sampling = Clock::now();
+    const auto enough = [&] {
+        const double spent = std::chrono::duration<double>(Clock::now() - sampling).count();
+        return static_cast<int>(per_call.size()) >= options.min_samples &&
+               spent >= options.min_time_s;
+    };
+    while (per_call.size() < 500 && !enough()) {
+        per_call.push_back(batch_seconds(batch) / batch);
+    }
+    const auto middle = per_call.begin() + static_cast<std::ptrdiff_t>(per_call.size() / 2);
+    std::nth_element(per_call.begin(), middle, per_call.end());
+    return *middle * 1e3;
 }
 
 // Every point of `region` (the product of its axes, the last axis fastest) that the kernel allows

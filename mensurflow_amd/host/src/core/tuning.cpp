@@ -9,6 +9,8 @@
 #include <cstdlib>
 #include <cstring>
 #include <fstream>
+#include <iomanip>
+#include <regex>
 #include <sstream>
 #include <stdexcept>
 #include <string_view>
@@ -133,92 +135,107 @@ std::int64_t setting(const TuningValues& values, const std::string& name, std::i
 
 // ---- the results file --------------------------------------------------------------------------
 
+namespace {
+
+// One result line, "<op> <device> v<version> <key words> -> <settings> | <best> ms (default <ms>
+// ms) <mode>", taken apart by one pattern; the key is every word between the version and the
+// arrow. The error texts name the part that did not match, as the file format's readers expect.
+TuningEntry parse_result(const std::string& line, const std::string& machine) {
+    static const std::regex whole(
+        R"(^(\S+)\s+(\S+)\s+(\S+)((?:\s+\S+)*?)\s+->\s*(.*?)\s*\|\s*(.*)$)");
+    static const std::regex times(R"(^(\S+)\s+ms\s+\(default\s+(\S+)\s+ms\)\s+(\S+)$)");
+    std::smatch part;
+    if (!std::regex_match(line, part, whole)) {
+        throw std::invalid_argument("expected '<op> <device> v<version> <key> -> <settings> | "
+                                    "<ms> ms (default <ms> ms) <mode>'");
+    }
+    const std::string version = part[3].str();
+    if (version.size() < 2 || version[0] != 'v') {
+        throw std::invalid_argument("expected '<op> <device> v<version>' at the start");
+    }
+    TuningEntry entry;
+    entry.machine = machine;
+    entry.op = part[1].str();
+    entry.device = part[2].str();
+    std::size_t used = 0;
+    entry.version = std::stoi(version.substr(1), &used);
+    if (used + 1 != version.size()) {
+        throw std::invalid_argument("expected '<op> <device> v<version>' at the start");
+    }
+    entry.key = joined(words(part[4].str()), 0); // runs of blanks in the key count as one
+    entry.config = parse_settings(part[5].str());
+    const std::string tail = part[6].str();
+    std::smatch timing;
+    if (!std::regex_match(tail, timing, times)) {
+        throw std::invalid_argument("expected '<ms> ms (default <ms> ms) <mode>' after '|'");
+    }
+    entry.best_ms = std::stod(timing[1].str());
+    entry.default_ms = std::stod(timing[2].str());
+    entry.mode = timing[3].str();
+    return entry;
+}
+
+} // namespace
+
 void TuningCache::load(const std::string& path) {
     std::ifstream file(path);
     if (!file) {
-        return;
+        return; // no results stored yet
     }
-    std::vector<TuningEntry> read;
+    std::vector<TuningEntry> parsed;
     std::string machine;
-    int line_number = 0;
-    for (std::string raw; std::getline(file, raw);) {
-        ++line_number;
-        const std::string_view line = strip(raw);
-        const auto bad = [&](const std::string& why) {
-            return std::runtime_error(path + ":" + std::to_string(line_number) + ": " + why);
-        };
-        if (line.empty() || line.front() == '#') {
-            continue;
-        }
-        if (line.rfind("machine ", 0) == 0) {
-            machine = std::string(strip(line.substr(8)));
-            continue;
-        }
-        if (machine.empty()) {
-            throw bad("a result before any 'machine' line");
-        }
-        if (line.rfind("place ", 0) == 0) {
-            continue; // an older device-choice form: ignored, measured again when tuned
-        }
-        const std::size_t arrow = line.find(" -> ");
-        const std::size_t bar = arrow == std::string_view::npos ? arrow : line.find(" | ", arrow);
-        if (bar == std::string_view::npos) {
-            throw bad("expected '<op> <device> v<version> <key> -> <settings> | <ms> ms (default "
-                      "<ms> ms) <mode>'");
-        }
-        TuningEntry entry;
-        entry.machine = machine;
+    std::string raw;
+    for (int number = 1; std::getline(file, raw); ++number) {
+        const std::string line(strip(raw));
         try {
-            const std::vector<std::string> head = words(line.substr(0, arrow));
-            if (head.size() < 3 || head[2].size() < 2 || head[2][0] != 'v') {
-                throw bad("expected '<op> <device> v<version>' at the start");
+            if (line.empty() || line.front() == '#') {
+                continue;
             }
-            entry.op = head[0];
-            entry.device = head[1];
-            entry.version = std::stoi(head[2].substr(1));
-            entry.key = joined(head, 3);
-            entry.config = parse_settings(line.substr(arrow + 4, bar - arrow - 4));
-            const std::string tail(line.substr(bar + 3));
-            char mode[64] = {};
-            if (std::sscanf(tail.c_str(), "%lf ms (default %lf ms) %63s", &entry.best_ms,
-                            &entry.default_ms, mode) != 3) {
-                throw bad("expected '<ms> ms (default <ms> ms) <mode>' after '|'");
+            if (line.compare(0, 8, "machine ") == 0) {
+                machine = std::string(strip(std::string_view(line).substr(8)));
+            } else if (machine.empty()) {
+                throw std::invalid_argument("a result before any 'machine' line");
+            } else if (line.compare(0, 6, "place ") != 0) {
+                // ("place" lines are the older device-choice form: skipped, measured again
+                // when tuned.)
+                parsed.push_back(parse_result(line, machine));
             }
-            entry.mode = mode;
-        } catch (const std::invalid_argument& e) {
-            throw bad(e.what());
         } catch (const std::out_of_range& e) {
-            throw bad(std::string("number out of range: ") + e.what());
+            throw std::runtime_error(path + ":" + std::to_string(number) +
+                                     ": number out of range: " + e.what());
+        } catch (const std::invalid_argument& e) {
+            throw std::runtime_error(path + ":" + std::to_string(number) + ": " + e.what());
         }
-        read.push_back(std::move(entry));
     }
-    entries_ = std::move(read);
+    entries_.swap(parsed);
 }
 
 void TuningCache::write(std::ostream& out) const {
-    out << "# mensurflow tuning results (format: src/core/tuning.hpp)\n"
-        << "# <op> <device> v<version> <key> -> <settings> | <best> ms (default <ms> ms) <mode>\n"
-        << "# device 'auto': the device for Execution::Auto, gpu=0 or gpu=1 (times include the "
-           "copies)\n";
-    std::vector<std::string> machines;
+    // The entries grouped by machine, machines in the order they first appear.
+    std::vector<std::pair<std::string, std::vector<const TuningEntry*>>> groups;
     for (const TuningEntry& entry : entries_) {
-        if (std::find(machines.begin(), machines.end(), entry.machine) == machines.end()) {
-            machines.push_back(entry.machine);
+        auto group = std::find_if(groups.begin(), groups.end(),
+                                  [&](const auto& g) { return g.first == entry.machine; });
+        if (group == groups.end()) {
+            group = groups.insert(groups.end(), {entry.machine, {}});
+        }
+        group->second.push_back(&entry);
+    }
+    std::ostringstream text;
+    text << "# mensurflow tuning results (format: src/core/tuning.hpp)\n"
+         << "# <op> <device> v<version> <key> -> <settings> | <best> ms (default <ms> ms) <mode>\n"
+         << "# device 'auto': the device for Execution::Auto, gpu=0 or gpu=1 (times include the "
+            "copies)\n";
+    text << std::fixed << std::setprecision(4);
+    for (const auto& [machine, members] : groups) {
+        text << "\nmachine " << machine << '\n';
+        for (const TuningEntry* e : members) {
+            text << e->op << ' ' << e->device << " v" << e->version << ' ' << e->key << " -> "
+                 << mensurflow::to_string(e->config) << " | " << e->best_ms << " ms (default "
+                 << e->default_ms << " ms) " << e->mode << '\n';
         }
     }
-    for (const std::string& machine : machines) {
-        out << "\nmachine " << machine << '\n';
-        for (const TuningEntry& e : entries_) {
-            if (e.machine != machine) {
-                continue;
-            }
-            char times[96];
-            std::snprintf(times, sizeof times, "%.4f ms (default %.4f ms) ", e.best_ms,
-                          e.default_ms);
-            out << e.op << ' ' << e.device << " v" << e.version << ' ' << e.key << " -> "
-                << mensurflow::to_string(e.config) << " | " << times << e.mode << '\n';
-        }
-    }
+    out << text.str();
 }
 
 void TuningCache::save(const std::string& path) const {
