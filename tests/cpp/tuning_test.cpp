@@ -271,6 +271,46 @@ void test_results_file_round_trip() {
         threw = std::string(e.what()).find(":3: ") != std::string::npos;
     }
     test::require(threw, "a malformed line is reported with its number");
+    // Each malformed form is reported with its line number and the part that did not match.
+    const std::pair<const char*, const char*> malformed[] = {
+        {"matmul rocm v2 m=1 -> tile=5 | 1 ms (default 2 ms) tested\n",
+         ":1: a result before any 'machine' line"},
+        {"machine A\nmatmul rocm v2 m=1 -> tile=5 1 ms (default 2 ms) tested\n",
+         ":2: expected '<op> <device> v<version> <key> -> <settings> | "},
+        {"machine A\nmatmul rocm 2 m=1 -> tile=5 | 1 ms (default 2 ms) tested\n",
+         ":2: expected '<op> <device> v<version>' at the start"},
+        {"machine A\nmatmul rocm v2x m=1 -> tile=5 | 1 ms (default 2 ms) tested\n",
+         ":2: expected '<op> <device> v<version>' at the start"},
+        {"machine A\n\n# note\nmatmul rocm v2 m=1 -> tile=5 | 1 ms tested\n",
+         ":4: expected '<ms> ms (default <ms> ms) <mode>' after '|'"},
+        {"machine A\nmatmul rocm v2 m=1 -> tile=99999999999999999999 | 1 ms (default 2 ms) t\n",
+         ":2: number out of range: "},
+    };
+    for (const auto& [text, message] : malformed) {
+        {
+            std::ofstream out(path);
+            out << text;
+        }
+        std::string what;
+        try {
+            back.load(path);
+        } catch (const std::runtime_error& e) {
+            what = e.what();
+        }
+        test::require(what.find(message) != std::string::npos,
+                      std::string("malformed line reported as '") + message + "', got '" + what + "'");
+    }
+    // Older "place" lines are skipped; empty settings and an empty key read back as empty.
+    {
+        std::ofstream out(path);
+        out << "  machine  A | B  \nplace matmul 1x2 -> cpu\n"
+            << "matmul rocm v2  ->  | 0.5 ms (default 0.5 ms) tested\n";
+    }
+    back.load(path);
+    test::require(back.entries().size() == 1 && back.entries()[0].machine == "A | B" &&
+                      back.entries()[0].key.empty() && back.entries()[0].config.empty() &&
+                      back.entries()[0].best_ms == 0.5 && back.entries()[0].mode == "tested",
+                  "place lines skipped, empty key and settings read");
     std::remove(path.c_str());
 }
 
