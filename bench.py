@@ -59,7 +59,9 @@ def cpp_api_timing():
                    "0.5), gemv (16384^2, N and T), gemm_epilogue (the MLP with bias and tanh "
                    "gelu) and attention (config 5, causal) with Execution::GPU, each returning "
                    "a new tensor; after 50 ms of untimed calls, runs of 20 calls ended by a "
-                   "read-back until at least 50 ms are timed")
+                   "read-back until at least 50 ms are timed; host_resident_*: the same GEMM and "
+                   "gemv N with the operands in host memory, so each call also copies them in "
+                   "and the result out over PCIe (pageable, synchronous), one call per run")
     return out
 
 

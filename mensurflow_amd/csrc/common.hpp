@@ -77,6 +77,15 @@ struct mfr_stream {
     int compute_units = 256; // of the stream's device, read at creation
     std::mutex workspace_mutex;
 
+    // Pinned host staging for copies from and to pageable host memory (allocated on first use,
+    // freed with the stream): two slots, each with an event recorded after the DMA that last
+    // read or filled it, so the CPU's copy into (or out of) one slot overlaps the DMA of the
+    // other. `staging_mutex` is held for a whole copy.
+    static constexpr size_t kStagingBytes = size_t{16} << 20;
+    void* staging[2] = {nullptr, nullptr};
+    hipEvent_t staging_done[2] = {nullptr, nullptr};
+    std::mutex staging_mutex;
+
     // Makes this stream's device current on the calling thread (each ABI call does, as the
     // reference's CudaStream::activate does per call).
     void activate() const { mfr::check(hipSetDevice(device), "hipSetDevice"); }

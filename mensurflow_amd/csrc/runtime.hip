@@ -2,6 +2,7 @@
 // runtime half of the reference's Backend/Buffer/Stream interface (src/backends/backend.hpp).
 #include "common.hpp"
 
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 #include <vector>
@@ -350,6 +351,26 @@ void collapse(CopyShape& s) {
     s = out;
 }
 
+// Copies between pageable host memory and the device of at least this many bytes go through
+// the stream's pinned staging slots. From pageable memory directly, the runtime's own path
+// measured about 4 GB/s for 1 GiB on an MI355X box; small copies keep it (one call, no staging).
+constexpr size_t kStagedCopyBytes = size_t{1} << 20;
+
+// The stream's two pinned staging slots and their events, allocated once. The caller holds
+// s.staging_mutex.
+void ensure_staging(mfr_stream& s) {
+    for (int slot = 0; slot < 2; ++slot) {
+        if (s.staging[slot] == nullptr) {
+            check(hipHostMalloc(&s.staging[slot], mfr_stream::kStagingBytes, hipHostMallocDefault),
+                  "hipHostMalloc(staging)");
+        }
+        if (s.staging_done[slot] == nullptr) {
+            check(hipEventCreateWithFlags(&s.staging_done[slot], hipEventDisableTiming),
+                  "hipEventCreateWithFlags(staging)");
+        }
+    }
+}
+
 } // namespace
 
 extern "C" {
@@ -453,6 +474,14 @@ int mfr_stream_destroy(mfr_stream_t stream) {
         if (stream->workspace != nullptr) {
             check(hipFree(stream->workspace), "hipFree(workspace)");
         }
+        for (int slot = 0; slot < 2; ++slot) {
+            if (stream->staging[slot] != nullptr) {
+                check(hipHostFree(stream->staging[slot]), "hipHostFree(staging)");
+            }
+            if (stream->staging_done[slot] != nullptr) {
+                check(hipEventDestroy(stream->staging_done[slot]), "hipEventDestroy(staging)");
+            }
+        }
         if (stream->owned && stream->stream != nullptr) {
             check(hipStreamDestroy(stream->stream), "hipStreamDestroy");
         }
@@ -491,8 +520,27 @@ int mfr_memcpy_h2d(mfr_stream_t stream, void* dst, const void* src, size_t bytes
             return;
         }
         require(dst != nullptr && src != nullptr, "mfr_memcpy_h2d: null pointer");
-        check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s.stream), "hipMemcpyAsync");
-        // Pageable source: complete before returning so the caller may reuse it.
+        if (bytes < kStagedCopyBytes) {
+            check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s.stream),
+                  "hipMemcpyAsync");
+        } else {
+            std::lock_guard<std::mutex> hold(s.staging_mutex);
+            ensure_staging(s);
+            const auto* from = static_cast<const unsigned char*>(src);
+            auto* to = static_cast<unsigned char*>(dst);
+            for (size_t off = 0, i = 0; off < bytes; off += mfr_stream::kStagingBytes, ++i) {
+                const size_t n = std::min(mfr_stream::kStagingBytes, bytes - off);
+                const int slot = static_cast<int>(i & 1);
+                // The DMA that last read this slot (two chunks back) has finished.
+                check(hipEventSynchronize(s.staging_done[slot]), "hipEventSynchronize");
+                std::memcpy(s.staging[slot], from + off, n);
+                check(hipMemcpyAsync(to + off, s.staging[slot], n, hipMemcpyHostToDevice,
+                                     s.stream),
+                      "hipMemcpyAsync");
+                check(hipEventRecord(s.staging_done[slot], s.stream), "hipEventRecord");
+            }
+        }
+        // Complete before returning, so the caller may reuse or free the source.
         check(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
     });
 }
@@ -505,7 +553,37 @@ int mfr_memcpy_d2h(mfr_stream_t stream, void* dst, const void* src, size_t bytes
             return;
         }
         require(dst != nullptr && src != nullptr, "mfr_memcpy_d2h: null pointer");
-        check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s.stream), "hipMemcpyAsync");
+        if (bytes < kStagedCopyBytes) {
+            check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s.stream),
+                  "hipMemcpyAsync");
+            check(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
+            return;
+        }
+        std::lock_guard<std::mutex> hold(s.staging_mutex);
+        ensure_staging(s);
+        const auto* from = static_cast<const unsigned char*>(src);
+        auto* to = static_cast<unsigned char*>(dst);
+        const size_t chunk = mfr_stream::kStagingBytes;
+        const size_t chunks = (bytes + chunk - 1) / chunk;
+        // Chunk i goes device -> slot i % 2 -> dst. Chunk i + 1's DMA is queued before chunk i is
+        // copied out; its slot held chunk i - 1, which the previous step finished copying out.
+        const auto queue = [&](size_t i) {
+            const size_t n = std::min(chunk, bytes - i * chunk);
+            const int slot = static_cast<int>(i & 1);
+            check(hipMemcpyAsync(s.staging[slot], from + i * chunk, n, hipMemcpyDeviceToHost,
+                                 s.stream),
+                  "hipMemcpyAsync");
+            check(hipEventRecord(s.staging_done[slot], s.stream), "hipEventRecord");
+        };
+        queue(0);
+        for (size_t i = 0; i < chunks; ++i) {
+            if (i + 1 < chunks) {
+                queue(i + 1);
+            }
+            const int slot = static_cast<int>(i & 1);
+            check(hipEventSynchronize(s.staging_done[slot]), "hipEventSynchronize");
+            std::memcpy(to + i * chunk, s.staging[slot], std::min(chunk, bytes - i * chunk));
+        }
         check(hipStreamSynchronize(s.stream), "hipStreamSynchronize");
     });
 }

@@ -109,12 +109,28 @@ int main(int argc, char** argv) {
     const double attention_us =
         time_us([&] { (void)attention(q, k, v, nullptr, true, 0.0f, on); }, calls, probe);
 
+    // The same GEMM and gemv N with the operands in host memory: Execution::GPU copies them to
+    // the device, runs the kernel and copies the result back (pageable, synchronous copies, as
+    // the reference's GPU backends do), so these calls include the PCIe transfers. One call per
+    // run; the result is a host tensor, so each call has finished when it returns.
+    const Device cpu{DeviceType::CPU, 0};
+    const Tensor ha = a.to(cpu), hb = b.to(cpu), hc0 = c0.to(cpu);
+    const double host_gemm_us =
+        time_us([&] { (void)gemm(ha, hb, 1.5f, &hc0, 0.5f, false, true, on); }, 1, probe);
+    const Tensor hga = ga.to(cpu), hgx = gx.to(cpu), hgy = gy.to(cpu);
+    const double host_gemv_us =
+        time_us([&] { (void)gemv(hga, hgx, 2.0f, &hgy, 0.5f, false, on); }, 1, probe);
+
     const double gemm_tflops = 2.0 * n * n * n / (gemm_us * 1e-6) / 1e12;
     const double gemv_bytes = 4.0 * (static_cast<double>(g) * g + 3.0 * g);
     std::printf("{\"calls_per_run\": %d, \"gemm_4096_us\": %.1f, \"gemm_4096_tflops\": %.2f, "
                 "\"gemv_n_us\": %.2f, \"gemv_n_gbs\": %.1f, \"gemv_t_us\": %.2f, "
-                "\"gemv_t_gbs\": %.1f, \"mlp_us\": %.1f, \"attention_cfg5_us\": %.1f}\n",
+                "\"gemv_t_gbs\": %.1f, \"mlp_us\": %.1f, \"attention_cfg5_us\": %.1f, "
+                "\"host_resident_gemm_4096_ms\": %.2f, \"host_resident_gemm_4096_tflops\": %.2f, "
+                "\"host_resident_gemv_n_ms\": %.2f, \"host_resident_gemv_n_gbs\": %.1f}\n",
                 calls, gemm_us, gemm_tflops, gemv_n_us, gemv_bytes / (gemv_n_us * 1e-6) / 1e9,
-                gemv_t_us, gemv_bytes / (gemv_t_us * 1e-6) / 1e9, mlp_us, attention_us);
+                gemv_t_us, gemv_bytes / (gemv_t_us * 1e-6) / 1e9, mlp_us, attention_us,
+                host_gemm_us * 1e-3, 2.0 * n * n * n / (host_gemm_us * 1e-6) / 1e12,
+                host_gemv_us * 1e-3, gemv_bytes / (host_gemv_us * 1e-6) / 1e9);
     return 0;
 }

@@ -5,6 +5,7 @@
 #include "core/dispatcher.hpp"
 
 #include "core/registry.hpp"
+#include "core/tensor_access.hpp"
 #include "core/tuning.hpp"
 
 #include <stdexcept>
@@ -86,7 +87,14 @@ class Relocation {
     void write_back(Device home) const {
         for (std::size_t i = 0; i < moved_.outputs.size(); ++i) {
             Tensor destination = original_.outputs[i]; // shares the caller's storage
-            destination.copy_from(moved_.outputs[i].to(home));
+            std::byte* host = TensorAccess::storage(destination).host_data();
+            if (host != nullptr && destination.is_contiguous()) {
+                // Straight into the caller's host memory: no host temporary and no second copy.
+                moved_.outputs[i].copy_to_host(host + static_cast<std::size_t>(destination.offset()) *
+                                                          destination.itemsize());
+            } else {
+                destination.copy_from(moved_.outputs[i].to(home));
+            }
         }
     }
 

@@ -242,8 +242,34 @@ Tensor Tensor::to(Device target) const {
     if (device() == target) {
         return *this;
     }
+    // A strided host view bound for a device that packs views: the bytes it spans go over as
+    // they lie, and the device packs them (a transposed 4096^2 operand is one 64 MiB transfer
+    // and a device transpose instead of a host gather). Taken while the span is at most 4 times
+    // the view's own bytes, so a sparse slice does not drag its whole base along.
+    if (const std::byte* src = storage_->host_data();
+        src != nullptr && !is_contiguous() && packs_on_device(target, dtype_)) {
+        const std::int64_t span = reach(shape_, strides_);
+        if (span > 0 && span <= 4 * numel()) {
+            Tensor raw = empty({span}, dtype_, target);
+            raw.storage_->copy_from_host(0, src + static_cast<std::size_t>(offset_) * itemsize(),
+                                         static_cast<std::size_t>(span) * itemsize());
+            return Tensor(raw.storage_, 0, shape_, strides_, dtype_).contiguous();
+        }
+    }
     Tensor out = empty(shape_, dtype_, target);
-    if (out.nbytes() > 0) {
+    if (out.nbytes() == 0) {
+        return out;
+    }
+    // Host memory on either side is read or written in place. A temporary host copy is made
+    // only between two devices or from a strided host view that the branch above leaves:
+    // building one for every transfer cost a fill, page faults and one more pass over host
+    // memory (a 1 GiB operand moved at ~4 GB/s).
+    if (std::byte* dst = out.storage_->host_data()) {
+        copy_to_host(dst);
+    } else if (const std::byte* src = storage_->host_data(); src != nullptr && is_contiguous()) {
+        out.storage_->copy_from_host(0, src + static_cast<std::size_t>(offset_) * itemsize(),
+                                     out.nbytes());
+    } else {
         std::vector<std::byte> bounce(out.nbytes());
         copy_to_host(bounce.data());
         out.storage_->copy_from_host(0, bounce.data(), bounce.size());

@@ -136,6 +136,23 @@ void test_transfers(Device device) {
     const Tensor back = t.to({DeviceType::CPU, 0});
     test::require(back.device() == (Device{DeviceType::CPU, 0}) && back.to_vector<float>() == values,
                   "to(cpu)");
+    // to() from host views onto this device: a transposed view and a broadcast (their spans
+    // move and the device packs them), a sparse slice (packed on the host), a view with an
+    // offset; each arrives on another device contiguous, with the view's values.
+    const Device cpu{DeviceType::CPU, 0};
+    const auto big = iota(64 * 48);
+    const Tensor host = Tensor::from_vector(big, {64, 48}, cpu);
+    const Tensor host_row = Tensor::from_vector(std::vector<float>{5, -1, 2}, {1, 3}, cpu);
+    const std::vector<Tensor> views = {host.transpose(0, 1), host_row.expand({40, 3}),
+                                       host.slice(1, 0, 48, 16), host.slice(0, 3, 60).slice(1, 5, 41)};
+    for (const Tensor& view : views) {
+        const Tensor moved = view.to(device);
+        // (On the CPU, to() returns the view itself.)
+        test::require(moved.device() == device && (device == cpu || moved.is_contiguous()) &&
+                          moved.shape() == view.shape() &&
+                          moved.to_vector<float>() == view.to_vector<float>(),
+                      "to(" + to_string(device) + ") of a host view " + to_string(view.shape()));
+    }
     // Empty tensors.
     test::require(Tensor::empty({0, 5}, DType::F32, device).to_vector<float>().empty(), "empty");
 }

@@ -80,3 +80,34 @@ def test_stream_wrap_device_memcpy_and_events(stream):
     x = dev(np.ones(8, np.float32), stream)
     mf.fill(x, 2.0)
     assert np.all(x.numpy() == 2.0)
+
+
+@pytest.mark.parametrize("nbytes", [1, 4093, (1 << 20) - 1, 1 << 20, (16 << 20) - 3, 16 << 20,
+                                    (16 << 20) + 5, (32 << 20) + 1, (41 << 20) + 7])
+def test_host_copies_every_size_around_the_staging_chunks(stream, nbytes):
+    """mfr_memcpy_h2d and mfr_memcpy_d2h from and to pageable memory: 1 MiB and more go through
+    the stream's two pinned staging slots in 16 MiB chunks, less goes directly. Every size around
+    the chunk edges, from and to odd host addresses, comes back byte for byte; the device bytes
+    are also read back through a device-to-device copy into a second buffer, and a second upload
+    of other bytes overwrites the first completely (the slots are reused across calls)."""
+    lib = abi.load()
+    rng = np.random.default_rng(nbytes)
+    first = rng.integers(0, 256, nbytes + 3, dtype=np.uint8)[3:]   # an odd host address
+    second = rng.integers(0, 256, nbytes + 1, dtype=np.uint8)[1:]
+    buf = mf.DeviceArray.empty((nbytes,), stream, dtype=np.uint8)
+    other = mf.DeviceArray.empty((nbytes,), stream, dtype=np.uint8)
+    for want in (first, second):
+        abi.check(lib.mfr_memcpy_h2d(stream.handle, ctypes.c_void_p(buf.ptr),
+                                     want.ctypes.data, nbytes), "mfr_memcpy_h2d")
+        back = np.empty(nbytes + 5, np.uint8)
+        view = back[5:]                                                  # an odd host address
+        back[:5] = 7
+        abi.check(lib.mfr_memcpy_d2h(stream.handle, view.ctypes.data, ctypes.c_void_p(buf.ptr),
+                                     nbytes), "mfr_memcpy_d2h")
+        assert np.array_equal(view, want)
+        assert np.all(back[:5] == 7), "the copy wrote before its destination"
+        abi.check(lib.mfr_memcpy_d2d(stream.handle, ctypes.c_void_p(other.ptr),
+                                     ctypes.c_void_p(buf.ptr), nbytes), "mfr_memcpy_d2d")
+        assert np.array_equal(other.numpy(), want)
+    buf.close()
+    other.close()
