@@ -82,7 +82,10 @@ int mfr_stream_sync(mfr_stream_t stream);
 void* mfr_stream_handle(mfr_stream_t stream);
 int mfr_stream_device(mfr_stream_t stream);
 
-/* Host -> device; complete on return, so src may be reused (Stream::copy_h2d). */
+/* Host -> device; complete on return, so src may be reused (Stream::copy_h2d). Copies of 1 MiB
+ * or more from pageable memory go through the stream's two 16 MiB pinned staging slots (allocated
+ * on first use, freed with the stream), the CPU's copy into one overlapping the DMA of the other;
+ * mfr_memcpy_d2h likewise. Calls on one stream from several threads take turns. */
 int mfr_memcpy_h2d(mfr_stream_t stream, void* dst, const void* src, size_t bytes);
 /* Device -> host; waits for all earlier work on the stream (Stream::copy_d2h). */
 int mfr_memcpy_d2h(mfr_stream_t stream, void* dst, const void* src, size_t bytes);
