@@ -178,13 +178,24 @@ enum {
     MFR_TILE_64x128 = 4,  /* 4 wavefronts of 32x64, depth slice 16 */
     MFR_TILE_64x64 = 5,   /* 4 wavefronts of 32x32, 4 per CU */
     MFR_TILE_THIN = 6,    /* no MFMA: at most 8 output columns (or rows) as dot products */
-    MFR_TILE_COUNT = 7
+    MFR_TILE_PANEL = 7,   /* k <= 64: 8 wavefronts keep 256 rows of A, stream B and C past them */
+    MFR_TILE_COUNT = 8
 };
 
 /* The thin path (MFR_TILE_THIN) streams the long operand once and keeps the other, at most 8
  * columns wide, in LDS: for n <= 8 with A read along k (unit stride along K), or m <= 8 with B
  * read along k. Elsewhere a fixed THIN fails with MFR_E_UNSUPPORTED; it runs no split. AUTO
  * prices it against the MFMA tiles. */
+
+/* The panel path (MFR_TILE_PANEL) is for a short depth and a large output, such as attention's
+ * scores q k^T: a workgroup holds 256 rows of A in registers for the whole launch and walks the
+ * columns of C, 64 at a time, with the matching rows of B copied into LDS and C written while
+ * the next columns are multiplied, so the stores overlap the MFMA work instead of following it.
+ * It takes 1 <= k <= 64 with both operands read along k (unit stride along K) by 16-byte loads
+ * (their k, other strides and bases 16-byte aligned), no activation and no split; alpha, beta *
+ * C0 and a bias as everywhere. The sums are the MFMA tiles' own, so the results are the same bit
+ * for bit. Elsewhere a fixed PANEL fails with MFR_E_UNSUPPORTED. AUTO takes it where it fits for
+ * outputs of more than 128 rows and at least 2^22 elements. */
 
 /* Split-K of mfr_sgemm. A product with few output tiles and a long depth (256 x 256 x 16384)
  * would leave most compute units idle, so its depth may be cut into `splits` ranges (each a

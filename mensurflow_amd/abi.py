@@ -34,7 +34,8 @@ TILE_128x64 = 3
 TILE_64x128 = 4
 TILE_64x64 = 5
 TILE_THIN = 6
-TILE_COUNT = 7
+TILE_PANEL = 7
+TILE_COUNT = 8
 STAGE_AUTO = 0
 STAGE_NEVER = 1
 STAGE_ALWAYS = 2

@@ -44,6 +44,7 @@
 //     split_reduce_kernel; edge peeling runs a thin remainder of the output as launches of its
 //     own; the thin path (thin_kernel.hpp) takes products with at most 8 output columns or rows.
 #include "gemm_kernel.hpp"
+#include "panel_kernel.hpp"
 #include "thin_kernel.hpp"
 
 #include <cstring>
@@ -72,6 +73,7 @@ constexpr TileInfo kTiles[MFR_TILE_COUNT] = {
     {64, 128, 5, 4, 116.0},    // 4 wavefronts of 32x64, depth slice 16
     {64, 64, 4, 4, 111.4},     // 4 wavefronts of 32x32, depth slice 32
     {0, 0, 0, 0, 0.0},         // THIN (no tile; priced by thin_us)
+    {0, 0, 0, 0, 0.0},         // PANEL (chosen by its own rule, panel_fits)
 };
 constexpr int kGroupM = 8;
 
@@ -669,6 +671,31 @@ bool big_tile_ok(const Plan& plan) {
            fits(operand_b(p, plan.bk), plan.bk, plan.stage_b);
 }
 
+// Whether the panel path (panel_kernel.hpp) can take the plan's product: a depth of 1 to 64, both
+// operands read along k with 16-byte loads in place, no activation, and every byte offset its
+// buffer resources use (within a batch matrix) below 2^31.
+bool panel_fits(const Plan& plan) {
+    const GemmParams& p = plan.p;
+    if (!plan.ak || !plan.bk || plan.va != 4 || plan.vb != 4 || plan.stage_a || plan.stage_b) {
+        return false;
+    }
+    if (p.k < 1 || p.k > kPanelMaxDepth || p.act != MFR_ACT_NONE) {
+        return false;
+    }
+    const double limit = 2147483648.0;
+    const double m = static_cast<double>(p.m);
+    return (m + 32.0) * p.c_rs * 4.0 < limit && (!plan.c0 || (m + 32.0) * p.c0_rs * 4.0 < limit) &&
+           m * p.a_rs * 4.0 + 4.0 * p.k < limit && (kPanelCols + 1.0) * p.b_cs * 4.0 < limit;
+}
+
+// AUTO takes the panel path for products it fits with more than one panel of rows and at least
+// 16 MiB of output, where the tile kernels pay their store time on top of their MFMA time.
+bool panel_preferred(const Plan& plan) {
+    const GemmParams& p = plan.p;
+    return panel_fits(plan) && p.m > kPanelRows / 2 &&
+           static_cast<double>(p.m) * p.n * p.batch_count >= 4194304.0;
+}
+
 // Validates d (the checks and error codes of mfr_sgemm) and makes the plan for a device with
 // `cus` compute units.
 Plan plan_sgemm(const mfr_gemm_desc& d, int cus) {
@@ -772,6 +799,16 @@ Plan plan_sgemm(const mfr_gemm_desc& d, int cus) {
     }
     plan.c0 = p.c0 != nullptr && p.beta != 0.0f;
     const auto tile_plan = [&](Plan& q) {
+        if (d.tile == MFR_TILE_PANEL ||
+            (d.tile == MFR_TILE_AUTO && d.splits <= 1 && panel_preferred(q))) {
+            if (!panel_fits(q) || d.splits > 1) {
+                throw mfr::Error(MFR_E_UNSUPPORTED,
+                                 "sgemm: the panel path takes k <= 64 with both operands read "
+                                 "along k by 16-byte loads in place, no activation and no split");
+            }
+            single_region(q, Choice{MFR_TILE_PANEL, 1, p.k, 0.0});
+            return;
+        }
         const Choice choice = choose(p.m, p.n, p.k, batch_count, cus, d.tile, d.splits, q.c0,
                                      q.ak, q.bk, thin_b_layout(q.p, q, p.m, p.n), big_tile_ok(q));
         single_region(q, choice);
@@ -989,6 +1026,11 @@ void launch_region(const Plan& plan, const GemmParams& p, const Region& r, int v
     q.bias = p.bias != nullptr ? p.bias + r.n_off : nullptr;
     if (r.tile == MFR_TILE_THIN) {
         launch_thin(plan, q, va, vb, stream, stage, stage_rs);
+        return;
+    }
+    if (r.tile == MFR_TILE_PANEL) {
+        launch_panel(q, streamed_output(q), cus, stream);
+        mfr::check_launch("sgemm_panel_kernel");
         return;
     }
     const int tile = r.tile;

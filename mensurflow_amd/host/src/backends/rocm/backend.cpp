@@ -425,7 +425,7 @@ template <OpId Op> std::vector<SearchRegion> gemm_space(const OpArgs& args) {
     region.name = "mfma";
     region.start = tuning_of(tile, stage, splits);
     region.axes = {{0, {MFR_TILE_THIN, MFR_TILE_64x64, MFR_TILE_128x64, MFR_TILE_64x128,
-                        MFR_TILE_128x128, MFR_TILE_256x256}},
+                        MFR_TILE_128x128, MFR_TILE_256x256, MFR_TILE_PANEL}},
                    {1, {MFR_STAGE_NEVER, MFR_STAGE_ALWAYS}},
                    {2, {1, 2, 4, 8, 16, 32}}};
     return {region};

@@ -69,11 +69,12 @@ std::int64_t ranges_run(std::int64_t k, std::int64_t splits) {
 }
 
 // Runs every point of `op`'s space that `allowed` accepts and checks the output each time.
-// Points refused are exactly the thin path (no product here is thin) and split counts the depth
-// k is too short for; with staging off, the 256x256 tile reads an operand 16-byte loads cannot
-// read (the matmul and batched cases) in place.
+// Points refused are exactly the thin path (no product here is thin), the panel path where the
+// product does not fit it (panel: it does, and then only unsplit), and split counts the depth k
+// is too short for; with staging off, the 256x256 tile reads an operand 16-byte loads cannot read
+// (the matmul and batched cases) in place.
 void sweep(Device device, OpId op, OpArgs args, const std::vector<float>& want, std::int64_t k,
-           const std::string& what) {
+           const std::string& what, bool panel = false) {
     Registry& registry = Registry::instance();
     const TunableKernel& tunable = *registry.dispatcher().tunable({op, DeviceType::ROCm, DType::F32});
     const KernelFn kernel = registry.dispatcher().lookup({op, DeviceType::ROCm, DType::F32});
@@ -93,7 +94,9 @@ void sweep(Device device, OpId op, OpArgs args, const std::vector<float>& want, 
                 const TuningConfig config = point(tile, stage, splits);
                 const bool allowed = tunable.allowed(args, config);
                 // None of these products is thin enough (m, n > 8) for the thin path.
-                const bool expected = tile != MFR_TILE_THIN && ranges_run(k, splits) == splits;
+                const bool expected =
+                    tile != MFR_TILE_THIN && ranges_run(k, splits) == splits &&
+                    (tile != MFR_TILE_PANEL || (panel && splits == 1));
                 const std::string name = "tile " + std::to_string(tile) + " stage " +
                                          std::to_string(stage) + " splits " +
                                          std::to_string(splits);
@@ -109,7 +112,8 @@ void sweep(Device device, OpId op, OpArgs args, const std::vector<float>& want, 
             }
         }
     }
-    test::require(counts >= 2 && ran == 10 * counts, what + ": every allowed point ran");
+    test::require(counts >= 2 && ran == 10 * counts + (panel ? 2 : 0),
+                  what + ": every allowed point ran");
     // Not a point: AUTO is only the default, and unknown values are refused.
     test::require(!tunable.allowed(args, point(MFR_TILE_AUTO, MFR_STAGE_NEVER, 1)) &&
                       !tunable.allowed(args, point(MFR_TILE_64x64, 7, 1)) &&
@@ -198,6 +202,35 @@ void test_batched(Device device) {
         }
     }
     sweep(device, OpId::GemmBatched, args, want, k, "batched 2x3x70x45x63");
+}
+
+void test_batched_scores(Device device) {
+    // Attention's scores q k^T: a short, aligned depth with both operands read along k, so the
+    // panel path is a point of the space (unsplit only).
+    const std::int64_t bs = 3, m = 300, n = 130, k = 64;
+    const auto qv = test::quarter_input(bs * m * k, 69);
+    const auto kv = test::quarter_input(bs * n * k, 70);
+    OpArgs args;
+    args.inputs = {Tensor::from_vector(qv, {bs, m, k}, device),
+                   Tensor::from_vector(kv, {bs, n, k}, device).transpose(1, 2)};
+    args.outputs = {Tensor::empty({bs, m, n}, DType::F32, device)};
+    args.alpha = 0.125f;
+    args.beta = 0.0f;
+    std::vector<float> want;
+    for (std::int64_t i = 0; i < bs; ++i) {
+        const std::vector<float> a(qv.begin() + static_cast<std::ptrdiff_t>(i * m * k),
+                                   qv.begin() + static_cast<std::ptrdiff_t>((i + 1) * m * k));
+        std::vector<float> b(static_cast<std::size_t>(k * n));
+        for (std::int64_t p = 0; p < k; ++p) {
+            for (std::int64_t j = 0; j < n; ++j) {
+                b[static_cast<std::size_t>(p * n + j)] =
+                    kv[static_cast<std::size_t>((i * n + j) * k + p)];
+            }
+        }
+        const auto c = exact_gemm(a, b, m, n, k, 0.125, nullptr, 0.0, nullptr);
+        want.insert(want.end(), c.begin(), c.end());
+    }
+    sweep(device, OpId::GemmBatched, args, want, k, "batched scores 3x300x130x64", true);
 }
 
 void test_start_is_the_automatic_choice(Device device) {
@@ -442,6 +475,7 @@ int main(int argc, char** argv) {
             test_matmul(device);
             test_gemm_fused(device);
             test_batched(device);
+            test_batched_scores(device);
             test_start_is_the_automatic_choice(device);
             test_tuner_places_auto_on_rocm(device);
         }

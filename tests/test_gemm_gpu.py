@@ -288,8 +288,7 @@ def test_strip_staging_with_alpha_beta_c0(stream, oracle):
 def test_plan_on_baseline_shapes(stream):
     """mfr_sgemm_plan reports what AUTO runs: the 256x256 tile in place for configs[2], staged
     operands for configs[3] (whose rows 16-byte loads cannot take), the 256x256 tile reading them
-    in place (straight into LDS) when staging is off, a short-depth tile for the attention
-    scores."""
+    in place (straight into LDS) when staging is off, the panel path for the attention scores."""
     abi = mf.abi
     big = mf.DeviceArray.empty((4096, 4096), stream)
     assert mf.gemm_plan(big, big.T, big) == (abi.TILE_256x256, abi.STAGE_NEVER, 1, 1)
@@ -302,7 +301,13 @@ def test_plan_on_baseline_shapes(stream):
                                                                   abi.STAGE_NEVER)
     q = mf.DeviceArray.empty((128, 1024, 64), stream)
     scores = mf.DeviceArray.empty((128, 1024, 1024), stream)
-    assert mf.gemm_plan(q, q.transpose(-2, -1), scores)[0] in (abi.TILE_128x64, abi.TILE_64x128)
+    assert mf.gemm_plan(q, q.transpose(-2, -1), scores) == (abi.TILE_PANEL, abi.STAGE_NEVER, 1, 1)
+    # Small outputs, and operands the panel path cannot read, keep the short-depth tiles.
+    assert mf.gemm_plan(q.slice(0, 0, 1).slice(1, 0, 128), q.slice(0, 0, 1).slice(1, 0, 128)
+                        .transpose(-2, -1), scores.slice(0, 0, 1).slice(1, 0, 128)
+                        .slice(2, 0, 128))[0] in (abi.TILE_128x64, abi.TILE_64x128)
+    v = mf.DeviceArray.empty((128, 64, 1024), stream)
+    assert mf.gemm_plan(q, v, scores)[0] in (abi.TILE_128x64, abi.TILE_64x128)
     assert mf.gemm_plan(x, w, out, tile=abi.TILE_256x256, stage=abi.STAGE_NEVER)[:2] == (
         abi.TILE_256x256, abi.STAGE_NEVER)
     assert mf.gemm_plan(x, w, out, tile=abi.TILE_256x256)[:2] == (abi.TILE_256x256,
@@ -315,6 +320,107 @@ def test_plan_on_baseline_shapes(stream):
     b = quarter_matrix(k, n, 98)
     got = mf.gemm(dev(a, stream), dev(b, stream), tile=abi.TILE_256x256).numpy()
     assert same_bits(got, exact_product(a, b))
+
+
+# ---- the panel path ------------------------------------------------------------------------------
+
+PANEL = mf.abi.TILE_PANEL
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 4), (1, 300, 64), (255, 63, 64), (256, 64, 64),
+                                   (257, 65, 60), (300, 200, 36), (513, 1000, 16), (1000, 129, 4),
+                                   (129, 1, 8), (700, 777, 32), (2100, 1100, 64), (64, 4100, 12)])
+def test_exact_panel(stream, m, n, k):
+    """The panel path (B read along k) on shapes around its 256-row panels, 64-column tiles and
+    depth groups: alpha, beta * C0 (separate and in place) and a bias; bits equal the exact
+    product and the guard bands survive."""
+    a = quarter_matrix(m, k, 101)
+    bt = quarter_matrix(n, k, 102)
+    c0 = quarter_matrix(m, n, 103)
+    bias = quarter_matrix(1, n, 104)[0]
+    a_d, b_d, bias_d = dev(a, stream), dev(bt, stream).T, dev(bias, stream)
+    product = exact_product(a, bt.T)
+    want = ((np.float32(1.5) * product) + np.float32(0.5) * c0 + bias).astype(np.float32)
+    c, buf = guarded_output(stream, (m, n))
+    assert mf.gemm_plan(a_d, b_d, c, tile=PANEL)[0] == PANEL
+    mf.gemm_batched(a_d, b_d, c, alpha=1.5, c0=dev(c0, stream), beta=0.5, bias=bias_d, tile=PANEL)
+    assert same_bits(c.numpy(), want), f"{m}x{n}x{k}"
+    check_guards(buf)
+    c_in = dev(c0, stream)
+    mf.gemm_batched(a_d, b_d, c_in, alpha=1.5, c0=c_in, beta=0.5, bias=bias_d, tile=PANEL)
+    assert same_bits(c_in.numpy(), want), f"{m}x{n}x{k} in place"
+    plain, buf = guarded_output(stream, (m, n))
+    mf.gemm_batched(a_d, b_d, plain, tile=PANEL)
+    assert same_bits(plain.numpy(), product), f"{m}x{n}x{k} plain"
+    check_guards(buf)
+
+
+def test_exact_panel_batched_broadcast(stream):
+    """Two batch dimensions, B broadcast over the first and A over the second; row strides wider
+    than k; the output's rows wider than n (a padded row stride)."""
+    bsz, heads, m, n, k = 2, 3, 300, 130, 40
+    a = quarter_matrix(bsz * m, k, 111).reshape(bsz, 1, m, k)
+    bt = quarter_matrix(heads * n, k, 112).reshape(1, heads, n, k)
+    a_st = np.full((bsz, 1, m, k + 8), -5.0, np.float32)
+    a_st[..., :k] = a
+    a_d = dev(a_st, stream).slice(-1, 0, k).expand((bsz, heads, m, k))
+    b_d = dev(bt, stream).expand((bsz, heads, n, k)).transpose(-2, -1)
+    wide = mf.DeviceArray.empty((bsz, heads, m, n + 12), stream)
+    mf.fill(wide, POISON)
+    out = wide.slice(-1, 0, n)
+    mf.gemm_batched(a_d, b_d, out, alpha=0.125, tile=PANEL)
+    got = wide.numpy()
+    assert np.all(got[..., n:] == POISON)
+    for i in range(bsz):
+        for h in range(heads):
+            want = (np.float32(0.125) * exact_product(a[i, 0], bt[0, h].T)).astype(np.float32)
+            assert same_bits(got[i, h, :, :n], want), (i, h)
+
+
+def test_panel_matches_tiles_bitwise(stream, oracle):
+    """Realistic inputs: the panel path sums in the MFMA tiles' order, so the scores of a causal
+    attention-sized product come out bit for bit as on the 128x64 tile, AUTO picks the panel
+    path, and the result is within the parity bar of the oracle."""
+    bsz, m, n, k = 4, 1024, 1024, 64
+    q = normal(oracle, (bsz, m, k), 0.0, 1.0, 121, 0)
+    kk = normal(oracle, (bsz, n, k), 0.0, 1.0, 122, 0)
+    q_d, k_d = dev(q, stream), dev(kk, stream).transpose(-2, -1)
+    out = mf.DeviceArray.empty((bsz, m, n), stream)
+    assert mf.gemm_plan(q_d, k_d, out)[0] == PANEL
+    mf.gemm_batched(q_d, k_d, out, alpha=0.125)
+    got = out.numpy()
+    mf.gemm_batched(q_d, k_d, out, alpha=0.125, tile=mf.abi.TILE_128x64)
+    assert np.array_equal(got.view(np.uint32), out.numpy().view(np.uint32))
+    for b in range(bsz):
+        want = oracle.gemm(q[b], kk[b], alpha=0.125, trans_b=True)
+        scale = 0.125 * magnitude(oracle, q[b], kk[b].T)
+        assert_gemm_parity(got[b], want, scale, k, f"panel scores batch {b}")
+
+
+@pytest.mark.parametrize("case", ["depth 68", "depth 6", "B along n", "A along m",
+                                  "activation", "split", "unaligned A"])
+def test_panel_refusals(stream, case):
+    """A fixed PANEL point it cannot take fails with MFR_E_UNSUPPORTED and leaves C untouched."""
+    m, n, k = 300, 200, 68 if case == "depth 68" else 6 if case == "depth 6" else 32
+    a = dev(quarter_matrix(m, k, 131), stream)
+    bt = dev(quarter_matrix(n, k, 132), stream)
+    b = bt.T
+    kwargs = {}
+    if case == "B along n":
+        b = dev(quarter_matrix(k, n, 133), stream)
+    elif case == "A along m":
+        a = dev(quarter_matrix(k, m, 134), stream).T
+    elif case == "activation":
+        kwargs["act"] = mf.ACT_GELU_TANH
+    elif case == "split":
+        kwargs["splits"] = 2
+    elif case == "unaligned A":
+        a = dev(quarter_matrix(m, k + 1, 135), stream).slice(1, 1, k + 1)
+    c = mf.DeviceArray.empty((m, n), stream)
+    mf.fill(c, POISON)
+    with pytest.raises(NotImplementedError):
+        mf.gemm_batched(a, b, c, tile=PANEL, **kwargs)
+    assert np.all(c.numpy() == POISON)
 
 
 # ---- split-K -----------------------------------------------------------------------------------
