@@ -11,9 +11,11 @@ Inputs are synthetic (seeded numpy uniform[-1,1] / N(0,1)), as the configs descr
 Timing: W untimed warmup steps (continued until at least MIN_WARMUP_MS of GPU work has run,
 because every leg starts after host-side setup with the GPU idle, and the first ~10 ms after
 idle run slower while the clocks ramp: the MLP leg measured 446 us per call over its first 20
-calls and 377 us after), then K steps bracketed by stream synchronisation; the per-launch
-duration of the dominant kernel comes from HIP events recorded on the stream the kernel runs
-on. The CPU baseline (rank 0, N=1 only) times the reference's own packed
+calls and 377 us after), then K timed steps (at least MIN_SAMPLES), bracketed by stream
+synchronisation. Each step is one sample, timed by HIP events recorded on the stream the
+kernels run on before the first step and after every step; each leg reports the median, min and
+max of its samples, and value / ms_per_step / every roofline fraction come from the median (the
+reference's bench::measure reports the median of 9 samples, benchmarks/bench.hpp:23-30). The CPU baseline (rank 0, N=1 only) times the reference's own packed
 AVX2/OpenMP GEMM and its double-accumulating gemv (oracle/_ref, compiled from the reference
 sources) on bounded samples.
 `cpp_api` repeats the workloads through the mensurflow C++ API (mensurflow_amd/_lib/
@@ -81,12 +83,21 @@ def load_traffic(kernel: str):
         return None
 
 
-def time_launches(mf, stream, launch, steps: int, warmup: int):
-    """(ms per step from host-synchronised wall clock, ms per step from HIP events), after
-    `warmup` untimed steps and then more until MIN_WARMUP_MS of them have run. The first call
-    (which carries one-time costs: code loading, the plan) is not counted towards that time: it
-    once made the estimate of a call's duration so large that the GEMM leg warmed up for ~5 ms,
-    and its timed steps ran 3 % slower than after a proper warm-up."""
+MIN_SAMPLES = 9                 # per leg, at least (the reference's bench::measure takes 9)
+
+
+def time_launches(mf, stream, launch, steps: int, warmup: int, exact: bool = False) -> dict:
+    """Times `steps` launches after `warmup` untimed ones (continued until MIN_WARMUP_MS of them
+    have run). The first call (which carries one-time costs: code loading, the plan) is not
+    counted towards that time: it once made the estimate of a call's duration so large that the
+    GEMM leg warmed up for ~5 ms, and its timed steps ran 3 % slower than after a proper warm-up.
+
+    Each timed step is one sample: a HIP event is recorded on the launch stream before the first
+    step and after every step, so consecutive events bracket one step's device time. Returns the
+    samples' median, min and max (ms) and the host wall time per step over the whole block,
+    bracketed by stream synchronisation. At least MIN_SAMPLES steps are timed, or exactly
+    `steps` when `exact` (the headline leg, whose step count the command line fixes)."""
+    steps = steps if exact else max(steps, MIN_SAMPLES)
     launch()
     stream.synchronize()
     t0 = time.perf_counter()
@@ -97,16 +108,41 @@ def time_launches(mf, stream, launch, steps: int, warmup: int):
         if done >= warmup:
             stream.synchronize()
     stream.synchronize()
-    start, end = mf.Event(), mf.Event()
+    events = [mf.Event() for _ in range(steps + 1)]
     t0 = time.perf_counter()
-    start.record(stream)
-    for _ in range(steps):
+    events[0].record(stream)
+    for i in range(steps):
         launch()
-    end.record(stream)
+        events[i + 1].record(stream)
     stream.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    event_ms = start.elapsed_ms(end) / steps
-    return wall_ms, event_ms
+    samples = sorted(events[i].elapsed_ms(events[i + 1]) for i in range(steps))
+    return {"wall_ms": wall_ms, "event_ms": float(np.median(samples)), "min_ms": samples[0],
+            "max_ms": samples[-1], "samples": steps}
+
+
+def time_host_calls(call, sync, steps: int, warmup: int) -> dict:
+    """Host wall time per call (a call that launches several kernels and allocates), one sample
+    per call, each ended by a synchronisation: median, min and max (ms)."""
+    steps = max(steps, MIN_SAMPLES)
+    for _ in range(max(1, warmup)):
+        call()
+    sync()
+    samples = []
+    for _ in range(steps):
+        t0 = time.perf_counter()
+        call()
+        sync()
+        samples.append((time.perf_counter() - t0) * 1e3)
+    samples.sort()
+    return {"event_ms": float(np.median(samples)), "min_ms": samples[0], "max_ms": samples[-1],
+            "samples": steps}
+
+
+def spread(leg: dict) -> dict:
+    """The sampling record of one leg for the JSON line (ms)."""
+    return {"samples": leg["samples"], "median": round(leg["event_ms"], 5),
+            "min": round(leg["min_ms"], 5), "max": round(leg["max_ms"], 5)}
 
 
 def bench_gemm(mf, stream, steps, warmup):
@@ -120,9 +156,9 @@ def bench_gemm(mf, stream, steps, warmup):
     def launch():
         mf.gemm(a, b, alpha=1.5, c0=c0, beta=0.5, trans_b=True, out=c)
 
-    wall_ms, event_ms = time_launches(mf, stream, launch, steps, warmup)
-    flops = 2.0 * n * n * n
-    return {"wall_ms": wall_ms, "event_ms": event_ms, "flops": flops}
+    leg = time_launches(mf, stream, launch, steps, warmup, exact=True)
+    leg["flops"] = 2.0 * n * n * n
+    return leg
 
 
 def bench_gemv(mf, stream, steps, warmup, trans):
@@ -136,10 +172,10 @@ def bench_gemv(mf, stream, steps, warmup, trans):
     def launch():
         mf.sgemv(a, x, alpha=2.0, y0=y0, beta=0.5, trans=trans, out=y)
 
-    wall_ms, event_ms = time_launches(mf, stream, launch, steps, warmup)
-    nbytes = 4.0 * (n * n + 3 * n)  # A, x, y0 read; y written
+    leg = time_launches(mf, stream, launch, steps, warmup)
+    leg["bytes"] = 4.0 * (n * n + 3 * n)  # A, x, y0 read; y written
     a.close()
-    return {"wall_ms": wall_ms, "event_ms": event_ms, "bytes": nbytes}
+    return leg
 
 
 def bench_mlp(mf, stream, steps, warmup):
@@ -155,8 +191,9 @@ def bench_mlp(mf, stream, steps, warmup):
     def launch():
         mf.gemm(x, w, bias=bias, act=mf.ACT_GELU_TANH, out=out)
 
-    wall_ms, event_ms = time_launches(mf, stream, launch, steps, warmup)
-    return {"event_ms": event_ms, "flops": 2.0 * m * n * k}
+    leg = time_launches(mf, stream, launch, steps, warmup)
+    leg["flops"] = 2.0 * m * n * k
+    return leg
 
 
 def bench_attention(mf, stream, steps, warmup):
@@ -169,23 +206,21 @@ def bench_attention(mf, stream, steps, warmup):
                                          stream) for _ in range(3))
     scores = mf.DeviceArray.empty((b, h, s, s), stream)
     out = mf.DeviceArray.empty((b, h, s, d), stream)
-    _, qk_ms = time_launches(mf, stream, lambda: mf.gemm_batched(
+    qk = time_launches(mf, stream, lambda: mf.gemm_batched(
         q, k.transpose(-2, -1), scores, alpha=0.125), steps, warmup)
-    _, sm_ms = time_launches(mf, stream, lambda: mf.softmax(scores, out=scores), steps, warmup)
-    _, pv_ms = time_launches(mf, stream, lambda: mf.gemm_batched(scores, v, out), steps, warmup)
-    total_steps = max(3, steps // 5)
-    wall_ms, _ = time_launches(mf, stream, lambda: mf.attention(q, k, v, causal=True, fused=False),
-                               total_steps, 1)
+    sm = time_launches(mf, stream, lambda: mf.softmax(scores, out=scores), steps, warmup)
+    pv = time_launches(mf, stream, lambda: mf.gemm_batched(scores, v, out), steps, warmup)
     scores.close()
-    _, fused_ms = time_launches(mf, stream, lambda: mf.attention_fused(q, k, v, causal=True,
-                                                                       out=out), steps, warmup)
+    total = time_host_calls(lambda: mf.attention(q, k, v, causal=True, fused=False),
+                            stream.synchronize, steps, 1)
+    fused = time_launches(mf, stream, lambda: mf.attention_fused(q, k, v, causal=True, out=out),
+                          steps, warmup)
     gemm_flops = 2.0 * b * h * s * s * d
     # What causal attention needs: both products over the s(s+1)/2 kept (query, key) pairs.
     causal_flops = 4.0 * b * h * d * s * (s + 1) / 2
-    return {"qk_ms": qk_ms, "softmax_ms": sm_ms, "pv_ms": pv_ms, "total_ms": wall_ms,
+    return {"qk": qk, "softmax": sm, "pv": pv, "total": total, "fused": fused,
             "flops": 2 * gemm_flops, "gemm_flops": gemm_flops,
-            "scores_bytes": 4.0 * b * h * s * s, "fused_ms": fused_ms,
-            "causal_flops": causal_flops}
+            "scores_bytes": 4.0 * b * h * s * s, "causal_flops": causal_flops}
 
 
 def bench_copy(mf, stream, steps, warmup):
@@ -199,8 +234,9 @@ def bench_copy(mf, stream, steps, warmup):
     def launch():
         mf.strided_copy(src, out=dst)
 
-    wall_ms, event_ms = time_launches(mf, stream, launch, steps, warmup)
-    return {"event_ms": event_ms, "bytes": 8.0 * n}
+    leg = time_launches(mf, stream, launch, steps, warmup)
+    leg["bytes"] = 8.0 * n
+    return leg
 
 
 def host_description() -> str:
@@ -340,30 +376,34 @@ def main() -> int:
         result["gemv_t"] = bench_gemv(mf, stream, args.steps, args.warmup, trans=True)
     if args.only in ("all", "mlp"):
         log("mlp 4093x1023x4099 + bias + gelu ...")
-        result["mlp"] = bench_mlp(mf, stream, max(5, args.steps // 5), args.warmup)
+        result["mlp"] = bench_mlp(mf, stream, args.steps, args.warmup)
     if args.only in ("all", "attention"):
         log("attention 8x16x1024x64 causal ...")
-        result["attention"] = bench_attention(mf, stream, max(5, args.steps // 5), args.warmup)
+        result["attention"] = bench_attention(mf, stream, max(MIN_SAMPLES, args.steps // 2),
+                                              args.warmup)
     if args.only in ("all", "copy"):
         log("copy 1 GiB ...")
-        result["copy"] = bench_copy(mf, stream, max(5, args.steps // 5), args.warmup)
+        result["copy"] = bench_copy(mf, stream, MIN_SAMPLES, args.warmup)
     if args.only != "all":
         print(json.dumps(result))
         return 0
 
+    def tflops_of(flops, leg):
+        return flops / (leg["event_ms"] * 1e-3) / 1e12
+
     g = result["gemm"]
-    tflops = g["flops"] / (g["wall_ms"] * 1e-3) / 1e12
-    kernel_tflops = g["flops"] / (g["event_ms"] * 1e-3) / 1e12
+    kernel_tflops = tflops_of(g["flops"], g)
     gemv = {}
     for key, trans in (("gemv_n", False), ("gemv_t", True)):
         r = result[key]
-        gbs = r["bytes"] / (r["wall_ms"] * 1e-3) / 1e9
         kernel_gbs = r["bytes"] / (r["event_ms"] * 1e-3) / 1e9
         traffic = load_traffic("sgemv_t" if trans else "sgemv_n")
         gemv["T" if trans else "N"] = {
-            "value": round(gbs, 1),
+            "value": round(kernel_gbs, 1),
             "unit": "GB/s",
             "us_per_call": round(r["event_ms"] * 1e3, 2),
+            "wall_gbs": round(r["bytes"] / (r["wall_ms"] * 1e-3) / 1e9, 1),
+            "timing_ms": spread(r),
             "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 1), "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": round(kernel_gbs / PEAK_HBM_GBS, 4),
                          "traffic": traffic},
@@ -372,12 +412,12 @@ def main() -> int:
     att = result["attention"]
     line = {
         "metric": METRIC,
-        "value": round(tflops, 3),
+        "value": round(kernel_tflops, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(g["wall_ms"], 4),
+        "ms_per_step": round(g["event_ms"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -389,38 +429,53 @@ def main() -> int:
             "m": GEMM_N, "n": GEMM_N, "k": GEMM_N,
             "device": info.name, "compute_units": info.compute_units,
         },
+        "timing": {
+            "rule": "each timed step is one sample (HIP events on the launch stream around every "
+                    "step); value, ms_per_step and every frac come from the median sample, as the "
+                    "reference's bench::measure reports the median of its samples; "
+                    "wall_ms_per_step is host time over all timed steps, bracketed by "
+                    "stream synchronisation",
+            "gemm_ms": spread(g),
+            "wall_ms_per_step": round(g["wall_ms"], 4),
+            "wall_tflops": round(g["flops"] / (g["wall_ms"] * 1e-3) / 1e12, 3),
+        },
         "roofline": {"bound": "mfma", "achieved": round(kernel_tflops, 3),
                      "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(kernel_tflops / PEAK_FP32_MFMA_TFLOPS, 4),
                      "traffic": load_traffic("sgemm_4096_nt")},
         "gemv": gemv,
-        "mlp_fused": {"tflops": round(mlp["flops"] / (mlp["event_ms"] * 1e-3) / 1e12, 3),
+        "mlp_fused": {"tflops": round(tflops_of(mlp["flops"], mlp), 3),
                       "note": "bias + gelu-tanh in the epilogue; two launches: the 3-column "
                               "remainder of N = 4099, whose launch also copies the odd-strided X "
                               "into an aligned copy, then 4093 x 4096 on the 256x256 tile (W read "
                               "in place: its buffer loads write the slices straight into LDS)",
                       "ms_per_call": round(mlp["event_ms"], 4),
+                      "timing_ms": spread(mlp),
                       "traffic": load_traffic("sgemm_mlp"),
-                      "frac": round(mlp["flops"] / (mlp["event_ms"] * 1e-3) / 1e12
-                                    / PEAK_FP32_MFMA_TFLOPS, 4)},
+                      "frac": round(tflops_of(mlp["flops"], mlp) / PEAK_FP32_MFMA_TFLOPS, 4)},
         "attention": {
-            "fused_ms_per_call": round(att["fused_ms"], 4),
-            "fused_tflops": round(att["causal_flops"] / (att["fused_ms"] * 1e-3) / 1e12, 2),
-            "fused_frac": round(att["causal_flops"] / (att["fused_ms"] * 1e-3) / 1e12
+            "fused_ms_per_call": round(att["fused"]["event_ms"], 4),
+            "fused_tflops": round(tflops_of(att["causal_flops"], att["fused"]), 2),
+            "fused_frac": round(tflops_of(att["causal_flops"], att["fused"])
                                 / PEAK_FP32_MFMA_TFLOPS, 4),
+            "fused_timing_ms": spread(att["fused"]),
             "fused_traffic": load_traffic("attention_fused"),
-            "composed_ms_per_call": round(att["total_ms"], 3),
-            "composed_qk_gemm_tflops": round(att["gemm_flops"] / (att["qk_ms"] * 1e-3) / 1e12, 2),
-            "composed_pv_gemm_tflops": round(att["gemm_flops"] / (att["pv_ms"] * 1e-3) / 1e12, 2),
-            "composed_softmax_gbs": round(2 * att["scores_bytes"] / (att["softmax_ms"] * 1e-3)
-                                          / 1e9, 1),
+            "composed_ms_per_call": round(att["total"]["event_ms"], 3),
+            "composed_timing_ms": spread(att["total"]),
+            "composed_qk_gemm_tflops": round(tflops_of(att["gemm_flops"], att["qk"]), 2),
+            "composed_qk_timing_ms": spread(att["qk"]),
+            "composed_pv_gemm_tflops": round(tflops_of(att["gemm_flops"], att["pv"]), 2),
+            "composed_pv_timing_ms": spread(att["pv"]),
+            "composed_softmax_gbs": round(2 * att["scores_bytes"] / (att["softmax"]["event_ms"]
+                                                                   * 1e-3) / 1e9, 1),
             "note": "fused: one kernel, online softmax, FLOP = 4*B*H*D*S(S+1)/2 (causal pairs); "
-                    "composed: the reference's 2 batched GEMMs (4*B*H*S^2*D FLOP, dense), where "
-                    "(the [S, S] causal mask and a -inf scalar read through broadcast views, the "
-                    "scores masked in place: only the removed keys' -inf is written), softmax "
-                    "over the materialized scores; its ms_per_call is host wall time per call, "
-                    "with the 512 MiB scores kept as the stream's scratch array between calls and "
-                    "the 32 MiB output allocated per call"},
+                    "composed: the reference's 2 batched GEMMs (4*B*H*S^2*D FLOP, dense; the "
+                    "scores q k^T on the panel path), where (the [S, S] causal mask and a -inf "
+                    "scalar read through broadcast views, the scores masked in place: only the "
+                    "removed keys' -inf is written), softmax over the materialized scores; its "
+                    "ms_per_call is host wall time per call (median of one-call samples), with "
+                    "the 512 MiB scores kept as the stream's scratch array between calls and the "
+                    "32 MiB output allocated per call"},
         "copy_1gib": {"gbs": round(result["copy"]["bytes"] / (result["copy"]["event_ms"] * 1e-3)
                                    / 1e9, 1),
                       "note": "plain device copy, read+write bytes; the practical HBM ceiling"},
