@@ -1011,6 +1011,14 @@ bool streamed_output(const GemmParams& q) {
     return true;
 }
 
+// Whether the 128x64 tile runs as sgemm_pair_kernel on q: A read along k and B along n, both by
+// 16-byte loads, one tile of columns (n <= 64), and each slice's byte offsets below 2^30 (the
+// direct-to-LDS loaders' 32-bit offsets, as big_tile_ok).
+bool pair_fits(const Plan& plan, const GemmParams& q, int va, int vb) {
+    return plan.ak && !plan.bk && va == 4 && vb == 4 && q.n <= 64 &&
+           127.0 * q.a_rs + 32.0 < 268435456.0 && 31.0 * q.b_rs + 64.0 < 268435456.0;
+}
+
 // Launches the kernel (and the reduce, when split) for region r of the product p describes.
 void launch_region(const Plan& plan, const GemmParams& p, const Region& r, int va, int vb,
                    float* partial, int cus, hipStream_t stream, float* stage = nullptr,
@@ -1049,7 +1057,9 @@ void launch_region(const Plan& plan, const GemmParams& p, const Region& r, int v
     q.stream_c = q.partial == nullptr && streamed_output(q) ? 1 : 0;
     const unsigned grid = static_cast<unsigned>(blocks);
     const bool one_per_cu = blocks <= cus;
-    if (plan.ak && plan.bk) {
+    if (tile == MFR_TILE_128x64 && pair_fits(plan, q, va, vb)) {
+        sgemm_pair_kernel<32><<<grid, 256, 0, stream>>>(q);
+    } else if (plan.ak && plan.bk) {
         launch_layout<true, true>(tile, q, va, vb, grid, one_per_cu, stream);
     } else if (plan.ak) {
         launch_layout<true, false>(tile, q, va, vb, grid, one_per_cu, stream);
@@ -1172,10 +1182,29 @@ void run_sgemm(mfr_stream& s, const mfr_gemm_desc& d, float* scratch = nullptr,
     float* ws = nullptr;
     std::unique_lock<std::mutex> hold(s.workspace_mutex, std::defer_lock);
     if (scratch != nullptr) {
-        const size_t need = 4 * static_cast<size_t>(partial_floats(plan) + fa + fb);
-        if (need > scratch_bytes) {
+        // The fixed array instead of the stream's workspace. A plan that needs more than it holds
+        // takes the fallbacks the workspace path takes when memory cannot be had, where the
+        // caller left them open: automatic splits become one range, automatic staging reads the
+        // operands in place. Anything still over the maximum is refused before any launch.
+        const auto need = [&] { return 4 * static_cast<size_t>(partial_floats(plan) + fa + fb); };
+        if (need() > scratch_bytes && partial_floats(plan) > 0 && d.splits == 0) {
+            single_region(plan, choose(p.m, p.n, p.k, p.batch_count, s.compute_units, d.tile, 1,
+                                       plan.c0, plan.ak, plan.bk,
+                                       thin_b_layout(p, plan, p.m, p.n), big_tile_ok(plan)));
+        }
+        if (need() > scratch_bytes && fa + fb > 0 && d.stage == MFR_STAGE_AUTO) {
+            plan.stage_a = plan.stage_b = false;
+            fa = fb = 0;
+            if (d.tile == MFR_TILE_AUTO) {
+                single_region(plan, choose(p.m, p.n, p.k, p.batch_count, s.compute_units,
+                                           MFR_TILE_AUTO, d.splits == 0 ? 1 : d.splits, plan.c0,
+                                           plan.ak, plan.bk, thin_b_layout(p, plan, p.m, p.n),
+                                           big_tile_ok(plan)));
+            }
+        }
+        if (need() > scratch_bytes) {
             throw mfr::Error(MFR_E_INVALID,
-                             "sgemm_noalloc: this product needs " + std::to_string(need) +
+                             "sgemm_noalloc: this product needs " + std::to_string(need()) +
                                  " bytes of scratch (split-K sums and staged operands), more "
                                  "than the " + std::to_string(scratch_bytes) + "-byte maximum");
         }

@@ -150,8 +150,10 @@ enum { kC0None = 0, kC0Batched = 1, kC0Checked = 2 };
 // ROWS_PAST_M: a tile whose columns are all inside C and whose rows may run past m; every element
 // is computed and stored through a buffer resource of m rows, which drops the stores to rows past
 // m (no per-element test; the caller checks that (m + 256) * c_rs * 4 fits 32 bits).
+// JS: the column step between accumulator blocks: 32 (block j holds columns col0 + 32 j ..), or
+// 1 for the paired layout of sgemm_pair_kernel (a lane's block j holds column col0 + j, col0 even).
 template <int FM, int FN, int ACT, bool INTERIOR, bool RAW, int C0, bool STREAM = false,
-          bool ROWS_PAST_M = false>
+          bool ROWS_PAST_M = false, int JS = 32>
 __device__ __forceinline__ void write_tile(const floatx16 (&acc)[FM][FN], float* c, int64_t c_rs,
                                            const float* c0, int64_t c0_rs, const GemmParams& p,
                                            int64_t row0, int64_t col0,
@@ -173,7 +175,7 @@ __device__ __forceinline__ void write_tile(const floatx16 (&acc)[FM][FN], float*
     float bias_of[FN];
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-        const int64_t col = col0 + 32 * j;
+        const int64_t col = col0 + JS * j;
         bias_of[j] = bias_base != nullptr && (INTERIOR || col < p.n) ? bias_base[col] : -0.0f;
         asm volatile("" ::"v"(bias_of[j]));
     }
@@ -189,14 +191,14 @@ __device__ __forceinline__ void write_tile(const floatx16 (&acc)[FM][FN], float*
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int dr = 8 * (e / 4) + e % 4;
-                    const bool inside = INTERIOR || (col0 + 32 * j < p.n && row_i + dr < p.m);
-                    c0v[j][e] = inside ? c0_i[dr * c0_rs + 32 * j] : 0.0f;
+                    const bool inside = INTERIOR || (col0 + JS * j < p.n && row_i + dr < p.m);
+                    c0v[j][e] = inside ? c0_i[dr * c0_rs + JS * j] : 0.0f;
                 }
             }
         }
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-            const int64_t col = col0 + 32 * j;
+            const int64_t col = col0 + JS * j;
             if (!INTERIOR && !ROWS_PAST_M && col >= p.n) {
                 continue;
             }
@@ -229,14 +231,14 @@ __device__ __forceinline__ void write_tile(const floatx16 (&acc)[FM][FN], float*
                 }
                 if constexpr (ROWS_PAST_M) {
                     const uint32_t offset =
-                        static_cast<uint32_t>(4 * ((row_i + dr) * c_rs + col0 + 32 * j));
+                        static_cast<uint32_t>(4 * ((row_i + dr) * c_rs + col0 + JS * j));
                     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), c_rsrc,
                                                           offset, 0, 0);
                 } else if (row_ok) {
                     if constexpr (STREAM) {
-                        __builtin_nontemporal_store(v, &c_i[dr * c_rs + 32 * j]);
+                        __builtin_nontemporal_store(v, &c_i[dr * c_rs + JS * j]);
                     } else {
-                        c_i[dr * c_rs + 32 * j] = v;
+                        c_i[dr * c_rs + JS * j] = v;
                     }
                 }
             }
@@ -249,43 +251,43 @@ __device__ __forceinline__ void write_tile(const floatx16 (&acc)[FM][FN], float*
 // whose rows alone run past m (stores through a buffer resource that drops those rows), and other
 // edges. With C0 tested and loaded between the elements, each element would wait for the memory
 // counter, which also counts the stores before it. Every other gelu epilogue is one checked copy.
-template <int FM, int FN, int ACT>
+template <int FM, int FN, int ACT, int JS = 32>
 __device__ __forceinline__ void epilogue(const floatx16 (&acc)[FM][FN], float* c, int64_t c_rs,
                                          const float* c0, int64_t c0_rs, const GemmParams& p,
                                          int64_t row0, int64_t col0, bool interior,
                                          bool rows_only_edge, const double* exp_table) {
     if constexpr (ACT == MFR_ACT_GELU_TANH) {
         if (interior && c0 == nullptr) {
-            write_tile<FM, FN, ACT, true, false, kC0None>(acc, c, c_rs, c0, c0_rs, p, row0, col0,
+            write_tile<FM, FN, ACT, true, false, kC0None, false, false, JS>(acc, c, c_rs, c0, c0_rs, p, row0, col0,
                                                           exp_table);
         } else if (rows_only_edge && c0 == nullptr) {
-            write_tile<FM, FN, ACT, false, false, kC0None, false, true>(acc, c, c_rs, c0, c0_rs, p,
+            write_tile<FM, FN, ACT, false, false, kC0None, false, true, JS>(acc, c, c_rs, c0, c0_rs, p,
                                                                         row0, col0, exp_table);
         } else if (c0 == nullptr) {
-            write_tile<FM, FN, ACT, false, false, kC0None>(acc, c, c_rs, c0, c0_rs, p, row0, col0,
+            write_tile<FM, FN, ACT, false, false, kC0None, false, false, JS>(acc, c, c_rs, c0, c0_rs, p, row0, col0,
                                                            exp_table);
         } else {
-            write_tile<FM, FN, ACT, false, false, kC0Checked>(acc, c, c_rs, c0, c0_rs, p, row0,
+            write_tile<FM, FN, ACT, false, false, kC0Checked, false, false, JS>(acc, c, c_rs, c0, c0_rs, p, row0,
                                                               col0, exp_table);
         }
     } else if constexpr (ACT != MFR_ACT_NONE) {
-        write_tile<FM, FN, ACT, false, false, kC0Checked>(acc, c, c_rs, c0, c0_rs, p, row0, col0);
+        write_tile<FM, FN, ACT, false, false, kC0Checked, false, false, JS>(acc, c, c_rs, c0, c0_rs, p, row0, col0);
     } else if (c0 != nullptr) {
         if (interior) {
-            write_tile<FM, FN, ACT, true, false, kC0Batched>(acc, c, c_rs, c0, c0_rs, p, row0,
+            write_tile<FM, FN, ACT, true, false, kC0Batched, false, false, JS>(acc, c, c_rs, c0, c0_rs, p, row0,
                                                              col0);
         } else {
-            write_tile<FM, FN, ACT, false, false, kC0Batched>(acc, c, c_rs, c0, c0_rs, p, row0,
+            write_tile<FM, FN, ACT, false, false, kC0Batched, false, false, JS>(acc, c, c_rs, c0, c0_rs, p, row0,
                                                               col0);
         }
     } else {
         if (interior && p.stream_c) {
-            write_tile<FM, FN, ACT, true, false, kC0None, true>(acc, c, c_rs, c0, c0_rs, p, row0,
+            write_tile<FM, FN, ACT, true, false, kC0None, true, false, JS>(acc, c, c_rs, c0, c0_rs, p, row0,
                                                                 col0);
         } else if (interior) {
-            write_tile<FM, FN, ACT, true, false, kC0None>(acc, c, c_rs, c0, c0_rs, p, row0, col0);
+            write_tile<FM, FN, ACT, true, false, kC0None, false, false, JS>(acc, c, c_rs, c0, c0_rs, p, row0, col0);
         } else {
-            write_tile<FM, FN, ACT, false, false, kC0None>(acc, c, c_rs, c0, c0_rs, p, row0,
+            write_tile<FM, FN, ACT, false, false, kC0None, false, false, JS>(acc, c, c_rs, c0, c0_rs, p, row0,
                                                            col0);
         }
     }
@@ -387,14 +389,14 @@ __device__ __forceinline__ void slice_mfma(floatx16 (&acc)[FM][FN], const float*
 }
 
 // The end of a tile: split-K partial sums, or the epilogue with the activation chosen once.
-template <int BM, int BN, int WM, int WN, int FM, int FN>
+template <int BM, int BN, int WM, int WN, int FM, int FN, int JS = 32>
 __device__ __forceinline__ void finish_tile(const floatx16 (&acc)[FM][FN], const GemmParams& p,
                                             const TileWork& w, int wave_m, int wave_n, int half,
                                             int r32, const double* exp_table) {
     // Accumulator e of block (i, j) is C(row, col) with row = 32i + 8(e/4) + 4*half + e%4,
-    // col = 32j + lane%32 (v_mfma_f32_32x32x2_f32 layout).
+    // col = 32j + lane%32 (v_mfma_f32_32x32x2_f32 layout), or 2 (lane%32) + j when paired.
     const int64_t row0 = w.m0 + wave_m * WM + 4 * half;
-    const int64_t col0 = w.n0 + wave_n * WN + r32;
+    const int64_t col0 = w.n0 + wave_n * WN + (JS == 32 ? r32 : 2 * r32);
     const bool interior = w.m0 + BM <= p.m && w.n0 + BN <= p.n;
     // Rows past m only, and C's byte offsets (rows past m included) within 32 bits.
     const bool rows_only_edge = !interior && w.n0 + BN <= p.n &&
@@ -403,11 +405,11 @@ __device__ __forceinline__ void finish_tile(const floatx16 (&acc)[FM][FN], const
         // Split-K: raw sums only, to partial[split][batch] (dense m x n).
         float* part = p.partial + (w.split * p.batch_count + w.batch_linear) * p.m * p.n;
         if (interior) {
-            write_tile<FM, FN, MFR_ACT_NONE, true, true, kC0None>(acc, part, p.n, nullptr, 0, p,
-                                                                  row0, col0);
+            write_tile<FM, FN, MFR_ACT_NONE, true, true, kC0None, false, false, JS>(
+                acc, part, p.n, nullptr, 0, p, row0, col0);
         } else {
-            write_tile<FM, FN, MFR_ACT_NONE, false, true, kC0None>(acc, part, p.n, nullptr, 0, p,
-                                                                   row0, col0);
+            write_tile<FM, FN, MFR_ACT_NONE, false, true, kC0None, false, false, JS>(
+                acc, part, p.n, nullptr, 0, p, row0, col0);
         }
         return;
     }
@@ -416,13 +418,13 @@ __device__ __forceinline__ void finish_tile(const floatx16 (&acc)[FM][FN], const
     // One activation per branch (uniform), so each epilogue is straight-line code: unrolled
     // over every accumulator, the three would not fit the instruction cache together.
     if (p.act == MFR_ACT_NONE) {
-        epilogue<FM, FN, MFR_ACT_NONE>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
+        epilogue<FM, FN, MFR_ACT_NONE, JS>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
                                        interior, rows_only_edge, exp_table);
     } else if (p.act == MFR_ACT_GELU_TANH) {
-        epilogue<FM, FN, MFR_ACT_GELU_TANH>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
+        epilogue<FM, FN, MFR_ACT_GELU_TANH, JS>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
                                             interior, rows_only_edge, exp_table);
     } else {
-        epilogue<FM, FN, MFR_ACT_GELU_ERF>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
+        epilogue<FM, FN, MFR_ACT_GELU_ERF, JS>(acc, c_base, p.c_rs, c0_base, p.c0_rs, p, row0, col0,
                                            interior, rows_only_edge, exp_table);
     }
 }
@@ -795,6 +797,172 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_direct_kernel(Ge
         __syncthreads(); // the gelu table's copy (no slice barrier has made it visible)
     }
     finish_tile<BM, BN, WM, WN, FM, FN>(acc, p, w, wave_m, wave_n, half, r32, gelu_table);
+}
+
+// ---- the paired form: 64 columns of an N-major B ----------------------------------------------
+
+// Direct-to-LDS copy of an M/N-major slice whose lines (KT of them, ROWS floats each, padded to
+// ROWS + 8) are narrower than one wave-instruction (ROWS = 64): the image is filled as one run
+// of floats, each lane's 4 floats (16 bytes, within one line) from wherever they live. The last
+// instruction may run past the image, so the LDS buffer holds kAlloc floats. Elements outside the
+// matrix and the pads get an offset past the record limit and load zeros.
+template <int ROWS, int KT, int THREADS> struct DirectNarrowLoader {
+    static constexpr int kPitch = ROWS + 8;
+    static constexpr int kFloats = KT * kPitch;
+    static constexpr int kInstr = (kFloats + 255) / 256;
+    static constexpr int kAlloc = kInstr * 256;
+    static constexpr int kWaves = THREADS / 64;
+    static constexpr int kPerWave = (kInstr + kWaves - 1) / kWaves;
+    uint32_t off[kPerWave]; // this lane's offsets in a whole slice
+    uint32_t k_bytes;
+
+    // (line, position) of this lane's 4 floats in instruction j of this wave; false past the
+    // image.
+    __device__ __forceinline__ static bool place(int j, int& line, int& at) {
+        const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / 64));
+        const int f = ((wave * kPerWave + j) * 64 + static_cast<int>(__lane_id())) * 4;
+        line = f / kPitch;
+        at = f - line * kPitch;
+        return f < kFloats;
+    }
+
+    __device__ __forceinline__ explicit DirectNarrowLoader(int64_t k_stride) {
+        k_bytes = static_cast<uint32_t>(k_stride) * 4u;
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            int line, at;
+            const bool in_image = place(j, line, at);
+            off[j] = in_image && at < ROWS ? static_cast<uint32_t>(line) * k_bytes +
+                                                 static_cast<uint32_t>(at) * 4u
+                                           : kDirectLimit;
+        }
+    }
+
+    // base: element (depth 0, row 0) of the slice; rows_left / k_left as DirectSliceLoader's.
+    __device__ __forceinline__ void issue(float* lds, const float* base, int rows_left,
+                                          int k_left) const {
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(base), 0, static_cast<int>(kDirectLimit - 1), kBufferWord3);
+        const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / 64));
+        const bool whole = rows_left >= ROWS && k_left >= KT;
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            const int instr = wave * kPerWave + j;
+            if (kInstr % kWaves != 0 && instr >= kInstr) {
+                break; // uniform: this wave's block ended
+            }
+            uint32_t offset = off[j];
+            if (!whole) {
+                int line, at;
+                place(j, line, at);
+                offset = at < rows_left && line < k_left ? offset : kDirectLimit;
+            }
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds + instr * 256, 16,
+                                                     static_cast<int>(offset), 0, 0, 0);
+        }
+    }
+};
+
+// The 128x64 tile on a K-major A and an N-major B, both read by 16-byte direct-to-LDS loads:
+// attention's P V (128 x [1024 x 1024] x [1024 x 64]). Four wavefronts of 32 rows x all 64
+// columns. B's N-major fragments would take four 4-byte LDS reads per column block and depth
+// group; here lane l's two accumulator blocks hold the column pair 2 (l % 32) and 2 (l % 32) + 1,
+// so one 8-byte read feeds both blocks' MFMAs: 5 LDS reads per 8 MFMAs instead of 9. The depth
+// order is the tile kernels' (the same sums, bit for bit). Double-buffered 32-deep slices, the
+// copy of slice s + 1 issued before slice s's MFMAs and waited for before the barrier that ends
+// it (no stores in the loop). The epilogue writes the paired layout (finish_tile, JS = 1). KT is
+// the depth slice (32; split-K ranges are multiples of it).
+// Config 5's P V on one MI355X: 165.7-169.6 us against 181.6-184.0 us for the register-copy
+// 128x64 kernel (one process each).
+template <int KT>
+__global__ __launch_bounds__(256) void sgemm_pair_kernel(GemmParams p) {
+    constexpr int BM = 128, BN = 64, THREADS = 256;
+    using LoadA = DirectSliceLoader<BM, KT, true, 4, THREADS>;
+    using LoadB = DirectNarrowLoader<BN, KT, THREADS>;
+    using FragA = SliceLoader<BM, KT, true, 4, THREADS>;
+    constexpr int PB = LoadB::kPitch;
+    __shared__ __align__(16) float tile_a0[LoadA::kFloats];
+    __shared__ __align__(16) float tile_a1[LoadA::kFloats];
+    __shared__ __align__(16) float tile_b0[LoadB::kAlloc];
+    __shared__ __align__(16) float tile_b1[LoadB::kAlloc];
+    __shared__ double gelu_table[64];
+    if (p.act == MFR_ACT_GELU_TANH && threadIdx.x < 64) {
+        gelu_table[threadIdx.x] = gelu_math::kExp2Table[threadIdx.x];
+    }
+
+    const TileWork w = tile_work<BM, BN>(p);
+    const float* a_base = p.a + w.off_a + w.m0 * p.a_rs + w.k_begin * p.a_cs;
+    const float* b_base = p.b + w.off_b + w.n0 * p.b_cs + w.k_begin * p.b_rs;
+    const int64_t a_step = KT * p.a_cs;
+    const int64_t b_step = KT * p.b_rs;
+    const int lane = threadIdx.x % 64;
+    const int wave = threadIdx.x / 64;
+    const int half = lane / 32;
+    const int r32 = lane % 32;
+
+    floatx16 acc[1][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            acc[0][j][e] = 0.0f;
+        }
+    }
+    const auto slice = [&](const float* sa, const float* sb) {
+#pragma unroll
+        for (int g = 0; g < KT / 8; ++g) {
+            float fa[4];
+            FragA::fragment(sa, wave * 32 + r32, g, half, fa);
+            float2 fb[4];
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                fb[st] = *reinterpret_cast<const float2*>(sb + (8 * g + 4 * half + st) * PB +
+                                                          2 * r32);
+            }
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[st], fb[st].x, acc[0][0], 0,
+                                                                 0, 0);
+                acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[st], fb[st].y, acc[0][1], 0,
+                                                                 0, 0);
+            }
+        }
+    };
+
+    // Slices in pairs (buffer 0 then 1) with no exit between the halves; an odd count runs one
+    // slice past the end, which loads zeros and adds nothing (as sgemm_direct_kernel).
+    const int64_t kk = w.kk;
+    const int64_t slices = kk > 0 ? (kk + KT - 1) / KT : 0;
+    const auto k_left_of = [&](int64_t s) {
+        const int64_t left = kk - s * KT;
+        return left <= 0 ? 0 : left < KT ? static_cast<int>(left) : KT;
+    };
+    const LoadA load_a(p.a_rs, p.a_cs);
+    const LoadB load_b(p.b_rs);
+    if (slices > 0) {
+        load_a.issue(tile_a0, a_base, w.rows_a, k_left_of(0));
+        load_b.issue(tile_b0, b_base, w.rows_b, k_left_of(0));
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+    for (int64_t s = 0; s < slices; s += 2) {
+        load_a.issue(tile_a1, a_base + (s + 1) * a_step, w.rows_a, k_left_of(s + 1));
+        load_b.issue(tile_b1, b_base + (s + 1) * b_step, w.rows_b, k_left_of(s + 1));
+        slice(tile_a0, tile_b0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (s + 2 < slices) {
+            load_a.issue(tile_a0, a_base + (s + 2) * a_step, w.rows_a, k_left_of(s + 2));
+            load_b.issue(tile_b0, b_base + (s + 2) * b_step, w.rows_b, k_left_of(s + 2));
+        }
+        slice(tile_a1, tile_b1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+    if (slices == 0) {
+        __syncthreads(); // the gelu table's copy
+    }
+    finish_tile<BM, BN, 32, BN, 1, 2, 1>(acc, p, w, wave, 0, half, r32, gelu_table);
 }
 
 } // namespace mfr::gemm

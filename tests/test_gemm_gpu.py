@@ -423,6 +423,61 @@ def test_panel_refusals(stream, case):
     assert np.all(c.numpy() == POISON)
 
 
+# ---- the paired 128x64 kernel (B read along n, at most 64 columns) ------------------------------
+
+@pytest.mark.parametrize("m,n,k", [(1, 64, 4), (127, 64, 32), (128, 60, 36), (129, 32, 100),
+                                   (300, 4, 1024), (1000, 16, 68), (513, 64, 257 * 4)])
+def test_exact_pair_tile(stream, m, n, k):
+    """The 128x64 tile on a K-major A and an N-major B of at most 64 columns (sgemm_pair_kernel,
+    whose lanes hold column pairs): alpha, beta * C0, a bias and the tanh gelu, a split-K run, and
+    rows, columns and depths past the tile edges. Bits equal the exact result."""
+    a = quarter_matrix(m, k, 141)
+    b = quarter_matrix(k, n, 142)
+    c0 = quarter_matrix(m, n, 143)
+    bias = quarter_matrix(1, n, 144)[0]
+    a_d, b_d, c0_d, bias_d = dev(a, stream), dev(b, stream), dev(c0, stream), dev(bias, stream)
+    tile = mf.abi.TILE_128x64
+    pre = ((np.float32(1.5) * exact_product(a, b)) + np.float32(0.5) * c0 + bias).astype(
+        np.float32)
+    c, buf = guarded_output(stream, (m, n))
+    mf.gemm_batched(a_d, b_d, c, alpha=1.5, c0=c0_d, beta=0.5, bias=bias_d, tile=tile, splits=1)
+    assert same_bits(c.numpy(), pre), f"{m}x{n}x{k}"
+    check_guards(buf)
+    mf.gemm_batched(a_d, b_d, c, alpha=1.5, c0=c0_d, beta=0.5, bias=bias_d,
+                    act=mf.ACT_GELU_TANH, tile=tile, splits=1)
+    from oracle import Oracle
+    assert same_bits(c.numpy(), Oracle().gelu(pre, approximate=True)), f"{m}x{n}x{k} gelu"
+    if k >= 512:
+        split, buf = guarded_output(stream, (m, n))
+        mf.gemm_batched(a_d, b_d, split, alpha=1.5, c0=c0_d, beta=0.5, bias=bias_d, tile=tile,
+                        splits=4)
+        assert mf.gemm_plan(a_d, b_d, split, tile=tile, splits=4)[2] == 4
+        assert same_bits(split.numpy(), pre), f"{m}x{n}x{k} split"
+        check_guards(buf)
+
+
+def test_pair_tile_attention_pv_bitwise(stream, oracle):
+    """Attention's P V at 4 x [1024 x 1024] x [1024 x 64] on the 128x64 tile (the paired kernel,
+    which AUTO picks at config 5's 128 batches) gives the 64x64 tile's bits (the tiles share one
+    summation order) and is within the parity bar of the oracle."""
+    bsz, m, n, k = 4, 1024, 64, 1024
+    pm = uniform(oracle, (bsz, m, k), 0.0, 1.0 / 512.0, 151, 0)
+    v = normal(oracle, (bsz, k, n), 0.0, 1.0, 152, 0)
+    p_d, v_d = dev(pm, stream), dev(v, stream)
+    out = mf.DeviceArray.empty((bsz, m, n), stream)
+    scores = mf.DeviceArray.empty((128, m, k), stream)
+    values = mf.DeviceArray.empty((128, k, n), stream)
+    assert mf.gemm_plan(scores, values, mf.DeviceArray.empty((128, m, n), stream))[0] == (
+        mf.abi.TILE_128x64)
+    mf.gemm_batched(p_d, v_d, out, tile=mf.abi.TILE_128x64)
+    got = out.numpy()
+    mf.gemm_batched(p_d, v_d, out, tile=mf.abi.TILE_64x64)
+    assert np.array_equal(got.view(np.uint32), out.numpy().view(np.uint32))
+    for b in range(bsz):
+        want = oracle.matmul(pm[b], v[b])
+        assert_gemm_parity(got[b], want, magnitude(oracle, pm[b], v[b]), k, f"P V batch {b}")
+
+
 # ---- split-K -----------------------------------------------------------------------------------
 
 def ranges_run(k, splits):
@@ -888,10 +943,10 @@ def test_config4_mlp_fused_bias_gelu(stream, oracle):
     """X[4093,1023] x W[1023,4099] + bias, gelu-tanh fused in the epilogue,
     against the reference's three-op chain gelu(bias_add(matmul(X, W), b), true).
 
-    Row argmax: the index must be the oracle's on every row whose top two values differ by more
-    than twice the error bar, and on every other row the value the GPU's index selects must be
-    within the bar of the row's maximum (a near tie that summation order can flip). The counts
-    of decided, near-tie and differing rows are recorded."""
+    Row argmax is bit-exact, as the north star asks: the GPU's index equals the oracle's on every
+    one of the 4093 rows (both sides are deterministic). The rows whose top two values lie within
+    twice the error bar (near ties that another summation order could flip) are counted and
+    recorded as a diagnostic, with the number of rows that differ (0)."""
     m, k, n = 4093, 1023, 4099
     x = normal(oracle, (m, k), 0.0, 1.0, 7, 0)
     w = normal(oracle, (k, n), 0.0, float(np.sqrt(1.0 / 1023.0)), 8, 0)
@@ -908,22 +963,16 @@ def test_config4_mlp_fused_bias_gelu(stream, oracle):
     margin = top2[:, 1] - top2[:, 0]
     bar = 1e-5 * np.sqrt(k) * scale.max(axis=1)
     decided = margin > 2 * bar
-    assert np.array_equal(gpu_argmax[decided], want_arg[decided])
     differ = np.nonzero(gpu_argmax != want_arg)[0]
-    rows = np.arange(m)
-    # On a differing row the GPU's chosen entry must still be a maximum within the bar.
-    shortfall = want.max(axis=1)[differ] - want[differ, gpu_argmax[differ]]
-    assert np.all(shortfall <= bar[differ]), (differ, shortfall, bar[differ])
-    worst = float(np.max(shortfall / bar[differ])) if differ.size else 0.0
-    print(f"cfg4: rel err vs magnitude {rel_mag:.3e}, vs max|C| {rel_max:.3e}; argmax equal on "
+    print(f"cfg4: rel err vs magnitude {rel_mag:.3e}, vs max|C| {rel_max:.3e}; argmax: "
           f"{int(decided.sum())} decided rows, {int((~decided).sum())} near-tie rows, "
-          f"{differ.size} rows differ in total")
+          f"{differ.size} rows differ")
     record_parity("cfg4_mlp_bias_gelu", rel_err_vs_magnitude=rel_mag, rel_err_vs_max=rel_max,
                   bar=tolerance(k), bit_identical_share=float(np.mean(same_elements(out, want))),
                   argmax_rows=m, argmax_decided_rows=int(decided.sum()),
                   argmax_near_tie_rows=int((~decided).sum()), argmax_differing_rows=int(differ.size),
-                  argmax_differing_row_ids=[int(r) for r in rows[differ]],
-                  argmax_worst_shortfall_over_bar=worst)
+                  argmax_differing_row_ids=[int(r) for r in differ])
+    assert np.array_equal(gpu_argmax, want_arg), f"argmax differs on rows {differ.tolist()}"
 
 
 def test_deterministic(stream):
