@@ -216,8 +216,11 @@ int mfr_sgemm(mfr_stream_t stream, const mfr_gemm_desc* desc);
  * partial sums and staged operands in a fixed scratch array of MFR_SGEMM_SCRATCH_BYTES per device
  * (a static device array, resident until the process ends) instead of the stream's workspace. A
  * plan that needs more (the split-K sums are splits*m*n*batch floats, a staged operand its
- * zero-padded copy) fails with MFR_E_INVALID before anything is launched; products with aligned
- * operands and no split need none. Every call on one device shares that device's array, so calls
+ * zero-padded copy) takes the fallbacks mfr_sgemm takes when its workspace cannot be had, where
+ * the descriptor leaves them to AUTO (automatic splits become one range, automatic staging reads
+ * the operands in place: the same results up to summation order); what still needs more fails
+ * with MFR_E_INVALID before anything is launched. Products with aligned operands and no split
+ * need none. Every call on one device shares that device's array, so calls
  * that overlap on one device (on two streams, or from two threads) race; the array keeps the last
  * call's contents, and nothing in it needs to start at zero. The first call on a device looks up
  * the array's address there. */

@@ -3,7 +3,9 @@
 Called through the C ABI, it must give exactly mfr_sgemm's bits on products that use its fixed
 scratch array (staged operands, split-K partial sums), on consecutive calls whose second input is
 smaller (the array keeps the first call's contents), and refuse a product whose plan needs more
-than MFR_SGEMM_SCRATCH_BYTES before launching anything.
+than MFR_SGEMM_SCRATCH_BYTES before launching anything. Automatic staging and splits that would
+need more take the fallbacks mfr_sgemm takes without workspace memory (operands read in place,
+one depth range) instead of a refusal.
 """
 import ctypes
 
@@ -12,7 +14,7 @@ import pytest
 
 import mensurflow_amd as mf
 from mensurflow_amd import abi
-from helpers import normal, same_bits, uniform
+from helpers import normal, quarter_matrix, same_bits, uniform
 
 pytestmark = pytest.mark.gpu
 
@@ -99,3 +101,26 @@ def test_noalloc_without_scratch_use(stream, oracle):
     want, got, plan = _both(stream, a, b, splits=1)
     assert plan[1] == abi.STAGE_NEVER and plan[2] == 1, plan
     assert same_bits(got, want)
+
+
+def test_noalloc_falls_back_to_in_place_reads_over_the_maximum(stream):
+    """AUTO staging (and AUTO splits) that would need more than the scratch array: the no-alloc
+    entry point reads the operands in place in one depth range instead, as mfr_sgemm does when
+    its workspace cannot be had. Quarter-integer inputs make every sum exact in any order, so both
+    entry points must give the exact product."""
+    m, n, k = 4096, 256, 4097
+    a = quarter_matrix(m, k, 91)  # rows of 4097 floats, which 16-byte loads cannot take
+    b = quarter_matrix(k, n, 92)
+    da, db = _dev(a, stream), _dev(b, stream)
+    probe = mf.DeviceArray.empty((m, n), stream)
+    plan = mf.gemm_plan(da, db, probe)
+    # mfr_sgemm stages A: 4096 rows of 4100 floats, 67,174,400 bytes, just over the maximum.
+    assert plan[1] == abi.STAGE_ALWAYS, plan
+    assert 4 * m * 4100 > abi.SGEMM_SCRATCH_BYTES
+    want = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
+    for entry in ("mfr_sgemm", "mfr_sgemm_noalloc"):
+        c = _dev(np.full((m, n), np.float32(123.0), np.float32), stream)
+        desc = mf._gemm_desc(da, db, c, 1.0, None, 0.0, None, abi.ACT_NONE, 0, abi.STAGE_AUTO, 0)
+        print(f"no_alloc: {entry} m={m} n={n} k={k} over the maximum", flush=True)
+        _run(entry, stream, desc)
+        assert same_bits(c.numpy(), want), entry
