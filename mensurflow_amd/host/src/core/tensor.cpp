@@ -159,6 +159,28 @@ bool packs_on_device(Device device, DType dtype) {
                {detail::OpId::StridedCopy, device.type, dtype}) != nullptr;
 }
 
+// Packs the view (shape, strides) at element `offset` of device storage into host memory `dst`:
+// only the bytes the view reaches come over, then they are packed on the host.
+void gather_through_host(const detail::Storage& storage, std::int64_t offset, const Shape& shape,
+                         const Strides& strides, std::size_t item, void* dst) {
+    std::vector<std::byte> span(static_cast<std::size_t>(reach(shape, strides)) * item);
+    storage.copy_to_host(span.data(), static_cast<std::size_t>(offset) * item, span.size());
+    gather(span.data(), static_cast<std::byte*>(dst), shape, strides, item);
+}
+
+// Packs `view` (device memory) into `out` (contiguous, same shape, on the same device) with the
+// device's strided copy. False when the device copy does not take the layout (it throws
+// NotImplemented, e.g. for more dimensions than it handles): the caller packs through host
+// memory instead.
+bool pack_on_device(const Tensor& view, const Tensor& out) {
+    try {
+        detail::dispatch(detail::OpId::StridedCopy, {{view}, {out}}, Execution::GPU);
+        return true;
+    } catch (const detail::NotImplemented&) {
+        return false;
+    }
+}
+
 } // namespace
 
 // ---- construction ---------------------------------------------------------------------------------
@@ -246,6 +268,7 @@ Tensor Tensor::to(Device target) const {
     // they lie, and the device packs them (a transposed 4096^2 operand is one 64 MiB transfer
     // and a device transpose instead of a host gather). Taken while the span is at most 4 times
     // the view's own bytes, so a sparse slice does not drag its whole base along.
+    // A layout the device copy does not take goes on to the host gather below.
     if (const std::byte* src = storage_->host_data();
         src != nullptr && !is_contiguous() && packs_on_device(target, dtype_)) {
         const std::int64_t span = reach(shape_, strides_);
@@ -253,7 +276,10 @@ Tensor Tensor::to(Device target) const {
             Tensor raw = empty({span}, dtype_, target);
             raw.storage_->copy_from_host(0, src + static_cast<std::size_t>(offset_) * itemsize(),
                                          static_cast<std::size_t>(span) * itemsize());
-            return Tensor(raw.storage_, 0, shape_, strides_, dtype_).contiguous();
+            Tensor packed = empty(shape_, dtype_, target);
+            if (pack_on_device(Tensor(raw.storage_, 0, shape_, strides_, dtype_), packed)) {
+                return packed;
+            }
         }
     }
     Tensor out = empty(shape_, dtype_, target);
@@ -286,11 +312,10 @@ Tensor Tensor::contiguous() const {
     if (std::byte* host = storage_->host_data()) {
         gather(host + static_cast<std::size_t>(offset_) * itemsize(), out.storage_->host_data(),
                shape_, strides_, itemsize());
-    } else if (packs_on_device(device(), dtype_)) {
-        detail::dispatch(detail::OpId::StridedCopy, {{*this}, {out}}, Execution::GPU);
-    } else {
+    } else if (!packs_on_device(device(), dtype_) || !pack_on_device(*this, out)) {
+        // Through host memory: the span the view reaches comes over and is packed there.
         std::vector<std::byte> packed(out.nbytes());
-        copy_to_host(packed.data());
+        gather_through_host(*storage_, offset_, shape_, strides_, itemsize(), packed.data());
         out.storage_->copy_from_host(0, packed.data(), packed.size());
     }
     return out;
@@ -311,15 +336,18 @@ void Tensor::copy_to_host(void* dst) const {
         storage_->copy_to_host(out, origin, nbytes());
     } else if (const std::byte* host = storage_->host_data()) {
         gather(host + origin, out, shape_, strides_, item);
-    } else if (packs_on_device(device(), dtype_)) {
-        contiguous().copy_to_host(out);
     } else {
-        // Only the bytes the view reaches come over, then they are packed on the host.
-        std::vector<std::byte> span(static_cast<std::size_t>(reach(shape_, strides_)) * item);
-        storage_->copy_to_host(span.data(), origin, span.size());
-        gather(span.data(), out, shape_, strides_, item);
+        if (packs_on_device(device(), dtype_)) {
+            Tensor packed = empty(shape_, dtype_, device());
+            if (pack_on_device(*this, packed)) {
+                packed.copy_to_host(out);
+                return;
+            }
+        }
+        gather_through_host(*storage_, offset_, shape_, strides_, item, out);
     }
 }
+
 
 void Tensor::copy_from(const Tensor& source) {
     require_defined();

@@ -153,6 +153,25 @@ void test_transfers(Device device) {
                           moved.to_vector<float>() == view.to_vector<float>(),
                       "to(" + to_string(device) + ") of a host view " + to_string(view.shape()));
     }
+    // A 9-dimensional transposed view: more dimensions than a device's strided copy takes
+    // (MFR_MAX_COPY_DIMS on rocm), so to() gathers it on the host, and contiguous() and the
+    // read-back of the device-resident view go through host memory.
+    {
+        const Shape shape9 = {2, 1, 3, 1, 2, 1, 2, 3, 2};
+        const auto nine = iota(numel(shape9));
+        const Tensor host9 = Tensor::from_vector(nine, shape9, cpu).transpose(0, 8);
+        const std::vector<float> want9 = host9.to_vector<float>();
+        const Tensor moved9 = host9.to(device);
+        test::require(moved9.device() == device && moved9.shape() == host9.shape() &&
+                          moved9.to_vector<float>() == want9,
+                      "to(" + to_string(device) + ") of a 9-D transposed host view");
+        const Tensor dev9 = Tensor::from_vector(nine, shape9, device).transpose(0, 8);
+        test::require(dev9.to_vector<float>() == want9, "read-back of a 9-D device view");
+        const Tensor packed9 = dev9.contiguous();
+        test::require(packed9.is_contiguous() && packed9.device() == device &&
+                          packed9.to_vector<float>() == want9,
+                      "contiguous() of a 9-D view on " + to_string(device));
+    }
     // Empty tensors.
     test::require(Tensor::empty({0, 5}, DType::F32, device).to_vector<float>().empty(), "empty");
 }
