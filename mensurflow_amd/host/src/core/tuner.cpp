@@ -11,6 +11,7 @@
 #include <functional>
 #include <iostream>
 #include <limits>
+#include <numeric>
 #include <sstream>
 #include <stdexcept>
 
@@ -28,52 +29,49 @@ using detail::TuningEntry;
 
 using Clock = std::chrono::steady_clock;
 
-// The call's arguments with its inputs on `device` and fresh outputs there, so measuring never
-// writes the algorithm's own tensors.
-OpArgs staged_on(const OpArgs& args, Device device) {
+// A measuring copy of a recorded call: every input resident on `device` (moved there when it lives
+// elsewhere) and fresh outputs there, so a measurement never writes the algorithm's own tensors.
+OpArgs measuring_copy(const OpArgs& args, Device device) {
     OpArgs copy = args;
-    for (Tensor& input : copy.inputs) {
-        input = input.device() == device ? input : input.to(device);
-    }
-    for (Tensor& output : copy.outputs) {
-        output = Tensor::empty(output.shape(), output.dtype(), device);
-    }
+    std::transform(copy.inputs.begin(), copy.inputs.end(), copy.inputs.begin(),
+                   [device](const Tensor& t) { return t.device() == device ? t : t.to(device); });
+    std::transform(copy.outputs.begin(), copy.outputs.end(), copy.outputs.begin(),
+                   [device](const Tensor& t) { return Tensor::empty(t.shape(), t.dtype(), device); });
     return copy;
 }
 
-std::vector<std::vector<float>> host_outputs(const OpArgs& args) {
-    std::vector<std::vector<float>> values;
-    for (const Tensor& out : args.outputs) {
-        values.push_back(out.dtype() == DType::F32 ? out.to_vector<float>() : std::vector<float>{});
-    }
+// A call's fp32 outputs as host vectors (empty for outputs of other types): what the result of a
+// tuned point is compared by.
+using Readback = std::vector<std::vector<float>>;
+
+Readback read_back(const OpArgs& args) {
+    Readback values(args.outputs.size());
+    std::transform(args.outputs.begin(), args.outputs.end(), values.begin(), [](const Tensor& t) {
+        return t.dtype() == DType::F32 ? t.to_vector<float>() : std::vector<float>{};
+    });
     return values;
 }
 
-// Each output element within 1e-3 of the default output's largest magnitude (tiles sum in
-// different orders), NaN where the default has NaN.
-bool agrees(const std::vector<std::vector<float>>& want,
-            const std::vector<std::vector<float>>& got) {
-    if (want.size() != got.size()) {
-        return false;
-    }
-    for (std::size_t o = 0; o < want.size(); ++o) {
-        if (want[o].size() != got[o].size()) {
+// Whether `got` is `want` up to the summation-order differences between kernel settings: per
+// output, every element within 1e-3 of that output's largest magnitude (plus 1e-6), and NaN
+// exactly where `want` has NaN.
+bool within_rounding(const Readback& want, const Readback& got) {
+    const auto same_output = [](const std::vector<float>& w, const std::vector<float>& g) {
+        if (w.size() != g.size()) {
             return false;
         }
-        double largest = 0.0;
-        for (const float v : want[o]) {
-            largest = std::max(largest, std::fabs(static_cast<double>(v)));
-        }
+        const double largest = std::accumulate(
+            w.begin(), w.end(), 0.0,
+            [](double most, float v) { return std::max(most, std::fabs(static_cast<double>(v))); });
         const double slack = 1e-3 * largest + 1e-6;
-        for (std::size_t i = 0; i < want[o].size(); ++i) {
-            const double w = want[o][i], g = got[o][i];
-            const bool both_nan = std::isnan(w) && std::isnan(g);
-            if (!both_nan && !(std::fabs(g - w) <= slack)) {
-                return false;
-            }
-        }
-    }
-    return true;
+        return std::equal(w.begin(), w.end(), g.begin(), [slack](float a, float b) {
+            return std::isnan(a) ? std::isnan(b)
+                                 : std::fabs(static_cast<double>(b) - static_cast<double>(a)) <=
+                                       slack;
+        });
+    };
+    return want.size() == got.size() &&
+           std::equal(want.begin(), want.end(), got.begin(), same_output);
 }
 
 // Median milliseconds per call of `run`, which waits for its own work. Calls are timed in
@@ -262,13 +260,13 @@ TuneReport Tuner::tune(const Algorithm& algorithm, const std::vector<Tensor>& in
                     detail::Stream& stream = registry.get(device).stream(device.index);
                     const double ms = median_ms(
                         [&] {
-                            OpArgs moved = staged_on(call.args, device);
+                            OpArgs moved = measuring_copy(call.args, device);
                             kernel(moved, stream);
                             for (Tensor& out : moved.outputs) {
                                 out = out.to(call.data_device);
                             }
                             if (!moved.outputs.empty()) {
-                                (void)host_outputs(moved);
+                                (void)read_back(moved);
                             }
                         },
                         options);
@@ -302,7 +300,7 @@ TuneReport Tuner::tune(const Algorithm& algorithm, const std::vector<Tensor>& in
         if (tunable == nullptr) {
             continue;
         }
-        const OpArgs base = staged_on(call.args, target);
+        const OpArgs base = measuring_copy(call.args, target);
         TunedCall result;
         result.op = tunable->name;
         result.device = to_string(target);
@@ -313,12 +311,12 @@ TuneReport Tuner::tune(const Algorithm& algorithm, const std::vector<Tensor>& in
         }
         const KernelFn kernel = registry.dispatcher().lookup({op, target.type, dtype});
         detail::Stream& stream = registry.get(target).stream(target.index);
-        const auto timed = [&](const TuningConfig& config, std::vector<std::vector<float>>* out) {
-            OpArgs args = staged_on(base, target);
+        const auto timed = [&](const TuningConfig& config, Readback* out) {
+            OpArgs args = measuring_copy(base, target);
             args.tuning = config;
             kernel(args, stream);
             if (out != nullptr) {
-                *out = host_outputs(args);
+                *out = read_back(args);
             }
             return median_ms(
                 [&] {
@@ -327,13 +325,13 @@ TuneReport Tuner::tune(const Algorithm& algorithm, const std::vector<Tensor>& in
                 },
                 options);
         };
-        std::vector<std::vector<float>> reference;
+        Readback reference;
         result.default_ms = timed(tunable->defaults(), &reference);
         result.best_ms = result.default_ms;
         result.best_settings = result.default_settings;
         for (const detail::SearchRegion& region : tunable->space(base)) {
             for (const TuningConfig& point : points_of(*tunable, region, base)) {
-                std::vector<std::vector<float>> outputs;
+                Readback outputs;
                 double ms = std::numeric_limits<double>::infinity();
                 try {
                     ms = timed(point, &outputs);
@@ -341,7 +339,7 @@ TuneReport Tuner::tune(const Algorithm& algorithm, const std::vector<Tensor>& in
                     continue; // a point the kernel refuses at run time
                 }
                 ++result.space_size;
-                if (ms < result.best_ms && agrees(reference, outputs)) {
+                if (ms < result.best_ms && within_rounding(reference, outputs)) {
                     result.best_ms = ms;
                     result.best_settings = detail::from_config(*tunable, point);
                 }

@@ -10,6 +10,8 @@
 #include <cstring>
 #include <fstream>
 #include <iomanip>
+#include <iterator>
+#include <optional>
 #include <regex>
 #include <sstream>
 #include <stdexcept>
@@ -24,7 +26,8 @@ namespace mensurflow::detail {
 
 namespace {
 
-thread_local TuningContext* t_context = nullptr;
+// The contexts of the calling thread's open scopes, innermost last.
+thread_local std::vector<TuningContext> t_scopes;
 
 std::string_view strip(std::string_view text) {
     const char* const blanks = " \t\r\n";
@@ -140,10 +143,13 @@ namespace {
 // One result line, "<op> <device> v<version> <key words> -> <settings> | <best> ms (default <ms>
 // ms) <mode>", taken apart by one pattern; the key is every word between the version and the
 // arrow. The error texts name the part that did not match, as the file format's readers expect.
+// As lenient as the format's first reader: the version is the number at the start of what follows
+// 'v' (so "v1x" is version 1), the mode is the first word after the timings (63 characters at
+// most) and anything after it is ignored.
 TuningEntry parse_result(const std::string& line, const std::string& machine) {
     static const std::regex whole(
         R"(^(\S+)\s+(\S+)\s+(\S+)((?:\s+\S+)*?)\s+->\s*(.*?)\s*\|\s*(.*)$)");
-    static const std::regex times(R"(^(\S+)\s+ms\s+\(default\s+(\S+)\s+ms\)\s+(\S+)$)");
+    static const std::regex times(R"(^(\S+)\s+ms\s+\(default\s+(\S+)\s+ms\)\s+(\S+).*$)");
     std::smatch part;
     if (!std::regex_match(line, part, whole)) {
         throw std::invalid_argument("expected '<op> <device> v<version> <key> -> <settings> | "
@@ -157,11 +163,7 @@ TuningEntry parse_result(const std::string& line, const std::string& machine) {
     entry.machine = machine;
     entry.op = part[1].str();
     entry.device = part[2].str();
-    std::size_t used = 0;
-    entry.version = std::stoi(version.substr(1), &used);
-    if (used + 1 != version.size()) {
-        throw std::invalid_argument("expected '<op> <device> v<version>' at the start");
-    }
+    entry.version = std::stoi(version.substr(1));
     entry.key = joined(words(part[4].str()), 0); // runs of blanks in the key count as one
     entry.config = parse_settings(part[5].str());
     const std::string tail = part[6].str();
@@ -171,7 +173,7 @@ TuningEntry parse_result(const std::string& line, const std::string& machine) {
     }
     entry.best_ms = std::stod(timing[1].str());
     entry.default_ms = std::stod(timing[2].str());
-    entry.mode = timing[3].str();
+    entry.mode = timing[3].str().substr(0, 63);
     return entry;
 }
 
@@ -271,43 +273,66 @@ void TuningCache::store(TuningEntry entry) {
 
 // ---- keys ----------------------------------------------------------------------------------------
 
+namespace {
+
+// The name of the first registered device that is not the CPU, "" when there is none.
+std::string first_accelerator_name() {
+    const Registry& registry = Registry::instance();
+    const std::vector<Device> devices = registry.devices();
+    const auto found = std::find_if(devices.begin(), devices.end(),
+                                    [](const Device& d) { return d.type != DeviceType::CPU; });
+    return found == devices.end() ? std::string() : registry.get(*found).info(found->index).name;
+}
+
+// "name=value" words joined by single spaces: the key and settings text of the results file.
+class KeyWriter {
+  public:
+    void add(const std::string& name, std::int64_t value) {
+        text_ += text_.empty() ? "" : " ";
+        text_ += name;
+        text_ += '=';
+        text_ += std::to_string(value);
+    }
+    std::string take() { return std::move(text_); }
+
+  private:
+    std::string text_;
+};
+
+} // namespace
+
+// The CPU model, then " | " and the first accelerator's name where there is one; worked out
+// once per process.
 const std::string& machine_name() {
     static const std::string name = [] {
-        std::string text = processor_name();
-        const Registry& registry = Registry::instance();
-        for (const Device& device : registry.devices()) {
-            if (device.type != DeviceType::CPU) {
-                text += " | " + registry.get(device).info(device.index).name;
-                break;
-            }
-        }
-        return text;
+        const std::string accelerator = first_accelerator_name();
+        return accelerator.empty() ? processor_name() : processor_name() + " | " + accelerator;
     }();
     return name;
 }
 
+// The tunable's key values under their names; on the CPU also the thread count, which its
+// kernels' best settings depend on.
 std::string call_key(const TunableKernel& tunable, const OpArgs& args, Device device) {
     const std::vector<std::int64_t> values = tunable.key(args);
-    TuningValues named;
-    for (std::size_t i = 0; i < std::min(values.size(), tunable.key_names.size()); ++i) {
-        named.emplace_back(tunable.key_names[i], values[i]);
+    const std::size_t named = std::min(values.size(), tunable.key_names.size());
+    KeyWriter key;
+    for (std::size_t i = 0; i < named; ++i) {
+        key.add(tunable.key_names[i], values[i]);
     }
     if (device.type == DeviceType::CPU) {
-        // The CPU's kernels split work over threads, so their best settings depend on the count.
-        named.emplace_back("threads", cpu_threads());
+        key.add("threads", cpu_threads());
     }
-    return mensurflow::to_string(named);
+    return key.take();
 }
 
+// "data=<device type> <dtype of the first input> <shape of each input>".
 std::string placement_key(const OpArgs& args, Device data_device) {
-    std::string key = "data=";
-    key += device_type_name(data_device.type);
-    key += ' ';
-    key += dtype_name(args.inputs.at(0).dtype());
-    for (const Tensor& input : args.inputs) {
-        key += ' ' + shape_words(input.shape());
-    }
-    return key;
+    std::vector<std::string> parts{std::string("data=") + device_type_name(data_device.type),
+                                   dtype_name(args.inputs.at(0).dtype())};
+    std::transform(args.inputs.begin(), args.inputs.end(), std::back_inserter(parts),
+                   [](const Tensor& input) { return shape_words(input.shape()); });
+    return joined(parts, 0);
 }
 
 TuningConfig to_config(const TunableKernel& tunable, const TuningValues& settings) {
@@ -331,43 +356,61 @@ TuningValues from_config(const TunableKernel& tunable, const TuningConfig& confi
 
 // ---- scopes and the hook -------------------------------------------------------------------------
 
-TuningScope::TuningScope(TuningContext context) : context_(context), outer_(t_context) {
-    t_context = &context_;
+TuningScope::TuningScope(TuningContext context) { t_scopes.push_back(context); }
+
+TuningScope::~TuningScope() { t_scopes.pop_back(); }
+
+bool tuning_active() { return !t_scopes.empty(); }
+
+namespace {
+
+// Where an Auto call with a stored placement runs (GPU when its "gpu" setting is nonzero); the
+// requested execution when there is no stored placement or the call is not Auto.
+Execution stored_placement(const TuningCache* results, OpId op, Execution execution,
+                           Device data_device, const OpArgs& args) {
+    if (results == nullptr || execution != Execution::Auto || args.inputs.empty()) {
+        return execution;
+    }
+    const TuningEntry* placed = results->find(machine_name(), op_name(op), kAutoDevice, 1,
+                                              placement_key(args, data_device));
+    if (placed == nullptr) {
+        return execution;
+    }
+    return setting(placed->config, "gpu", 0) != 0 ? Execution::GPU : Execution::CPU;
 }
 
-TuningScope::~TuningScope() { t_context = outer_; }
+// The stored settings of the kernel that runs `op` on `target`, if it is tunable and has any.
+std::optional<TuningConfig> stored_settings(const TuningCache* results, OpId op, Device target,
+                                            const OpArgs& args) {
+    if (results == nullptr) {
+        return std::nullopt;
+    }
+    const Tensor& first = args.inputs.empty() ? args.outputs.at(0) : args.inputs.front();
+    const TunableKernel* tunable =
+        Registry::instance().dispatcher().tunable({op, target.type, first.dtype()});
+    if (tunable == nullptr) {
+        return std::nullopt;
+    }
+    const TuningEntry* stored =
+        results->find(machine_name(), tunable->name, device_type_name(target.type),
+                      tunable->version, call_key(*tunable, args, target));
+    if (stored == nullptr) {
+        return std::nullopt;
+    }
+    return to_config(*tunable, stored->config);
+}
 
-bool tuning_active() { return t_context != nullptr; }
+} // namespace
 
 Device apply_tuning(OpId op, Execution execution, Device data_device, OpArgs& args) {
-    const TuningContext& context = *t_context;
-    const TuningCache* results = context.cache;
-    // 1. The device: a stored choice replaces Auto; everything else resolves as usual.
-    Execution resolved = execution;
-    if (results != nullptr && execution == Execution::Auto && !args.inputs.empty()) {
-        const TuningEntry* choice = results->find(machine_name(), op_name(op), kAutoDevice, 1,
-                                                  placement_key(args, data_device));
-        if (choice != nullptr) {
-            resolved = setting(choice->config, "gpu", 0) != 0 ? Execution::GPU : Execution::CPU;
-        }
-    }
-    const Device target = execution_device(resolved, data_device);
+    const TuningContext context = t_scopes.back();
+    const Device target = execution_device(
+        stored_placement(context.cache, op, execution, data_device, args), data_device);
     if (context.record != nullptr) {
         context.record->push_back(RecordedCall{op, execution, data_device, target, args});
     }
-    // 2. The settings of the kernel that runs there, when it is tunable and a result is stored.
-    if (results != nullptr) {
-        const DType dtype = (args.inputs.empty() ? args.outputs.at(0) : args.inputs[0]).dtype();
-        const TunableKernel* tunable =
-            Registry::instance().dispatcher().tunable({op, target.type, dtype});
-        if (tunable != nullptr) {
-            const TuningEntry* stored =
-                results->find(machine_name(), tunable->name, device_type_name(target.type),
-                              tunable->version, call_key(*tunable, args, target));
-            if (stored != nullptr) {
-                args.tuning = to_config(*tunable, stored->config);
-            }
-        }
+    if (const std::optional<TuningConfig> tuned = stored_settings(context.cache, op, target, args)) {
+        args.tuning = *tuned;
     }
     return target;
 }

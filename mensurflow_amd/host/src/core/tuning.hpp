@@ -78,17 +78,14 @@ struct TuningContext {
     std::vector<RecordedCall>* record = nullptr; // calls are appended here
 };
 
-// Makes `context` the calling thread's tuning context until the scope ends (scopes nest).
+// Makes `context` the calling thread's tuning context until the scope ends. Scopes nest: each
+// thread keeps a stack of the contexts of its open scopes, and the innermost one applies.
 class TuningScope {
   public:
     explicit TuningScope(TuningContext context);
     ~TuningScope();
     TuningScope(const TuningScope&) = delete;
     TuningScope& operator=(const TuningScope&) = delete;
-
-  private:
-    TuningContext context_;
-    TuningContext* outer_;
 };
 
 bool tuning_active();
