@@ -1,6 +1,7 @@
 """Builds mensurflow itself with this repository's ROCm backend wired in, and runs mensurflow's own
 test suite against it. CPU container only: it needs the reference sources, and nothing it builds
-is used by the product or leaves `--work`.
+is used by the product or leaves the work directory (`--work`; by default a fresh temporary
+directory outside the repository, removed at the end).
 
 Steps:
   1. copy the reference tree (without .git) to <work>/tree;
@@ -20,7 +21,7 @@ so the suite checks that the wiring compiles, links and leaves the CPU path as i
 gfx950 device the device-generic tests run on rocm:0 too.
 
 Usage: python mensurflow_amd/host/integration/check_in_reference.py [--reference DIR]
-       [--work DIR] [--jobs N]
+       [--work DIR] [--keep] [--jobs N]
 """
 from __future__ import annotations
 
@@ -32,6 +33,7 @@ import shutil
 import subprocess
 import sys
 import tarfile
+import tempfile
 import time
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -83,7 +85,9 @@ def run(cmd: list[str], cwd: str, what: str) -> str:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--reference", default="/root/reference")
-    ap.add_argument("--work", default=os.path.join(REPO, "_work", "refdrop"))
+    ap.add_argument("--work", default=None,
+                    help="work directory (default: a temporary directory, removed afterwards)")
+    ap.add_argument("--keep", action="store_true", help="keep the temporary work directory")
     ap.add_argument("--jobs", type=int, default=min(8, os.cpu_count() or 1))
     ap.add_argument("--test-timeout", type=int, default=600)
     args = ap.parse_args()
@@ -93,9 +97,19 @@ def main() -> int:
     if not os.path.exists(os.path.join(LIBDIR, "libmfr_rocm.so")):
         log("mensurflow_amd/_lib/libmfr_rocm.so is missing: build it first (python -m mensurflow_amd.build)")
         return 2
+    temporary = args.work is None
+    work = tempfile.mkdtemp(prefix="mfr_refdrop_") if temporary else args.work
+    try:
+        return check(args, work)
+    finally:
+        if temporary and not args.keep:
+            shutil.rmtree(work, ignore_errors=True)
+
+
+def check(args: argparse.Namespace, work: str) -> int:
     start = time.time()
-    tree = os.path.join(args.work, "tree")
-    build = os.path.join(args.work, "build")
+    tree = os.path.join(work, "tree")
+    build = os.path.join(work, "build")
     log(f"[1/5] copying {args.reference} -> {tree}")
     copy_tree(args.reference, tree)
     log("[2/5] applying rocm_wiring.patch")
