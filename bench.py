@@ -464,13 +464,15 @@ def main() -> int:
             "composed_timing_ms": spread(att["total"]),
             "composed_qk_gemm_tflops": round(tflops_of(att["gemm_flops"], att["qk"]), 2),
             "composed_qk_timing_ms": spread(att["qk"]),
+            "composed_qk_traffic": load_traffic("attention_scores_panel"),
             "composed_pv_gemm_tflops": round(tflops_of(att["gemm_flops"], att["pv"]), 2),
             "composed_pv_timing_ms": spread(att["pv"]),
+            "composed_pv_traffic": load_traffic("attention_pv_pair"),
             "composed_softmax_gbs": round(2 * att["scores_bytes"] / (att["softmax"]["event_ms"]
                                                                    * 1e-3) / 1e9, 1),
             "note": "fused: one kernel, online softmax, FLOP = 4*B*H*D*S(S+1)/2 (causal pairs); "
                     "composed: the reference's 2 batched GEMMs (4*B*H*S^2*D FLOP, dense; the "
-                    "scores q k^T on the panel path), where (the [S, S] causal mask and a -inf "
+                    "scores q k^T on the panel path, P V on the paired 128x64 kernel), where (the [S, S] causal mask and a -inf "
                     "scalar read through broadcast views, the scores masked in place: only the "
                     "removed keys' -inf is written), softmax over the materialized scores; its "
                     "ms_per_call is host wall time per call (median of one-call samples), with "
