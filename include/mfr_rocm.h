@@ -151,8 +151,15 @@ typedef struct mfr_gemm_desc {
     int32_t tile;                             /* MFR_TILE_AUTO or a fixed MFR_TILE_* */
     int32_t stage;                            /* MFR_STAGE_* */
     int32_t splits;                           /* 0 = AUTO, or 1 .. MFR_MAX_SPLITS depth ranges */
-    int32_t reserved;                         /* must be 0 */
+    int32_t flags;                            /* 0 or MFR_GEMM_CAUSAL */
 } mfr_gemm_desc;
+
+/* mfr_gemm_desc.flags. MFR_GEMM_CAUSAL: in every batch matrix, C(i, j) = -inf wherever j > i (the
+ * top-left causal mask of attention's scores, as where(keep, scores, -inf) with keep(i, j) =
+ * j <= i writes them: src/ops/attention.cpp:85-96), and those outputs are not computed; the rest
+ * as without the flag. Only the panel path takes it (MFR_TILE_PANEL, or AUTO where the panel
+ * path fits); anything else is MFR_E_UNSUPPORTED. */
+enum { MFR_GEMM_CAUSAL = 1 };
 
 /* Operand staging of mfr_sgemm. The fast loads read 4 floats at once, which needs an operand's
  * unit-stride extent and its other strides to be multiples of 4 and its base 16-byte aligned

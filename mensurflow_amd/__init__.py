@@ -307,7 +307,7 @@ def _fill_batch(field, values, dims):
 
 def gemm_batched(a: DeviceArray, b: DeviceArray, c: DeviceArray, *, alpha=1.0,
                  c0: DeviceArray | None = None, beta=0.0, bias: DeviceArray | None = None,
-                 act=ACT_NONE, tile=0, stage=0, splits=0) -> None:
+                 act=ACT_NONE, tile=0, stage=0, splits=0, causal=False) -> None:
     """c[...] = act(alpha*a@b + beta*c0 + bias) over the leading (batch) dimensions.
 
     a is [..., m, k], b is [..., k, n] (any strides with a unit stride in one matrix dimension;
@@ -315,18 +315,22 @@ def gemm_batched(a: DeviceArray, b: DeviceArray, c: DeviceArray, *, alpha=1.0,
     must already agree (expand them first). tile is an abi.TILE_* value, stage an abi.STAGE_*
     value (copy operands that 16-byte loads cannot read into an aligned workspace first), splits
     the number of depth ranges (0 = automatic, 1 = none; split-K, abi.MAX_SPLITS at most).
+    causal: c[..., i, j] = -inf wherever j > i (abi.GEMM_CAUSAL, attention's scores); only the
+    panel path takes it, NotImplementedError elsewhere.
     """
-    sgemm(c.stream, _gemm_desc(a, b, c, alpha, c0, beta, bias, act, tile, stage, splits))
+    sgemm(c.stream, _gemm_desc(a, b, c, alpha, c0, beta, bias, act, tile, stage, splits,
+                               causal))
 
 
 def gemm_plan(a: DeviceArray, b: DeviceArray, c: DeviceArray, *, tile=0, stage=0, splits=0,
-              c0: DeviceArray | None = None, beta=0.0) -> tuple[int, int, int, int]:
+              c0: DeviceArray | None = None, beta=0.0,
+              causal=False) -> tuple[int, int, int, int]:
     """(tile, stage, splits, regions) that gemm_batched(a, b, c, ...) would run with
     (mfr_sgemm_plan): AUTO resolved to a fixed tile, stage reported as STAGE_ALWAYS (operands
     copied first) or STAGE_NEVER, splits the depth ranges (1 = no split) -- both of the main
     region -- and regions the output rectangles launched separately (more than 1 when AUTO peels
     edge strips). Raises as gemm_batched would for a point that cannot run."""
-    d = _gemm_desc(a, b, c, 1.0, c0, beta, None, ACT_NONE, tile, stage, splits)
+    d = _gemm_desc(a, b, c, 1.0, c0, beta, None, ACT_NONE, tile, stage, splits, causal)
     t, st, sp, rg = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
     abi.check(abi.load().mfr_sgemm_plan(c.stream.device, ctypes.byref(d), ctypes.byref(t),
                                         ctypes.byref(st), ctypes.byref(sp), ctypes.byref(rg)),
@@ -334,7 +338,8 @@ def gemm_plan(a: DeviceArray, b: DeviceArray, c: DeviceArray, *, tile=0, stage=0
     return t.value, st.value, sp.value, rg.value
 
 
-def _gemm_desc(a, b, c, alpha, c0, beta, bias, act, tile, stage, splits=0) -> GemmDesc:
+def _gemm_desc(a, b, c, alpha, c0, beta, bias, act, tile, stage, splits=0,
+               causal=False) -> GemmDesc:
     m, k = a.shape[-2:]
     k2, n = b.shape[-2:]
     if k != k2:
@@ -372,6 +377,7 @@ def _gemm_desc(a, b, c, alpha, c0, beta, bias, act, tile, stage, splits=0) -> Ge
     d.tile = tile
     d.stage = stage
     d.splits = splits
+    d.flags = abi.GEMM_CAUSAL if causal else 0
     return d
 
 
@@ -562,9 +568,11 @@ def attention_composed(q: DeviceArray, k: DeviceArray, v: DeviceArray,
     gemm_batched(q, k^T, alpha=scale), where(mask, scores, -inf) with the mask and the -inf
     scalar read through broadcast views (mfr_where_nd; mensurflow::where packs them to the
     scores' shape), the causal mask the same way, softmax over the keys, gemm_batched(weights,
-    v). q [..., Lq, D], k [..., Lk, D], v [..., Lk, Dv] with equal batch shapes; mask a Bool
-    (uint8) array broadcastable to [..., Lq, Lk]. Every array is on q's stream; the scores are
-    that stream's scratch array, reused by later calls."""
+    v). The causal mask is the scores GEMM's own (causal=True: the same bits as the where over
+    the lower triangle, without the pass over the scores) where the GEMM takes it, the where
+    otherwise. q [..., Lq, D], k [..., Lk, D], v [..., Lk, Dv] with equal batch shapes; mask a
+    Bool (uint8) array broadcastable to [..., Lq, Lk]. Every array is on q's stream; the scores
+    are that stream's scratch array, reused by later calls."""
     stream = q.stream
     lq, depth = q.shape[-2:]
     lk = k.shape[-2]
@@ -572,7 +580,15 @@ def attention_composed(q: DeviceArray, k: DeviceArray, v: DeviceArray,
     if scale == 0.0:
         scale = float(np.float32(1.0 / np.sqrt(depth))) if depth > 0 else 1.0
     scores = stream.scratch("attention.scores", batch + (lq, lk))
-    gemm_batched(q, k.transpose(-2, -1), scores, alpha=scale)
+    causal_done = False
+    if causal:
+        try:
+            gemm_batched(q, k.transpose(-2, -1), scores, alpha=scale, causal=True)
+            causal_done = True
+        except NotImplementedError:
+            pass
+    if not causal_done:
+        gemm_batched(q, k.transpose(-2, -1), scores, alpha=scale)
     minus_inf = None
 
     def masked(keep: DeviceArray) -> DeviceArray:
@@ -585,7 +601,7 @@ def attention_composed(q: DeviceArray, k: DeviceArray, v: DeviceArray,
 
     if mask is not None:
         masked(mask)
-    if causal:
+    if causal and not causal_done:
         # The [Lq, Lk] lower triangle, kept on the stream until a call needs another shape.
         lower = stream._scratch.get("attention.causal")
         if lower is None or lower.shape != (lq, lk):

@@ -36,6 +36,7 @@ TILE_64x64 = 5
 TILE_THIN = 6
 TILE_PANEL = 7
 TILE_COUNT = 8
+GEMM_CAUSAL = 1  # mfr_gemm_desc.flags: C(i, j) = -inf wherever j > i (panel path only)
 STAGE_AUTO = 0
 STAGE_NEVER = 1
 STAGE_ALWAYS = 2
@@ -65,7 +66,7 @@ class GemmDesc(ctypes.Structure):
         ("c0", _vp), ("c0_rs", _i64), ("c0_bs", _i64 * MAX_BATCH_DIMS),
         ("bias", _vp),
         ("alpha", _f32), ("beta", _f32),
-        ("tile", _i32), ("stage", _i32), ("splits", _i32), ("reserved", _i32),
+        ("tile", _i32), ("stage", _i32), ("splits", _i32), ("flags", _i32),
     ]
 
 

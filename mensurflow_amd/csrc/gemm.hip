@@ -709,7 +709,7 @@ Plan plan_sgemm(const mfr_gemm_desc& d, int cus) {
     require(d.stage == MFR_STAGE_AUTO || d.stage == MFR_STAGE_NEVER || d.stage == MFR_STAGE_ALWAYS,
             "sgemm: unknown stage mode");
     require(d.splits >= 0 && d.splits <= kMaxSplits, "sgemm: splits out of range");
-    require(d.reserved == 0, "sgemm: reserved field not 0");
+    require(d.flags == 0 || d.flags == MFR_GEMM_CAUSAL, "sgemm: unknown flags");
     Plan plan;
     GemmParams& p = plan.p;
     int64_t batch_count = 1;
@@ -749,6 +749,7 @@ Plan plan_sgemm(const mfr_gemm_desc& d, int cus) {
     p.alpha = d.alpha;
     p.beta = d.beta;
     p.batch_count = batch_count;
+    p.causal = d.flags == MFR_GEMM_CAUSAL ? 1 : 0;
     if (p.beta != 0.0f && p.c0 != nullptr) {
         require(p.m == 1 || p.c0_rs >= p.n, "sgemm: c0 row stride smaller than n");
     }
@@ -799,7 +800,11 @@ Plan plan_sgemm(const mfr_gemm_desc& d, int cus) {
     }
     plan.c0 = p.c0 != nullptr && p.beta != 0.0f;
     const auto tile_plan = [&](Plan& q) {
-        if (d.tile == MFR_TILE_PANEL ||
+        if (p.causal != 0 && !(d.tile == MFR_TILE_PANEL || d.tile == MFR_TILE_AUTO)) {
+            throw mfr::Error(MFR_E_UNSUPPORTED,
+                             "sgemm: the causal mask is taken by the panel path only");
+        }
+        if (d.tile == MFR_TILE_PANEL || p.causal != 0 ||
             (d.tile == MFR_TILE_AUTO && d.splits <= 1 && panel_preferred(q))) {
             if (!panel_fits(q) || d.splits > 1) {
                 throw mfr::Error(MFR_E_UNSUPPORTED,
@@ -1119,7 +1124,7 @@ PlanKey plan_key(const mfr_gemm_desc& d, int cus) {
     put(d.tile);
     put(d.stage);
     put(d.splits);
-    put(d.reserved);
+    put(d.flags);
     put((d.a == nullptr ? 1 : 0) | (d.b == nullptr ? 2 : 0) | (d.c == nullptr ? 4 : 0) |
         (d.c0 == nullptr ? 8 : 0) | (d.beta != 0.0f ? 16 : 0) | (mfr::aligned16(d.a) ? 32 : 0) |
         (mfr::aligned16(d.b) ? 64 : 0));

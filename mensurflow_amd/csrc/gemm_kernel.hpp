@@ -43,6 +43,8 @@ struct GemmParams {
     // an activation. Set for outputs larger than the last-level cache whose rows all start on
     // 128-byte lines (partial lines would be merged in L2 otherwise).
     int32_t stream_c;
+    // Nonzero: C(i, j) = -inf for j > i in every batch matrix (MFR_GEMM_CAUSAL; panel path only).
+    int32_t causal;
 };
 
 // Global -> register -> LDS copy of one operand slice: ROWS rows (M for A, N for B) by KT depth.

@@ -3,6 +3,25 @@
 
 namespace mfr::gemm {
 
+namespace {
+
+// The kernel for depth groups KG with non-temporal stores or not, and the full epilogue (beta *
+// C0, bias) or alpha alone.
+template <int KG>
+void launch_depth(bool nt, bool full, unsigned grid, const PanelParams& pp, hipStream_t stream) {
+    if (nt && full) {
+        sgemm_panel_kernel<KG, true, true><<<grid, kPanelThreads, 0, stream>>>(pp);
+    } else if (nt) {
+        sgemm_panel_kernel<KG, true, false><<<grid, kPanelThreads, 0, stream>>>(pp);
+    } else if (full) {
+        sgemm_panel_kernel<KG, false, true><<<grid, kPanelThreads, 0, stream>>>(pp);
+    } else {
+        sgemm_panel_kernel<KG, false, false><<<grid, kPanelThreads, 0, stream>>>(pp);
+    }
+}
+
+} // namespace
+
 // The panel path on q: row panels of kPanelRows, column tiles of kPanelCols, and the tiles of
 // each panel cut into ranges (workgroups of their own) until the grid holds at least two
 // workgroups per CU. nt: non-temporal stores.
@@ -26,22 +45,13 @@ void launch_panel(const GemmParams& q, bool nt, int cus, hipStream_t stream) {
     pp.chunks = static_cast<int32_t>(chunks);
     pp.per_chunk = static_cast<int32_t>(per_chunk);
     const unsigned grid = static_cast<unsigned>(blocks);
+    const bool full = (q.c0 != nullptr && q.beta != 0.0f) || q.bias != nullptr;
     if (q.k <= 16) {
-        if (nt) {
-            sgemm_panel_kernel<2, true><<<grid, kPanelThreads, 0, stream>>>(pp);
-        } else {
-            sgemm_panel_kernel<2, false><<<grid, kPanelThreads, 0, stream>>>(pp);
-        }
+        launch_depth<2>(nt, full, grid, pp, stream);
     } else if (q.k <= 32) {
-        if (nt) {
-            sgemm_panel_kernel<4, true><<<grid, kPanelThreads, 0, stream>>>(pp);
-        } else {
-            sgemm_panel_kernel<4, false><<<grid, kPanelThreads, 0, stream>>>(pp);
-        }
-    } else if (nt) {
-        sgemm_panel_kernel<8, true><<<grid, kPanelThreads, 0, stream>>>(pp);
+        launch_depth<4>(nt, full, grid, pp, stream);
     } else {
-        sgemm_panel_kernel<8, false><<<grid, kPanelThreads, 0, stream>>>(pp);
+        launch_depth<8>(nt, full, grid, pp, stream);
     }
 }
 

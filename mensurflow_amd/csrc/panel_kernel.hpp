@@ -24,10 +24,16 @@
 //     columns (config 5's scores, store-only: 136 -> 110 us).
 //   - Rows past m are dropped by the store resource's record count (it ends at row m); columns
 //     past n get an offset past it; depths past k and B rows past n load as zeros.
-// Measured on config 5's scores (one MI355X): 161-173 us against 204-216 us for the 128x64 tile,
-// bit for bit the same. The rest is the power limit: under MFMA work and the 512 MiB store
-// stream together the clock drops to ~1.94 GHz (2.21 GHz with the stores taken out, where the
-// same loop runs in 124-129 us), and at 1.94 GHz the MFMA work alone takes 135 us.
+//   - Under the causal flag (MFR_GEMM_CAUSAL, attention's scores) every output with column > row
+//     is -inf, and a wavefront's 32 x 64 block that lies wholly above the diagonal skips its
+//     MFMAs (about half of config 5's scores).
+//   - The scores' form (alpha and the mask only) fits 126 VGPRs: 4 wavefronts per SIMD, two
+//     workgroups per CU; with beta * C0 or a bias (FULL) 2.
+// Measured on config 5's scores (one MI355X): 151-161 us against 204-216 us for the 128x64 tile,
+// bit for bit the same (165-173 us with 2 wavefronts per SIMD); 147 us under the causal mask.
+// The rest is the power limit: under MFMA work and the 512 MiB store stream together the clock
+// drops to ~1.94 GHz (2.21 GHz with the stores taken out, where the same loop runs in 124-129
+// us), and at 1.94 GHz the MFMA work alone takes 135 us.
 #pragma once
 
 #include "gemm_kernel.hpp"
@@ -53,9 +59,13 @@ struct PanelParams {
 };
 
 // s_waitcnt with vmcnt N and the other counters left alone (gfx9 encoding: vmcnt bits 3:0 and
-// 15:14, expcnt 6:4, lgkmcnt 11:8).
+// 15:14, expcnt 6:4, lgkmcnt 11:8). The count is of the vector memory operations issued before
+// it, so none of them may be moved past it: the empty asm statement keeps the compiler from
+// sinking the tile's stores below the wait (which would let the wait pass before the LDS copy it
+// is there for had landed).
 template <int N> __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
@@ -69,9 +79,11 @@ __device__ __forceinline__ void bare_barrier() {
 }
 
 // KG: 8-deep depth groups held (k <= 8 KG). NT: non-temporal stores (outputs larger than the
-// last-level cache whose rows start on 128-byte lines).
-template <int KG, bool NT>
-__global__ __launch_bounds__(kPanelThreads) void sgemm_panel_kernel(PanelParams pp) {
+// last-level cache whose rows start on 128-byte lines). FULL: the epilogue with beta * C0 and a
+// bias; without it (the scores' case) only alpha and the causal mask, in the store loop itself,
+// which keeps the kernel at 4 wavefronts per SIMD.
+template <int KG, bool NT, bool FULL>
+__global__ __launch_bounds__(kPanelThreads, FULL ? 2 : 4) void sgemm_panel_kernel(PanelParams pp) {
     const GemmParams& p = pp.g;
     constexpr int KT = 8 * KG;
     constexpr int PITCH = KT + 4;               // LDS row pitch: the tile kernels' K-major image
@@ -189,7 +201,9 @@ __global__ __launch_bounds__(kPanelThreads) void sgemm_panel_kernel(PanelParams 
     const float beta = p.beta;
     const float* const bias = p.bias;
 
+    const bool causal = p.causal != 0;
     const auto compute_store = [&](const float* tile, int i) {
+        const int64_t n0 = static_cast<int64_t>(col_tile(i)) * kPanelCols;
         floatx16 acc[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
@@ -198,26 +212,31 @@ __global__ __launch_bounds__(kPanelThreads) void sgemm_panel_kernel(PanelParams 
                 acc[j][e] = 0.0f;
             }
         }
+        // Under the causal mask a block whose first column is past its last row is all -inf:
+        // its products are not computed (uniform over the wavefront).
+        const bool computed = !causal || n0 <= row0 + 31;
         const float* frag = tile + r32 * PITCH + 4 * half;
+        if (computed) {
 #pragma unroll
-        for (int g = 0; g < KG; ++g) {
-            float4 bf[2];
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                bf[j] = *reinterpret_cast<const float4*>(frag + 32 * j * PITCH + 8 * g);
-            }
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const float av = s == 0 ? af[g].x : s == 1 ? af[g].y : s == 2 ? af[g].z : af[g].w;
+            for (int g = 0; g < KG; ++g) {
+                float4 bf[2];
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const float bv =
-                        s == 0 ? bf[j].x : s == 1 ? bf[j].y : s == 2 ? bf[j].z : bf[j].w;
-                    acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc[j], 0, 0, 0);
+                    bf[j] = *reinterpret_cast<const float4*>(frag + 32 * j * PITCH + 8 * g);
+                }
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const float av =
+                        s == 0 ? af[g].x : s == 1 ? af[g].y : s == 2 ? af[g].z : af[g].w;
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const float bv =
+                            s == 0 ? bf[j].x : s == 1 ? bf[j].y : s == 2 ? bf[j].z : bf[j].w;
+                        acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc[j], 0, 0, 0);
+                    }
                 }
             }
         }
-        const int64_t n0 = static_cast<int64_t>(col_tile(i)) * kPanelCols;
         // One resource per tile at (row0, n0) whose record count ends at row m (rows past m are
         // dropped); columns past n get kPanelLimit, which stays past the record count after any
         // row step (the host keeps (m + 32) * c_rs * 4 below 2^31).
@@ -225,66 +244,97 @@ __global__ __launch_bounds__(kPanelThreads) void sgemm_panel_kernel(PanelParams 
         const __amdgpu_buffer_rsrc_t c_rsrc = __builtin_amdgcn_make_buffer_rsrc(
             c_mat + row0 * p.c_rs + n0, 0, static_cast<int>(records > 0 ? records * 4 : 0),
             kBufferWord3);
-        uint32_t col_ok[2];
+        // Each lane's offset of row row0 + 4 half and its column of block j, or past the record
+        // count when that column is past n (rows then step by multiples of the row stride; the
+        // per-tile value keeps the compiler from holding 32 invariant sums in registers).
+        uint32_t col_c[2], col_c0[2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            col_ok[j] = n0 + 32 * j + r32 < p.n ? 0u : kPanelLimit;
+            const uint32_t outside = n0 + 32 * j + r32 < p.n ? 0u : kPanelLimit;
+            col_c[j] = (lane_c + 128u * j) | outside;
+            col_c0[j] = (lane_c0 + 128u * j) | outside;
         }
-        float bias_of[2] = {-0.0f, -0.0f}; // x + -0 is x: no bias adds nothing
-        if (bias != nullptr) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int64_t col = n0 + 32 * j + r32;
-                bias_of[j] = col < p.n ? bias[col] : 0.0f;
-            }
-        }
-        float v[2][16];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        // -inf where column > row under the causal mask: column n0 + 32 j + r32, row row0 +
+        // 4 half + dr(e), i.e. where 32 j + r32 - 4 half - dr(e) > row0 - n0 (clamped: the left
+        // side lies in [-35, 63]). The value's own arithmetic is kept for the rest, so the bits
+        // are those of where(keep, scores, -inf).
+        const int64_t gap = row0 - n0;
+        const int limit = !causal ? 64 : static_cast<int>(gap < -64 ? -64 : gap > 64 ? 64 : gap);
+        const auto masked = [&](int j, int e) {
+            return 32 * j + r32 - 4 * half - (8 * (e / 4) + e % 4) > limit;
+        };
+        const auto store = [&](int j, int e, float out) {
+            const uint32_t step = static_cast<uint32_t>(8 * (e / 4) + e % 4) * c_rs4;
+            const uint32_t off = col_c[j] + step;
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out), c_rsrc,
+                                                  static_cast<int>(off), 0, NT ? 2 : 0);
+        };
+        if constexpr (!FULL) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                v[j][e] = alpha * acc[j][e];
-            }
-        }
-        if (c0_mat != nullptr) {
-            // All 32 C0 values are loaded before any is used (and before any store: C0 may be C).
-            const int64_t records0 = (p.m - row0) * p.c0_rs - n0;
-            const __amdgpu_buffer_rsrc_t c0_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<float*>(c0_mat + row0 * p.c0_rs + n0), 0,
-                static_cast<int>(records0 > 0 ? records0 * 4 : 0), kBufferWord3);
-            float c0v[2][16];
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const uint32_t step = static_cast<uint32_t>(8 * (e / 4) + e % 4) * c0_rs4;
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
-                    const uint32_t off = (lane_c0 + 128u * j + step) | col_ok[j];
-                    c0v[j][e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                        c0_rsrc, static_cast<int>(off), 0, 0));
+                    const float out = alpha * acc[j][e];
+                    store(j, e, masked(j, e) ? -INFINITY : out);
                 }
             }
+        } else {
+            float bias_of[2] = {-0.0f, -0.0f}; // x + -0 is x: no bias adds nothing
+            if (bias != nullptr) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int64_t col = n0 + 32 * j + r32;
+                    bias_of[j] = col < p.n ? bias[col] : 0.0f;
+                }
+            }
+            float v[2][16];
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    const float scaled = beta * c0v[j][e];
-                    v[j][e] = v[j][e] + scaled;
+                    v[j][e] = alpha * acc[j][e];
                 }
             }
-        }
+            if (c0_mat != nullptr) {
+                // All 32 C0 values are loaded before any is used (and before any store: C0 may
+                // be C).
+                const int64_t records0 = (p.m - row0) * p.c0_rs - n0;
+                const __amdgpu_buffer_rsrc_t c0_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+                    const_cast<float*>(c0_mat + row0 * p.c0_rs + n0), 0,
+                    static_cast<int>(records0 > 0 ? records0 * 4 : 0), kBufferWord3);
+                float c0v[2][16];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const uint32_t step = static_cast<uint32_t>(8 * (e / 4) + e % 4) * c_rs4;
+                for (int e = 0; e < 16; ++e) {
+                    const uint32_t step = static_cast<uint32_t>(8 * (e / 4) + e % 4) * c0_rs4;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const float out = v[j][e] + bias_of[j];
-                const uint32_t off = (lane_c + 128u * j + step) | col_ok[j];
-                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, out), c_rsrc,
-                                                      static_cast<int>(off), 0, NT ? 2 : 0);
+                    for (int j = 0; j < 2; ++j) {
+                        const uint32_t off = col_c0[j] + step;
+                        c0v[j][e] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                            c0_rsrc, static_cast<int>(off), 0, 0));
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const float scaled = beta * c0v[j][e];
+                        v[j][e] = v[j][e] + scaled;
+                    }
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const float out = v[j][e] + bias_of[j];
+                    store(j, e, masked(j, e) ? -INFINITY : out);
+                }
             }
         }
     };
 
+    // The first tile is read by every wavefront and copied by all of them: all copies (and this
+    // wavefront's A fragments) land before the walk starts.
     wait_vmcnt<0>();
     bare_barrier();
     // The walk, unrolled by two so each half names its buffers. Before each barrier: this

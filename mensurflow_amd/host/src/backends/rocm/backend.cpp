@@ -334,6 +334,7 @@ BatchedCall batched_desc(const OpArgs& args, const Tensor& a, const Tensor& b) {
         d.c0_bs[i] = dim.c0;
     }
     call.outer.assign(dims.begin(), dims.begin() + static_cast<std::ptrdiff_t>(outer));
+    d.flags = args.causal ? MFR_GEMM_CAUSAL : 0;
     apply_tuning(d, args.tuning);
     return call;
 }

@@ -91,7 +91,9 @@ struct OpArgs {
     // last input is the bias vector.
     int activation = 0;
     bool has_bias = false;
-    // Attention: causal masking, and whether the last input is a Bool mask.
+    // Attention: causal masking, and whether the last input is a Bool mask. GemmBatched (the
+    // ROCm kernel only, which attention's composition alone sends it to): out(..., i, j) = -inf
+    // wherever j > i; a layout the kernel cannot mask throws NotImplemented.
     bool causal = false;
     bool has_mask = false;
     TuningConfig tuning{}; // filled by dispatch() from an active tuning scope

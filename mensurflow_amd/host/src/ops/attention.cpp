@@ -3,7 +3,8 @@
 // execution device has a fused kernel (OpId::Attention) the op is that one dispatch; a layout the
 // kernel does not take (it throws NotImplemented), or a device without one, runs mensurflow's
 // composition: a batched GEMM for the scaled scores, where() with -inf for removed keys, softmax
-// over the keys, and a batched GEMM with v.
+// over the keys, and a batched GEMM with v. On ROCm the causal -inf comes from the scores GEMM
+// itself where it takes it (the same bits, without a pass over the scores).
 #include "mensurflow/ops/attention.hpp"
 
 #include "core/dispatcher.hpp"
@@ -101,6 +102,36 @@ Tensor causal_keep(std::int64_t lq, std::int64_t lk, Device device) {
     return Tensor::from_host(keep.data(), {lq, lk}, DType::Bool, device);
 }
 
+// The scaled scores q k^T with -inf above the diagonal, written by the ROCm batched GEMM's
+// causal epilogue (OpArgs::causal), when the scores GEMM runs on ROCm; undefined when it runs
+// elsewhere or the kernel does not take the layout (the composition then masks with where()).
+Tensor causal_scores(const Tensor& q, const Tensor& k, const Shape& batch, float scale,
+                     Execution execution) {
+    Device target;
+    try {
+        target = detail::execution_device(execution, q.device());
+    } catch (const std::exception&) {
+        return Tensor();
+    }
+    if (target.type != DeviceType::ROCm || target != q.device()) {
+        return Tensor();
+    }
+    const std::int64_t lq = q.size(-2), lk = k.size(-2), d = q.size(-1);
+    OpArgs args;
+    args.inputs = {q.expand(matrix_shape(batch, lq, d)),
+                   k.transpose(-2, -1).expand(matrix_shape(batch, d, lk))};
+    args.outputs = {Tensor::empty(matrix_shape(batch, lq, lk), DType::F32, q.device())};
+    args.alpha = scale;
+    args.beta = 0.0f;
+    args.causal = true;
+    try {
+        detail::dispatch(OpId::GemmBatched, args, execution);
+    } catch (const detail::NotImplemented&) {
+        return Tensor();
+    }
+    return args.outputs.front();
+}
+
 } // namespace
 
 Tensor attention(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor* mask, bool causal,
@@ -150,11 +181,18 @@ Tensor attention(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor
         }
     }
     // The composition: the scaled scores come from the GEMM's alpha.
-    const Tensor scores = gemm_strided_batched(q, k, scale, nullptr, 0.0f, false, true, execution);
+    Tensor scores;
+    if (causal && numel(scores_shape) > 0 && depth > 0) {
+        scores = causal_scores(q, k, score_batch, scale, execution);
+    }
+    const bool causal_done = scores.defined();
+    if (!causal_done) {
+        scores = gemm_strided_batched(q, k, scale, nullptr, 0.0f, false, true, execution);
+    }
     if (mask != nullptr) {
         drop_where_not(*mask, scores, execution);
     }
-    if (causal) {
+    if (causal && !causal_done) {
         drop_where_not(causal_keep(lq, lk, q.device()), scores, execution);
     }
     const Tensor weights = softmax(scores, -1, execution);

@@ -78,6 +78,22 @@ void test_attention(Device device) {
             }
         }
     }
+    // The causal flag and the same lower triangle passed as a mask give the same bits (dv != d,
+    // so both compose; on rocm the first takes its -inf from the scores GEMM, the second from
+    // where()). With the mask as well, the two masks combine in either order.
+    std::vector<std::uint8_t> lower(static_cast<std::size_t>(lq * lk));
+    for (std::int64_t i = 0; i < lq; ++i) {
+        for (std::int64_t j = 0; j < lk; ++j) {
+            const bool kept = j <= i && keep[static_cast<std::size_t>((1 * lq + i) * lk + j)] != 0;
+            lower[static_cast<std::size_t>(i * lk + j)] = kept ? 1 : 0;
+        }
+    }
+    const Tensor tril = Tensor::from_host(lower.data(), {lq, lk}, DType::Bool, device);
+    const Tensor batch1_mask = mask.slice(0, 1, 2);
+    const auto flag = attention(q, k, v, &batch1_mask, true, 0.0f, on).to_vector<float>();
+    const auto given = attention(q, k, v, &tril, false, 0.0f, on).to_vector<float>();
+    test::require(std::memcmp(flag.data(), given.data(), flag.size() * sizeof(float)) == 0,
+                  "causal flag and lower-triangle mask agree bit for bit");
 }
 
 // d = 64: the fused kernel on rocm (the composition elsewhere), with ragged lengths around its

@@ -423,6 +423,102 @@ def test_panel_refusals(stream, case):
     assert np.all(c.numpy() == POISON)
 
 
+# ---- the causal flag (attention's scores, MFR_GEMM_CAUSAL) --------------------------------------
+
+def causal_where(x):
+    """where(keep, x, -inf) with keep(i, j) = j <= i over the last two dimensions (the reference's
+    top-left causal mask, src/ops/attention.cpp:85-96)."""
+    rows, cols = x.shape[-2:]
+    keep = np.tril(np.ones((rows, cols), bool))
+    return np.where(keep, x, np.float32(-np.inf)).astype(np.float32)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 4), (1, 300, 64), (64, 64, 4), (255, 63, 64),
+                                   (256, 64, 64), (300, 200, 40), (513, 700, 20), (200, 900, 64),
+                                   (900, 200, 8), (1024, 1024, 64), (2100, 1100, 60)])
+def test_exact_causal_panel(stream, m, n, k):
+    """-inf wherever column > row and the exact product elsewhere, with blocks wholly above the
+    diagonal skipped and blocks across it masked lane by lane: bits equal where(tril, product,
+    -inf), AUTO takes the flag to the panel path, and the guard bands survive."""
+    a = quarter_matrix(m, k, 151)
+    bt = quarter_matrix(n, k, 152)
+    a_d, b_d = dev(a, stream), dev(bt, stream).T
+    want = causal_where((np.float32(0.75) * exact_product(a, bt.T)).astype(np.float32))
+    for tile in (0, PANEL):
+        c, buf = guarded_output(stream, (m, n))
+        assert mf.gemm_plan(a_d, b_d, c, tile=tile, causal=True)[0] == PANEL
+        mf.gemm_batched(a_d, b_d, c, alpha=0.75, tile=tile, causal=True)
+        assert same_bits(c.numpy(), want), f"{m}x{n}x{k} tile {tile}"
+        check_guards(buf)
+
+
+def test_causal_panel_batched_with_epilogue(stream):
+    """Two broadcast batch dimensions, a padded output row stride, beta * C0 and a bias: the mask
+    applies after the epilogue (the masked outputs are -inf whatever C0 and the bias hold)."""
+    bsz, heads, m, n, k = 2, 3, 300, 280, 32
+    a = quarter_matrix(bsz * m, k, 161).reshape(bsz, 1, m, k)
+    bt = quarter_matrix(heads * n, k, 162).reshape(1, heads, n, k)
+    c0 = quarter_matrix(bsz * heads * m, n, 163).reshape(bsz, heads, m, n)
+    bias = quarter_matrix(1, n, 164)[0]
+    a_d = dev(a, stream).expand((bsz, heads, m, k))
+    b_d = dev(bt, stream).expand((bsz, heads, n, k)).transpose(-2, -1)
+    wide = mf.DeviceArray.empty((bsz, heads, m, n + 12), stream)
+    mf.fill(wide, POISON)
+    out = wide.slice(-1, 0, n)
+    mf.gemm_batched(a_d, b_d, out, alpha=0.5, c0=dev(c0, stream), beta=2.0,
+                    bias=dev(bias, stream), causal=True)
+    got = wide.numpy()
+    assert np.all(got[..., n:] == POISON)
+    for i in range(bsz):
+        for h in range(heads):
+            pre = ((np.float32(0.5) * exact_product(a[i, 0], bt[0, h].T)) +
+                   np.float32(2.0) * c0[i, h] + bias).astype(np.float32)
+            assert same_bits(got[i, h, :, :n], causal_where(pre)), (i, h)
+
+
+def test_causal_matches_plain_then_where(stream, oracle):
+    """Realistic inputs at attention's shape: the causal product is bit for bit the plain panel
+    product followed by where(tril, scores, -inf), the composition's own steps."""
+    bsz, m, n, k = 4, 1024, 1024, 64
+    q = normal(oracle, (bsz, m, k), 0.0, 1.0, 171, 0)
+    kk = normal(oracle, (bsz, n, k), 0.0, 1.0, 172, 0)
+    q_d, k_d = dev(q, stream), dev(kk, stream).transpose(-2, -1)
+    out = mf.DeviceArray.empty((bsz, m, n), stream)
+    mf.gemm_batched(q_d, k_d, out, alpha=0.125)
+    want = causal_where(out.numpy())
+    mf.gemm_batched(q_d, k_d, out, alpha=0.125, causal=True)
+    assert np.array_equal(out.numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("case", ["fixed 128x64", "depth 6", "depth 68", "activation", "split",
+                                  "B along n"])
+def test_causal_refusals(stream, case):
+    """The causal flag on a point the panel path cannot take (or with a fixed tile of another
+    path) fails with MFR_E_UNSUPPORTED and leaves C untouched; unknown flags are invalid."""
+    m, n, k = 300, 200, 68 if case == "depth 68" else 6 if case == "depth 6" else 32
+    a = dev(quarter_matrix(m, k, 181), stream)
+    b = dev(quarter_matrix(n, k, 182), stream).T
+    kwargs = {}
+    if case == "fixed 128x64":
+        kwargs["tile"] = mf.abi.TILE_128x64
+    elif case == "activation":
+        kwargs["act"] = mf.ACT_GELU_TANH
+    elif case == "split":
+        kwargs["splits"] = 2
+    elif case == "B along n":
+        b = dev(quarter_matrix(k, n, 183), stream)
+    c = mf.DeviceArray.empty((m, n), stream)
+    mf.fill(c, POISON)
+    with pytest.raises(NotImplementedError):
+        mf.gemm_batched(a, b, c, causal=True, **kwargs)
+    assert np.all(c.numpy() == POISON)
+    d = mf._gemm_desc(a, b, c, 1.0, None, 0.0, None, mf.ACT_NONE, 0, 0)
+    d.flags = 2
+    with pytest.raises(ValueError):
+        mf.sgemm(c.stream, d)
+    assert np.all(c.numpy() == POISON)
+
+
 # ---- the paired 128x64 kernel (B read along n, at most 64 columns) ------------------------------
 
 @pytest.mark.parametrize("m,n,k", [(1, 64, 4), (127, 64, 32), (128, 60, 36), (129, 32, 100),
