@@ -26,11 +26,15 @@
 //     past n get an offset past it; depths past k and B rows past n load as zeros.
 //   - Under the causal flag (MFR_GEMM_CAUSAL, attention's scores) every output with column > row
 //     is -inf, and a wavefront's 32 x 64 block that lies wholly above the diagonal skips its
-//     MFMAs (about half of config 5's scores).
+//     MFMAs (about half of config 5's scores). A workgroup then takes 128 rows from the top and
+//     their mirror image from the bottom instead of one 256-row panel, so that every SIMD has the
+//     same products to compute.
 //   - The scores' form (alpha and the mask only) fits 126 VGPRs: 4 wavefronts per SIMD, two
 //     workgroups per CU; with beta * C0 or a bias (FULL) 2.
 // Measured on config 5's scores (one MI355X): 151-161 us against 204-216 us for the 128x64 tile,
-// bit for bit the same (165-173 us with 2 wavefronts per SIMD); 147 us under the causal mask.
+// bit for bit the same (165-173 us with 2 wavefronts per SIMD); 116 us under the causal mask
+// (148 us with each workgroup on one contiguous panel: the CUs holding the bottom panels computed
+// nearly every block).
 // The rest is the power limit: under MFMA work and the 512 MiB store stream together the clock
 // drops to ~1.94 GHz (2.21 GHz with the stores taken out, where the same loop runs in 124-129
 // us), and at 1.94 GHz the MFMA work alone takes 135 us.
@@ -124,7 +128,17 @@ __global__ __launch_bounds__(kPanelThreads, FULL ? 2 : 4) void sgemm_panel_kerne
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / 64));
     const int half = lane / 32;
     const int r32 = lane % 32;
-    const int64_t row0 = static_cast<int64_t>(panel) * kPanelRows + wave * 32;
+    // This wavefront's 32-row block. Without the causal mask, block 8 panel + wave. Under it the
+    // blocks near the top skip most of their column tiles and those near the bottom almost none,
+    // so panel p takes blocks 4p .. 4p + 3 from the top (wavefronts 0-3) and their mirror images
+    // from the bottom of the 8 panels blocks (wavefronts 4-7): wavefronts w and w + 4 share a
+    // SIMD, and every SIMD then has the same products to compute (17 of the 32 tile-blocks of its
+    // two wavefronts when the matrix is square). Blocks past m compute nothing that is stored.
+    const bool causal = p.causal != 0;
+    const int block = !causal    ? 8 * static_cast<int>(panel) + wave
+                      : wave < 4 ? 4 * static_cast<int>(panel) + wave
+                                 : 8 * pp.panels - 1 - (4 * static_cast<int>(panel) + wave - 4);
+    const int64_t row0 = static_cast<int64_t>(block) * 32;
 
     const int t_first = static_cast<int>(chunk) * pp.per_chunk;
     const int t_left = pp.nblocks - t_first;
@@ -201,7 +215,6 @@ __global__ __launch_bounds__(kPanelThreads, FULL ? 2 : 4) void sgemm_panel_kerne
     const float beta = p.beta;
     const float* const bias = p.bias;
 
-    const bool causal = p.causal != 0;
     const auto compute_store = [&](const float* tile, int i) {
         const int64_t n0 = static_cast<int64_t>(col_tile(i)) * kPanelCols;
         floatx16 acc[2];
