@@ -39,7 +39,10 @@ HIP_FLAGS = [
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]
 
-HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra",
+# MENSURFLOW_ENABLE_TRACING: the trace spans of mensurflow/trace.hpp are compiled in (one relaxed
+# atomic load per span while no hook is attached); anything built against the library defines it
+# too, so it sees the same `trace::hook`.
+HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-DMENSURFLOW_ENABLE_TRACING",
               f"-I{INCLUDE}", f"-I{os.path.join(HOST, 'include')}", f"-I{os.path.join(HOST, 'src')}"]
 
 

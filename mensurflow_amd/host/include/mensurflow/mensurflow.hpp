@@ -12,3 +12,4 @@
 #include "mensurflow/ops/softmax.hpp"
 #include "mensurflow/shape.hpp"
 #include "mensurflow/tensor.hpp"
+#include "mensurflow/trace.hpp"

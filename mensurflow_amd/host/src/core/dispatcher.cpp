@@ -7,6 +7,7 @@
 #include "core/registry.hpp"
 #include "core/tensor_access.hpp"
 #include "core/tuning.hpp"
+#include "mensurflow/trace.hpp"
 
 #include <stdexcept>
 #include <string>
@@ -103,18 +104,31 @@ class Relocation {
     OpArgs moved_;
 };
 
+// The backend call inside its "kernel" span; under MENSURFLOW_TRACE_SYNC the span also covers
+// the device's work (trace.hpp).
+void run_kernel(KernelFn kernel, const OpArgs& args, Stream& stream, Device target) {
+    MENSURFLOW_TRACE("kernel", target, args.inputs, args.outputs);
+    kernel(args, stream);
+#ifdef MENSURFLOW_ENABLE_TRACING
+    if (trace::detail::waits_for_device()) {
+        stream.synchronize();
+    }
+#endif
+}
+
 void run_where(OpId op, const OpArgs& args, Device target, Device home) {
+    MENSURFLOW_TRACE(op_name(op), target, args.inputs, args.outputs);
     Registry& registry = Registry::instance();
     Backend& backend = registry.get(target);
     const KernelFn kernel =
         registry.dispatcher().lookup({op, target.type, anchor_of(op, args).dtype()});
     Stream& stream = backend.stream(target.index);
     if (target == home) {
-        kernel(args, stream);
+        run_kernel(kernel, args, stream, target);
         return;
     }
     const Relocation relocation(args, target);
-    kernel(relocation.args(), stream);
+    run_kernel(kernel, relocation.args(), stream, target);
     relocation.write_back(home);
 }
 

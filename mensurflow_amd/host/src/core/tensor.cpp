@@ -4,6 +4,7 @@
 // gather), unpacking (host scatter) and the exact byte span a view reaches all share. Device
 // views are packed on the device when its backend registers OpId::StridedCopy for the dtype.
 #include "mensurflow/tensor.hpp"
+#include "mensurflow/trace.hpp"
 
 #include "core/dispatcher.hpp"
 #include "core/registry.hpp"
@@ -192,6 +193,7 @@ Tensor::Tensor(std::shared_ptr<detail::Storage> storage, std::int64_t offset, Sh
 
 Tensor Tensor::empty(Shape shape, DType dtype, Device device) {
     validate_shape(shape);
+    MENSURFLOW_TRACE("Tensor::empty", device, shape, dtype);
     const std::size_t bytes = static_cast<std::size_t>(mensurflow::numel(shape)) * dtype_size(dtype);
     Strides strides = contiguous_strides(shape);
     return Tensor(std::make_shared<detail::Storage>(device, bytes), 0, std::move(shape),
@@ -246,6 +248,7 @@ Tensor Tensor::full_like(const Tensor& other, double value) {
 }
 
 Tensor Tensor::from_host(const void* data, Shape shape, DType dtype, Device device) {
+    MENSURFLOW_TRACE("Tensor::from_host", device, shape, dtype);
     Tensor out = empty(std::move(shape), dtype, device);
     if (out.nbytes() == 0) {
         return out;
@@ -264,6 +267,7 @@ Tensor Tensor::to(Device target) const {
     if (device() == target) {
         return *this;
     }
+    MENSURFLOW_TRACE("Tensor::to", target, shape_, dtype_);
     // A strided host view bound for a device that packs views: the bytes it spans go over as
     // they lie, and the device packs them (a transposed 4096^2 operand is one 64 MiB transfer
     // and a device transpose instead of a host gather). Taken while the span is at most 4 times
@@ -308,6 +312,7 @@ Tensor Tensor::contiguous() const {
     if (is_contiguous()) {
         return *this;
     }
+    MENSURFLOW_TRACE("Tensor::contiguous", device(), shape_, dtype_);
     Tensor out = empty(shape_, dtype_, device());
     if (std::byte* host = storage_->host_data()) {
         gather(host + static_cast<std::size_t>(offset_) * itemsize(), out.storage_->host_data(),
@@ -329,6 +334,7 @@ void Tensor::copy_to_host(void* dst) const {
     if (dst == nullptr) {
         throw std::invalid_argument("copy_to_host: dst is null");
     }
+    MENSURFLOW_TRACE("Tensor::copy_to_host", device(), shape_, dtype_);
     const std::size_t item = itemsize();
     const std::size_t origin = static_cast<std::size_t>(offset_) * item;
     auto* out = static_cast<std::byte*>(dst);
@@ -359,6 +365,7 @@ void Tensor::copy_from(const Tensor& source) {
     if (nbytes() == 0) {
         return;
     }
+    MENSURFLOW_TRACE("Tensor::copy_from", device(), shape_, dtype_);
     const Tensor packed = source.contiguous();
     const std::size_t item = itemsize();
     const std::size_t origin = static_cast<std::size_t>(offset_) * item;

@@ -8,6 +8,8 @@
 
 #include <cstdlib>
 #include <numeric>
+#include <string>
+#include <vector>
 
 using namespace mensurflow;
 using detail::Dispatcher;
@@ -233,9 +235,77 @@ void test_run_elsewhere() {
         [&] { matmul(a, b.to({DeviceType::ROCm, 0}), Execution::GPU); }, "mixed devices");
 }
 
+// ---- trace spans (mensurflow/trace.hpp) ------------------------------------------------------
+
+std::vector<trace::Event>& recorded() {
+    static std::vector<trace::Event> events;
+    return events;
+}
+
+void record(const trace::Event& event) { recorded().push_back(event); }
+
+const trace::Event* find_event(const std::vector<trace::Event>& events, const std::string& name) {
+    for (const trace::Event& e : events) {
+        if (name == e.name) {
+            return &e;
+        }
+    }
+    return nullptr;
+}
+
+// With a hook attached, a matmul on `device` reports its op span with the operands' shapes, a
+// "kernel" span inside it, the allocation of its result, and the read-back; detached, nothing.
+// main() sets MENSURFLOW_TRACE_SYNC before the first span, so on rocm a kernel span covers the
+// kernel itself: a 2048^3 product (~130 us on one MI355X) cannot close in the few microseconds
+// its launch takes.
+void test_trace_spans(Device device) {
+    const Execution on = test::execution_on(device);
+    const Tensor a = Tensor::full({64, 32}, 1.0, DType::F32, device);
+    const Tensor b = Tensor::full({32, 16}, 2.0, DType::F32, device);
+    recorded().clear();
+    trace::hook.store(&record);
+    const Tensor c = matmul(a, b, on);
+    const std::vector<float> values = c.to_vector<float>();
+    trace::hook.store(nullptr);
+    const std::vector<trace::Event> events = recorded();
+    test::require(values.size() == 64 * 16 && values[0] == 64.0f, "traced matmul's values");
+    const trace::Event* op = find_event(events, "matmul");
+    test::require(op != nullptr && op->device == device && op->dtype == DType::F32 &&
+                      op->inputs == (std::vector<Shape>{{64, 32}, {32, 16}}) &&
+                      op->outputs == (std::vector<Shape>{{64, 16}}),
+                  "matmul span: device, dtype, shapes");
+    const trace::Event* kernel = find_event(events, "kernel");
+    test::require(kernel != nullptr && kernel->device == device &&
+                      kernel->start_ns >= op->start_ns && kernel->end_ns <= op->end_ns &&
+                      kernel->start_ns <= kernel->end_ns,
+                  "kernel span inside the op span");
+    const trace::Event* alloc = find_event(events, "Tensor::empty");
+    test::require(alloc != nullptr && alloc->outputs == (std::vector<Shape>{{64, 16}}),
+                  "the result's allocation");
+    test::require(find_event(events, "Tensor::copy_to_host") != nullptr, "the read-back");
+    recorded().clear();
+    (void)matmul(a, b, on);
+    test::require(recorded().empty(), "no events without a hook");
+
+    if (device.type == DeviceType::ROCm) {
+        const Tensor x = Tensor::full({2048, 2048}, 0.5, DType::F32, device);
+        (void)matmul(x, x, on).to_vector<float>(); // the plan and code loading, untraced
+        recorded().clear();
+        trace::hook.store(&record);
+        const Tensor y = matmul(x, x, on);
+        trace::hook.store(nullptr);
+        const trace::Event* big = find_event(recorded(), "kernel");
+        test::require(big != nullptr && big->end_ns - big->start_ns >= 60000,
+                      "under MENSURFLOW_TRACE_SYNC the kernel span covers the device's work");
+        test::require(y.to_vector<float>()[0] == 512.0f, "traced 2048^3 product");
+    }
+}
+
 } // namespace
 
 int main(int argc, char** argv) {
+    // Read once, at the first span: the rocm kernel spans of test_trace_spans wait for the device.
+    setenv("MENSURFLOW_TRACE_SYNC", "1", 1);
     return test::run("core_test", argc, argv, [] {
         test::register_oracle_cpu_kernels();
         test_device_names();
@@ -246,6 +316,7 @@ int main(int argc, char** argv) {
             std::cout << "  transfers on " << to_string(device) << '\n';
             test_transfers(device);
             test_released_memory_reuse(device);
+            test_trace_spans(device);
         }
         test_run_elsewhere();
     });
