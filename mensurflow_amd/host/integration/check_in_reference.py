@@ -5,7 +5,7 @@ directory outside the repository, removed at the end).
 
 Steps:
   1. copy the reference tree (without .git) to <work>/tree;
-  2. apply rocm_wiring.patch (the hunks INTEGRATION.md lists: the DeviceType, registration,
+  2. apply rocm_wiring.patch (the additive core changes: the DeviceType, registration,
      execution and default device lists, OpId::Gemm/StridedCopy/Attention and their OpArgs
      fields, Stream::copy_d2d, device-side packing in Tensor, the fused gemm and attention
      dispatches, the CMake option, and the batched GEMM test's GPU expectation);
