@@ -240,10 +240,27 @@ __global__ __launch_bounds__(64 * kStripWaves) void strip_stage_kernel(ThinParam
     float a[kUnroll];
     load_group(lane, a);
     const int cols = static_cast<int>(p.cols);
-    for (int64_t i = threadIdx.x; i < p.k * C; i += blockDim.x) {
-        const int64_t d = i / C;
-        const int j = static_cast<int>(i % C);
-        b_lds[i] = j < cols ? p.b[d * p.b_rs + j * p.b_cs] : 0.0f;
+    // B' into LDS: a thread issues its loads for kFill entries before storing any, so the fill
+    // waits for one round trip to memory per kFill entries instead of one per entry (the MLP's
+    // strip, 4093 x 3 x 1023: 11.5-11.9 -> 10.5-11.0 us).
+    constexpr int kFill = 8;
+    const int64_t entries = p.k * C;
+    for (int64_t i0 = threadIdx.x; i0 < entries; i0 += kFill * blockDim.x) {
+        float v[kFill];
+#pragma unroll
+        for (int u = 0; u < kFill; ++u) {
+            const int64_t i = i0 + static_cast<int64_t>(u) * blockDim.x;
+            const int64_t d = i / C;
+            const int j = static_cast<int>(i % C);
+            v[u] = i < entries && j < cols ? p.b[d * p.b_rs + j * p.b_cs] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kFill; ++u) {
+            const int64_t i = i0 + static_cast<int64_t>(u) * blockDim.x;
+            if (i < entries) {
+                b_lds[i] = v[u];
+            }
+        }
     }
     __syncthreads();
     if (!active) {
