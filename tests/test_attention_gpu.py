@@ -75,6 +75,24 @@ def test_composed_calls_reuse_stream_scratch(oracle):
             assert_gemm_parity(got, want, mag + 1e-6, lk, f"composed call {index}")
 
 
+def test_composed_causal_where_fallback(stream, oracle):
+    """d = 18: q's rows (72 bytes) cannot take the panel path's 16-byte loads, so the scores
+    GEMM refuses the causal flag and the composition masks with where() over the lower triangle
+    instead; the result matches the oracle either way."""
+    b, h, lq, lk, d = 2, 2, 70, 90, 18
+    q = normal(oracle, (b, h, lq, d), 0.0, 1.0, 21)
+    k = normal(oracle, (b, h, lk, d), 0.0, 1.0, 22)
+    v = normal(oracle, (b, h, lk, d), 0.0, 1.0, 23)
+    q_d, k_d, v_d = dev(q, stream), dev(k, stream), dev(v, stream)
+    scores = mf.DeviceArray.empty((b, h, lq, lk), stream)
+    with pytest.raises(NotImplementedError):
+        mf.gemm_batched(q_d, k_d.transpose(-2, -1), scores, alpha=0.25, causal=True)
+    got = mf.attention(q_d, k_d, v_d, causal=True, fused=False).numpy()
+    keep = np.tril(np.ones((lq, lk), np.uint8))
+    want, mag = oracle_attention(oracle, q, k, v, keep, np.float32(1.0 / np.sqrt(d)))
+    assert_gemm_parity(got, want, mag + 1e-6, lk, "composed causal, where fallback")
+
+
 def test_config5_attention_full(stream, oracle):
     """configs[4] at full size: B=8, H=16, S=1024, D=64, causal -- the composition and the fused
     kernel against one oracle run."""
