@@ -171,10 +171,11 @@ int thin_b_layout(const GemmParams& p, const Plan& plan, int64_t m, int64_t n);
 // Modelled time (us): every byte read or written once, at kThinBytesPerUs for one column; the
 // kernel computes the columns rounded up to C = 1, 2, 4 or 8. Read one value at a time, B' costs
 // a cache-line access per value, so C > 1 takes 0.75 * C times as long (16384^2 x 1: 168 us;
-// 16384 x 4 x 4096: 125 us; 4096 x 8 x 1024: 22 us). Read in pieces, C = 2, 4, 8 take 1.0, 1.2
-// and 2.5 times as long (16384 x 2 x 4096: 43 us; 16384 x 4 x 4096: 51 us; 65536 x 4 x 512:
-// 25 us; 16384 x 8 x 4096: 91 us; 4096 x 8 x 1024: 11 us). Slower in proportion with fewer than
-// 512 workgroups.
+// 16384 x 4 x 4096: 125 us; 4096 x 8 x 1024: 22 us). Read in pieces, C = 2, 4 take 1.0 and 1.2
+// times as long (16384 x 2 x 4096: 43 us; 16384 x 4 x 4096: 51 us; 65536 x 4 x 512: 25 us);
+// C = 8 with B' staged in LDS 1.35 (16384 x 8 x 4096: 55.6 us; 65536 x 8 x 512: 31.6 us;
+// 16384 x 8 x 1000: 15.3 us), 2.5 without (fewer than 16 rows). Slower in proportion with fewer
+// than 1024 wavefronts.
 double thin_us(int64_t m, int64_t n, int64_t k, int64_t batch, bool c0, bool ak, bool bk,
                int thin_b) {
     bool along_n = true;
@@ -183,14 +184,19 @@ double thin_us(int64_t m, int64_t n, int64_t k, int64_t batch, bool c0, bool ak,
     const double cols = static_cast<double>(along_n ? n : m);
     const double rounded = cols <= 1 ? 1.0 : cols <= 2 ? 2.0 : cols <= 4 ? 4.0 : 8.0;
     const double bytes = 4.0 * batch * (rows * k + k * cols + rows * cols * (c0 ? 2.0 : 1.0));
-    const double blocks = batch * std::ceil(rows / kThinDotRows);
     const bool pieces = rounded > 1.0 && (thin_b == 2 || (thin_b == 1 && cols == rounded));
+    // 8 columns in pieces from kThinLdsMinRows rows: thin_dot_lds_kernel (B' staged in LDS).
+    const bool lds = pieces && rounded == 8.0 && rows >= kThinLdsMinRows;
+    const double waves =
+        lds ? batch * std::ceil(rows / thin_lds_rows<kThinLdsWaves>()) * kThinLdsWaves
+            : batch * std::ceil(rows / kThinDotRows) * kThinWaves;
     const double factor = rounded == 1.0 ? 1.0
                           : !pieces      ? 0.75 * rounded
                           : rounded == 2.0 ? 1.0
                           : rounded == 4.0 ? 1.2
-                                           : 2.5;
-    return bytes / kThinBytesPerUs * factor * std::max(1.0, 512.0 / blocks) + kThinLaunchUs;
+                          : lds          ? 1.35
+                                         : 2.5;
+    return bytes / kThinBytesPerUs * factor * std::max(1.0, 1024.0 / waves) + kThinLaunchUs;
 }
 
 struct Choice {
@@ -965,7 +971,18 @@ void launch_thin(const Plan& plan, const GemmParams& q, int va, int vb, hipStrea
             switch (c) {
             case 2: thin_dot_kernel<4, 2, true><<<grid, kThinThreads, 0, stream>>>(t); break;
             case 4: thin_dot_kernel<4, 4, true><<<grid, kThinThreads, 0, stream>>>(t); break;
-            default: thin_dot_kernel<4, kThinCols, true><<<grid, kThinThreads, 0, stream>>>(t);
+            default:
+                if (t.rows >= kThinLdsMinRows) {
+                    // B' staged in LDS: 16 rows per workgroup.
+                    constexpr int rows = thin_lds_rows<kThinLdsWaves>();
+                    t.blocks_per_batch = (t.rows + rows - 1) / rows;
+                    const unsigned lds_grid =
+                        static_cast<unsigned>(t.blocks_per_batch * q.batch_count);
+                    thin_dot_lds_kernel<kThinLdsWaves>
+                        <<<lds_grid, 64 * kThinLdsWaves, 0, stream>>>(t);
+                } else {
+                    thin_dot_kernel<4, kThinCols, true><<<grid, kThinThreads, 0, stream>>>(t);
+                }
             }
         } else {
             switch (c) {

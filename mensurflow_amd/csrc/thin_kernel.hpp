@@ -209,6 +209,150 @@ __global__ __launch_bounds__(kThinThreads) void thin_dot_kernel(ThinParams p) {
     }
 }
 
+// thin_dot_kernel<4, kThinCols, true>'s products and sums (every lane adds its depths in the same
+// order, so the same bits) with B' staged through LDS. There each wavefront reads all of B' (k
+// rows of 32 bytes) through the caches, twice the bytes of its own 4 rows of A, and with 8
+// columns those reads, not A's stream, set the time. Here a workgroup of WAVES wavefronts copies
+// each group of kStep depths of B' into LDS once (double-buffered, one barrier per group), and
+// every lane reads its 4 depths' rows from there. The launch takes it for 8 columns in 16-byte
+// pieces from kThinLdsMinRows rows. On one MI355X, against thin_dot_kernel (with 2 and 8
+// wavefronts in brackets): 16384 x 8 x 4096 91 -> 55.6 us (60.6, 63.1); 65536 x 8 x 512
+// 44 -> 31.6 us (46.9, 33.4); 16384 x 8 x 1000 25.7 -> 15.3 us; 4096 x 8 x 1024 10.9 -> 8.4 us;
+// 1024 x 8 x 8192 34.7 -> 34.0 us (30.5, 42.0); 3 x 8 x 5 5.3 -> 6.3 us.
+constexpr int kThinLdsWaves = 4;
+constexpr int64_t kThinLdsMinRows = 16;
+template <int WAVES> constexpr int thin_lds_rows() { return kThinRowsPerWave * WAVES; }
+
+template <int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void thin_dot_lds_kernel(ThinParams p) {
+    constexpr int VA = 4;
+    constexpr int C = kThinCols;
+    constexpr int THREADS = 64 * WAVES;
+    constexpr int kUnroll = thin_unroll(VA, C);
+    constexpr int kStep = 64 * VA * kUnroll; // depths per group
+    static_assert(kStep % THREADS == 0, "whole B' rows per thread per group");
+    constexpr int kFills = kStep / THREADS;  // B' rows each thread copies per group
+    // A group's LDS image: its depths in fours (one lane's), 4 C floats each, padded by 4 floats
+    // so that the 16 lanes of one 16-byte read pass hit 16 different 4-bank quads.
+    constexpr int kQuadPitch = 4 * C + 4;
+    constexpr int kGroupFloats = kStep / 4 * kQuadPitch;
+    __shared__ __align__(16) float b_lds[2][kGroupFloats];
+
+    const int64_t batch_index = blockIdx.x / p.blocks_per_batch;
+    const ThinBatch t = thin_batch(p, batch_index);
+    const int lane = threadIdx.x % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int64_t row0 = (blockIdx.x % p.blocks_per_batch) * thin_lds_rows<WAVES>() +
+                         wave * kThinRowsPerWave;
+    const int cols = static_cast<int>(p.cols);
+    float acc[kThinRowsPerWave][C] = {};
+    const float* a_row[kThinRowsPerWave];
+    bool valid[kThinRowsPerWave];
+#pragma unroll
+    for (int r = 0; r < kThinRowsPerWave; ++r) {
+        valid[r] = row0 + r < p.rows;
+        a_row[r] = t.a + (valid[r] ? row0 + r : 0) * p.a_rs;
+    }
+    // B' row `group + i * THREADS + threadIdx.x` of a group (zeros past k) into registers, then
+    // into the group's LDS image.
+    float4 w[kFills][2];
+    const auto fetch = [&](int64_t group) {
+#pragma unroll
+        for (int i = 0; i < kFills; ++i) {
+            const int64_t d = group + i * THREADS + threadIdx.x;
+            if (d < p.k) {
+                const float* src = t.b + d * p.b_rs;
+                w[i][0] = *reinterpret_cast<const float4*>(src);
+                w[i][1] = *reinterpret_cast<const float4*>(src + 4);
+            } else {
+                w[i][0] = make_float4(0.f, 0.f, 0.f, 0.f);
+                w[i][1] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+    };
+    const auto put = [&](int buffer) {
+#pragma unroll
+        for (int i = 0; i < kFills; ++i) {
+            const int row = i * THREADS + static_cast<int>(threadIdx.x);
+            float* dst = b_lds[buffer] + (row / 4) * kQuadPitch + (row % 4) * C;
+            *reinterpret_cast<float4*>(dst) = w[i][0];
+            *reinterpret_cast<float4*>(dst + 4) = w[i][1];
+        }
+    };
+    fetch(0);
+    put(0);
+    __syncthreads();
+    int buffer = 0;
+    for (int64_t group = 0; group < p.k; group += kStep) {
+        const bool more = group + kStep < p.k;
+        if (more) {
+            fetch(group + kStep);
+        }
+        // This lane's depths as thin_dot_kernel takes them: base, base + 64 VA, ... A lane whose
+        // first depth is past k takes no step there (it would add 0 * 0, turning -0 into +0).
+        const int64_t base = group + static_cast<int64_t>(lane) * VA;
+        if (base < p.k) {
+            float a[kUnroll][kThinRowsPerWave][VA];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const int64_t kk = base + u * 64 * VA;
+                const bool in_k = kk < p.k;
+#pragma unroll
+                for (int r = 0; r < kThinRowsPerWave; ++r) {
+                    const float4 v = valid[r] && in_k ? mfr::dev::load_streaming(a_row[r] + kk)
+                                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+                    a[u][r][0] = v.x;
+                    a[u][r][1] = v.y;
+                    a[u][r][2] = v.z;
+                    a[u][r][3] = v.w;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const float* quad = b_lds[buffer] + (u * 64 + lane) * kQuadPitch;
+#pragma unroll
+                for (int v = 0; v < VA; ++v) {
+                    float b[C];
+#pragma unroll
+                    for (int h = 0; h < C / 4; ++h) {
+                        const float4 x = *reinterpret_cast<const float4*>(quad + v * C + 4 * h);
+                        b[4 * h + 0] = 4 * h + 0 < cols ? x.x : 0.0f;
+                        b[4 * h + 1] = 4 * h + 1 < cols ? x.y : 0.0f;
+                        b[4 * h + 2] = 4 * h + 2 < cols ? x.z : 0.0f;
+                        b[4 * h + 3] = 4 * h + 3 < cols ? x.w : 0.0f;
+                    }
+#pragma unroll
+                    for (int r = 0; r < kThinRowsPerWave; ++r) {
+#pragma unroll
+                        for (int j = 0; j < C; ++j) {
+                            acc[r][j] = __builtin_fmaf(a[u][r][v], b[j], acc[r][j]);
+                        }
+                    }
+                }
+            }
+        }
+        if (more) {
+            put(buffer ^ 1);
+        }
+        __syncthreads();
+        buffer ^= 1;
+    }
+    float mine = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kThinRowsPerWave; ++r) {
+#pragma unroll
+        for (int j = 0; j < C; ++j) {
+            const float v = mfr::dev::butterfly_sum(acc[r][j]);
+            mine = lane == r * C + j ? v : mine;
+        }
+    }
+    const int r = lane / C;
+    const int j = lane % C;
+    if (r < kThinRowsPerWave && row0 + r < p.rows && j < cols) {
+        thin_store(p, t, row0 + r, j, mine);
+    }
+}
+
 // A peeled strip of at most 8 columns over every row of a K-major A whose rows 16-byte loads
 // cannot take, and the staging of that A for the MFMA tiles, in one launch: each wavefront takes
 // one row of A' = A, copies it to p.stage (zero-padded from k to stage_rs) as it reads it, and sums

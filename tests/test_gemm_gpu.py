@@ -875,6 +875,32 @@ def test_thin_b_pieces_and_batch_strides(stream, n, pad):
         assert same_bits(got[i], exact_product(a[i], bv[i])), (n, pad, i)
 
 
+@pytest.mark.parametrize("batch,m,n,k", [(1, 2000, 8, 1300), (3, 500, 8, 700), (1, 16, 8, 513),
+                                         (2, 37, 6, 2049), (1, 1000, 7, 4096)])
+def test_thin_lds_exact(stream, batch, m, n, k):
+    """8 computed columns read as 16-byte pieces from 16 rows on: B' staged through LDS in groups
+    of 512 depths (thin_dot_lds_kernel). Depths past the last group's end, a batch with B
+    broadcast, 6 and 7 columns (B staged, its lines padded to 8), alpha, beta*C0 and a bias:
+    bits equal the exact product, no stray writes."""
+    a = quarter_matrix(batch * m, k, 291).reshape(batch, m, k)
+    b = quarter_matrix(k, n, 292)
+    c0 = quarter_matrix(batch * m, n, 293).reshape(batch, m, n)
+    bias = quarter_matrix(1, n, 294)[0]
+    want = np.stack([(np.float32(0.5) * exact_product(a[i], b)) + np.float32(2.0) * c0[i]
+                     for i in range(batch)])
+    want = (want + bias).astype(np.float32)
+    # Staged, A's lines (odd k) take 16-byte loads and B's lines are padded to 8 columns.
+    stage = mf.abi.STAGE_ALWAYS if n % 4 or k % 4 else mf.abi.STAGE_AUTO
+    b_d = dev(b, stream).expand((batch, k, n))
+    buf = mf.DeviceArray.empty((batch * m * n + 128,), stream)
+    mf.fill(buf, POISON)
+    c = buf.slice(0, 64, 64 + batch * m * n).view((batch, m, n))
+    mf.gemm_batched(dev(a, stream), b_d, c, alpha=0.5, c0=dev(c0, stream), beta=2.0,
+                    bias=dev(bias, stream), tile=THIN, stage=stage)
+    assert same_bits(c.numpy(), want)
+    check_guards(buf)
+
+
 def test_thin_k_zero_and_refusals(stream):
     m, n = 33, 4
     c0 = quarter_matrix(m, n, 251)
@@ -926,6 +952,8 @@ def test_thin_automatic_choice(stream):
     assert plan(16384, 1, 16384)[0] == THIN
     # 4 aligned columns: B rows read as 16-byte pieces (51 us against 101 us on 64x64 tiles).
     assert plan(16384, 4, 4096)[0] == THIN
+    # 8 aligned columns: B' staged in LDS (55.6 us against 101 us for 64x64 split 4).
+    assert plan(16384, 8, 4096)[0] == THIN
     assert plan(4096, 4096, 4096)[0] == mf.abi.TILE_256x256
 
 
