@@ -278,6 +278,14 @@ int mfr_sgemv(mfr_stream_t stream, int trans, int64_t rows, int64_t cols, float 
 int mfr_smatvec(mfr_stream_t stream, int64_t m, int64_t k, const float* a, int64_t lda,
                 const float* x, float* y);
 
+/* *out = sum over i < n of x[i] * y[i] (unit strides; out is one float of device memory, 0 for
+ * n = 0): each product in double (exact), the sum in double in a fixed order that depends on n
+ * alone, rounded once, as the reference's dot_f32 (src/backends/cpu/ops/blas/blas.cpp:14-21)
+ * adds them in double. Replaces the Dot kernel that mensurflow::dot dispatches
+ * (src/ops/blas.cpp:41-68), which the CUDA backend serves with cublasSdot
+ * (src/backends/cuda/backend.cpp:131-133). */
+int mfr_sdot(mfr_stream_t stream, int64_t n, const float* x, const float* y, float* out);
+
 /* ---- elementwise, softmax, argmax ---------------------------------------------------------- */
 
 /* y[r, j] = act(x[r, j] + bias[j]) over a contiguous [rows, cols] matrix; bias may be NULL
@@ -313,12 +321,14 @@ int mfr_softmax(mfr_stream_t stream, const float* x, float* y, int64_t outer, in
  * NaN wins. Replaces Argmax (src/backends/cpu/backend.cpp:799-803, reduction.cpp:284-296). */
 int mfr_argmax(mfr_stream_t stream, const float* x, int64_t* out, int64_t rows, int64_t width);
 
-/* out[i] = a[i] + b[i] (op MFR_EW_ADD), a[i] * b[i] (MFR_EW_MUL), or alpha * a[i] (MFR_EW_SCAL,
- * b unused) over n contiguous elements, one fp32 rounding each. Replaces the Add, Mul and Scal
- * kernels (registered at src/backends/cpu/backend.cpp:856-867; add_f32/mul_f32 at
- * src/backends/cpu/ops/elementwise/elementwise.cpp:72-91, scal_f32 at ops/blas/blas.cpp:23-28) that
- * mensurflow::gemm's unfused composition dispatches (src/ops/blas.cpp:246-257). */
-enum { MFR_EW_ADD = 0, MFR_EW_MUL = 1, MFR_EW_SCAL = 2 };
+/* out[i] = a[i] + b[i] (op MFR_EW_ADD), a[i] - b[i] (MFR_EW_SUB), a[i] * b[i] (MFR_EW_MUL), or
+ * alpha * a[i] (MFR_EW_SCAL, b unused) over n contiguous elements, one fp32 rounding each.
+ * Replaces the Add, Sub, Mul and Scal kernels (registered at src/backends/cpu/backend.cpp:856-867;
+ * add_f32/sub_f32/mul_f32 at src/backends/cpu/ops/elementwise/elementwise.cpp:72-91, scal_f32 at
+ * ops/blas/blas.cpp:23-28) that mensurflow::gemm's unfused composition dispatches
+ * (src/ops/blas.cpp:246-257); Add, Sub and Mul are also the ops the CUDA backend registers
+ * (src/backends/cuda/backend.cpp:231-235). */
+enum { MFR_EW_ADD = 0, MFR_EW_MUL = 1, MFR_EW_SCAL = 2, MFR_EW_SUB = 3 };
 int mfr_elementwise(mfr_stream_t stream, int op, const float* a, const float* b, float alpha,
                     float* out, int64_t n);
 

@@ -24,7 +24,7 @@ from .abi import ACT_GELU_ERF, ACT_GELU_TANH, ACT_NONE, GemmDesc  # noqa: F401
 
 __all__ = [
     "ACT_NONE", "ACT_GELU_TANH", "ACT_GELU_ERF", "GemmDesc", "device_count", "device_info",
-    "Stream", "DeviceArray", "Event", "sgemm", "gemm", "gemm_batched", "sgemv", "matvec",
+    "Stream", "DeviceArray", "Event", "sgemm", "gemm", "gemm_batched", "sgemv", "matvec", "dot",
     "bias_act", "where", "where_nd", "elementwise", "softmax", "argmax", "strided_copy", "fill", "attention",
     "attention_fused", "attention_composed", "gemm_plan",
 ]
@@ -418,6 +418,18 @@ def matvec(a: DeviceArray, x: DeviceArray, out: DeviceArray | None = None) -> De
     return out
 
 
+def dot(x: DeviceArray, y: DeviceArray, out: DeviceArray | None = None) -> DeviceArray:
+    """mensurflow::dot (src/ops/blas.cpp:41-68) through mfr_sdot: sum of x[i] * y[i] over two
+    contiguous vectors of equal length, the products and their sum in double, rounded once; a
+    0-d array."""
+    if x.size != y.size:
+        raise ValueError(f"dot: lengths differ ({x.size} and {y.size})")
+    if out is None:
+        out = DeviceArray.empty((), x.stream)
+    abi.check(abi.load().mfr_sdot(x.stream.handle, x.size, x.ptr, y.ptr, out.ptr), "mfr_sdot")
+    return out
+
+
 def bias_act(x: DeviceArray, bias: DeviceArray | None, act=ACT_NONE,
              out: DeviceArray | None = None) -> DeviceArray:
     rows, cols = (x.shape if len(x.shape) == 2 else (1, x.size))
@@ -457,8 +469,8 @@ def where_nd(cond: DeviceArray, x: DeviceArray, y: DeviceArray,
 
 def elementwise(op: int, a: DeviceArray, b: DeviceArray | None = None, alpha=1.0,
                 out: DeviceArray | None = None) -> DeviceArray:
-    """out = a + b (abi.EW_ADD), a * b (abi.EW_MUL) or alpha * a (abi.EW_SCAL, b unused) over
-    contiguous arrays of a's size (mfr_elementwise)."""
+    """out = a + b (abi.EW_ADD), a - b (abi.EW_SUB), a * b (abi.EW_MUL) or alpha * a
+    (abi.EW_SCAL, b unused) over contiguous arrays of a's size (mfr_elementwise)."""
     if out is None:
         out = DeviceArray.empty(a.shape, a.stream)
     b_ptr = None if b is None else b.ptr

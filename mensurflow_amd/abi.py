@@ -26,6 +26,7 @@ ACT_GELU_ERF = 2
 EW_ADD = 0
 EW_MUL = 1
 EW_SCAL = 2
+EW_SUB = 3
 
 TILE_AUTO = 0
 TILE_256x256 = 1
@@ -119,6 +120,7 @@ SIGNATURES = {
     "mfr_sgemv": (ctypes.c_int, [_vp, ctypes.c_int, _i64, _i64, _f32, _vp, _i64, _vp, _f32, _vp,
                                  _vp]),
     "mfr_smatvec": (ctypes.c_int, [_vp, _i64, _i64, _vp, _i64, _vp, _vp]),
+    "mfr_sdot": (ctypes.c_int, [_vp, _i64, _vp, _vp, _vp]),
     "mfr_bias_act": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_int]),
     "mfr_where": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i64]),
     "mfr_where_nd": (ctypes.c_int, [_vp, _i32, ctypes.POINTER(_i64), _vp, ctypes.POINTER(_i64),

@@ -177,6 +177,9 @@ __global__ __launch_bounds__(kStreamThreads) void binary4_kernel(const float4* _
                 if constexpr (OP == MFR_EW_ADD) {
                     v = make_float4(av[u].x + bv[u].x, av[u].y + bv[u].y, av[u].z + bv[u].z,
                                     av[u].w + bv[u].w);
+                } else if constexpr (OP == MFR_EW_SUB) {
+                    v = make_float4(av[u].x - bv[u].x, av[u].y - bv[u].y, av[u].z - bv[u].z,
+                                    av[u].w - bv[u].w);
                 } else if constexpr (OP == MFR_EW_MUL) {
                     v = make_float4(av[u].x * bv[u].x, av[u].y * bv[u].y, av[u].z * bv[u].z,
                                     av[u].w * bv[u].w);
@@ -589,6 +592,8 @@ __global__ void binary_kernel(int op, const float* __restrict__ a, const float* 
         float v;
         if (op == MFR_EW_ADD) {
             v = a[i] + b[i];
+        } else if (op == MFR_EW_SUB) {
+            v = a[i] - b[i];
         } else if (op == MFR_EW_MUL) {
             v = a[i] * b[i];
         } else {
@@ -606,7 +611,8 @@ int mfr_elementwise(mfr_stream_t stream, int op, const float* a, const float* b,
                     float* out, int64_t n) {
     return mfr::guarded([&] {
         auto& s = mfr::stream_of(stream);
-        mfr::require(op == MFR_EW_ADD || op == MFR_EW_MUL || op == MFR_EW_SCAL,
+        mfr::require(op == MFR_EW_ADD || op == MFR_EW_SUB || op == MFR_EW_MUL ||
+                         op == MFR_EW_SCAL,
                      "elementwise: unknown op");
         mfr::require(n >= 0, "elementwise: negative count");
         if (n == 0) {
@@ -631,24 +637,24 @@ int mfr_elementwise(mfr_stream_t stream, int op, const float* a, const float* b,
                     <<<blocks, kStreamThreads, 0, s.stream>>>(a4, b4, alpha, o4, quads, chunk);
             };
             using Add = std::integral_constant<int, MFR_EW_ADD>;
+            using Sub = std::integral_constant<int, MFR_EW_SUB>;
             using Mul = std::integral_constant<int, MFR_EW_MUL>;
             using Scal = std::integral_constant<int, MFR_EW_SCAL>;
+            const auto with_stream = [&](auto stream_tag) {
+                if (op == MFR_EW_ADD) {
+                    run(Add{}, stream_tag);
+                } else if (op == MFR_EW_SUB) {
+                    run(Sub{}, stream_tag);
+                } else if (op == MFR_EW_MUL) {
+                    run(Mul{}, stream_tag);
+                } else {
+                    run(Scal{}, stream_tag);
+                }
+            };
             if (stream_out) {
-                if (op == MFR_EW_ADD) {
-                    run(Add{}, std::true_type{});
-                } else if (op == MFR_EW_MUL) {
-                    run(Mul{}, std::true_type{});
-                } else {
-                    run(Scal{}, std::true_type{});
-                }
+                with_stream(std::true_type{});
             } else {
-                if (op == MFR_EW_ADD) {
-                    run(Add{}, std::false_type{});
-                } else if (op == MFR_EW_MUL) {
-                    run(Mul{}, std::false_type{});
-                } else {
-                    run(Scal{}, std::false_type{});
-                }
+                with_stream(std::false_type{});
             }
             mfr::check_launch("binary4_kernel");
             done = 4 * quads;

@@ -306,9 +306,113 @@ void launch_gemv(mfr_stream& s, bool trans, int64_t rows, int64_t cols, float al
     mfr::check_launch("gemv_t_finish_kernel");
 }
 
+// ---- dot --------------------------------------------------------------------------------------
+//
+// dot(x, y) = sum of x[i] y[i], as the reference's dot_f32 (src/backends/cpu/ops/blas/blas.cpp:
+// 14-21): each product in double (exact), the sum in double, rounded once. Two passes in a fixed
+// order that depends on n alone (so every device and every call gives the same bits): chunk c of
+// kDotChunk elements is one workgroup, its threads walk it in float4 steps (thread t takes
+// elements 4t .. 4t + 3 of each 1024, adding them in increasing order), and the threads' sums
+// are added in a fixed tree; the second pass adds the chunks' sums the same way. HBM-bound:
+// 8 bytes per element read.
+constexpr int kDotThreads = 256;
+constexpr int64_t kDotStep = 4 * kDotThreads;  // elements per workgroup step
+constexpr int64_t kDotChunk = 16 * kDotStep;   // elements per workgroup (16384)
+
+// The sum of v over the workgroup's threads in a fixed order: halves added pairwise in LDS.
+__device__ inline double block_sum(double v, double* lds) {
+    lds[threadIdx.x] = v;
+    __syncthreads();
+#pragma unroll
+    for (int half = kDotThreads / 2; half > 0; half >>= 1) {
+        if (static_cast<int>(threadIdx.x) < half) {
+            lds[threadIdx.x] += lds[threadIdx.x + half];
+        }
+        __syncthreads();
+    }
+    return lds[0];
+}
+
+// VEC4: x and y 16-byte aligned (chunks start on multiples of kDotChunk elements, so every
+// full float4 group is aligned too).
+template <bool VEC4>
+__global__ __launch_bounds__(kDotThreads) void dot_partial_kernel(const float* __restrict__ x,
+                                                                  const float* __restrict__ y,
+                                                                  int64_t n,
+                                                                  double* __restrict__ partial) {
+    __shared__ double lds[kDotThreads];
+    const int64_t begin = static_cast<int64_t>(blockIdx.x) * kDotChunk;
+    const int64_t end = begin + kDotChunk < n ? begin + kDotChunk : n;
+    double sum = 0.0;
+    for (int64_t i = begin + 4 * static_cast<int64_t>(threadIdx.x); i < end; i += kDotStep) {
+        if (VEC4 && i + 3 < end) {
+            const float4 a = mfr::dev::load_streaming(x + i);
+            const float4 b = mfr::dev::load_streaming(y + i);
+            sum = fma(static_cast<double>(a.x), static_cast<double>(b.x), sum);
+            sum = fma(static_cast<double>(a.y), static_cast<double>(b.y), sum);
+            sum = fma(static_cast<double>(a.z), static_cast<double>(b.z), sum);
+            sum = fma(static_cast<double>(a.w), static_cast<double>(b.w), sum);
+        } else {
+            for (int64_t e = i; e < i + 4 && e < end; ++e) {
+                sum = fma(static_cast<double>(x[e]), static_cast<double>(y[e]), sum);
+            }
+        }
+    }
+    const double total = block_sum(sum, lds);
+    if (threadIdx.x == 0) {
+        partial[blockIdx.x] = total;
+    }
+}
+
+// *out = the chunks' sums added in a fixed order (thread t takes chunks t, t + 256, ... in
+// order, then the tree), rounded to float.
+__global__ __launch_bounds__(kDotThreads) void dot_finish_kernel(const double* __restrict__ partial,
+                                                                 int64_t chunks,
+                                                                 float* __restrict__ out) {
+    __shared__ double lds[kDotThreads];
+    double sum = 0.0;
+    for (int64_t c = threadIdx.x; c < chunks; c += kDotThreads) {
+        sum += partial[c];
+    }
+    const double total = block_sum(sum, lds);
+    if (threadIdx.x == 0) {
+        *out = static_cast<float>(total);
+    }
+}
+
+void launch_dot(mfr_stream& s, int64_t n, const float* x, const float* y, float* out) {
+    mfr::require(n >= 0, "dot: negative length");
+    mfr::require(out != nullptr, "dot: null out");
+    mfr::require(n == 0 || (x != nullptr && y != nullptr), "dot: null x or y");
+    const int64_t chunks = (n + kDotChunk - 1) / kDotChunk;
+    mfr::require(chunks < (int64_t{1} << 31), "dot: vector too long");
+    // Held until both kernels are queued (another thread's reserve() may not free `partial`).
+    std::lock_guard<std::mutex> hold(s.workspace_mutex);
+    double* partial = nullptr;
+    if (chunks > 0) {
+        partial = static_cast<double*>(s.reserve(static_cast<size_t>(chunks) * sizeof(double)));
+        const unsigned grid = static_cast<unsigned>(chunks);
+        if (mfr::aligned16(x) && mfr::aligned16(y)) {
+            dot_partial_kernel<true><<<grid, kDotThreads, 0, s.stream>>>(x, y, n, partial);
+        } else {
+            dot_partial_kernel<false><<<grid, kDotThreads, 0, s.stream>>>(x, y, n, partial);
+        }
+        mfr::check_launch("dot_partial_kernel");
+    }
+    dot_finish_kernel<<<1, kDotThreads, 0, s.stream>>>(partial, chunks, out);
+    mfr::check_launch("dot_finish_kernel");
+}
+
 } // namespace
 
 extern "C" {
+
+int mfr_sdot(mfr_stream_t stream, int64_t n, const float* x, const float* y, float* out) {
+    return mfr::guarded([&] {
+        auto& s = mfr::stream_of(stream);
+        launch_dot(s, n, x, y, out);
+    });
+}
 
 int mfr_sgemv(mfr_stream_t stream, int trans, int64_t rows, int64_t cols, float alpha,
               const float* a, int64_t lda, const float* x, float beta, const float* y0, float* y) {

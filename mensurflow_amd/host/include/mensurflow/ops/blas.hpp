@@ -43,4 +43,7 @@ Tensor gemm_strided_batched(const Tensor& a, const Tensor& b, float alpha = 1.0f
 // alpha * x for a vector x (a new contiguous tensor).
 Tensor scal(float alpha, const Tensor& x, Execution execution = Execution::Auto);
 
+// The 0-d sum of a[i] * b[i] over two vectors of one length (0 for empty ones).
+Tensor dot(const Tensor& a, const Tensor& b, Execution execution = Execution::Auto);
+
 } // namespace mensurflow

@@ -7,8 +7,9 @@
 
 namespace mensurflow {
 
-// NumPy-broadcast a + b and a * b.
+// NumPy-broadcast a + b, a - b and a * b.
 Tensor add(const Tensor& a, const Tensor& b, Execution execution = Execution::Auto);
+Tensor sub(const Tensor& a, const Tensor& b, Execution execution = Execution::Auto);
 Tensor mul(const Tensor& a, const Tensor& b, Execution execution = Execution::Auto);
 
 // x[batch, features] + bias[features].

@@ -609,6 +609,13 @@ template <int Op> void binary_kernel(const OpArgs& args, Stream& stream) {
                           ptr<float>(out), out.numel()));
 }
 
+// OpId::Dot: two unit-stride vectors of one length (the op checks them), a 0-d output.
+void dot_kernel(const OpArgs& args, Stream& stream) {
+    const Tensor& x = args.inputs[0];
+    check(mfr_sdot(handle(stream), x.numel(), ptr<float>(x), ptr<float>(args.inputs[1]),
+                   ptr<float>(args.outputs[0])));
+}
+
 // Packs a strided view (any dtype) into the contiguous output on the device.
 void strided_copy_kernel(const OpArgs& args, Stream& stream) {
     const Tensor& x = args.inputs[0];
@@ -674,6 +681,8 @@ class RocmBackend final : public Backend {
         add(OpId::Argmax, argmax_kernel);
         add(OpId::Add, binary_kernel<MFR_EW_ADD>);
         add(OpId::Mul, binary_kernel<MFR_EW_MUL>);
+        add(OpId::Sub, binary_kernel<MFR_EW_SUB>);
+        add(OpId::Dot, dot_kernel);
         add(OpId::Scal, binary_kernel<MFR_EW_SCAL>);
         dispatcher.register_tunable({OpId::Matmul, DeviceType::ROCm, DType::F32},
                                     gemm_tunable<OpId::Matmul>("matmul"));

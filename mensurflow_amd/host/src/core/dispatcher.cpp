@@ -20,9 +20,10 @@ constexpr const char* kOpNames[] = {
     "scal",    "copy",     "add",         "mul",     "matvec",  "gemv",
     "matmul",  "gelu",     "where",       "bias_add", "argmax", "gemm_strided_batched",
     "uniform", "normal",   "softmax",     "gemm",    "strided_copy", "attention",
+    "dot",     "sub",
 };
 constexpr std::size_t kOpCount = sizeof(kOpNames) / sizeof(kOpNames[0]);
-static_assert(kOpCount == static_cast<std::size_t>(OpId::Attention) + 1, "a name for every op");
+static_assert(kOpCount == static_cast<std::size_t>(OpId::Sub) + 1, "a name for every op");
 
 constexpr std::size_t kDeviceTypeCount = static_cast<std::size_t>(DeviceType::ROCm) + 1;
 constexpr std::size_t kDTypeCount = static_cast<std::size_t>(DType::Bool) + 1;

@@ -43,7 +43,9 @@ enum class OpId {
     Softmax,
     Gemm,
     StridedCopy,
-    Attention
+    Attention,
+    Dot,
+    Sub
 };
 
 // "gemm_strided_batched", "bias_add", ...: the name errors and tuning results use.

@@ -124,6 +124,22 @@ Tensor scal(float alpha, const Tensor& x, Execution execution) {
     return out;
 }
 
+Tensor dot(const Tensor& a, const Tensor& b, Execution execution) {
+    // The checks and messages of src/ops/blas.cpp:41-68.
+    const OpCheck check("dot");
+    check.operand(a, "a", 1).operand(b, "b", 1).same_dtype(a, b).same_device(a, b);
+    if (a.size(0) != b.size(0)) {
+        check.fail("lengths differ (" + std::to_string(a.size(0)) + " and " +
+                   std::to_string(b.size(0)) + ")");
+    }
+    if (a.size(0) == 0) {
+        return Tensor::zeros({}, a.dtype(), a.device()); // the sum of no products
+    }
+    Tensor out = Tensor::empty({}, a.dtype(), a.device());
+    detail::dispatch(OpId::Dot, {{unit_stride(a), unit_stride(b)}, {out}}, execution);
+    return out;
+}
+
 Tensor matvec(const Tensor& a, const Tensor& x, Execution execution) {
     const OpCheck check("matvec");
     check.operand(a, "a", 2).operand(x, "x", 1).same_dtype(a, x).same_device(a, x);

@@ -1,5 +1,5 @@
-// Elementwise ops of the hot path: add and mul (used by gemm's unfused composition), bias_add,
-// gelu and where. Checks, messages and broadcasting rules are mensurflow's
+// Elementwise ops of the hot path: add and mul (used by gemm's unfused composition), sub (the
+// third binary op the reference's CUDA backend serves), bias_add, gelu and where. Checks, messages and broadcasting rules are mensurflow's
 // (src/ops/elementwise.cpp:18,140-201,251-309,454-481). Operands that broadcast, or are not
 // packed, become packed tensors of the output's shape before the kernel sees them, except where a
 // device's where kernel reads broadcast views itself (ROCm), which saves materializing them.
@@ -43,6 +43,10 @@ bool where_reads_views(Device device) { return device.type == DeviceType::ROCm; 
 
 Tensor add(const Tensor& a, const Tensor& b, Execution execution) {
     return pairwise(OpId::Add, a, b, execution);
+}
+
+Tensor sub(const Tensor& a, const Tensor& b, Execution execution) {
+    return pairwise(OpId::Sub, a, b, execution);
 }
 
 Tensor mul(const Tensor& a, const Tensor& b, Execution execution) {

@@ -73,8 +73,12 @@ class _Lib:
         getattr(L, p + "where_f32").argtypes = [_u8p, _f32p, _f32p, _f32p, _i64]
         getattr(L, p + "softmax_f32").argtypes = [_f32p, _f32p, _i64, _i64, _i64]
         getattr(L, p + "argmax_f32").argtypes = [_f32p, _i64p, _i64, _i64]
+        getattr(L, p + "sub_f32").argtypes = [_f32p, _f32p, _f32p, _i64]
+        getattr(L, p + "dot_f32").argtypes = [_f32p, _f32p, _i64]
+        getattr(L, p + "dot_f32").restype = ctypes.c_float
         for name in ("philox4x32_10", "uniform_f32", "normal_f32", "matvec_f32", "gemv_f32",
-                     "bias_add_f32", "gelu_f32", "where_f32", "softmax_f32", "argmax_f32"):
+                     "bias_add_f32", "gelu_f32", "where_f32", "softmax_f32", "argmax_f32",
+                     "sub_f32"):
             getattr(L, p + name).restype = None
 
     # -- shared wrappers ------------------------------------------------------------------------
@@ -111,6 +115,18 @@ class _Lib:
         self.fn("gemv_f32")(_ptr(a), _ptr(x), _ptr(y), rows, cols, alpha, beta, _ptr(y0c),
                             1 if trans else 0)
         return y
+
+    def dot(self, x, y):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.ascontiguousarray(y, dtype=np.float32)
+        return np.float32(self.fn("dot_f32")(_ptr(x), _ptr(y), x.size))
+
+    def sub(self, a, b):
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        b = np.ascontiguousarray(b, dtype=np.float32)
+        out = np.empty_like(a)
+        self.fn("sub_f32")(_ptr(a), _ptr(b), _ptr(out), a.size)
+        return out
 
     def bias_add(self, x, bias):
         x = np.ascontiguousarray(x, dtype=np.float32)

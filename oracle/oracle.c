@@ -210,6 +210,21 @@ void orc_add_f32(const float* a, const float* b, float* out, int64_t n) {
     }
 }
 
+void orc_sub_f32(const float* a, const float* b, float* out, int64_t n) {
+#pragma omp parallel for schedule(static) if (n > 65536)
+    for (int64_t i = 0; i < n; ++i) {
+        out[i] = a[i] - b[i];
+    }
+}
+
+float orc_dot_f32(const float* x, const float* y, int64_t n) {
+    double sum = 0.0;
+    for (int64_t i = 0; i < n; ++i) {
+        sum += (double)x[i] * (double)y[i];
+    }
+    return (float)sum;
+}
+
 void orc_mul_f32(const float* a, const float* b, float* out, int64_t n) {
 #pragma omp parallel for schedule(static) if (n > 65536)
     for (int64_t i = 0; i < n; ++i) {

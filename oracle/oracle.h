@@ -42,9 +42,14 @@ void orc_sgemm_packed(int64_t m, int64_t n, int64_t k, const float* a, int64_t r
  * (src/ops/blas.cpp:246-257) and of the batched finish pass (gemm_batched.cpp:12-28). */
 void orc_axpby_f32(float* out, const float* x, float alpha, const float* y0, float beta, int64_t n);
 
-/* add_f32 / mul_f32 (src/backends/cpu/ops/elementwise/elementwise.cpp:72-91). */
+/* add_f32 / sub_f32 / mul_f32 (src/backends/cpu/ops/elementwise/elementwise.cpp:72-91). */
 void orc_add_f32(const float* a, const float* b, float* out, int64_t n);
+void orc_sub_f32(const float* a, const float* b, float* out, int64_t n);
 void orc_mul_f32(const float* a, const float* b, float* out, int64_t n);
+
+/* dot_f32 (src/backends/cpu/ops/blas/blas.cpp:14-21): the products in double (exact), summed in
+ * double in increasing index order (the reference's single-thread order), rounded once. */
+float orc_dot_f32(const float* x, const float* y, int64_t n);
 
 /* matvec_f32 / gemv_f32 (src/backends/cpu/ops/blas/blas.cpp:55-79): double accumulation in
  * increasing index, one rounding. */

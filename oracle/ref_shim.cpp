@@ -87,6 +87,14 @@ void ref_add_f32(const float* a, const float* b, float* out, std::int64_t n) {
     cpu::add_f32(a, b, out, n);
 }
 
+// sub (src/backends/cpu/ops/elementwise/elementwise.cpp:79) and dot (blas.cpp:14-21), the two
+// ops the reference's CUDA backend registers besides add and mul.
+void ref_sub_f32(const float* a, const float* b, float* out, std::int64_t n) {
+    cpu::sub_f32(a, b, out, n);
+}
+
+float ref_dot_f32(const float* x, const float* y, std::int64_t n) { return cpu::dot_f32(x, y, n); }
+
 // gemm_strided_batched's CPU kernel (gemm_batched.cpp:58-70): packed GEMM per matrix, then the
 // finish pass alpha * C + beta * C0 (gemm_batched.cpp:12-28). C and C0 are contiguous
 // [batch, m, n]; matrix i of A / B starts at the given element offsets.

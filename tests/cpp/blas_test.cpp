@@ -4,6 +4,7 @@
 // inputs and errors. Quarter-integer inputs make every fp32 sum exact, so CPU and GPU results
 // must agree in every bit with the exact product.
 #include "core/dispatcher.hpp"
+#include "oracle.h"
 #include "oracle_cpu.hpp"
 #include "reference_math.hpp"
 #include "test_util.hpp"
@@ -290,6 +291,62 @@ void test_batched(Device device) {
         "batch 2 and 3 do not broadcast");
 }
 
+// dot and sub, the ops the reference's CUDA backend serves besides add and mul (the cases of the
+// reference's tests/ops/dot_test.cpp:50-120): known values, empty vectors, a strided slice, an
+// offset slice, a broadcast scalar, the errors; the products summed in double, so every device
+// gives the oracle's bits here; sub with broadcasting.
+void test_dot_and_sub(Device device) {
+    const Execution on = test::execution_on(device);
+    const Tensor a = Tensor::from_vector(std::vector<float>{1, 2, 3}, {3}, device);
+    const Tensor b = Tensor::from_vector(std::vector<float>{4, -5, 6}, {3}, device);
+    test::require(dot(a, b, on).item<float>() == 12.0f, "1*4 + 2*-5 + 3*6 = 12");
+    test::require(dot(a, a, on).item<float>() == 14.0f, "a . a");
+    const Tensor none = Tensor::empty({0}, DType::F32, device);
+    const Tensor zero = dot(none, none, on);
+    test::require(zero.dim() == 0 && zero.device() == device && zero.item<float>() == 0.0f,
+                  "empty dot is 0");
+    const std::int64_t n = 100003;
+    const Tensor x = normal({n}, 0.0f, 1.0f, 31, 0).to(device);
+    const Tensor y = normal({n}, 0.0f, 1.0f, 32, 0).to(device);
+    const auto xv = x.to_vector<float>();
+    const auto yv = y.to_vector<float>();
+    const auto oracle_dot = [](const std::vector<float>& p, const std::vector<float>& q) {
+        return orc_dot_f32(p.data(), q.data(), static_cast<std::int64_t>(p.size()));
+    };
+    const float got = dot(x, y, on).item<float>();
+    test::require(got == oracle_dot(xv, yv), "dot of 100003 normals: the oracle's bits");
+    std::vector<float> ex, ey;
+    for (std::int64_t i = 0; i < n; i += 3) {
+        ex.push_back(xv[static_cast<std::size_t>(i)]);
+        ey.push_back(yv[static_cast<std::size_t>(i)]);
+    }
+    test::require(dot(x.slice(0, 0, n, 3), y.slice(0, 0, n, 3), on).item<float>() ==
+                      oracle_dot(ex, ey),
+                  "strided slice");
+    const std::vector<float> ox(xv.begin() + 101, xv.begin() + 90101);
+    const std::vector<float> oy(yv.begin() + 101, yv.begin() + 90101);
+    test::require(dot(x.slice(0, 101, 90101), y.slice(0, 101, 90101), on).item<float>() ==
+                      oracle_dot(ox, oy),
+                  "offset slice (unaligned start)");
+    const Tensor three = Tensor::from_vector(std::vector<float>{3}, {1}, device).expand({n});
+    test::require(dot(three, y, on).item<float>() ==
+                      oracle_dot(std::vector<float>(static_cast<std::size_t>(n), 3.0f), yv),
+                  "expanded scalar");
+    const Tensor v4 = Tensor::from_vector(std::vector<float>{1, 2, 3, 4}, {4}, device);
+    const Tensor m = Tensor::from_vector(std::vector<float>{1, 2, 3, 4}, {2, 2}, device);
+    test::require_throws<std::invalid_argument>([&] { dot(a, v4, on); }, "dot lengths differ");
+    test::require_throws<std::invalid_argument>([&] { dot(m, m, on); }, "dot of a matrix");
+
+    // sub: a - b with a row broadcast over a matrix, and elementwise on a long vector.
+    const Tensor mat = Tensor::from_vector(std::vector<float>{1, 2, 3, 4, 5, 6}, {2, 3}, device);
+    test::require(sub(mat, a, on).to_vector<float>() == (std::vector<float>{0, 0, 0, 3, 3, 3}),
+                  "sub with a broadcast row");
+    const auto diff = sub(x, y, on).to_vector<float>();
+    std::vector<float> want(xv.size());
+    orc_sub_f32(xv.data(), yv.data(), want.data(), n);
+    test::require(diff == want, "sub of 100003 normals");
+}
+
 } // namespace
 
 int main(int argc, char** argv) {
@@ -301,6 +358,7 @@ int main(int argc, char** argv) {
             test_gemm(device);
             test_gemv(device);
             test_batched(device);
+            test_dot_and_sub(device);
         }
     });
 }

@@ -129,6 +129,20 @@ void add(const OpArgs& args, Stream&) {
                 out.numel());
 }
 
+void sub(const OpArgs& args, Stream&) {
+    const Tensor& out = args.outputs[0];
+    orc_sub_f32(ptr<float>(args.inputs[0]), ptr<float>(args.inputs[1]), ptr<float>(out),
+                out.numel());
+}
+
+// The reference's Dot adapter (src/backends/cpu/backend.cpp) writes dot_f32's float into the
+// 0-d output.
+void dot(const OpArgs& args, Stream&) {
+    const Tensor& x = args.inputs[0];
+    *ptr<float>(args.outputs[0]) = orc_dot_f32(ptr<float>(x), ptr<float>(args.inputs[1]),
+                                               x.numel());
+}
+
 void mul(const OpArgs& args, Stream&) {
     const Tensor& out = args.outputs[0];
     orc_mul_f32(ptr<float>(args.inputs[0]), ptr<float>(args.inputs[1]), ptr<float>(out),
@@ -169,6 +183,8 @@ void register_oracle_cpu_kernels() {
     add_kernel(OpId::Argmax, argmax);
     add_kernel(OpId::Add, add);
     add_kernel(OpId::Mul, mul);
+    add_kernel(OpId::Sub, sub);
+    add_kernel(OpId::Dot, dot);
     add_kernel(OpId::Scal, scal);
     add_kernel(OpId::Uniform, uniform);
     add_kernel(OpId::Normal, normal);

@@ -133,7 +133,7 @@ def test_argmax_bit_exact(stream, vectors, oracle):
 @pytest.mark.parametrize("n", [1, 3, 4, 5, 8, 1023, 4096, 4099, (1 << 20) + 3])
 @pytest.mark.parametrize("offset", [0, 1, 3])
 def test_where_and_binary_sizes_and_alignment(stream, n, offset):
-    """where, add, mul and scal bit for bit against numpy on every size class (multiples of 4 go
+    """where, add, sub, mul and scal bit for bit against numpy on every size class (multiples of 4 go
     through the 16-byte streaming kernels, the rest of n through the scalar ones) and on views
     starting 1 or 3 elements into their buffers (misaligned: the scalar kernels only)."""
     rng = np.random.default_rng(n + offset)
@@ -148,6 +148,7 @@ def test_where_and_binary_sizes_and_alignment(stream, n, offset):
     abi = mf.abi
     assert same_bits(mf.elementwise(abi.EW_ADD, x, y).numpy(), xv + yv)
     assert same_bits(mf.elementwise(abi.EW_MUL, x, y).numpy(), xv * yv)
+    assert same_bits(mf.elementwise(abi.EW_SUB, x, y).numpy(), xv - yv)
     assert same_bits(mf.elementwise(abi.EW_SCAL, x, alpha=-1.5).numpy(), np.float32(-1.5) * xv)
 
 

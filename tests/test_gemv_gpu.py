@@ -113,3 +113,40 @@ def test_beta_without_y0_is_invalid(stream):
     x = dev(np.ones(4, np.float32), stream)
     with pytest.raises(ValueError):
         mf.sgemv(a, x, beta=1.0)
+
+
+# ---- dot (mfr_sdot) ------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [0, 1, 3, 4, 1000, 16383, 16384, 16385, 1_000_003])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_dot_exact_on_quarter_integers(stream, n, offset):
+    """Quarter-integer inputs: every product and partial sum is exact in double, so the result is
+    the exact sum rounded once, whatever the order; around the 16384-element chunks, at aligned
+    (16-byte loads) and unaligned starts, and n = 0 (0)."""
+    rng = np.random.default_rng(n + 7 * offset)
+    xs = (rng.integers(-16, 17, n + offset) / 4).astype(np.float32)
+    ys = (rng.integers(-16, 17, n + offset) / 4).astype(np.float32)
+    x = dev(xs, stream).slice(0, offset, offset + n)
+    y = dev(ys, stream).slice(0, offset, offset + n)
+    # The reference's sum starts at +0.0 (blas.cpp:15), so an exact -0 sum comes out +0.
+    want = np.float32(0.0 + np.dot(xs[offset:].astype(np.float64), ys[offset:].astype(np.float64)))
+    got = mf.dot(x, y).numpy()
+    assert got.shape == () and same_bits(np.array([got]), np.array([want])), (n, offset)
+
+
+@pytest.mark.parametrize("n", [5, 100_003, 1 << 24])
+def test_dot_matches_oracle_bits(stream, oracle, n):
+    """Normal inputs: the double sums in two orders round to the same float (the oracle adds in
+    index order as the reference's single-thread dot_f32 does); repeated calls give the same
+    bits."""
+    x = normal(oracle, (n,), 0.0, 1.0, 41, 0)
+    y = normal(oracle, (n,), 0.0, 1.0, 42, 0)
+    x_d, y_d = dev(x, stream), dev(y, stream)
+    got = mf.dot(x_d, y_d).numpy()
+    assert same_bits(np.array([got]), np.array([oracle.dot(x, y)])), n
+    assert same_bits(np.array([mf.dot(x_d, y_d).numpy()]), np.array([got]))
+
+
+def test_dot_lengths_must_agree(stream):
+    with pytest.raises(ValueError):
+        mf.dot(dev(np.ones(3, np.float32), stream), dev(np.ones(4, np.float32), stream))

@@ -141,6 +141,42 @@ def test_live_reference_gemv_softmax(oracle, reference):
     assert same_bits(oracle.softmax(s), reference.softmax(s))
 
 
+def test_dot_sub_known_answers_and_live_reference(oracle, reference):
+    """dot and sub, the two ops the reference's CUDA backend registers besides add and mul: the
+    known answers of tests/ops/dot_test.cpp:50-57, and the reference's own dot_f32 and sub_f32
+    (single thread, so its order is the restatement's) on random inputs, bit for bit."""
+    a = np.array([1, 2, 3], np.float32)
+    b = np.array([4, -5, 6], np.float32)
+    assert oracle.dot(a, b) == np.float32(12.0) and oracle.dot(a, a) == np.float32(14.0)
+    assert oracle.dot(a[:0], b[:0]) == np.float32(0.0)
+    rng = np.random.default_rng(21)
+    reference.set_threads(1)
+    try:
+        for n in (1, 7, 1000, 300001):
+            x = rng.standard_normal(n).astype(np.float32)
+            y = rng.standard_normal(n).astype(np.float32)
+            assert same_bits(np.array([oracle.dot(x, y)]), np.array([reference.dot(x, y)])), n
+            assert same_bits(oracle.sub(x, y), reference.sub(x, y)), n
+    finally:
+        reference.set_threads(reference.max_threads())
+
+
+def test_dot_closed_form_and_planted_float_accumulation(oracle):
+    """The products are summed in double: quarter-integer inputs give the exact sum's float, and
+    a cancellation that a float accumulator loses (1e8 + 1 - 1e8) keeps its 1."""
+    x = quarter_input(4097, 22)
+    y = quarter_input(4097, 23)
+    exact = np.float32(np.dot(x.astype(np.float64), y.astype(np.float64)))
+    assert oracle.dot(x, y) == exact
+    big = np.array([1e8, 1.0, -1e8], np.float32)
+    ones = np.ones(3, np.float32)
+    assert oracle.dot(big, ones) == np.float32(1.0)
+    float_sum = np.float32(0.0)
+    for v in big * ones:
+        float_sum = np.float32(float_sum + v)
+    assert float_sum != oracle.dot(big, ones), "a float accumulator must be told apart"
+
+
 # ---- 3. closed forms -------------------------------------------------------------------------------
 
 
