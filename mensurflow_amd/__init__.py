@@ -15,6 +15,7 @@ library, or without a gfx950 device, every call raises.
 from __future__ import annotations
 
 import ctypes
+import threading
 from dataclasses import dataclass
 
 import numpy as np
@@ -58,7 +59,19 @@ def device_info(device: int = 0) -> DeviceInfo:
 
 
 class Stream:
-    """An mfr_stream_t: one HIP stream on one device with its kernel workspace."""
+    """An mfr_stream_t: one HIP stream on one device with its kernel workspace.
+
+    The stream keeps the device memory of arrays released on it for its later allocations.
+    Kernels and copies on one stream run in order, so work on a new array that takes a released
+    block is queued after every use of the old array, and neither the release nor the allocation
+    waits for the device (hipFree waits for the whole device; hipMalloc of a large block costs
+    tens of microseconds). Blocks come in size classes (powers of two below 1 MiB, at least
+    512 B; multiples of 2 MiB above); idle blocks are kept up to 1/8 of the device's memory
+    (at least 1 GiB), past that a released block is freed. An array used by work queued on
+    another stream must be released only after that work is done, as before."""
+
+    _SMALL = 1 << 20
+    _LARGE_STEP = 2 << 20
 
     def __init__(self, device: int = 0):
         lib = abi.load()
@@ -67,6 +80,58 @@ class Stream:
         abi.check(lib.mfr_stream_create(device, ctypes.byref(handle)), "mfr_stream_create")
         self.handle = handle
         self._scratch: dict = {}
+        self._idle: dict = {}
+        self._idle_bytes = 0
+        self._pool_lock = threading.Lock()   # host threads may share a stream
+        mem = ctypes.c_size_t(0)
+        lib.mfr_get_device_info(device, None, 0, ctypes.byref(mem), None, None)
+        self._idle_limit = max(mem.value // 8, 1 << 30)
+
+    @classmethod
+    def size_class(cls, nbytes: int) -> int:
+        if nbytes >= cls._SMALL:
+            return (nbytes + cls._LARGE_STEP - 1) // cls._LARGE_STEP * cls._LARGE_STEP
+        size = 512
+        while size < nbytes:
+            size *= 2
+        return size
+
+    def _take(self, size: int) -> int:
+        """A device block of `size` bytes (a size class): an idle one, else a new allocation."""
+        with self._pool_lock:
+            blocks = self._idle.get(size)
+            if blocks:
+                self._idle_bytes -= size
+                return blocks.pop()
+        lib = abi.load()
+        ptr = ctypes.c_void_p()
+        if lib.mfr_malloc(self.device, size, ctypes.byref(ptr)) != abi.MFR_OK:
+            self.release_idle()
+            abi.check(lib.mfr_malloc(self.device, size, ctypes.byref(ptr)), "mfr_malloc")
+        return ptr.value or 0
+
+    def _give(self, size: int, ptr: int) -> None:
+        with self._pool_lock:
+            if self.handle is not None and self._idle_bytes + size <= self._idle_limit:
+                self._idle.setdefault(size, []).append(ptr)
+                self._idle_bytes += size
+                return
+        if self.handle is not None:
+            self.synchronize()
+        abi.check(abi.load().mfr_free(self.device, ptr), "mfr_free")
+
+    def release_idle(self) -> None:
+        """Free the idle blocks (after the work queued on the stream is done)."""
+        if not self._idle:
+            return
+        if self.handle is not None:
+            self.synchronize()
+        lib = abi.load()
+        with self._pool_lock:
+            idle, self._idle, self._idle_bytes = self._idle, {}, 0
+        for blocks in idle.values():
+            for ptr in blocks:
+                abi.check(lib.mfr_free(self.device, ptr), "mfr_free")
 
     def scratch(self, tag, shape, dtype=np.float32) -> "DeviceArray":
         """A device array of `shape` for temporaries of work queued on this stream. Each tag
@@ -94,6 +159,7 @@ class Stream:
         for held in self._scratch.values():
             held.close()
         self._scratch.clear()
+        self.release_idle()
         if self.handle is not None and self.handle.value:
             abi.check(abi.load().mfr_stream_destroy(self.handle), "mfr_stream_destroy")
         self.handle = None
@@ -158,12 +224,19 @@ class DeviceArray:
         self.strides = tuple(int(s) for s in _strides)
         if _base is None:
             nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
-            self.nbytes_alloc = nbytes
-            ptr = ctypes.c_void_p()
-            dev = stream.device if stream is not None else 0
-            abi.check(abi.load().mfr_malloc(dev, nbytes, ctypes.byref(ptr)), "mfr_malloc")
-            self._ptr = ptr.value or 0
-            self._device = dev
+            if stream is not None and stream.handle is not None and nbytes > 0:
+                # A block of the stream's pool, returned to it by close().
+                self.nbytes_alloc = Stream.size_class(nbytes)
+                self._ptr = stream._take(self.nbytes_alloc)
+                self._device = stream.device
+            else:
+                self.nbytes_alloc = nbytes
+                ptr = ctypes.c_void_p()
+                dev = stream.device if stream is not None else 0
+                abi.check(abi.load().mfr_malloc(dev, nbytes, ctypes.byref(ptr)), "mfr_malloc")
+                self._ptr = ptr.value or 0
+                self._device = dev
+            self._pooled = self._ptr != 0 and stream is not None and stream.handle is not None
         else:
             self._ptr = _ptr
             self._device = _base._device
@@ -275,11 +348,15 @@ class DeviceArray:
 
     def close(self) -> None:
         if self._base is None and self._ptr:
+            ptr, self._ptr = self._ptr, 0
+            if self._pooled and self.stream.handle is not None:
+                # Later users of the block are queued after the work still using this array.
+                self.stream._give(self.nbytes_alloc, ptr)
+                return
             # Kernels queued on the stream may still read or write this memory.
             if self.stream is not None and self.stream.handle is not None:
                 self.stream.synchronize()
-            abi.check(abi.load().mfr_free(self._device, self._ptr), "mfr_free")
-            self._ptr = 0
+            abi.check(abi.load().mfr_free(self._device, ptr), "mfr_free")
 
     def __del__(self):
         try:

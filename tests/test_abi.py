@@ -80,3 +80,17 @@ def test_status_codes_map_to_reference_exceptions():
         abi.check(abi.MFR_E_UNSUPPORTED)
     with pytest.raises(RuntimeError):
         abi.check(abi.MFR_E_RUNTIME)
+
+
+def test_stream_pool_size_classes():
+    """The size classes of a stream's released blocks, as the host backend's pool has them:
+    powers of two from 512 B below 1 MiB, multiples of 2 MiB from 1 MiB up."""
+    import mensurflow_amd as mf
+
+    size = mf.Stream.size_class
+    assert [size(b) for b in (1, 512, 513, 4096, 4097)] == [512, 512, 1024, 4096, 8192]
+    assert size((1 << 20) - 1) == 1 << 20
+    assert size(1 << 20) == 2 << 20
+    assert size(2 << 20) == 2 << 20
+    assert size((2 << 20) + 1) == 4 << 20
+    assert size(32 << 20) == 32 << 20

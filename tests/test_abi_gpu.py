@@ -111,3 +111,30 @@ def test_host_copies_every_size_around_the_staging_chunks(stream, nbytes):
         assert np.array_equal(other.numpy(), want)
     buf.close()
     other.close()
+
+
+def test_released_blocks_serve_later_arrays_in_stream_order(stream):
+    """A released array's block goes back to its stream without a wait and serves the stream's
+    next array of the same size class. Work queued before the release still reads the old bytes:
+    a 2048^3 GEMM reading A is queued, A is released, and a new array taking A's block is
+    filled by an upload queued behind the GEMM; the product is exact and the new array holds
+    the upload. A slightly smaller array takes the same block, and release_idle gives every idle
+    block back to the device."""
+    n = 2048
+    av, bv = quarter_matrix(n, n, 21), quarter_matrix(n, n, 22)
+    a, b = dev(av, stream), dev(bv, stream)
+    c = mf.gemm(a, b)
+    block = a._ptr
+    a.close()
+    again = dev(np.full((n, n), 3.0, np.float32), stream)
+    assert again._ptr == block
+    exact = (av.astype(np.float64) @ bv.astype(np.float64)).astype(np.float32)
+    assert same_bits(c.numpy(), exact)
+    assert np.all(again.numpy() == 3.0)
+    again.close()
+    smaller = mf.DeviceArray.empty((n * n - 1000,), stream)
+    assert smaller._ptr == block
+    smaller.close()
+    assert stream._idle_bytes >= n * n * 4
+    stream.release_idle()
+    assert stream._idle_bytes == 0 and not stream._idle
