@@ -87,3 +87,27 @@ def test_split_gemm_from_many_threads(oracle):
             results[mode] = [o.numpy() for o in outs]
     for i, (got, want) in enumerate(zip(results["threads"], results["serial"])):
         assert same_bits(got, want), f"split gemm case {i} differs when called from threads"
+
+
+def test_large_copies_from_several_threads():
+    """Host threads each moving a little over 24 MiB to the device and back, at once, each on a
+    stream of its own. The CPU side of a staged copy is split over the library's helper threads
+    when they are free and done by the calling thread alone when another copy holds them; either
+    way every byte comes back, from and to odd host addresses, in every round."""
+    streams = [mf.Stream(0) for _ in range(THREADS)]
+    rngs = [np.random.default_rng(100 + t) for t in range(THREADS)]
+    try:
+        def copier(t):
+            def fn():
+                n = (24 << 20) + 4093 * t
+                data = rngs[t].integers(0, 256, n + 1, dtype=np.uint8)[1:]  # an odd address
+                buf = mf.DeviceArray.empty((n,), streams[t], dtype=np.uint8)
+                buf.upload(data)
+                back = buf.numpy()
+                assert np.array_equal(back, data), f"thread {t}"
+            return fn
+
+        _run_threads([copier(t) for t in range(THREADS)])
+    finally:
+        for s in streams:
+            s.close()
