@@ -702,7 +702,15 @@ struct DirectSliceLoader {
 // The 256x256 tile (16 wavefronts of 64x64) with direct-to-LDS slices. The depth loop is
 // unrolled by two so each half knows at compile time which buffer it reads and which it fills;
 // the copy of slice s + 1 is issued before slice s's MFMAs and waited for (vmcnt 0) before the
-// barrier that ends the slice. Same arithmetic as sgemm_kernel, so the same bits.
+// barrier that ends the slice. Within a slice each wavefront reads group g + 1's fragments
+// before group g's MFMAs (two register sets), and the slice's last group is held back across
+// the barrier: its fragments are read before it (so the buffer may be refilled), its MFMAs run
+// after it while the next slice's first fragments are read. Without the hold-back every
+// wavefront waited after each barrier for its first reads, with the 16 wavefronts reading at
+// once. Taken with both operands K-major (each fragment one 16-byte LDS read): configs[2] 972 ->
+// 960 us. With an M/N-major operand it measured slower (4096^3 NN 950 -> 959 us, the MLP's
+// rectangle 267 -> 269), so those take each slice's groups in order with no hold-back. Same
+// arithmetic as sgemm_kernel, so the same bits.
 template <int BM, int BN, int KT, int WAVES_M, int WAVES_N, bool AK, bool BK, int VA, int VB>
 __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_direct_kernel(GemmParams p) {
     constexpr int THREADS = WAVES_M * WAVES_N * 64;
@@ -759,6 +767,53 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_direct_kernel(Ge
         }
     }
 
+    // Fragments of one 8-deep group in two register sets: set (g & 1) for group g of a slice.
+    constexpr int KG = KT / 8;
+    static_assert(KG % 2 == 0, "a slice's first group takes register set 0");
+    [[maybe_unused]] float fa[2][FM][4], fb[2][FN][4];
+    const auto frags = [&](int set, const float* sa, const float* sb, int g) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            FragA::fragment(sa, wave_m * WM + i * 32 + r32, g, half, fa[set][i]);
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            FragB::fragment(sb, wave_n * WN + j * 32 + r32, g, half, fb[set][j]);
+        }
+    };
+    const auto mfmas = [&](int set) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) {
+#pragma unroll
+                for (int j = 0; j < FN; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[set][i][st],
+                                                                      fb[set][j][st], acc[i][j],
+                                                                      0, 0, 0);
+                }
+            }
+        }
+    };
+    // Groups 0 .. KG - 2 of the slice in (sa, sb), each after the next group's reads (the
+    // scheduling barriers keep the reads ahead of the MFMAs that do not need them).
+    const auto body = [&](const float* sa, const float* sb) {
+#pragma unroll
+        for (int g = 0; g + 1 < KG; ++g) {
+            frags((g + 1) & 1, sa, sb, g + 1);
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(g & 1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // After the slice barrier: the next slice's first fragments, then the held-back last group.
+    const auto cross = [&](const float* na, const float* nb) {
+        frags(0, na, nb, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas((KG - 1) & 1);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
     // Slices are taken in pairs, buffer 0 then buffer 1, with no exit between the two halves (an
     // exit there splits the accumulators' live ranges and they spill). An odd count gets one
     // more slice past the end, all of whose elements are outside the matrix: the buffer unit
@@ -771,29 +826,49 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_direct_kernel(Ge
     };
     const LoadA load_a(p.a_rs, p.a_cs);
     const LoadB load_b(p.b_cs, p.b_rs);
+    constexpr bool kHold = AK && BK;
     if (slices > 0) {
         load_a.issue(tile_a0, a_base, w.rows_a, k_left_of(0));
         load_b.issue(tile_b0, b_base, w.rows_b, k_left_of(0));
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+        if constexpr (kHold) {
+            frags(0, tile_a0, tile_b0, 0);
+        }
     }
     for (int64_t s = 0; s < slices; s += 2) {
-        // Slice s from buffer 0; slice s + 1 (zeros past the end) into buffer 1.
+        // Slice s from buffer 0; slice s + 1 (zeros past the end) into buffer 1, whose last
+        // reads came before the previous barrier.
         load_a.issue(tile_a1, a_base + (s + 1) * a_step, w.rows_a, k_left_of(s + 1));
         load_b.issue(tile_b1, b_base + (s + 1) * b_step, w.rows_b, k_left_of(s + 1));
-        slice_mfma<FragA, FragB, KT, FM, FN, WM, WN, 1>(acc, tile_a0, tile_b0, wave_m, wave_n, 0,
-                                                         half, r32);
+        if constexpr (kHold) {
+            body(tile_a0, tile_b0);
+        } else {
+            slice_mfma<FragA, FragB, KT, FM, FN, WM, WN, 1>(acc, tile_a0, tile_b0, wave_m, wave_n,
+                                                             0, half, r32);
+        }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        // Slice s + 1 from buffer 1; slice s + 2 into buffer 0.
+        if constexpr (kHold) {
+            cross(tile_a1, tile_b1);
+        }
+        // Slice s + 1 from buffer 1; slice s + 2 into buffer 0 (all of whose reads came before
+        // the barrier above).
         if (s + 2 < slices) {
             load_a.issue(tile_a0, a_base + (s + 2) * a_step, w.rows_a, k_left_of(s + 2));
             load_b.issue(tile_b0, b_base + (s + 2) * b_step, w.rows_b, k_left_of(s + 2));
         }
-        slice_mfma<FragA, FragB, KT, FM, FN, WM, WN, 1>(acc, tile_a1, tile_b1, wave_m, wave_n, 0,
-                                                         half, r32);
+        if constexpr (kHold) {
+            body(tile_a1, tile_b1);
+        } else {
+            slice_mfma<FragA, FragB, KT, FM, FN, WM, WN, 1>(acc, tile_a1, tile_b1, wave_m, wave_n,
+                                                             0, half, r32);
+        }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+        if constexpr (kHold) {
+            cross(tile_a0, tile_b0); // past the last slice the fragments read here go unused
+        }
     }
     if (slices == 0) {
         __syncthreads(); // the gelu table's copy (no slice barrier has made it visible)
