@@ -322,6 +322,37 @@ def test_plan_on_baseline_shapes(stream):
     assert same_bits(got, exact_product(a, b))
 
 
+@pytest.mark.parametrize("m,n,k", [(256, 256, 4), (256, 256, 28), (256, 256, 32), (300, 260, 36),
+                                   (256, 256, 64), (300, 260, 96), (256, 512, 100),
+                                   (512, 200, 128), (260, 300, 160), (256, 256, 260)])
+def test_held_back_slices_exact(stream, m, n, k):
+    """The 256x256 tile with both operands read along k (A row-major, B a transposed view of an
+    [n, k] array, 16-byte loads, in place) holds each 32-deep slice's last group of MFMAs back
+    across the slice barrier and reads one group past the last slice. Depths of one to nine
+    slices, odd and even counts and ragged last slices, on whole and ragged tiles: the exact
+    product of quarter integers, and the same bits as the same product read N-major (the
+    in-order loop); one case with alpha, beta and C0."""
+    a = quarter_matrix(m, k, 300 + k)
+    bt = quarter_matrix(n, k, 400 + k)
+    a_d, bt_d = dev(a, stream), dev(bt, stream)
+    view, buf = guarded_output(stream, (m, n))
+    mf.gemm(a_d, bt_d, trans_b=True, tile=mf.abi.TILE_256x256, stage=mf.abi.STAGE_NEVER,
+            out=view)
+    got = view.numpy()
+    check_guards(buf)
+    want = exact_product(a, bt.T)
+    assert same_bits(got, want), f"{m}x{n}x{k}"
+    b_nmajor = dev(np.ascontiguousarray(bt.T), stream)
+    other = mf.gemm(a_d, b_nmajor, tile=mf.abi.TILE_256x256, stage=mf.abi.STAGE_NEVER).numpy()
+    assert same_bits(got, other), f"{m}x{n}x{k}: K-major and N-major B differ"
+    if k == 100:
+        c0 = quarter_matrix(m, n, 500)
+        got = mf.gemm(a_d, bt_d, trans_b=True, alpha=1.5, c0=dev(c0, stream), beta=0.5,
+                      tile=mf.abi.TILE_256x256, stage=mf.abi.STAGE_NEVER).numpy()
+        want = (np.float32(1.5) * exact_product(a, bt.T) + np.float32(0.5) * c0).astype(np.float32)
+        assert same_bits(got, want), "alpha, beta and C0"
+
+
 # ---- the panel path ------------------------------------------------------------------------------
 
 PANEL = mf.abi.TILE_PANEL
