@@ -3,9 +3,11 @@
 // transfer_test.cpp and device tests pin).
 #include "core/dispatcher.hpp"
 #include "core/registry.hpp"
+#include "core/tensor_access.hpp"
 #include "oracle_cpu.hpp"
 #include "test_util.hpp"
 
+#include <cstdint>
 #include <cstdlib>
 #include <numeric>
 #include <string>
@@ -301,6 +303,27 @@ void test_trace_spans(Device device) {
     }
 }
 
+// Host tensors of 4 MiB or more start on a 2 MiB boundary (their memory asks for transparent huge
+// pages, so a first write faults once per 2 MiB); smaller ones on a 64-byte line. A large one
+// goes to every device and back unchanged.
+void test_large_host_buffers() {
+    const Device cpu{DeviceType::CPU, 0};
+    const Tensor small = Tensor::zeros({1000}, DType::F32, cpu);
+    const auto small_at = reinterpret_cast<std::uintptr_t>(detail::TensorAccess::data<float>(small));
+    test::require(small_at % 64 == 0, "a small host buffer starts on a 64-byte line");
+    const std::int64_t n = (std::int64_t{6} << 20) / 4 + 7; // a little over 6 MiB
+    const auto values = iota(n);
+    const Tensor big = Tensor::from_vector(values, {n}, cpu);
+    const auto big_at = reinterpret_cast<std::uintptr_t>(detail::TensorAccess::data<float>(big));
+    test::require(big_at % (std::uintptr_t{2} << 20) == 0,
+                  "a host buffer of 4 MiB or more starts on a 2 MiB boundary");
+    for (Device device : test::devices()) {
+        const Tensor there = big.to(device);
+        test::require(there.to(cpu).to_vector<float>() == values,
+                      "a 6 MiB host tensor through " + to_string(device) + " and back");
+    }
+}
+
 } // namespace
 
 int main(int argc, char** argv) {
@@ -319,5 +342,6 @@ int main(int argc, char** argv) {
             test_trace_spans(device);
         }
         test_run_elsewhere();
+        test_large_host_buffers();
     });
 }
