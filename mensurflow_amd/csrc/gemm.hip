@@ -363,9 +363,20 @@ void launch_vec(const GemmParams& p, int va, int vb, unsigned blocks, hipStream_
 // CU the 4 wavefronts are faster (4096^3 1075 against 1105 us). Unsplit, the 128x128 tile
 // then runs 16 wavefronts in two sets and the 64x64 tile 16 in four, the sets sharing each
 // depth slice.
+// direct_ok: each depth slice's byte offsets fit the direct-to-LDS loaders' 32 bits (as
+// big_tile_ok checks for 256 rows, which covers the smaller tiles).
 template <bool AK, bool BK>
 void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned blocks, bool one_per_cu,
-                   hipStream_t stream) {
+                   bool direct_ok, hipStream_t stream) {
+    // With one workgroup per CU, no split, 16-byte operands and only whole tiles, the 64x64 and
+    // 128x128 tiles run the direct-to-LDS kernel (one accumulation chain, the tile kernels' depth
+    // order) in place of the wavefront sets: 1024^3 NN 29.1 -> 26.3 us on 64x64, 2048^3 NN
+    // 151.2 -> 137.8 us on 128x128. Ragged edges keep the sets (1000^3: 28.1 against 31.6 us on
+    // the direct form, whose edge slices work out each lane's element).
+    const auto direct_mid = [&](int64_t bm, int64_t bn) {
+        return one_per_cu && p.splits == 1 && direct_ok && va == 4 && vb == 4 && p.m % bm == 0 &&
+               p.n % bn == 0;
+    };
     switch (tile) {
     case MFR_TILE_256x256:
         // The direct-to-LDS form for every load width: with 16-byte operands it also beats the
@@ -388,7 +399,9 @@ void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned block
         launch_vec<64, 128, 16, 2, 2, AK, BK>(p, va, vb, blocks, stream);
         break;
     case MFR_TILE_64x64:
-        if (one_per_cu && p.splits == 1) {
+        if (direct_mid(64, 64)) {
+            sgemm_direct_kernel<64, 64, 32, 2, 2, AK, BK, 4, 4><<<blocks, 256, 0, stream>>>(p);
+        } else if (one_per_cu && p.splits == 1) {
             // 16 wavefronts: four sets of 2x2 share each 64-deep slice (4 per SIMD). 1024^3:
             // 31.0 -> 27.7 us; 16384 x 4 x 4096: 113.7 -> 94.2 us. Split depth ranges are
             // short and keep the 4-wavefront form (512^3 in two: 14.5 against 14.1 us).
@@ -398,7 +411,9 @@ void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned block
         }
         break;
     default:
-        if (one_per_cu && p.splits == 1) {
+        if (direct_mid(128, 128)) {
+            sgemm_direct_kernel<128, 128, 32, 4, 4, AK, BK, 4, 4><<<blocks, 1024, 0, stream>>>(p);
+        } else if (one_per_cu && p.splits == 1) {
             // 16 wavefronts: two sets of 2x4 share each 64-deep slice (4 per SIMD). 2048^3:
             // 150.2 -> 145.6 us; 2048 x 2048 x 8192: 583.9 -> 560.9 us (32-deep slices: 149.3
             // and 574.1 us).
@@ -1079,16 +1094,17 @@ void launch_region(const Plan& plan, const GemmParams& p, const Region& r, int v
     q.stream_c = q.partial == nullptr && streamed_output(q) ? 1 : 0;
     const unsigned grid = static_cast<unsigned>(blocks);
     const bool one_per_cu = blocks <= cus;
+    const bool direct_ok = big_tile_ok(plan);
     if (tile == MFR_TILE_128x64 && pair_fits(plan, q, va, vb)) {
         sgemm_pair_kernel<32><<<grid, 256, 0, stream>>>(q);
     } else if (plan.ak && plan.bk) {
-        launch_layout<true, true>(tile, q, va, vb, grid, one_per_cu, stream);
+        launch_layout<true, true>(tile, q, va, vb, grid, one_per_cu, direct_ok, stream);
     } else if (plan.ak) {
-        launch_layout<true, false>(tile, q, va, vb, grid, one_per_cu, stream);
+        launch_layout<true, false>(tile, q, va, vb, grid, one_per_cu, direct_ok, stream);
     } else if (plan.bk) {
-        launch_layout<false, true>(tile, q, va, vb, grid, one_per_cu, stream);
+        launch_layout<false, true>(tile, q, va, vb, grid, one_per_cu, direct_ok, stream);
     } else {
-        launch_layout<false, false>(tile, q, va, vb, grid, one_per_cu, stream);
+        launch_layout<false, false>(tile, q, va, vb, grid, one_per_cu, direct_ok, stream);
     }
     mfr::check_launch("sgemm_kernel");
     if (q.partial != nullptr) {

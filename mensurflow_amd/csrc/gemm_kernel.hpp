@@ -699,6 +699,94 @@ struct DirectSliceLoader {
     }
 };
 
+// Direct-to-LDS copy of an M/N-major slice whose lines (KT of them, ROWS floats each, padded to
+// ROWS + 8) are narrower than one wave-instruction (ROWS = 64): the image is filled as one run
+// of floats, each lane's 4 floats (16 bytes, within one line) from wherever they live. The last
+// instruction may run past the image, so the LDS buffer holds kAlloc floats. Elements outside the
+// matrix and the pads get an offset past the record limit and load zeros.
+template <int ROWS, int KT, int THREADS> struct DirectNarrowLoader {
+    static constexpr int kPitch = ROWS + 8;
+    static constexpr int kFloats = KT * kPitch;
+    static constexpr int kInstr = (kFloats + 255) / 256;
+    static constexpr int kAlloc = kInstr * 256;
+    static constexpr int kWaves = THREADS / 64;
+    static constexpr int kPerWave = (kInstr + kWaves - 1) / kWaves;
+    uint32_t off[kPerWave]; // this lane's offsets in a whole slice
+    uint32_t k_bytes;
+
+    // (line, position) of this lane's 4 floats in instruction j of this wave; false past the
+    // image.
+    __device__ __forceinline__ static bool place(int j, int& line, int& at) {
+        const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / 64));
+        const int f = ((wave * kPerWave + j) * 64 + static_cast<int>(__lane_id())) * 4;
+        line = f / kPitch;
+        at = f - line * kPitch;
+        return f < kFloats;
+    }
+
+    __device__ __forceinline__ explicit DirectNarrowLoader(int64_t k_stride) {
+        k_bytes = static_cast<uint32_t>(k_stride) * 4u;
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            int line, at;
+            const bool in_image = place(j, line, at);
+            off[j] = in_image && at < ROWS ? static_cast<uint32_t>(line) * k_bytes +
+                                                 static_cast<uint32_t>(at) * 4u
+                                           : kDirectLimit;
+        }
+    }
+
+    // base: element (depth 0, row 0) of the slice; rows_left / k_left as DirectSliceLoader's.
+    __device__ __forceinline__ void issue(float* lds, const float* base, int rows_left,
+                                          int k_left) const {
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(base), 0, static_cast<int>(kDirectLimit - 1), kBufferWord3);
+        const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / 64));
+        const bool whole = rows_left >= ROWS && k_left >= KT;
+#pragma unroll
+        for (int j = 0; j < kPerWave; ++j) {
+            const int instr = wave * kPerWave + j;
+            if (kInstr % kWaves != 0 && instr >= kInstr) {
+                break; // uniform: this wave's block ended
+            }
+            uint32_t offset = off[j];
+            if (!whole) {
+                int line, at;
+                place(j, line, at);
+                offset = at < rows_left && line < k_left ? offset : kDirectLimit;
+            }
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds + instr * 256, 16,
+                                                     static_cast<int>(offset), 0, 0, 0);
+        }
+    }
+};
+
+
+// Whether a loader declares kAlloc (the narrow loader's buffer size).
+template <typename L, typename = void> struct has_alloc : std::false_type {};
+template <typename L> struct has_alloc<L, std::void_t<decltype(L::kAlloc)>> : std::true_type {};
+
+// LDS floats a direct loader's buffer holds: the image, or for the narrow loader the whole
+// instructions that fill it (the last may run past the image).
+template <typename L> constexpr int direct_alloc() {
+    if constexpr (has_alloc<L>::value) {
+        return L::kAlloc;
+    } else {
+        return L::kFloats;
+    }
+}
+
+// A direct loader from the operand's strides: along its rows (M for A, N for B) and along k. The
+// narrow loader takes only the k stride (its lines are depth lines).
+template <typename L, bool NARROW> __device__ __forceinline__ L make_direct_loader(int64_t row_stride,
+                                                                                    int64_t k_stride) {
+    if constexpr (NARROW) {
+        return L(k_stride);
+    } else {
+        return L(row_stride, k_stride);
+    }
+}
+
 // The 256x256 tile (16 wavefronts of 64x64) with direct-to-LDS slices. The depth loop is
 // unrolled by two so each half knows at compile time which buffer it reads and which it fills;
 // the copy of slice s + 1 is issued before slice s's MFMAs and waited for (vmcnt 0) before the
@@ -721,19 +809,32 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_direct_kernel(Ge
     static_assert(KT % 8 == 0 && WM % 32 == 0 && WN % 32 == 0, "tile shape");
     // Two 4-byte K-major operands: 18 hoisted offsets do not fit beside the accumulators.
     constexpr bool kHoist = !(AK && BK && VA == 1 && VB == 1);
-    using LoadA = DirectSliceLoader<BM, KT, AK, VA, THREADS, kHoist>;
-    using LoadB = DirectSliceLoader<BN, KT, BK, VB, THREADS, kHoist>;
+    // An M/N-major operand whose lines are narrower than one 256-float wave-instruction (the
+    // 64x64 and 128x128 tiles) is filled as one run of 16-byte pieces over its padded image
+    // (DirectNarrowLoader, pitch ROWS + 8, the fragment reads' pitch).
+    constexpr bool kNarrowA = !AK && BM < 256;
+    constexpr bool kNarrowB = !BK && BN < 256;
+    static_assert((!kNarrowA || VA == 4) && (!kNarrowB || VB == 4),
+                  "narrow lines are copied in 16-byte pieces");
+    using LoadA = std::conditional_t<kNarrowA, DirectNarrowLoader<BM, KT, THREADS>,
+                                     DirectSliceLoader<BM, KT, AK, VA, THREADS, kHoist>>;
+    using LoadB = std::conditional_t<kNarrowB, DirectNarrowLoader<BN, KT, THREADS>,
+                                     DirectSliceLoader<BN, KT, BK, VB, THREADS, kHoist>>;
     using FragA = SliceLoader<BM, KT, AK, VA, THREADS>;
     using FragB = SliceLoader<BN, KT, BK, VB, THREADS>;
-    static_assert(LoadA::kFloats == FragA::kFloats && LoadB::kFloats == FragB::kFloats,
+    static_assert(LoadA::kFloats == FragA::kFloats && LoadB::kFloats == FragB::kFloats &&
+                      LoadA::kPitch == FragA::kPitch && LoadB::kPitch == FragB::kPitch,
                   "one LDS image");
+    // The narrow loader's last instruction may run past the image.
+    constexpr int kAllocA = direct_alloc<LoadA>();
+    constexpr int kAllocB = direct_alloc<LoadB>();
     // One LDS object per buffer: the compiler tells LDS objects apart, so it sees that the copy
     // into one buffer does not write the one the MFMAs read (within one object it would wait for
     // the copy to land before the first LDS read of every slice).
-    __shared__ __align__(16) float tile_a0[LoadA::kFloats];
-    __shared__ __align__(16) float tile_a1[LoadA::kFloats];
-    __shared__ __align__(16) float tile_b0[LoadB::kFloats];
-    __shared__ __align__(16) float tile_b1[LoadB::kFloats];
+    __shared__ __align__(16) float tile_a0[kAllocA];
+    __shared__ __align__(16) float tile_a1[kAllocA];
+    __shared__ __align__(16) float tile_b0[kAllocB];
+    __shared__ __align__(16) float tile_b1[kAllocB];
     // The tanh gelu's exp table, copied into LDS: the epilogue's per-lane reads of it then wait
     // on the LDS counter alone. From global memory, each value's wait for its table load would
     // also wait for the output stores issued before it (one counter covers both).
@@ -824,8 +925,8 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_direct_kernel(Ge
         const int64_t left = kk - s * KT;
         return left <= 0 ? 0 : left < KT ? static_cast<int>(left) : KT;
     };
-    const LoadA load_a(p.a_rs, p.a_cs);
-    const LoadB load_b(p.b_cs, p.b_rs);
+    const LoadA load_a = make_direct_loader<LoadA, kNarrowA>(p.a_rs, p.a_cs);
+    const LoadB load_b = make_direct_loader<LoadB, kNarrowB>(p.b_cs, p.b_rs);
     constexpr bool kHold = AK && BK;
     if (slices > 0) {
         load_a.issue(tile_a0, a_base, w.rows_a, k_left_of(0));
@@ -877,68 +978,6 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_direct_kernel(Ge
 }
 
 // ---- the paired form: 64 columns of an N-major B ----------------------------------------------
-
-// Direct-to-LDS copy of an M/N-major slice whose lines (KT of them, ROWS floats each, padded to
-// ROWS + 8) are narrower than one wave-instruction (ROWS = 64): the image is filled as one run
-// of floats, each lane's 4 floats (16 bytes, within one line) from wherever they live. The last
-// instruction may run past the image, so the LDS buffer holds kAlloc floats. Elements outside the
-// matrix and the pads get an offset past the record limit and load zeros.
-template <int ROWS, int KT, int THREADS> struct DirectNarrowLoader {
-    static constexpr int kPitch = ROWS + 8;
-    static constexpr int kFloats = KT * kPitch;
-    static constexpr int kInstr = (kFloats + 255) / 256;
-    static constexpr int kAlloc = kInstr * 256;
-    static constexpr int kWaves = THREADS / 64;
-    static constexpr int kPerWave = (kInstr + kWaves - 1) / kWaves;
-    uint32_t off[kPerWave]; // this lane's offsets in a whole slice
-    uint32_t k_bytes;
-
-    // (line, position) of this lane's 4 floats in instruction j of this wave; false past the
-    // image.
-    __device__ __forceinline__ static bool place(int j, int& line, int& at) {
-        const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / 64));
-        const int f = ((wave * kPerWave + j) * 64 + static_cast<int>(__lane_id())) * 4;
-        line = f / kPitch;
-        at = f - line * kPitch;
-        return f < kFloats;
-    }
-
-    __device__ __forceinline__ explicit DirectNarrowLoader(int64_t k_stride) {
-        k_bytes = static_cast<uint32_t>(k_stride) * 4u;
-#pragma unroll
-        for (int j = 0; j < kPerWave; ++j) {
-            int line, at;
-            const bool in_image = place(j, line, at);
-            off[j] = in_image && at < ROWS ? static_cast<uint32_t>(line) * k_bytes +
-                                                 static_cast<uint32_t>(at) * 4u
-                                           : kDirectLimit;
-        }
-    }
-
-    // base: element (depth 0, row 0) of the slice; rows_left / k_left as DirectSliceLoader's.
-    __device__ __forceinline__ void issue(float* lds, const float* base, int rows_left,
-                                          int k_left) const {
-        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float*>(base), 0, static_cast<int>(kDirectLimit - 1), kBufferWord3);
-        const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / 64));
-        const bool whole = rows_left >= ROWS && k_left >= KT;
-#pragma unroll
-        for (int j = 0; j < kPerWave; ++j) {
-            const int instr = wave * kPerWave + j;
-            if (kInstr % kWaves != 0 && instr >= kInstr) {
-                break; // uniform: this wave's block ended
-            }
-            uint32_t offset = off[j];
-            if (!whole) {
-                int line, at;
-                place(j, line, at);
-                offset = at < rows_left && line < k_left ? offset : kDirectLimit;
-            }
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds + instr * 256, 16,
-                                                     static_cast<int>(offset), 0, 0, 0);
-        }
-    }
-};
 
 // The 128x64 tile on a K-major A and an N-major B, both read by 16-byte direct-to-LDS loads:
 // attention's P V (128 x [1024 x 1024] x [1024 x 64]). Four wavefronts of 32 rows x all 64
