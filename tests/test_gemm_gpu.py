@@ -225,6 +225,7 @@ TILE_BN = {1: 256, 2: 128, 3: 64, 4: 128, 5: 64}  # output columns per tile, by 
     (2045, 2049, 1021, True),   # B read along k through a transposed view, staged as well
     (2045, 2049, 1023, False),  # one column (the 1-column kernel)
     (2045, 2050, 999, False),   # two columns, an odd depth (the copy's line padded by one zero)
+    (2045, 2051, 2101, False),  # rows loaded in three chunks of 1024 depths, the last partial
 ])
 def test_strip_stages_a_in_one_launch(stream, oracle, m, n, k, b_kmajor):
     """AUTO stages a K-major A whose rows 16-byte loads cannot take; when a peeled strip of at
