@@ -368,14 +368,12 @@ void launch_vec(const GemmParams& p, int va, int vb, unsigned blocks, hipStream_
 template <bool AK, bool BK>
 void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned blocks, bool one_per_cu,
                    bool direct_ok, hipStream_t stream) {
-    // With one workgroup per CU, no split, 16-byte operands and only whole tiles, the 64x64 and
-    // 128x128 tiles run the direct-to-LDS kernel (one accumulation chain, the tile kernels' depth
-    // order) in place of the wavefront sets: 1024^3 NN 29.1 -> 26.3 us on 64x64, 2048^3 NN
-    // 151.2 -> 137.8 us on 128x128. Ragged edges keep the sets (1000^3: 28.1 against 31.6 us on
-    // the direct form, whose edge slices work out each lane's element).
-    const auto direct_mid = [&](int64_t bm, int64_t bn) {
-        return one_per_cu && p.splits == 1 && direct_ok && va == 4 && vb == 4 && p.m % bm == 0 &&
-               p.n % bn == 0;
+    // With one workgroup per CU, no split and 16-byte operands, the 64x64 and 128x128 tiles run
+    // the direct-to-LDS kernel (one accumulation chain, the tile kernels' depth order) in place of
+    // the wavefront sets: 1024^3 NN 29.1 -> 26.3 us on 64x64, 2048^3 NN 151.2 -> 137.8 us on
+    // 128x128.
+    const auto direct_mid = [&]() {
+        return one_per_cu && p.splits == 1 && direct_ok && va == 4 && vb == 4;
     };
     switch (tile) {
     case MFR_TILE_256x256:
@@ -399,7 +397,7 @@ void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned block
         launch_vec<64, 128, 16, 2, 2, AK, BK>(p, va, vb, blocks, stream);
         break;
     case MFR_TILE_64x64:
-        if (direct_mid(64, 64)) {
+        if (direct_mid()) {
             sgemm_direct_kernel<64, 64, 32, 2, 2, AK, BK, 4, 4><<<blocks, 256, 0, stream>>>(p);
         } else if (one_per_cu && p.splits == 1) {
             // 16 wavefronts: four sets of 2x2 share each 64-deep slice (4 per SIMD). 1024^3:
@@ -411,7 +409,7 @@ void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned block
         }
         break;
     default:
-        if (direct_mid(128, 128)) {
+        if (direct_mid()) {
             sgemm_direct_kernel<128, 128, 32, 4, 4, AK, BK, 4, 4><<<blocks, 1024, 0, stream>>>(p);
         } else if (one_per_cu && p.splits == 1) {
             // 16 wavefronts: two sets of 2x4 share each 64-deep slice (4 per SIMD). 2048^3:

@@ -595,18 +595,23 @@ struct DirectSliceLoader {
     // (the line and the instruction's place in it come as the scalar offset).
     uint32_t off[KMAJ && HOIST ? kPerWave : 1];
     uint32_t row_bytes, k_bytes;
+    int rows; // rows of the tile inside the matrix (at most ROWS), fixed for the depth loop
 
-    // The K-major offset of this lane in instruction j of this wave.
+    // The K-major offset of this lane in instruction j of this wave; the limit for a row outside
+    // the matrix.
     __device__ __forceinline__ uint32_t kmaj_offset(int j) const {
         const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / 64));
         const int f = ((wave * kPerWave + j) * 64 + static_cast<int>(__lane_id())) * V;
         const int row = f / kPitch;
         const int at = f - row * kPitch;
         const int d = at < KT ? at : KT - V;
-        return static_cast<uint32_t>(row) * row_bytes + static_cast<uint32_t>(d) * 4u;
+        return row < rows ? static_cast<uint32_t>(row) * row_bytes + static_cast<uint32_t>(d) * 4u
+                          : kDirectLimit;
     }
 
-    __device__ __forceinline__ DirectSliceLoader(int64_t row_stride, int64_t k_stride) {
+    __device__ __forceinline__ DirectSliceLoader(int64_t row_stride, int64_t k_stride,
+                                                 int rows_inside)
+        : rows(rows_inside) {
         row_bytes = static_cast<uint32_t>(row_stride) * 4u;
         k_bytes = static_cast<uint32_t>(k_stride) * 4u;
         if constexpr (KMAJ && HOIST) {
@@ -634,15 +639,17 @@ struct DirectSliceLoader {
         }
     }
 
-    // base: element (row 0, depth 0) of the slice; rows_left / k_left: rows and depths inside
-    // (a multiple of V along the unit-stride dimension). A whole slice uses the fixed offsets;
-    // an edge slice works out each lane's element and sends the ones outside to the limit.
-    __device__ __forceinline__ void issue(float* lds, const float* base, int rows_left,
-                                          int k_left) const {
+    // base: element (row 0, depth 0) of the slice; k_left: depths inside (a multiple of V when
+    // k is the unit-stride dimension). A full-depth slice uses the fixed offsets, whose rows
+    // outside the matrix already point at the limit (K-major), or compares each lane's row (a
+    // depth line; no division, and only in a tile with rows outside). A partial-depth slice (the
+    // last) works out each lane's element and sends the ones outside to the limit.
+    __device__ __forceinline__ void issue(float* lds, const float* base, int k_left) const {
         const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<float*>(base), 0, static_cast<int>(kDirectLimit - 1), kBufferWord3);
         const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / 64));
-        if (rows_left >= ROWS && k_left >= KT) {
+        const int lane = static_cast<int>(__lane_id());
+        if (k_left >= KT) {
 #pragma unroll
             for (int j = 0; j < kPerWave; ++j) {
                 const int instr = wave * kPerWave + j;
@@ -654,17 +661,23 @@ struct DirectSliceLoader {
                          0u);
                 } else {
                     // The line and the instruction's place in it come as the scalar offset (the
-                    // immediate offset would move the LDS destination as well).
+                    // immediate offset would move the LDS destination as well). A lane outside
+                    // the matrix sends its offset to the limit; the scalar part stays below 2^30,
+                    // so the sum does not wrap back into the record.
                     const int line = instr / kPerLine;
                     const int q = instr % kPerLine;
-                    load(rsrc, lds + line * kPitch + q * 64 * V, off[0],
+                    uint32_t voffset = off[0];
+                    if (rows < ROWS) {
+                        voffset = q * 64 * V + lane * V < rows ? voffset : kDirectLimit;
+                    }
+                    load(rsrc, lds + line * kPitch + q * 64 * V, voffset,
                          static_cast<uint32_t>(line) * k_bytes +
                              static_cast<uint32_t>(q * 64 * V * 4));
                 }
             }
             return;
         }
-        const int lane = static_cast<int>(__lane_id());
+        const int rows_left = rows;
         const int depth_end = k_left < KT ? k_left : KT; // depths of the slice inside the matrix
 #pragma unroll
         for (int j = 0; j < kPerWave; ++j) {
@@ -711,7 +724,7 @@ template <int ROWS, int KT, int THREADS> struct DirectNarrowLoader {
     static constexpr int kAlloc = kInstr * 256;
     static constexpr int kWaves = THREADS / 64;
     static constexpr int kPerWave = (kInstr + kWaves - 1) / kWaves;
-    uint32_t off[kPerWave]; // this lane's offsets in a whole slice
+    uint32_t off[kPerWave]; // this lane's offsets in a full-depth slice (the limit outside)
     uint32_t k_bytes;
 
     // (line, position) of this lane's 4 floats in instruction j of this wave; false past the
@@ -724,25 +737,26 @@ template <int ROWS, int KT, int THREADS> struct DirectNarrowLoader {
         return f < kFloats;
     }
 
-    __device__ __forceinline__ explicit DirectNarrowLoader(int64_t k_stride) {
+    // rows_inside: rows of the tile inside the matrix (at most ROWS); the others load zeros.
+    __device__ __forceinline__ DirectNarrowLoader(int64_t k_stride, int rows_inside) {
         k_bytes = static_cast<uint32_t>(k_stride) * 4u;
 #pragma unroll
         for (int j = 0; j < kPerWave; ++j) {
             int line, at;
             const bool in_image = place(j, line, at);
-            off[j] = in_image && at < ROWS ? static_cast<uint32_t>(line) * k_bytes +
-                                                 static_cast<uint32_t>(at) * 4u
-                                           : kDirectLimit;
+            off[j] = in_image && at < ROWS && at < rows_inside
+                         ? static_cast<uint32_t>(line) * k_bytes + static_cast<uint32_t>(at) * 4u
+                         : kDirectLimit;
         }
     }
 
-    // base: element (depth 0, row 0) of the slice; rows_left / k_left as DirectSliceLoader's.
-    __device__ __forceinline__ void issue(float* lds, const float* base, int rows_left,
-                                          int k_left) const {
+    // base: element (depth 0, row 0) of the slice; k_left as DirectSliceLoader's. Only a
+    // partial-depth slice (the last) works out each lane's depth line.
+    __device__ __forceinline__ void issue(float* lds, const float* base, int k_left) const {
         const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<float*>(base), 0, static_cast<int>(kDirectLimit - 1), kBufferWord3);
         const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / 64));
-        const bool whole = rows_left >= ROWS && k_left >= KT;
+        const bool whole = k_left >= KT;
 #pragma unroll
         for (int j = 0; j < kPerWave; ++j) {
             const int instr = wave * kPerWave + j;
@@ -753,7 +767,7 @@ template <int ROWS, int KT, int THREADS> struct DirectNarrowLoader {
             if (!whole) {
                 int line, at;
                 place(j, line, at);
-                offset = at < rows_left && line < k_left ? offset : kDirectLimit;
+                offset = line < k_left ? offset : kDirectLimit;
             }
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, lds + instr * 256, 16,
                                                      static_cast<int>(offset), 0, 0, 0);
@@ -778,12 +792,12 @@ template <typename L> constexpr int direct_alloc() {
 
 // A direct loader from the operand's strides: along its rows (M for A, N for B) and along k. The
 // narrow loader takes only the k stride (its lines are depth lines).
-template <typename L, bool NARROW> __device__ __forceinline__ L make_direct_loader(int64_t row_stride,
-                                                                                    int64_t k_stride) {
+template <typename L, bool NARROW>
+__device__ __forceinline__ L make_direct_loader(int64_t row_stride, int64_t k_stride, int rows) {
     if constexpr (NARROW) {
-        return L(k_stride);
+        return L(k_stride, rows);
     } else {
-        return L(row_stride, k_stride);
+        return L(row_stride, k_stride, rows);
     }
 }
 
@@ -925,12 +939,12 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_direct_kernel(Ge
         const int64_t left = kk - s * KT;
         return left <= 0 ? 0 : left < KT ? static_cast<int>(left) : KT;
     };
-    const LoadA load_a = make_direct_loader<LoadA, kNarrowA>(p.a_rs, p.a_cs);
-    const LoadB load_b = make_direct_loader<LoadB, kNarrowB>(p.b_cs, p.b_rs);
+    const LoadA load_a = make_direct_loader<LoadA, kNarrowA>(p.a_rs, p.a_cs, w.rows_a);
+    const LoadB load_b = make_direct_loader<LoadB, kNarrowB>(p.b_cs, p.b_rs, w.rows_b);
     constexpr bool kHold = AK && BK;
     if (slices > 0) {
-        load_a.issue(tile_a0, a_base, w.rows_a, k_left_of(0));
-        load_b.issue(tile_b0, b_base, w.rows_b, k_left_of(0));
+        load_a.issue(tile_a0, a_base, k_left_of(0));
+        load_b.issue(tile_b0, b_base, k_left_of(0));
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if constexpr (kHold) {
@@ -940,8 +954,8 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_direct_kernel(Ge
     for (int64_t s = 0; s < slices; s += 2) {
         // Slice s from buffer 0; slice s + 1 (zeros past the end) into buffer 1, whose last
         // reads came before the previous barrier.
-        load_a.issue(tile_a1, a_base + (s + 1) * a_step, w.rows_a, k_left_of(s + 1));
-        load_b.issue(tile_b1, b_base + (s + 1) * b_step, w.rows_b, k_left_of(s + 1));
+        load_a.issue(tile_a1, a_base + (s + 1) * a_step, k_left_of(s + 1));
+        load_b.issue(tile_b1, b_base + (s + 1) * b_step, k_left_of(s + 1));
         if constexpr (kHold) {
             body(tile_a0, tile_b0);
         } else {
@@ -956,8 +970,8 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_direct_kernel(Ge
         // Slice s + 1 from buffer 1; slice s + 2 into buffer 0 (all of whose reads came before
         // the barrier above).
         if (s + 2 < slices) {
-            load_a.issue(tile_a0, a_base + (s + 2) * a_step, w.rows_a, k_left_of(s + 2));
-            load_b.issue(tile_b0, b_base + (s + 2) * b_step, w.rows_b, k_left_of(s + 2));
+            load_a.issue(tile_a0, a_base + (s + 2) * a_step, k_left_of(s + 2));
+            load_b.issue(tile_b0, b_base + (s + 2) * b_step, k_left_of(s + 2));
         }
         if constexpr (kHold) {
             body(tile_a1, tile_b1);
@@ -1053,23 +1067,23 @@ __global__ __launch_bounds__(256) void sgemm_pair_kernel(GemmParams p) {
         const int64_t left = kk - s * KT;
         return left <= 0 ? 0 : left < KT ? static_cast<int>(left) : KT;
     };
-    const LoadA load_a(p.a_rs, p.a_cs);
-    const LoadB load_b(p.b_rs);
+    const LoadA load_a(p.a_rs, p.a_cs, w.rows_a);
+    const LoadB load_b(p.b_rs, w.rows_b);
     if (slices > 0) {
-        load_a.issue(tile_a0, a_base, w.rows_a, k_left_of(0));
-        load_b.issue(tile_b0, b_base, w.rows_b, k_left_of(0));
+        load_a.issue(tile_a0, a_base, k_left_of(0));
+        load_b.issue(tile_b0, b_base, k_left_of(0));
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
     }
     for (int64_t s = 0; s < slices; s += 2) {
-        load_a.issue(tile_a1, a_base + (s + 1) * a_step, w.rows_a, k_left_of(s + 1));
-        load_b.issue(tile_b1, b_base + (s + 1) * b_step, w.rows_b, k_left_of(s + 1));
+        load_a.issue(tile_a1, a_base + (s + 1) * a_step, k_left_of(s + 1));
+        load_b.issue(tile_b1, b_base + (s + 1) * b_step, k_left_of(s + 1));
         slice(tile_a0, tile_b0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (s + 2 < slices) {
-            load_a.issue(tile_a0, a_base + (s + 2) * a_step, w.rows_a, k_left_of(s + 2));
-            load_b.issue(tile_b0, b_base + (s + 2) * b_step, w.rows_b, k_left_of(s + 2));
+            load_a.issue(tile_a0, a_base + (s + 2) * a_step, k_left_of(s + 2));
+            load_b.issue(tile_b0, b_base + (s + 2) * b_step, k_left_of(s + 2));
         }
         slice(tile_a1, tile_b1);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");

@@ -1192,14 +1192,17 @@ def test_repeated_shapes_with_new_operands(stream, oracle):
     (mf.abi.TILE_128x128, 300, 260, 1023), (mf.abi.TILE_128x128, 129, 127, 70),
     (mf.abi.TILE_64x64, 1024, 1024, 1000), (mf.abi.TILE_64x64, 1024, 1024, 1023),
     (mf.abi.TILE_64x64, 512, 256, 36), (mf.abi.TILE_128x128, 2048, 2048, 300),
-    (mf.abi.TILE_128x128, 1024, 2048, 1023), (mf.abi.TILE_128x128, 128, 128, 4)])
+    (mf.abi.TILE_128x128, 1024, 2048, 1023), (mf.abi.TILE_128x128, 128, 128, 4),
+    (mf.abi.TILE_128x128, 1500, 1460, 300), (mf.abi.TILE_64x64, 1000, 940, 68),
+    (mf.abi.TILE_128x128, 4, 8, 40)])
 def test_exact_sixteen_wave_set_forms(stream, tile, m, n, k):
-    """Unsplit with at most one workgroup per CU, the 64x64 tile runs 16 wavefronts in four sets
-    and the 128x128 tile 16 in two, the sets sharing each depth slice and adding their
-    accumulators through LDS; when both operands take 16-byte loads and the output has whole
-    tiles only, the direct-to-LDS kernel runs instead (one chain per lane). Either way bits equal
-    the exact result in all four layouts (4-byte loads, so the sets, for odd k), with alpha,
-    beta*C0 and a bias."""
+    """Unsplit with at most one workgroup per CU, the 64x64 and 128x128 tiles run the
+    direct-to-LDS kernel (one chain per lane) when both operands take 16-byte loads, edge tiles
+    included (their rows outside the matrix load zeros through the fixed offsets); with a 4-byte
+    operand the 64x64 tile runs 16 wavefronts in four sets and the 128x128 tile 16 in two, the
+    sets sharing each depth slice and adding their accumulators through LDS. Either way bits
+    equal the exact result in all four layouts (4-byte loads, so the sets, for odd k), with
+    alpha, beta*C0 and a bias."""
     size = 64 if tile == mf.abi.TILE_64x64 else 128
     assert ((m + size - 1) // size) * ((n + size - 1) // size) <= mf.device_info(0).compute_units
     a = quarter_matrix(m, k, 91)
