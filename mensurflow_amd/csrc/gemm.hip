@@ -370,8 +370,9 @@ void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned block
                    bool direct_ok, hipStream_t stream) {
     // With one workgroup per CU, no split and 16-byte operands, the 64x64 and 128x128 tiles run
     // the direct-to-LDS kernel (one accumulation chain, the tile kernels' depth order) in place of
-    // the wavefront sets: 1024^3 NN 29.1 -> 26.3 us on 64x64, 2048^3 NN 151.2 -> 137.8 us on
-    // 128x128.
+    // the wavefront sets, on slices as deep as the CU's LDS allows (128 and 64: 138-148 KiB), so
+    // each slice's MFMA work covers the next slice's load: 1024^3 28.9-29.5 -> 25.1-25.4 us,
+    // 2048^3 146.2-152.2 -> 135.7-138.3 us across the four layouts.
     const auto direct_mid = [&]() {
         return one_per_cu && p.splits == 1 && direct_ok && va == 4 && vb == 4;
     };
@@ -398,7 +399,7 @@ void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned block
         break;
     case MFR_TILE_64x64:
         if (direct_mid()) {
-            sgemm_direct_kernel<64, 64, 32, 2, 2, AK, BK, 4, 4><<<blocks, 256, 0, stream>>>(p);
+            sgemm_direct_kernel<64, 64, 128, 2, 2, AK, BK, 4, 4><<<blocks, 256, 0, stream>>>(p);
         } else if (one_per_cu && p.splits == 1) {
             // 16 wavefronts: four sets of 2x2 share each 64-deep slice (4 per SIMD). 1024^3:
             // 31.0 -> 27.7 us; 16384 x 4 x 4096: 113.7 -> 94.2 us. Split depth ranges are
@@ -410,7 +411,7 @@ void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned block
         break;
     default:
         if (direct_mid()) {
-            sgemm_direct_kernel<128, 128, 32, 4, 4, AK, BK, 4, 4><<<blocks, 1024, 0, stream>>>(p);
+            sgemm_direct_kernel<128, 128, 64, 4, 4, AK, BK, 4, 4><<<blocks, 1024, 0, stream>>>(p);
         } else if (one_per_cu && p.splits == 1) {
             // 16 wavefronts: two sets of 2x4 share each 64-deep slice (4 per SIMD). 2048^3:
             // 150.2 -> 145.6 us; 2048 x 2048 x 8192: 583.9 -> 560.9 us (32-deep slices: 149.3

@@ -886,7 +886,10 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_direct_kernel(Ge
     constexpr int KG = KT / 8;
     static_assert(KG % 2 == 0, "a slice's first group takes register set 0");
     [[maybe_unused]] float fa[2][FM][4], fb[2][FN][4];
-    const auto frags = [&](int set, const float* sa, const float* sb, int g) {
+    // The slice lambdas capture the accumulators by reference and are always inlined: one left
+    // as a call (deep slices make them long) would keep the accumulators in scratch memory.
+    const auto frags = [&](int set, const float* sa, const float* sb, int g)
+                           __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
             FragA::fragment(sa, wave_m * WM + i * 32 + r32, g, half, fa[set][i]);
@@ -896,7 +899,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_direct_kernel(Ge
             FragB::fragment(sb, wave_n * WN + j * 32 + r32, g, half, fb[set][j]);
         }
     };
-    const auto mfmas = [&](int set) {
+    const auto mfmas = [&](int set) __attribute__((always_inline)) {
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
 #pragma unroll
@@ -911,18 +914,26 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void sgemm_direct_kernel(Ge
         }
     };
     // Groups 0 .. KG - 2 of the slice in (sa, sb), each after the next group's reads (the
-    // scheduling barriers keep the reads ahead of the MFMAs that do not need them).
-    const auto body = [&](const float* sa, const float* sb) {
+    // scheduling barriers keep the reads ahead of the MFMAs that do not need them). Two groups
+    // per step, so each names its register set as a constant even where the loop stays rolled
+    // (a set index known only at run time puts both sets in scratch memory).
+    const auto body = [&](const float* sa, const float* sb) __attribute__((always_inline)) {
 #pragma unroll
-        for (int g = 0; g + 1 < KG; ++g) {
-            frags((g + 1) & 1, sa, sb, g + 1);
+        for (int g = 0; g + 1 < KG; g += 2) {
+            frags(1, sa, sb, g + 1);
             __builtin_amdgcn_sched_barrier(0);
-            mfmas(g & 1);
+            mfmas(0);
             __builtin_amdgcn_sched_barrier(0);
+            if (g + 2 < KG) {
+                frags(0, sa, sb, g + 2);
+                __builtin_amdgcn_sched_barrier(0);
+                mfmas(1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     };
     // After the slice barrier: the next slice's first fragments, then the held-back last group.
-    const auto cross = [&](const float* na, const float* nb) {
+    const auto cross = [&](const float* na, const float* nb) __attribute__((always_inline)) {
         frags(0, na, nb, 0);
         __builtin_amdgcn_sched_barrier(0);
         mfmas((KG - 1) & 1);
