@@ -363,18 +363,33 @@ void launch_vec(const GemmParams& p, int va, int vb, unsigned blocks, hipStream_
 // CU the 4 wavefronts are faster (4096^3 1075 against 1105 us). Unsplit, the 128x128 tile
 // then runs 16 wavefronts in two sets and the 64x64 tile 16 in four, the sets sharing each
 // depth slice.
-// direct_ok: each depth slice's byte offsets fit the direct-to-LDS loaders' 32 bits (as
-// big_tile_ok checks for 256 rows, which covers the smaller tiles).
+// Whether the direct-to-LDS loaders' 32-bit byte offsets hold a bm x kt slice of A and a bn x kt
+// slice of B: every element of a slice lies below 2^30 bytes from its first (A(m, k) at
+// a + m a_rs + k a_cs, B(k, n) at b + k b_rs + n b_cs; a K-major operand's lines are its rows, an
+// M/N-major one's its depths, so deep slices of an M/N-major operand span kt - 1 line strides).
+template <bool AK, bool BK>
+bool direct_slices_fit(const GemmParams& p, int64_t bm, int64_t bn, int64_t kt) {
+    const auto extent = [kt](bool kmaj, int64_t rows, int64_t line) {
+        return kmaj ? (rows - 1) * line + kt : (kt - 1) * line + rows;
+    };
+    const int64_t a_line = AK ? p.a_rs : p.a_cs;
+    const int64_t b_line = BK ? p.b_cs : p.b_rs;
+    constexpr int64_t kLimit = int64_t{1} << 28; // floats
+    return a_line >= 0 && b_line >= 0 && a_line < kLimit && b_line < kLimit &&
+           extent(AK, bm, a_line) < kLimit && extent(BK, bn, b_line) < kLimit;
+}
+
 template <bool AK, bool BK>
 void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned blocks, bool one_per_cu,
-                   bool direct_ok, hipStream_t stream) {
+                   hipStream_t stream) {
     // With one workgroup per CU, no split and 16-byte operands, the 64x64 and 128x128 tiles run
     // the direct-to-LDS kernel (one accumulation chain, the tile kernels' depth order) in place of
     // the wavefront sets, on slices as deep as the CU's LDS allows (128 and 64: 138-148 KiB), so
     // each slice's MFMA work covers the next slice's load: 1024^3 28.9-29.5 -> 25.1-25.4 us,
     // 2048^3 146.2-152.2 -> 135.7-138.3 us across the four layouts.
-    const auto direct_mid = [&]() {
-        return one_per_cu && p.splits == 1 && direct_ok && va == 4 && vb == 4;
+    const auto direct_mid = [&](int64_t bm, int64_t bn, int64_t kt) {
+        return one_per_cu && p.splits == 1 && va == 4 && vb == 4 &&
+               direct_slices_fit<AK, BK>(p, bm, bn, kt);
     };
     switch (tile) {
     case MFR_TILE_256x256:
@@ -398,7 +413,7 @@ void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned block
         launch_vec<64, 128, 16, 2, 2, AK, BK>(p, va, vb, blocks, stream);
         break;
     case MFR_TILE_64x64:
-        if (direct_mid()) {
+        if (direct_mid(64, 64, 128)) {
             sgemm_direct_kernel<64, 64, 128, 2, 2, AK, BK, 4, 4><<<blocks, 256, 0, stream>>>(p);
         } else if (one_per_cu && p.splits == 1) {
             // 16 wavefronts: four sets of 2x2 share each 64-deep slice (4 per SIMD). 1024^3:
@@ -410,7 +425,7 @@ void launch_layout(int tile, const GemmParams& p, int va, int vb, unsigned block
         }
         break;
     default:
-        if (direct_mid()) {
+        if (direct_mid(128, 128, 64)) {
             sgemm_direct_kernel<128, 128, 64, 4, 4, AK, BK, 4, 4><<<blocks, 1024, 0, stream>>>(p);
         } else if (one_per_cu && p.splits == 1) {
             // 16 wavefronts: two sets of 2x4 share each 64-deep slice (4 per SIMD). 2048^3:
@@ -1093,17 +1108,16 @@ void launch_region(const Plan& plan, const GemmParams& p, const Region& r, int v
     q.stream_c = q.partial == nullptr && streamed_output(q) ? 1 : 0;
     const unsigned grid = static_cast<unsigned>(blocks);
     const bool one_per_cu = blocks <= cus;
-    const bool direct_ok = big_tile_ok(plan);
     if (tile == MFR_TILE_128x64 && pair_fits(plan, q, va, vb)) {
         sgemm_pair_kernel<32><<<grid, 256, 0, stream>>>(q);
     } else if (plan.ak && plan.bk) {
-        launch_layout<true, true>(tile, q, va, vb, grid, one_per_cu, direct_ok, stream);
+        launch_layout<true, true>(tile, q, va, vb, grid, one_per_cu, stream);
     } else if (plan.ak) {
-        launch_layout<true, false>(tile, q, va, vb, grid, one_per_cu, direct_ok, stream);
+        launch_layout<true, false>(tile, q, va, vb, grid, one_per_cu, stream);
     } else if (plan.bk) {
-        launch_layout<false, true>(tile, q, va, vb, grid, one_per_cu, direct_ok, stream);
+        launch_layout<false, true>(tile, q, va, vb, grid, one_per_cu, stream);
     } else {
-        launch_layout<false, false>(tile, q, va, vb, grid, one_per_cu, direct_ok, stream);
+        launch_layout<false, false>(tile, q, va, vb, grid, one_per_cu, stream);
     }
     mfr::check_launch("sgemm_kernel");
     if (q.partial != nullptr) {

@@ -1185,6 +1185,28 @@ def test_repeated_shapes_with_new_operands(stream, oracle):
         check_guards(buf)
 
 
+@pytest.mark.parametrize("tile,k,line", [(mf.abi.TILE_64x64, 128, 2**22 + 2**18),
+                                         (mf.abi.TILE_128x128, 64, 2**23 + 2**19)])
+def test_deep_slices_with_long_lines(stream, tile, k, line):
+    """The one-workgroup-per-CU 64x64 and 128x128 tiles read 128- and 64-deep slices straight
+    into LDS through 32-bit byte offsets. An N-major B whose line stride puts such a slice past
+    2^31 bytes (127 or 63 lines of ~17.8 or ~35.7 MB), while a 32-deep slice would stay inside,
+    must not take that form: the product runs on the wavefront sets instead, exact."""
+    size = 64 if tile == mf.abi.TILE_64x64 else 128
+    a = quarter_matrix(size, k, 141)
+    b = quarter_matrix(k, size, 142)
+    stored = np.zeros((k, line), np.float32)  # ~2.3 GB, mostly untouched zero pages
+    stored[:, :size] = b
+    b_store = dev(stored, stream)
+    del stored
+    c, buf = guarded_output(stream, (size, size))
+    mf.gemm(dev(a, stream), b_store.slice(1, 0, size), out=c, tile=tile, splits=1,
+            stage=mf.abi.STAGE_NEVER)
+    assert same_bits(c.numpy(), exact_product(a, b))
+    check_guards(buf)
+    b_store.close()
+
+
 @pytest.mark.parametrize("tile,m,n,k", [
     (mf.abi.TILE_64x64, 1000, 1000, 1000), (mf.abi.TILE_64x64, 300, 260, 1023),
     (mf.abi.TILE_64x64, 64, 64, 2000), (mf.abi.TILE_64x64, 37, 100, 65),
